@@ -1,0 +1,318 @@
+"""ctypes front end of the CPU oracle (TEST INFRASTRUCTURE, not product code).
+
+Loads ``oracle/liboracle_pbmoe.so`` (built by ``oracle/Makefile``), a plain-C
+restatement of the reference's CPU arithmetic for the FlashMoE MoE block.
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg may import this module; the product path never does.
+
+Each wrapper names the reference function it restates (paths relative to
+``src/inference/flashmoe/`` of Jc2k/pb).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle_pbmoe.so")
+
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+ORDER_CANONICAL, ORDER_REFERENCE_SLOT = 0, 1
+NORM_RENORMALIZE, NORM_DEEPSEEK_FLOOR, NORM_PRESERVE_FULL = 0, 1, 2
+ROUTING_SOFTMAX, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED = 0, 1, 2
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run make -C oracle)")
+        _lib = C.CDLL(LIB_PATH)
+    return _lib
+
+
+def _p(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def router_logits(w: np.ndarray, x: np.ndarray, dtype: int = DT_F16) -> np.ndarray:
+    """weights/store.rs:880-897 — sequential mul-then-add per expert row."""
+    w = np.ascontiguousarray(w)
+    x = _f32(x)
+    experts, hidden = w.shape
+    out = np.empty(experts, np.float32)
+    lib().or_router_logits(_p(w), C.c_int(dtype), _p(x), C.c_int(experts), C.c_int(hidden), _p(out))
+    return out
+
+
+def routing_top_k(scores, k: int):
+    """math.rs:746-769 — replacement-slot scan, slot order."""
+    s = _f32(scores)
+    ids = np.empty(max(k, 1), np.int32)
+    vals = np.empty(max(k, 1), np.float32)
+    n = lib().or_routing_top_k(_p(s), C.c_int(s.size), C.c_int(k), _p(ids), _p(vals))
+    return ids[:n].tolist(), vals[:n].tolist()
+
+
+def top_k_sorted(scores, k: int):
+    """math.rs:710-726 — stable sort, score desc then index asc."""
+    s = _f32(scores)
+    ids = np.empty(max(k, 1), np.int32)
+    vals = np.empty(max(k, 1), np.float32)
+    n = lib().or_top_k_sorted(_p(s), C.c_int(s.size), C.c_int(k), _p(ids), _p(vals))
+    return ids[:n].tolist(), vals[:n].tolist()
+
+
+def softmax_in_place(values) -> np.ndarray:
+    """math.rs:728-744."""
+    v = _f32(values).copy()
+    lib().or_softmax_in_place(_p(v), C.c_int(v.size))
+    return v
+
+
+def routing_softmax_top_k(logits, k: int, order: int = ORDER_REFERENCE_SLOT):
+    """math.rs:771-783."""
+    s = _f32(logits)
+    ids = np.empty(max(k, 1), np.int32)
+    p = np.empty(max(k, 1), np.float32)
+    n = lib().or_routing_softmax_top_k(_p(s), C.c_int(s.size), C.c_int(k), C.c_int(order), _p(ids), _p(p))
+    return ids[:n].tolist(), p[:n].copy()
+
+
+def routing_sigmoid_noaux_top_k(logits, bias, k: int, order: int = ORDER_REFERENCE_SLOT):
+    """math.rs:788-819."""
+    s = _f32(logits)
+    b = _f32(bias)
+    assert s.size == b.size
+    ids = np.empty(max(k, 1), np.int32)
+    w = np.empty(max(k, 1), np.float32)
+    n = lib().or_routing_sigmoid_noaux_top_k(_p(s), _p(b), C.c_int(s.size), C.c_int(k), C.c_int(order), _p(ids), _p(w))
+    return ids[:n].tolist(), w[:n].copy()
+
+
+def routing_sigmoid_grouped_top_k(logits, bias, k: int, n_group: int, topk_group: int):
+    """DeepSeek-V3 group-limited noaux routing (no reference implementation;
+    parity unpinned beyond the n_group=1 reduction to math.rs:788-819)."""
+    s = _f32(logits)
+    b = _f32(bias)
+    ids = np.empty(max(k, 1), np.int32)
+    w = np.empty(max(k, 1), np.float32)
+    n = lib().or_routing_sigmoid_grouped_top_k(_p(s), _p(b), C.c_int(s.size), C.c_int(k), C.c_int(n_group),
+                                               C.c_int(topk_group), _p(ids), _p(w))
+    if n < 0:
+        raise ValueError("invalid grouped routing shape")
+    return ids[:n].tolist(), w[:n].copy()
+
+
+def renormalize(p, policy: int, routed_scale: float):
+    """scheduler/expert_access.rs:80-135; returns (status, weights)."""
+    pp = _f32(p)
+    w = np.zeros(max(pp.size, 1), np.float32)
+    rc = lib().or_renormalize(_p(pp), C.c_int(pp.size), C.c_int(policy), C.c_float(routed_scale), _p(w))
+    return rc, w[: pp.size].copy()
+
+
+def validate_preselected(ids, scores, active_experts: int, experts: int) -> int:
+    """scheduler/protocol.rs:1044-1081; 0 = ok."""
+    i = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+    s = _f32(scores)
+    return lib().or_validate_preselected(_p(i), _p(s), C.c_int(i.size), C.c_int(active_experts), C.c_int(experts))
+
+
+def q4_dequantize_rows(packed, scales, biases, rows: int, cols: int, group: int, sb_dtype: int = DT_F32):
+    """math.rs:913-954 — w = fma(q, s, b)."""
+    pk = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
+    sc, bi = _sb(scales, sb_dtype), _sb(biases, sb_dtype)
+    out = np.empty(rows * cols, np.float32)
+    rc = lib().or_q4_dequantize_rows(_p(pk), _p(sc), _p(bi), C.c_int(sb_dtype), C.c_int(rows), C.c_int(cols),
+                                     C.c_int(group), _p(out))
+    assert rc == 0
+    return out.reshape(rows, cols)
+
+
+def _sb(a, dtype):
+    if dtype == DT_F32:
+        return _f32(a)
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint16))
+
+
+def q4_fma_matvec(packed, x, scales, biases, rows: int, cols: int, group: int, sb_dtype: int = DT_F32):
+    """math.rs:861-911 — acc += fma(q, s*x, b*x)."""
+    pk = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
+    sc, bi = _sb(scales, sb_dtype), _sb(biases, sb_dtype)
+    xx = _f32(x)
+    out = np.empty(rows, np.float32)
+    rc = lib().or_q4_fma_matvec(_p(pk), _p(xx), _p(sc), _p(bi), C.c_int(sb_dtype), C.c_int(rows), C.c_int(cols),
+                                C.c_int(group), _p(out))
+    assert rc == 0
+    return out
+
+
+def q4_explicit_matvec(packed, x, scales, biases, rows: int, cols: int, group: int, sb_dtype: int = DT_F32):
+    """tests/scheduler.rs:308-325 — sum of (q*s+b)*x."""
+    pk = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
+    sc, bi = _sb(scales, sb_dtype), _sb(biases, sb_dtype)
+    xx = _f32(x)
+    out = np.empty(rows, np.float32)
+    lib().or_q4_explicit_matvec(_p(pk), _p(xx), _p(sc), _p(bi), C.c_int(sb_dtype), C.c_int(rows), C.c_int(cols),
+                                C.c_int(group), _p(out))
+    return out
+
+
+def swiglu(g, u) -> np.ndarray:
+    gg, uu = _f32(g), _f32(u)
+    out = np.empty_like(gg)
+    lib().or_swiglu(_p(gg), _p(uu), C.c_int(gg.size), _p(out))
+    return out
+
+
+def rms_norm(x, w=None, eps: float = 1e-6) -> np.ndarray:
+    """math.rs:147-167."""
+    xx = _f32(x)
+    out = np.empty_like(xx)
+    ww = _f32(w) if w is not None else None
+    lib().or_rms_norm(_p(xx), _p(ww) if ww is not None else None, C.c_int(xx.size), C.c_float(eps), _p(out))
+    return out
+
+
+def layer_major_union(ids: np.ndarray, experts: int):
+    """scheduler/mod.rs:685-769 — sorted unique union + route slots."""
+    i = np.ascontiguousarray(ids, dtype=np.int32)
+    rows, k = i.shape
+    uniq = np.empty(experts, np.int32)
+    cnt = C.c_int(0)
+    slots = np.empty(rows * k, np.int32)
+    rc = lib().or_layer_major_union(_p(i), C.c_int(rows), C.c_int(k), C.c_int(experts), _p(uniq), C.byref(cnt),
+                                    _p(slots))
+    if rc:
+        raise ValueError(f"union failed: {rc}")
+    return uniq[: cnt.value].copy(), slots
+
+
+def group_plan(route_slots, unique: int, active: int):
+    """metal/mod.rs:3197-3233 — returns (src_rows, out_idx, groups) or raises."""
+    rs = np.ascontiguousarray(np.asarray(route_slots, dtype=np.int32))
+    src = np.empty(max(rs.size, 1), np.uint32)
+    out = np.empty(max(rs.size, 1), np.uint32)
+    groups = np.empty(max(2 * unique, 2), np.uint32)
+    rc = lib().or_group_plan(_p(rs), C.c_int(rs.size), C.c_int(unique), C.c_int(active), _p(src), _p(out),
+                             _p(groups))
+    if rc:
+        raise ValueError(f"group plan rejected: {rc}")
+    return src[: rs.size].copy(), out[: rs.size].copy(), [tuple(g) for g in groups[: 2 * unique].reshape(-1, 2).tolist()]
+
+
+class Q4Layout(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32),
+        ("intermediate", C.c_uint32),
+        ("group_size", C.c_uint32),
+        ("sb_dtype", C.c_uint32),
+        ("expert_bytes", C.c_uint64),
+        ("offset", C.c_uint64 * 9),
+    ]
+
+
+def make_layout(hidden: int, intermediate: int, group: int, sb_dtype: int, offsets, expert_bytes: int) -> Q4Layout:
+    lay = Q4Layout()
+    lay.hidden, lay.intermediate, lay.group_size, lay.sb_dtype = hidden, intermediate, group, sb_dtype
+    lay.expert_bytes = expert_bytes
+    for i, o in enumerate(offsets):
+        lay.offset[i] = int(o)
+    return lay
+
+
+def expert_mlp(layout: Q4Layout, slot: np.ndarray, x) -> np.ndarray:
+    """One expert's Q4 SwiGLU chain (reference_q4_swiglu, tests/scheduler.rs:327-336)."""
+    xx = _f32(x)
+    y = np.empty(layout.hidden, np.float32)
+    rc = lib().or_expert_mlp(C.byref(layout), _p(np.ascontiguousarray(slot)), _p(xx), _p(y))
+    assert rc == 0
+    return y
+
+
+def combine(residual, ys, weights, shared=None, shared_weight: float = 0.0) -> np.ndarray:
+    """qwen_layer_major_combine for one row (shaders.metal:1756-1786)."""
+    r = _f32(residual)
+    y = _f32(ys)
+    w = _f32(weights)
+    s = _f32(shared) if shared is not None else None
+    out = np.empty_like(r)
+    lib().or_combine(_p(r), _p(y), _p(w), C.c_int(w.size), _p(s) if s is not None else None,
+                     C.c_float(shared_weight), C.c_int(r.size), _p(out))
+    return out
+
+
+def moe_block(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarray, residual: np.ndarray,
+              ids: np.ndarray, weights: np.ndarray, shared_layout: Q4Layout | None = None,
+              shared_slot: np.ndarray | None = None, shared_gate_w: np.ndarray | None = None,
+              shared_gate_dtype: int = DT_F16, next_norm_w: np.ndarray | None = None, eps: float = 1e-6,
+              threads: int = 1):
+    """CMD3 per-row arithmetic (metal/mod.rs:4289-4765, shaders.metal:1756-1786).
+    Returns (hidden[T][H], next_normed[T][H] or None)."""
+    xx = _f32(x)
+    rr = _f32(residual)
+    rows, hidden = xx.shape
+    ii = np.ascontiguousarray(ids, dtype=np.int32)
+    ww = _f32(weights)
+    k = ii.shape[1]
+    out = np.empty((rows, hidden), np.float32)
+    nn = np.empty((rows, hidden), np.float32) if next_norm_w is not None else None
+    nw = _f32(next_norm_w) if next_norm_w is not None else None
+    sg = np.ascontiguousarray(shared_gate_w) if shared_gate_w is not None else None
+    rc = lib().or_moe_block(
+        C.byref(layout), _p(slots), C.c_int(experts),
+        C.byref(shared_layout) if shared_layout is not None else None,
+        _p(shared_slot) if shared_slot is not None else None,
+        _p(sg) if sg is not None else None, C.c_int(shared_gate_dtype),
+        _p(xx), _p(rr), C.c_int(rows), C.c_int(k), _p(ii), _p(ww),
+        _p(nw) if nw is not None else None, C.c_float(eps), _p(out),
+        _p(nn) if nn is not None else None, C.c_int(threads))
+    if rc:
+        raise ValueError(f"oracle moe_block failed: {rc}")
+    return out, nn
+
+
+def route_rows(logits: np.ndarray, k: int, kind: int = ROUTING_SOFTMAX, order: int = ORDER_REFERENCE_SLOT,
+               bias: np.ndarray | None = None, n_group: int = 1, topk_group: int = 1,
+               policy: int = NORM_RENORMALIZE, routed_scale: float = 1.0):
+    """Routing stage for T rows: selection (math.rs:771-819) then
+    renormalisation (expert_access.rs:80-135)."""
+    ll = _f32(logits)
+    rows, experts = ll.shape
+    bb = _f32(bias) if bias is not None else np.zeros(experts, np.float32)
+    ids = np.empty((rows, k), np.int32)
+    w = np.empty((rows, k), np.float32)
+    rc = lib().or_route_rows(_p(ll), _p(bb), C.c_int(rows), C.c_int(experts), C.c_int(k), C.c_int(kind),
+                             C.c_int(order), C.c_int(n_group), C.c_int(topk_group), C.c_int(policy),
+                             C.c_float(routed_scale), _p(ids), _p(w))
+    if rc:
+        raise ValueError(f"oracle routing failed: {rc}")
+    return ids, w
+
+
+def _declare():
+    L = lib()
+    L.or_routing_top_k.restype = C.c_int
+    L.or_top_k_sorted.restype = C.c_int
+    L.or_routing_softmax_top_k.restype = C.c_int
+    L.or_routing_sigmoid_noaux_top_k.restype = C.c_int
+    L.or_routing_sigmoid_grouped_top_k.restype = C.c_int
+    L.or_renormalize.restype = C.c_int
+
+
+if os.path.exists(LIB_PATH):
+    _declare()

@@ -1,0 +1,61 @@
+"""Build the in-tree native libraries of the pb_amd package.
+
+* ``pb_amd/libpbmoe.so``       — the gfx950 HIP kernels + C ABI (include/pbmoe.h)
+* ``pb_amd/libpbmoe_synth.so`` — host seeded generator (no HIP dependency)
+
+hipcc cross-compiles gfx950 code objects without a GPU present.  All HIP code
+is compiled with packed-fp32 instructions disabled.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+ROOT = os.path.dirname(HERE)
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+HIP_SOURCES = ["pbmoe_kernels.hip", "pbmoe_abi.cpp"]
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{os.path.join(ROOT, 'include')}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature
+    lines = [l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l]
+    if lines:
+        print("\n".join(lines), file=sys.stderr)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build failed ({proc.returncode}): {' '.join(cmd)}")
+
+
+def build_synth() -> str:
+    out = os.path.join(HERE, "libpbmoe_synth.so")
+    _run(["gcc", "-O3", "-mfma", "-std=c11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
+          "-Wall", "-o", out, os.path.join(CSRC, "synth_host.c"), "-lm"])
+    return out
+
+
+def build_hip() -> str:
+    out = os.path.join(HERE, "libpbmoe.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-o", tmp, *[os.path.join(CSRC, s) for s in HIP_SOURCES]])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all() -> None:
+    build_synth()
+    build_hip()
+
+
+if __name__ == "__main__":
+    build_all()

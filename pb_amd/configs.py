@@ -1,0 +1,44 @@
+"""The BASELINE workload shapes of the MoE block.
+
+C1  CPU-runnable single layer: H2048, E128, K8 softmax renormalised, I768.
+C2  Qwen3-Next decode: H2048, E512, K10, I512 + sigmoid-gated shared I512.
+C3  prefill of 2048 tokens through the C1 layer with drawn Zipf(1.1) logits.
+C5  DeepSeek-V3 shape: H7168, E256, K8 sigmoid, 8 groups / topk_group 4,
+    per-expert selection bias, I2048 + shared I2048 (ungated), routed
+    scale 2.5 (the DeepSeek-V3 routed_scaling_factor; BASELINE leaves it open).
+All: 4-bit affine, group 64, f16 scale/bias.
+"""
+from __future__ import annotations
+
+from .abi import (NORM_RENORMALIZE_SELECTED, ROUTING_SIGMOID_GROUPED, ROUTING_SOFTMAX_TOPK, DTYPE_F16)
+from .synth import MoeConfig
+
+C1 = MoeConfig("c1_decode", hidden=2048, intermediate=768, experts=128, k=8,
+               routing=ROUTING_SOFTMAX_TOPK, normalization=NORM_RENORMALIZE_SELECTED, sb_dtype=DTYPE_F16)
+C2 = MoeConfig("c2_qwen3next_decode", hidden=2048, intermediate=512, experts=512, k=10,
+               routing=ROUTING_SOFTMAX_TOPK, normalization=NORM_RENORMALIZE_SELECTED,
+               shared_intermediate=512, shared_gated=True, sb_dtype=DTYPE_F16)
+C3 = MoeConfig("c3_prefill_2048", hidden=2048, intermediate=768, experts=128, k=8,
+               routing=ROUTING_SOFTMAX_TOPK, normalization=NORM_RENORMALIZE_SELECTED, sb_dtype=DTYPE_F16,
+               tokens=2048)
+C5 = MoeConfig("c5_deepseekv3_decode", hidden=7168, intermediate=2048, experts=256, k=8,
+               routing=ROUTING_SIGMOID_GROUPED, normalization=NORM_RENORMALIZE_SELECTED, routed_scale=2.5,
+               n_group=8, topk_group=4, shared_intermediate=2048, shared_gated=False, sb_dtype=DTYPE_F16)
+
+CONFIGS = {c.name: c for c in (C1, C2, C3, C5)}
+
+
+def algorithmic_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:
+    """HBM bytes a decode call must move at minimum: each selected expert's
+    Q4 slot once, the shared slot, the router (f16) and shared gate, and the
+    f32 activations in (x, residual) and out (hidden)."""
+    def slot(h, i):
+        return 3 * (h * i // 2) + 3 * 2 * (h * i // cfg.group) * 2
+    b = unique_experts * slot(cfg.hidden, cfg.intermediate)
+    if cfg.shared_intermediate:
+        b += slot(cfg.hidden, cfg.shared_intermediate)
+        if cfg.shared_gated:
+            b += cfg.hidden * 2
+    b += cfg.experts * cfg.hidden * 2
+    b += tokens * cfg.hidden * 4 * 3
+    return b

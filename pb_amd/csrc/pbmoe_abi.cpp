@@ -1,0 +1,911 @@
+// C ABI of the MI355X MoE block (include/pbmoe.h).
+//
+// Host responsibilities: validate every shape, dtype, alignment and route
+// before anything is launched (as scheduler/protocol.rs:1564-1676 and
+// metal/mod.rs:3264-3319 do), own device copies of bound weights, size the
+// scratch buffers, and launch the gfx950 kernels on the context stream.
+// Errors are explicit status codes plus a thread-local message; there is no
+// fallback implementation behind any entry point.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <thread>
+
+#include "../../include/pbmoe.h"
+#include "pbmoe_internal.h"
+
+#define PBMOE_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok()
+{
+    return PBMOE_OK;
+}
+
+#define HIP_TRY(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(e_ == hipErrorOutOfMemory ? PBMOE_ERR_OUT_OF_MEMORY : PBMOE_ERR_DEVICE, \
+                        "%s: %s", #expr, hipGetErrorString(e_));                               \
+    } while (0)
+
+// Limits of the current kernels (explicitly rejected beyond them).
+constexpr uint32_t MAX_EXPERTS = 1024;
+constexpr uint32_t MAX_K = 16;
+constexpr uint32_t MAX_DECODE_TOKENS = 16;
+constexpr uint32_t MAX_HIDDEN = 8192;
+constexpr uint32_t MAX_INTERMEDIATE = 2048;
+
+struct DeviceBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct LayerBinding {
+    pbmoe_layer_desc desc{};
+    pbmoe_q4_layout layout{};
+    const uint8_t* slots = nullptr;
+    size_t slots_bytes = 0;
+    DeviceBuf slots_owned;
+    const void* router = nullptr;
+    uint32_t router_dtype = 0;
+    DeviceBuf router_owned;
+    const float* sel_bias = nullptr;
+    DeviceBuf bias_owned;
+    bool has_shared = false;
+    pbmoe_q4_layout shared_layout{};
+    const uint8_t* shared_slot = nullptr;
+    DeviceBuf shared_owned;
+    const void* shared_gate = nullptr;
+    uint32_t shared_gate_dtype = 0;
+    DeviceBuf gate_owned;
+};
+
+} // namespace
+
+struct pbmoe_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::map<uint32_t, LayerBinding> layers;
+    uint32_t* status = nullptr; // device status word
+    DeviceBuf logits, act, act_shared, shared_weight, plan;
+    DeviceBuf route_ids, route_w;
+};
+
+namespace {
+
+void free_buf(DeviceBuf& b)
+{
+    if (b.ptr)
+        (void)hipFree(b.ptr);
+    b.ptr = nullptr;
+    b.bytes = 0;
+}
+
+int ensure(pbmoe_ctx* ctx, DeviceBuf& b, size_t bytes)
+{
+    if (b.bytes >= bytes && b.ptr)
+        return ok();
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    free_buf(b);
+    size_t want = bytes < 256 ? 256 : bytes;
+    HIP_TRY(hipMalloc(&b.ptr, want));
+    b.bytes = want;
+    return ok();
+}
+
+int set_device(pbmoe_ctx* ctx)
+{
+    HIP_TRY(hipSetDevice(ctx->device));
+    return ok();
+}
+
+// Copy or reference a weight source.
+int adopt(pbmoe_ctx* ctx, const void* src, size_t bytes, uint32_t flags, DeviceBuf& owned,
+          const void** out)
+{
+    if (flags == PBMOE_MEM_DEVICE) {
+        *out = src;
+        return ok();
+    }
+    if (flags != PBMOE_MEM_HOST)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown memory flags %u", flags);
+    free_buf(owned);
+    HIP_TRY(hipMalloc(&owned.ptr, bytes));
+    owned.bytes = bytes;
+    HIP_TRY(hipMemcpyAsync(owned.ptr, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    *out = owned.ptr;
+    return ok();
+}
+
+bool aligned(const void* p, size_t a)
+{
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+// Q4 layout checks: QwenMoeQ4ExpertLayout::validate (model_family.rs:1132-1152)
+// plus component sizes for the given shape and kernel alignment.
+int check_layout(const pbmoe_q4_layout* l, uint32_t hidden, uint32_t intermediate)
+{
+    if (!l)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "layout is null");
+    uint64_t expected = 0;
+    for (uint32_t i = 0; i < 9; ++i) {
+        const pbmoe_component& c = l->components[i];
+        if (c.kind != i)
+            return fail(PBMOE_ERR_SHAPE, "expert component %u has kind %u, expected %u", i, c.kind, i);
+        if (c.offset != expected)
+            return fail(PBMOE_ERR_SHAPE, "expert component %u starts at %llu, expected %llu", i,
+                        (unsigned long long)c.offset, (unsigned long long)expected);
+        expected += c.bytes;
+    }
+    if (expected != l->expert_bytes)
+        return fail(PBMOE_ERR_SHAPE, "expert layout totals %llu bytes, expected %llu",
+                    (unsigned long long)expected, (unsigned long long)l->expert_bytes);
+    if (l->scale_bias_dtype == PBMOE_DTYPE_F32)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "F32 scale/bias is the import format only; bind BF16 or F16 slots");
+    if (l->scale_bias_dtype != PBMOE_DTYPE_F16 && l->scale_bias_dtype != PBMOE_DTYPE_BF16)
+        return fail(PBMOE_ERR_DTYPE, "unknown scale/bias dtype %u", l->scale_bias_dtype);
+    if (hidden == 0 && intermediate == 0)
+        return ok();
+    uint32_t g = l->group_size;
+    if (g != 32 && g != 64 && g != 128)
+        return fail(PBMOE_ERR_UNSUPPORTED, "group size %u not supported (32, 64, 128)", g);
+    if (hidden % g || intermediate % g)
+        return fail(PBMOE_ERR_SHAPE, "hidden=%u intermediate=%u must be divisible by group_size=%u",
+                    hidden, intermediate, g);
+    uint64_t packed = (uint64_t)hidden * intermediate / 2;
+    uint64_t sb = (uint64_t)hidden * (intermediate / g) * 2;
+    uint64_t sb_gu = (uint64_t)intermediate * (hidden / g) * 2;
+    for (int p = 0; p < 3; ++p) {
+        uint64_t want_sb = p == 2 ? sb : sb_gu;
+        if (l->components[3 * p].bytes != packed || l->components[3 * p + 1].bytes != want_sb ||
+            l->components[3 * p + 2].bytes != want_sb)
+            return fail(PBMOE_ERR_SHAPE, "projection %d component sizes do not match %ux%u group %u",
+                        p, hidden, intermediate, g);
+        if (l->components[3 * p].offset % 16)
+            return fail(PBMOE_ERR_ALIGNMENT, "projection %d packed weights not 16-byte aligned", p);
+        if (l->components[3 * p + 1].offset % 2 || l->components[3 * p + 2].offset % 2)
+            return fail(PBMOE_ERR_ALIGNMENT, "projection %d scale/bias not 2-byte aligned", p);
+    }
+    if (l->expert_bytes % 16)
+        return fail(PBMOE_ERR_ALIGNMENT, "expert slot stride %llu not a multiple of 16",
+                    (unsigned long long)l->expert_bytes);
+    return ok();
+}
+
+pbmoe::ExpertSet make_set(const uint8_t* base, const pbmoe_q4_layout& l, uint32_t count,
+                          uint32_t hidden, uint32_t intermediate)
+{
+    pbmoe::ExpertSet s{};
+    s.base = base;
+    s.stride = l.expert_bytes;
+    s.count = count;
+    s.group = l.group_size;
+    s.sb_dtype = l.scale_bias_dtype;
+    auto proj = [&](int p) {
+        pbmoe::Q4Proj q{};
+        q.w_off = l.components[3 * p].offset;
+        q.s_off = l.components[3 * p + 1].offset;
+        q.b_off = l.components[3 * p + 2].offset;
+        q.rows = p == 2 ? hidden : intermediate;
+        q.cols = p == 2 ? intermediate : hidden;
+        return q;
+    };
+    s.gate = proj(0);
+    s.up = proj(1);
+    s.down = proj(2);
+    return s;
+}
+
+int get_layer(pbmoe_ctx* ctx, uint32_t layer, LayerBinding** out)
+{
+    auto it = ctx->layers.find(layer);
+    if (it == ctx->layers.end())
+        return fail(PBMOE_ERR_NOT_BOUND, "layer %u is not bound", layer);
+    *out = &it->second;
+    return ok();
+}
+
+int plan_buffers(pbmoe_ctx* ctx, uint32_t experts, uint32_t routes, pbmoe::Plan* plan)
+{
+    size_t words = (size_t)experts * 3 + 1 + (size_t)routes * 3;
+    int rc = ensure(ctx, ctx->plan, words * 4);
+    if (rc)
+        return rc;
+    uint32_t* p = static_cast<uint32_t*>(ctx->plan.ptr);
+    plan->unique_ids = p;
+    plan->unique_count = p + experts;
+    plan->groups = p + experts + 1;
+    plan->route_slots = p + experts * 3 + 1;
+    plan->src_rows = plan->route_slots + routes;
+    plan->out_idx = plan->src_rows + routes;
+    return ok();
+}
+
+} // namespace
+
+// ---------------------------------------------------------------------------
+PBMOE_API int pbmoe_abi_version(void)
+{
+    return PBMOE_ABI_VERSION;
+}
+
+PBMOE_API const char* pbmoe_last_error(void)
+{
+    return g_last_error.c_str();
+}
+
+// QwenMoeQ4ExpertLayout::fixed_bf16, model_family.rs:954-1068
+PBMOE_API int pbmoe_q4_layout_fixed(uint32_t hidden, uint32_t intermediate, uint32_t group_size,
+                                    uint32_t sb_dtype, pbmoe_q4_layout* out)
+{
+    if (!out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "out is null");
+    if (hidden == 0 || intermediate == 0 || group_size == 0)
+        return fail(PBMOE_ERR_SHAPE,
+                    "fixed-Q4 expert layout requires non-zero hidden, intermediate, and group dimensions");
+    if (hidden % group_size || intermediate % group_size)
+        return fail(PBMOE_ERR_SHAPE,
+                    "fixed-Q4 expert dimensions hidden=%u intermediate=%u must be divisible by group_size=%u",
+                    hidden, intermediate, group_size);
+    if (sb_dtype != PBMOE_DTYPE_F16 && sb_dtype != PBMOE_DTYPE_BF16)
+        return fail(PBMOE_ERR_DTYPE, "fixed-Q4 scale/bias dtype must be F16 or BF16");
+    uint64_t values = (uint64_t)hidden * intermediate;
+    if (values % 2)
+        return fail(PBMOE_ERR_SHAPE, "fixed-Q4 projection element count %llu must be even",
+                    (unsigned long long)values);
+    uint64_t packed = values / 2;
+    uint64_t sb_gu = (uint64_t)intermediate * (hidden / group_size) * 2;
+    uint64_t sb_d = (uint64_t)hidden * (intermediate / group_size) * 2;
+    uint64_t sizes[9] = {packed, sb_gu, sb_gu, packed, sb_gu, sb_gu, packed, sb_d, sb_d};
+    uint64_t off = 0;
+    for (uint32_t i = 0; i < 9; ++i) {
+        out->components[i].kind = i;
+        out->components[i].reserved = 0;
+        out->components[i].offset = off;
+        out->components[i].bytes = sizes[i];
+        off += sizes[i];
+    }
+    out->expert_bytes = off;
+    out->group_size = group_size;
+    out->scale_bias_dtype = sb_dtype;
+    return ok();
+}
+
+PBMOE_API int pbmoe_q4_layout_validate(const pbmoe_q4_layout* layout)
+{
+    return check_layout(layout, 0, 0);
+}
+
+// validate_preselected, scheduler/protocol.rs:1044-1081
+PBMOE_API int pbmoe_validate_routes(const uint32_t* ids, const float* scores, uint32_t count,
+                                    uint32_t active_experts, uint32_t experts)
+{
+    if (active_experts == 0 || active_experts > experts)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT,
+                    "active expert count %u must be in 1..=%u", active_experts, experts);
+    if (count != active_experts)
+        return fail(PBMOE_ERR_ROUTE, "received %u preselected experts; expected %u", count,
+                    active_experts);
+    if (!ids || !scores)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ids/scores are null");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ids[i] >= experts)
+            return fail(PBMOE_ERR_ROUTE, "selected expert %u outside expert count %u", ids[i],
+                        experts);
+        if (!std::isfinite(scores[i]))
+            return fail(PBMOE_ERR_NONFINITE, "selected expert %u has non-finite score %g", ids[i],
+                        (double)scores[i]);
+        for (uint32_t j = 0; j < i; ++j)
+            if (ids[j] == ids[i])
+                return fail(PBMOE_ERR_ROUTE, "selected expert %u more than once", ids[i]);
+    }
+    return ok();
+}
+
+// ScheduledExpertRoutes::from_routes_with_policy, expert_access.rs:80-135
+PBMOE_API int pbmoe_renormalize_routes(const float* scores, uint32_t count, uint32_t normalization,
+                                       float routed_scale, float* weights)
+{
+    if (!scores || !weights)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "scores/weights are null");
+    if (!(std::isfinite(routed_scale) && routed_scale > 0.0f))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "routed expert scale must be positive and finite");
+    for (uint32_t i = 0; i < count; ++i)
+        if (!std::isfinite(scores[i]))
+            return fail(PBMOE_ERR_NONFINITE, "route score %u is not finite", i);
+    float sum = -0.0f;
+    for (uint32_t i = 0; i < count; ++i)
+        sum = sum + scores[i];
+    float inv;
+    if (normalization == PBMOE_NORM_RENORMALIZE_SELECTED) {
+        if (!(std::isfinite(sum) && sum > 0.0f))
+            return fail(PBMOE_ERR_ROUTE, "selected expert probabilities must have a positive finite sum");
+        inv = 1.0f / sum;
+    } else if (normalization == PBMOE_NORM_DEEPSEEK_FLOOR) {
+        if (!(std::isfinite(sum) && sum >= 0.0f))
+            return fail(PBMOE_ERR_ROUTE,
+                        "DeepSeek selected expert probabilities must have a finite non-negative sum");
+        inv = 1.0f / std::fmax(sum, 6.103515625e-5f);
+    } else if (normalization == PBMOE_NORM_PRESERVE_FULL_SOFTMAX) {
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "unsupported routing weights: preserving probabilities from the full expert softmax");
+    } else {
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown normalization %u", normalization);
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        if (scores[i] < 0.0f)
+            return fail(PBMOE_ERR_ROUTE, "selected expert probabilities must be non-negative");
+        weights[i] = scores[i] * inv;
+    }
+    for (uint32_t i = 0; i < count; ++i)
+        weights[i] = weights[i] * routed_scale;
+    return ok();
+}
+
+PBMOE_API int pbmoe_ctx_create(int device, pbmoe_ctx** out)
+{
+    if (!out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n)
+        return fail(PBMOE_ERR_DEVICE, "device %d not present (%d devices)", device, n);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(PBMOE_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950",
+                    device, prop.gcnArchName);
+    pbmoe_ctx* ctx = new pbmoe_ctx();
+    ctx->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess)
+        e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess)
+        e = hipMalloc(reinterpret_cast<void**>(&ctx->status), 256);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(ctx->status, 0, 256, ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        int rc = fail(PBMOE_ERR_DEVICE, "context setup failed: %s", hipGetErrorString(e));
+        if (ctx->stream)
+            (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return rc;
+    }
+    *out = ctx;
+    return ok();
+}
+
+PBMOE_API int pbmoe_ctx_destroy(pbmoe_ctx* ctx)
+{
+    if (!ctx)
+        return ok();
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->layers) {
+        free_buf(kv.second.slots_owned);
+        free_buf(kv.second.router_owned);
+        free_buf(kv.second.bias_owned);
+        free_buf(kv.second.shared_owned);
+        free_buf(kv.second.gate_owned);
+    }
+    for (DeviceBuf* b : {&ctx->logits, &ctx->act, &ctx->act_shared, &ctx->shared_weight,
+                         &ctx->plan, &ctx->route_ids, &ctx->route_w})
+        free_buf(*b);
+    (void)hipFree(ctx->status);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ok();
+}
+
+PBMOE_API int pbmoe_ctx_stream(pbmoe_ctx* ctx, void** stream)
+{
+    if (!ctx || !stream)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    *stream = ctx->stream;
+    return ok();
+}
+
+// commit_and_wait with the reference's 120 s limit (metal/mod.rs:539-540)
+PBMOE_API int pbmoe_sync(pbmoe_ctx* ctx)
+{
+    if (!ctx)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    auto t0 = std::chrono::steady_clock::now();
+    for (;;) {
+        hipError_t q = hipStreamQuery(ctx->stream);
+        if (q == hipSuccess)
+            break;
+        if (q != hipErrorNotReady)
+            return fail(PBMOE_ERR_DEVICE, "stream failed: %s", hipGetErrorString(q));
+        if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(120))
+            return fail(PBMOE_ERR_TIMEOUT, "device work did not complete within 120 s");
+        std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+    uint32_t st = 0;
+    HIP_TRY(hipMemcpy(&st, ctx->status, 4, hipMemcpyDeviceToHost));
+    if (st) {
+        HIP_TRY(hipMemset(ctx->status, 0, 4));
+        if (st & pbmoe::ST_NONFINITE)
+            return fail(PBMOE_ERR_NONFINITE, "router produced a non-finite score");
+        if (st & pbmoe::ST_ROUTE_RANGE)
+            return fail(PBMOE_ERR_ROUTE, "a route selected an expert outside the expert count");
+        if (st & (pbmoe::ST_BAD_SUM | pbmoe::ST_NEGATIVE))
+            return fail(PBMOE_ERR_ROUTE,
+                        "selected expert probabilities must have a positive finite sum");
+        return fail(PBMOE_ERR_DEVICE, "device status 0x%x", st);
+    }
+    return ok();
+}
+
+PBMOE_API int pbmoe_device_alloc(pbmoe_ctx* ctx, size_t bytes, void** dptr)
+{
+    if (!ctx || !dptr)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
+    return ok();
+}
+
+PBMOE_API int pbmoe_device_free(pbmoe_ctx* ctx, void* dptr)
+{
+    if (!ctx)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(dptr));
+    return ok();
+}
+
+PBMOE_API int pbmoe_upload(pbmoe_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    if (!ctx || (!dst && bytes) || (!src && bytes))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+PBMOE_API int pbmoe_download(pbmoe_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    if (!ctx || (!dst && bytes) || (!src && bytes))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+PBMOE_API int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc* d,
+                               const pbmoe_q4_layout* layout, const void* slots,
+                               size_t slots_bytes, uint32_t flags)
+{
+    if (!ctx || !d || !layout || !slots)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (d->experts == 0 || d->experts > MAX_EXPERTS)
+        return fail(PBMOE_ERR_UNSUPPORTED, "experts=%u outside 1..=%u", d->experts, MAX_EXPERTS);
+    if (d->active_experts == 0 || d->active_experts > d->experts)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "active expert count %u must be in 1..=%u",
+                    d->active_experts, d->experts);
+    if (d->active_experts > MAX_K)
+        return fail(PBMOE_ERR_UNSUPPORTED, "active experts %u > %u", d->active_experts, MAX_K);
+    if (d->hidden == 0 || d->hidden % 256 || d->hidden > MAX_HIDDEN)
+        return fail(PBMOE_ERR_UNSUPPORTED, "hidden=%u must be a multiple of 256 and <= %u",
+                    d->hidden, MAX_HIDDEN);
+    if (d->intermediate == 0 || d->intermediate % 256 || d->intermediate > MAX_INTERMEDIATE)
+        return fail(PBMOE_ERR_UNSUPPORTED, "intermediate=%u must be a multiple of 256 and <= %u",
+                    d->intermediate, MAX_INTERMEDIATE);
+    if (d->routing > PBMOE_ROUTING_SIGMOID_GROUPED)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown routing %u", d->routing);
+    if (d->normalization == PBMOE_NORM_PRESERVE_FULL_SOFTMAX)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "unsupported routing weights: preserving probabilities from the full expert "
+                    "softmax requires a declared scheduler implementation");
+    if (d->normalization > PBMOE_NORM_DEEPSEEK_FLOOR)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown normalization %u", d->normalization);
+    if (d->route_order > PBMOE_ORDER_REFERENCE_SLOT)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown route order %u", d->route_order);
+    if (!(std::isfinite(d->routed_scale) && d->routed_scale > 0.0f))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "routed expert scale must be positive and finite");
+    if (d->routing == PBMOE_ROUTING_SIGMOID_GROUPED) {
+        if (d->n_group == 0 || d->n_group > 64 || d->experts % d->n_group ||
+            d->topk_group == 0 || d->topk_group > d->n_group ||
+            (d->n_group > 1 && d->experts / d->n_group < 2))
+            return fail(PBMOE_ERR_SHAPE, "group-limited routing needs experts %% n_group == 0, "
+                                         "n_group <= 64, 1 <= topk_group <= n_group");
+        if (d->route_order == PBMOE_ORDER_REFERENCE_SLOT)
+            return fail(PBMOE_ERR_UNSUPPORTED,
+                        "group-limited routing has no reference slot order; use canonical");
+        if (d->active_experts > d->topk_group * (d->experts / d->n_group))
+            return fail(PBMOE_ERR_SHAPE, "K=%u exceeds the %u experts of the kept groups",
+                        d->active_experts, d->topk_group * (d->experts / d->n_group));
+    }
+    if (d->shared_intermediate && d->shared_intermediate != d->intermediate)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "shared intermediate %u must equal routed intermediate %u",
+                    d->shared_intermediate, d->intermediate);
+    int rc = check_layout(layout, d->hidden, d->intermediate);
+    if (rc)
+        return rc;
+    if (slots_bytes < (size_t)layout->expert_bytes * d->experts)
+        return fail(PBMOE_ERR_SHAPE, "slots hold %zu bytes, %u experts need %llu", slots_bytes,
+                    d->experts, (unsigned long long)layout->expert_bytes * d->experts);
+    if (flags == PBMOE_MEM_DEVICE && !aligned(slots, 16))
+        return fail(PBMOE_ERR_ALIGNMENT, "device slot base must be 16-byte aligned");
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    LayerBinding& b = ctx->layers[layer];
+    b.desc = *d;
+    b.layout = *layout;
+    const void* dev = nullptr;
+    rc = adopt(ctx, slots, (size_t)layout->expert_bytes * d->experts, flags, b.slots_owned, &dev);
+    if (rc) {
+        ctx->layers.erase(layer);
+        return rc;
+    }
+    b.slots = static_cast<const uint8_t*>(dev);
+    b.slots_bytes = (size_t)layout->expert_bytes * d->experts;
+    return ok();
+}
+
+PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weight, uint32_t dtype,
+                                const float* selection_bias, uint32_t flags)
+{
+    if (!ctx || !weight)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    if (dtype > PBMOE_DTYPE_BF16)
+        return fail(PBMOE_ERR_DTYPE, "router dtype %u not one of F32/F16/BF16", dtype);
+    if (b->desc.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !selection_bias)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT,
+                    "sigmoid routing requires the per-expert selection bias");
+    if (flags == PBMOE_MEM_DEVICE && !aligned(weight, 16))
+        return fail(PBMOE_ERR_ALIGNMENT, "device router weight must be 16-byte aligned");
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    size_t esz = dtype == PBMOE_DTYPE_F32 ? 4 : 2;
+    const void* dev = nullptr;
+    rc = adopt(ctx, weight, (size_t)b->desc.experts * b->desc.hidden * esz, flags, b->router_owned,
+               &dev);
+    if (rc)
+        return rc;
+    b->router = dev;
+    b->router_dtype = dtype;
+    b->sel_bias = nullptr;
+    if (selection_bias) {
+        rc = adopt(ctx, selection_bias, (size_t)b->desc.experts * 4, flags, b->bias_owned, &dev);
+        if (rc)
+            return rc;
+        b->sel_bias = static_cast<const float*>(dev);
+    }
+    return ok();
+}
+
+PBMOE_API int pbmoe_bind_shared(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_layout* sl,
+                                const void* shared_slot, const void* gate_weight,
+                                uint32_t gate_dtype, uint32_t flags)
+{
+    if (!ctx || !sl || !shared_slot)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    if (b->desc.shared_intermediate == 0)
+        return fail(PBMOE_ERR_SHAPE, "layer %u declares no shared expert", layer);
+    rc = check_layout(sl, b->desc.hidden, b->desc.shared_intermediate);
+    if (rc)
+        return rc;
+    if (sl->scale_bias_dtype != b->layout.scale_bias_dtype)
+        return fail(PBMOE_ERR_UNSUPPORTED, "shared and routed scale/bias dtypes must match");
+    if (b->desc.shared_gated && !gate_weight)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "layer declares a gated shared expert but no gate weight");
+    if (gate_weight && gate_dtype > PBMOE_DTYPE_BF16)
+        return fail(PBMOE_ERR_DTYPE, "shared gate dtype %u not one of F32/F16/BF16", gate_dtype);
+    if (flags == PBMOE_MEM_DEVICE && !aligned(shared_slot, 16))
+        return fail(PBMOE_ERR_ALIGNMENT, "device shared slot must be 16-byte aligned");
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    const void* dev = nullptr;
+    rc = adopt(ctx, shared_slot, sl->expert_bytes, flags, b->shared_owned, &dev);
+    if (rc)
+        return rc;
+    b->shared_layout = *sl;
+    b->shared_slot = static_cast<const uint8_t*>(dev);
+    b->shared_gate = nullptr;
+    if (b->desc.shared_gated && gate_weight) {
+        size_t esz = gate_dtype == PBMOE_DTYPE_F32 ? 4 : 2;
+        rc = adopt(ctx, gate_weight, (size_t)b->desc.hidden * esz, flags, b->gate_owned, &dev);
+        if (rc)
+            return rc;
+        b->shared_gate = dev;
+        b->shared_gate_dtype = gate_dtype;
+    }
+    b->has_shared = true;
+    return ok();
+}
+
+PBMOE_API int pbmoe_unbind_layer(pbmoe_ctx* ctx, uint32_t layer)
+{
+    if (!ctx)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
+    auto it = ctx->layers.find(layer);
+    if (it == ctx->layers.end())
+        return fail(PBMOE_ERR_NOT_BOUND, "layer %u is not bound", layer);
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    LayerBinding& b = it->second;
+    free_buf(b.slots_owned);
+    free_buf(b.router_owned);
+    free_buf(b.bias_owned);
+    free_buf(b.shared_owned);
+    free_buf(b.gate_owned);
+    ctx->layers.erase(it);
+    return ok();
+}
+
+static int route_common(pbmoe_ctx* ctx, LayerBinding* b, const float* logits, uint32_t tokens,
+                        uint32_t* ids, float* weights)
+{
+    const pbmoe_layer_desc& d = b->desc;
+    if (d.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+        return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
+    pbmoe::RouteParams p{};
+    p.experts = d.experts;
+    p.k = d.active_experts;
+    p.kind = d.routing;
+    p.order = d.route_order;
+    p.norm = d.normalization;
+    p.n_group = d.routing == PBMOE_ROUTING_SIGMOID_GROUPED ? d.n_group : 1;
+    p.topk_group = d.routing == PBMOE_ROUTING_SIGMOID_GROUPED ? d.topk_group : 1;
+    p.routed_scale = d.routed_scale;
+    HIP_TRY(pbmoe::launch_route_topk(ctx->stream, logits, b->sel_bias, tokens, p, ids, weights,
+                                     ctx->status));
+    return ok();
+}
+
+PBMOE_API int pbmoe_route(pbmoe_ctx* ctx, uint32_t layer, const float* x, uint32_t tokens,
+                          uint32_t* ids, float* weights, float* logits_out)
+{
+    if (!ctx || !x || !ids || !weights)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (tokens == 0)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "routing requires at least one token row");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    if (!b->router)
+        return fail(PBMOE_ERR_NOT_BOUND, "layer %u has no bound router projection", layer);
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    float* logits = logits_out;
+    if (!logits) {
+        rc = ensure(ctx, ctx->logits, (size_t)tokens * b->desc.experts * 4);
+        if (rc)
+            return rc;
+        logits = static_cast<float*>(ctx->logits.ptr);
+    }
+    HIP_TRY(pbmoe::launch_router_logits(ctx->stream, b->router, b->router_dtype, x, tokens,
+                                        b->desc.experts, b->desc.hidden, logits));
+    return route_common(ctx, b, logits, tokens, ids, weights);
+}
+
+PBMOE_API int pbmoe_route_logits(pbmoe_ctx* ctx, uint32_t layer, const float* logits,
+                                 uint32_t tokens, uint32_t* ids, float* weights)
+{
+    if (!ctx || !logits || !ids || !weights)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (tokens == 0)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "routing requires at least one token row");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    return route_common(ctx, b, logits, tokens, ids, weights);
+}
+
+static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
+                        uint32_t tokens, const uint32_t* ids, const float* weights,
+                        const float* next_norm_weight, float* hidden_out, float* next_normed_out)
+{
+    if (!ctx || !x || !residual || !ids || !weights || !hidden_out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (tokens == 0)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "expert phase requires at least one token row");
+    if ((next_norm_weight == nullptr) != (next_normed_out == nullptr))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT,
+                    "next_norm_weight and next_normed_out must be given together");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    const pbmoe_layer_desc& d = b->desc;
+    if (d.shared_intermediate && !b->has_shared)
+        return fail(PBMOE_ERR_NOT_BOUND, "layer %u declares a shared expert that is not bound",
+                    layer);
+    if (tokens > MAX_DECODE_TOKENS)
+        return fail(PBMOE_ERR_UNSUPPORTED, "decode expert phase supports at most %u tokens, got %u",
+                    MAX_DECODE_TOKENS, tokens);
+    for (const void* p : {(const void*)x, (const void*)residual, (const void*)hidden_out})
+        if (!aligned(p, 16))
+            return fail(PBMOE_ERR_ALIGNMENT, "activation buffers must be 16-byte aligned");
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    const uint32_t K = d.active_experts, H = d.hidden, I = d.intermediate;
+    const uint32_t routes = tokens * K;
+    if ((rc = ensure(ctx, ctx->act, (size_t)routes * I * 4)))
+        return rc;
+    if ((rc = ensure(ctx, ctx->act_shared, (size_t)tokens * (d.shared_intermediate + 1) * 4)))
+        return rc;
+    if ((rc = ensure(ctx, ctx->shared_weight, (size_t)tokens * 4)))
+        return rc;
+    pbmoe::ExpertSet ex = make_set(b->slots, b->layout, d.experts, H, I);
+    pbmoe::ExpertSet sh{};
+    if (b->has_shared)
+        sh = make_set(b->shared_slot, b->shared_layout, 1, H, d.shared_intermediate);
+    pbmoe::Plan plan{};
+    pbmoe::Plan* planp = nullptr;
+    if (tokens > 1) {
+        if ((rc = plan_buffers(ctx, d.experts, routes, &plan)))
+            return rc;
+        HIP_TRY(pbmoe::launch_dispatch_plan(ctx->stream, ids, routes, d.experts, K, plan,
+                                            ctx->status));
+        planp = &plan;
+    }
+    HIP_TRY(pbmoe::launch_decode_experts(
+        ctx->stream, ex, b->has_shared ? &sh : nullptr, b->shared_gate, b->shared_gate_dtype, x,
+        residual, tokens, K, H, ids, weights, planp, static_cast<float*>(ctx->act.ptr),
+        static_cast<float*>(ctx->act_shared.ptr), static_cast<float*>(ctx->shared_weight.ptr),
+        hidden_out, next_norm_weight, d.norm_epsilon > 0.0f ? d.norm_epsilon : 1e-6f,
+        next_normed_out, ctx->status));
+    return ok();
+}
+
+PBMOE_API int pbmoe_moe_decode(pbmoe_ctx* ctx, uint32_t layer, const float* x,
+                               const float* residual, uint32_t tokens, const uint32_t* ids,
+                               const float* weights, const float* next_norm_weight,
+                               float* hidden_out, float* next_normed_out)
+{
+    return expert_phase(ctx, layer, x, residual, tokens, ids, weights, next_norm_weight,
+                        hidden_out, next_normed_out);
+}
+
+PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
+                                const float* residual, uint32_t tokens, const uint32_t* ids,
+                                const float* weights, const float* next_norm_weight,
+                                float* hidden_out, float* next_normed_out)
+{
+    if (tokens > MAX_DECODE_TOKENS)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "grouped prefill GEMM path for %u tokens is not built yet", tokens);
+    return expert_phase(ctx, layer, x, residual, tokens, ids, weights, next_norm_weight,
+                        hidden_out, next_normed_out);
+}
+
+PBMOE_API int pbmoe_dispatch_plan(pbmoe_ctx* ctx, uint32_t experts, uint32_t active_experts,
+                                  uint32_t tokens, const uint32_t* ids, uint32_t* unique_ids,
+                                  uint32_t* unique_count, uint32_t* route_slots,
+                                  uint32_t* grouped_source_rows, uint32_t* grouped_output_indices,
+                                  uint32_t* groups)
+{
+    if (!ctx || !ids || !unique_ids || !unique_count || !route_slots || !grouped_source_rows ||
+        !grouped_output_indices || !groups)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (tokens == 0 || experts == 0 || active_experts == 0)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT,
+                    "layer-major group plan requires non-empty routes and experts");
+    if (experts > MAX_EXPERTS)
+        return fail(PBMOE_ERR_UNSUPPORTED, "experts=%u > %u", experts, MAX_EXPERTS);
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    pbmoe::Plan p;
+    p.unique_ids = unique_ids;
+    p.unique_count = unique_count;
+    p.route_slots = route_slots;
+    p.src_rows = grouped_source_rows;
+    p.out_idx = grouped_output_indices;
+    p.groups = groups;
+    HIP_TRY(pbmoe::launch_dispatch_plan(ctx->stream, ids, tokens * active_experts, experts,
+                                        active_experts, p, ctx->status));
+    return ok();
+}
+
+PBMOE_API int pbmoe_q4_dequantize(pbmoe_ctx* ctx, const void* packed, const void* scales,
+                                  const void* biases, uint32_t sb_dtype, uint32_t rows,
+                                  uint32_t cols, uint32_t group_size, float* out)
+{
+    if (!ctx || !packed || !scales || !biases || !out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (rows == 0 || cols == 0 || group_size == 0)
+        return fail(PBMOE_ERR_SHAPE, "dequantisation needs non-zero rows, cols and group size");
+    if (cols % 8 || cols % group_size || group_size % 8)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "device dequantisation needs cols and group size divisible by 8 and cols by group");
+    if (sb_dtype != PBMOE_DTYPE_F16 && sb_dtype != PBMOE_DTYPE_BF16)
+        return fail(PBMOE_ERR_DTYPE, "scale/bias dtype must be F16 or BF16");
+    if (!aligned(packed, 4) || !aligned(scales, 2) || !aligned(biases, 2))
+        return fail(PBMOE_ERR_ALIGNMENT, "packed must be 4-byte, scale/bias 2-byte aligned");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(pbmoe::launch_q4_dequantize(ctx->stream, static_cast<const uint8_t*>(packed), scales,
+                                        biases, sb_dtype, rows, cols, group_size, out));
+    return ok();
+}
+
+PBMOE_API int pbmoe_synth_fill_q4(pbmoe_ctx* ctx, void* slots_device,
+                                  const pbmoe_q4_layout* layout, uint32_t hidden,
+                                  uint32_t intermediate, uint64_t seed, uint32_t tensor,
+                                  uint32_t layer, uint32_t first_expert, uint32_t count)
+{
+    if (!ctx || !slots_device || !layout)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_layout(layout, hidden, intermediate);
+    if (rc)
+        return rc;
+    rc = set_device(ctx);
+    if (rc)
+        return rc;
+    uint64_t off[9];
+    for (int i = 0; i < 9; ++i)
+        off[i] = layout->components[i].offset;
+    HIP_TRY(pbmoe::launch_synth_fill(ctx->stream, static_cast<uint8_t*>(slots_device),
+                                     layout->expert_bytes, off, hidden, intermediate,
+                                     layout->group_size, layout->scale_bias_dtype, seed, tensor,
+                                     layer, first_expert, count));
+    return ok();
+}

@@ -1,0 +1,79 @@
+// Internal interface between the C ABI (pbmoe_abi.cpp) and the gfx950
+// kernels (pbmoe_kernels.hip).  Not part of the public boundary.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pbmoe {
+
+// Device status bits, OR-ed by kernels and mapped to pbmoe_status by
+// pbmoe_sync().
+enum : uint32_t {
+    ST_ROUTE_RANGE = 1u << 0,  // route id >= experts: route skipped
+    ST_NONFINITE = 1u << 1,    // non-finite router logit
+    ST_BAD_SUM = 1u << 2,      // renormalisation sum not positive/finite
+    ST_NEGATIVE = 1u << 3,     // negative selected probability
+    ST_PLAN_OVERFLOW = 1u << 4 // more routes than the plan buffers hold
+};
+
+// One projection inside a fixed expert slot.
+struct Q4Proj {
+    uint64_t w_off, s_off, b_off; // component byte offsets in the slot
+    uint32_t rows, cols;
+};
+
+// A set of fixed Q4 slots (a bound layer, or the one shared expert).
+struct ExpertSet {
+    const uint8_t* base; // slot 0
+    uint64_t stride;     // expert_bytes
+    uint32_t count;      // number of slots
+    uint32_t group;      // quantisation group size (32, 64 or 128)
+    uint32_t sb_dtype;   // 1 = f16, 2 = bf16
+    Q4Proj gate, up, down;
+};
+
+// Routing parameters for the routing kernel.
+struct RouteParams {
+    uint32_t experts, k, kind, order, norm, n_group, topk_group;
+    float routed_scale;
+};
+
+// Dispatch plan buffers (device), layout documented in pbmoe.h.
+struct Plan {
+    uint32_t* unique_ids;  // [experts]
+    uint32_t* unique_count;// [1]
+    uint32_t* route_slots; // [routes]
+    uint32_t* src_rows;    // [routes]
+    uint32_t* out_idx;     // [routes]
+    uint32_t* groups;      // [experts][2]
+};
+
+hipError_t launch_router_logits(hipStream_t s, const void* w, uint32_t w_dtype, const float* x,
+                                uint32_t tokens, uint32_t experts, uint32_t hidden, float* logits);
+hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bias, uint32_t tokens,
+                             const RouteParams& p, uint32_t* ids, float* weights,
+                             uint32_t* status);
+hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t routes,
+                                uint32_t experts, uint32_t k, const Plan& plan,
+                                uint32_t* status);
+// Decode expert phase.  plan == nullptr selects direct mode (tokens == 1:
+// one work item per route).  act: [routes][I], act_shared: [tokens][Is].
+hipError_t launch_decode_experts(hipStream_t s, const ExpertSet& ex, const ExpertSet* shared,
+                                 const void* shared_gate_w, uint32_t shared_gate_dtype,
+                                 const float* x, const float* residual, uint32_t tokens,
+                                 uint32_t k, uint32_t hidden, const uint32_t* ids,
+                                 const float* weights, const Plan* plan, float* act,
+                                 float* act_shared, float* shared_weight, float* hidden_out,
+                                 const float* next_norm_w, float eps, float* next_normed,
+                                 uint32_t* status);
+hipError_t launch_q4_dequantize(hipStream_t s, const uint8_t* packed, const void* scales,
+                                const void* biases, uint32_t sb_dtype, uint32_t rows,
+                                uint32_t cols, uint32_t group, float* out);
+hipError_t launch_synth_fill(hipStream_t s, uint8_t* slots, uint64_t stride,
+                             const uint64_t* offsets9, uint32_t hidden, uint32_t intermediate,
+                             uint32_t group, uint32_t sb_dtype, uint64_t seed, uint32_t tensor,
+                             uint32_t layer, uint32_t first_expert, uint32_t count);
+hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t value, uint64_t n);
+
+} // namespace pbmoe

@@ -1,0 +1,118 @@
+"""Host-side mirror of the reference's MoE operator seam, over the C ABI.
+
+The reference drives the MoE block through ``MetalExecutionFacade``
+(src/inference/flashmoe/runtime/mod.rs:648-1410): a router prep whose logits
+feed the CPU top-k (metal/mod.rs:2864-3036), ``submit_scheduled_expert_command``
+for decode CMD3 (runtime/mod.rs:922-961) and ``qwen_layer_major_experts`` for
+layer-major prefill (runtime/mod.rs:1151-1161).  ``MoeLayer`` keeps those
+operations and their argument meaning; each call goes straight to
+libpbmoe.so on the device.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import abi
+from .abi import Context, DeviceArray, LayerDesc, check, lib
+from .synth import HostLayer, MoeConfig
+
+
+def layer_desc(cfg: MoeConfig, route_order: int = abi.ORDER_CANONICAL) -> LayerDesc:
+    d = LayerDesc()
+    d.hidden, d.intermediate, d.experts, d.active_experts = cfg.hidden, cfg.intermediate, cfg.experts, cfg.k
+    d.routing, d.normalization, d.route_order = cfg.routing, cfg.normalization, route_order
+    d.routed_scale = cfg.routed_scale
+    d.n_group, d.topk_group = cfg.n_group, cfg.topk_group
+    d.shared_intermediate = cfg.shared_intermediate
+    d.shared_gated = 1 if cfg.shared_gated else 0
+    d.norm_epsilon = 1e-6
+    return d
+
+
+class MoeLayer:
+    """One bound MoE layer (resident experts, router, optional shared expert)."""
+
+    def __init__(self, ctx: Context, index: int, cfg: MoeConfig, layout, route_order: int = abi.ORDER_CANONICAL):
+        self.ctx, self.index, self.cfg, self.layout = ctx, index, cfg, layout
+        self.desc = layer_desc(cfg, route_order)
+        self._keep: list = []
+
+    # -- residency (prepare_resident_expert_backing, metal/mod.rs:1382-1402) --
+    def bind_host(self, host: HostLayer) -> "MoeLayer":
+        cfg = self.cfg
+        check(lib().pbmoe_bind_layer(self.ctx.handle, self.index, C.byref(self.desc), C.byref(self.layout),
+                                     host.slots.ctypes.data, host.slots.nbytes, abi.MEM_HOST))
+        bias = host.selection_bias
+        check(lib().pbmoe_bind_router(self.ctx.handle, self.index, host.router_f16.ctypes.data, abi.DTYPE_F16,
+                                      bias.ctypes.data if bias is not None else None, abi.MEM_HOST))
+        if cfg.shared_intermediate:
+            g = host.shared_gate_f16
+            check(lib().pbmoe_bind_shared(self.ctx.handle, self.index, C.byref(host.shared_layout),
+                                          host.shared_slot.ctypes.data, g.ctypes.data if g is not None else None,
+                                          abi.DTYPE_F16, abi.MEM_HOST))
+        return self
+
+    def bind_device(self, slots: DeviceArray, router: DeviceArray, selection_bias: DeviceArray | None = None,
+                    shared_layout=None, shared_slot: DeviceArray | None = None,
+                    shared_gate: DeviceArray | None = None) -> "MoeLayer":
+        self._keep = [slots, router, selection_bias, shared_slot, shared_gate]
+        check(lib().pbmoe_bind_layer(self.ctx.handle, self.index, C.byref(self.desc), C.byref(self.layout),
+                                     slots.ptr, slots.nbytes, abi.MEM_DEVICE))
+        check(lib().pbmoe_bind_router(self.ctx.handle, self.index, router.ptr, abi.DTYPE_F16,
+                                      selection_bias.ptr if selection_bias is not None else None, abi.MEM_DEVICE))
+        if shared_slot is not None:
+            check(lib().pbmoe_bind_shared(self.ctx.handle, self.index, C.byref(shared_layout), shared_slot.ptr,
+                                          shared_gate.ptr if shared_gate is not None else None, abi.DTYPE_F16,
+                                          abi.MEM_DEVICE))
+        return self
+
+    # -- router prep + routing stage (metal/mod.rs:2943-3013) ----------------
+    def route(self, x: DeviceArray, ids: DeviceArray, weights: DeviceArray, logits: DeviceArray | None = None):
+        tokens = x.shape[0]
+        check(lib().pbmoe_route(self.ctx.handle, self.index, x.ptr, tokens, ids.ptr, weights.ptr,
+                                logits.ptr if logits is not None else None))
+
+    def route_logits(self, logits: DeviceArray, ids: DeviceArray, weights: DeviceArray):
+        check(lib().pbmoe_route_logits(self.ctx.handle, self.index, logits.ptr, logits.shape[0], ids.ptr,
+                                       weights.ptr))
+
+    # -- CMD3 decode (submit_scheduled_expert_command) ------------------------
+    def submit_scheduled_expert_command(self, x: DeviceArray, residual: DeviceArray, ids: DeviceArray,
+                                        weights: DeviceArray, hidden_out: DeviceArray,
+                                        next_norm: DeviceArray | None = None,
+                                        next_normed: DeviceArray | None = None):
+        check(lib().pbmoe_moe_decode(self.ctx.handle, self.index, x.ptr, residual.ptr, x.shape[0], ids.ptr,
+                                     weights.ptr, next_norm.ptr if next_norm is not None else None, hidden_out.ptr,
+                                     next_normed.ptr if next_normed is not None else None))
+
+    # -- layer-major prefill (qwen_layer_major_experts) -----------------------
+    def qwen_layer_major_experts(self, x: DeviceArray, residual: DeviceArray, ids: DeviceArray,
+                                 weights: DeviceArray, hidden_out: DeviceArray,
+                                 next_norm: DeviceArray | None = None, next_normed: DeviceArray | None = None):
+        check(lib().pbmoe_moe_prefill(self.ctx.handle, self.index, x.ptr, residual.ptr, x.shape[0], ids.ptr,
+                                      weights.ptr, next_norm.ptr if next_norm is not None else None,
+                                      hidden_out.ptr, next_normed.ptr if next_normed is not None else None))
+
+    def unbind(self):
+        check(lib().pbmoe_unbind_layer(self.ctx.handle, self.index))
+
+
+def dispatch_plan(ctx: Context, ids: DeviceArray, experts: int):
+    """resolve_layer_major_experts + qwen_layer_major_group_plan on the device;
+    returns host arrays (unique_ids, route_slots, src_rows, out_idx, groups)."""
+    tokens, k = ids.shape
+    n = tokens * k
+    uniq = ctx.array(experts, np.uint32)
+    cnt = ctx.array(1, np.uint32)
+    slots = ctx.array(n, np.uint32)
+    src = ctx.array(n, np.uint32)
+    out = ctx.array(n, np.uint32)
+    groups = ctx.array((experts, 2), np.uint32)
+    check(lib().pbmoe_dispatch_plan(ctx.handle, experts, k, tokens, ids.ptr, uniq.ptr, cnt.ptr, slots.ptr, src.ptr,
+                                    out.ptr, groups.ptr))
+    ctx.sync()
+    u = int(cnt.download()[0])
+    return (uniq.download()[:u], slots.download(), src.download(), out.download(),
+            [tuple(int(v) for v in g) for g in groups.download()[:u]])

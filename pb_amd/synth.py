@@ -1,0 +1,164 @@
+"""Seeded synthetic MoE layers (host side), shared by tests and the benchmark.
+
+Wraps ``libpbmoe_synth.so`` (pb_amd/csrc/synth_host.c).  Q4 expert bytes are
+identical to the device fill kernel's (``pbmoe_synth_fill_q4``); normal draws
+are produced on the host only.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpbmoe_synth.so")
+
+T_EXPERT, T_ROUTER, T_SHARED, T_SHARED_GATE, T_INPUT, T_RESIDUAL, T_ROUTER_BIAS, T_LOGITS = range(1, 9)
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"synth library missing: {LIB_PATH}; run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        L.pbm_fill_q4_experts.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                          C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint64, C.c_void_p,
+                                          C.c_int]
+        L.pbm_fill_normal_f16.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64,
+                                          C.c_double, C.c_void_p, C.c_int]
+        L.pbm_f16_to_f32_array.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p]
+        L.pbm_f32_to_f16_array.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p]
+        L.pbm_f32_to_bf16_array.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p]
+        L.pbm_fill_uniform_f32.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64,
+                                           C.c_float, C.c_float, C.c_void_p]
+        L.pbm_drawn_logits_zipf.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_double,
+                                            C.c_void_p, C.c_void_p]
+        L.pbm_drawn_logits_zipf.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def q4_experts(seed: int, tensor: int, layer: int, first: int, count: int, hidden: int, intermediate: int,
+               group: int, sb_dtype: int, offsets, expert_bytes: int) -> np.ndarray:
+    """`count` fixed-slot Q4 experts back to back (uint8)."""
+    out = np.empty(count * expert_bytes, np.uint8)
+    off = np.ascontiguousarray(np.asarray(offsets, dtype=np.uint64))
+    lib().pbm_fill_q4_experts(seed, tensor, layer, first, count, hidden, intermediate, group, sb_dtype,
+                              off.ctypes.data, expert_bytes, out.ctypes.data, _threads())
+    return out
+
+
+def normal_f16(seed: int, tensor: int, layer: int, expert: int, part: int, n: int, sigma: float) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    lib().pbm_fill_normal_f16(seed, tensor, layer, expert, part, n, sigma, out.ctypes.data, _threads())
+    return out
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().pbm_f16_to_f32_array(h.ctypes.data, h.size, out.ctypes.data)
+    return out
+
+
+def f32_to_f16(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().pbm_f32_to_f16_array(f.ctypes.data, f.size, out.ctypes.data)
+    return out
+
+
+def f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().pbm_f32_to_bf16_array(f.ctypes.data, f.size, out.ctypes.data)
+    return out
+
+
+def uniform_f32(seed: int, tensor: int, layer: int, expert: int, part: int, n: int, lo: float, width: float):
+    out = np.empty(n, np.float32)
+    lib().pbm_fill_uniform_f32(seed, tensor, layer, expert, part, n, lo, width, out.ctypes.data)
+    return out
+
+
+def drawn_logits_zipf(seed: int, layer: int, tokens: int, experts: int, k: int, s: float = 1.1):
+    """Prefill router logits with a Zipf(s) expert load; returns (logits, hist)."""
+    logits = np.empty((tokens, experts), np.float32)
+    hist = np.empty(experts, np.uint32)
+    rc = lib().pbm_drawn_logits_zipf(seed, layer, tokens, experts, k, s, logits.ctypes.data, hist.ctypes.data)
+    if rc:
+        raise ValueError("invalid zipf logits request")
+    return logits, hist
+
+
+@dataclass
+class MoeConfig:
+    """One BASELINE workload shape (see configs in pb_amd.configs)."""
+    name: str
+    hidden: int
+    intermediate: int
+    experts: int
+    k: int
+    routing: int = 0            # pbmoe_routing
+    normalization: int = 0      # pbmoe_normalization
+    routed_scale: float = 1.0
+    n_group: int = 1
+    topk_group: int = 1
+    shared_intermediate: int = 0
+    shared_gated: bool = False
+    group: int = 64
+    sb_dtype: int = 1           # f16 scale/bias (BASELINE); 2 = bf16 (reference)
+    tokens: int = 1
+
+
+@dataclass
+class HostLayer:
+    """Host arrays of one seeded layer."""
+    cfg: MoeConfig
+    layer: int
+    layout: object
+    slots: np.ndarray
+    router_f16: np.ndarray           # [E][H] uint16 (f16 bits)
+    selection_bias: np.ndarray | None
+    shared_layout: object | None = None
+    shared_slot: np.ndarray | None = None
+    shared_gate_f16: np.ndarray | None = None
+    extra: dict = field(default_factory=dict)
+
+
+def make_layer(cfg: MoeConfig, seed: int, layer: int, layout_fn, with_slots: bool = True) -> HostLayer:
+    """Generate a full layer on the host.  layout_fn(hidden, inter, group, dtype)
+    returns a layout object with ``offsets`` and ``expert_bytes``."""
+    H, I, E = cfg.hidden, cfg.intermediate, cfg.experts
+    lay = layout_fn(H, I, cfg.group, cfg.sb_dtype)
+    slots = (q4_experts(seed, T_EXPERT, layer, 0, E, H, I, cfg.group, cfg.sb_dtype, lay.offsets,
+                        int(lay.expert_bytes)) if with_slots else np.empty(0, np.uint8))
+    router = normal_f16(seed, T_ROUTER, layer, 0, 0, E * H, 0.02).reshape(E, H)
+    bias = None
+    if cfg.routing != 0:
+        bias = uniform_f32(seed, T_ROUTER_BIAS, layer, 0, 0, E, -0.05, 0.1)
+    hl = HostLayer(cfg, layer, lay, slots, router, bias)
+    if cfg.shared_intermediate:
+        sl = layout_fn(H, cfg.shared_intermediate, cfg.group, cfg.sb_dtype)
+        hl.shared_layout = sl
+        hl.shared_slot = q4_experts(seed, T_SHARED, layer, 0, 1, H, cfg.shared_intermediate, cfg.group,
+                                    cfg.sb_dtype, sl.offsets, int(sl.expert_bytes))
+        if cfg.shared_gated:
+            hl.shared_gate_f16 = normal_f16(seed, T_SHARED_GATE, layer, 0, 0, H, 0.02).reshape(1, H)
+    return hl
+
+
+def activations(seed: int, layer: int, tokens: int, hidden: int):
+    """x and residual [tokens][hidden]: f16 N(0,1) draws widened to f32."""
+    x = f16_to_f32(normal_f16(seed, T_INPUT, layer, 0, 0, tokens * hidden, 1.0)).reshape(tokens, hidden)
+    r = f16_to_f32(normal_f16(seed, T_RESIDUAL, layer, 0, 0, tokens * hidden, 1.0)).reshape(tokens, hidden)
+    return x, r

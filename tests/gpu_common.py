@@ -1,0 +1,81 @@
+"""Shared set-up for the GPU parity tests: seeded layers built on the device
+through the C ABI, and the oracle-side view of the same bytes."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from oracle import oracle as orc
+from pb_amd import abi, synth
+from pb_amd.flashmoe import MoeLayer
+
+SEED = 20261201
+
+
+def max_abs_rel_l2(got: np.ndarray, ref: np.ndarray):
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    rel = float(np.linalg.norm(got.astype(np.float64) - ref) / max(np.linalg.norm(ref.astype(np.float64)), 1e-30))
+    return float(d.max()), rel
+
+
+def assert_layer_tolerance(got: np.ndarray, ref: np.ndarray, what: str = "hidden"):
+    """BASELINE bar: max-abs <= 1e-2 and relative L2 <= 2e-3 against the fp32 oracle."""
+    mx, rel = max_abs_rel_l2(got, ref)
+    assert mx <= 1e-2 and rel <= 2e-3, f"{what}: max_abs={mx:.3e} rel_l2={rel:.3e}"
+    return mx, rel
+
+
+class DeviceLayer:
+    """A seeded layer resident on the device, plus the host pieces the
+    oracle needs (expert slots are regenerated on the host on demand)."""
+
+    def __init__(self, ctx: abi.Context, cfg, layer: int, route_order: int = abi.ORDER_CANONICAL,
+                 index: int | None = None):
+        self.ctx, self.cfg, self.layer = ctx, cfg, layer
+        H, I, E = cfg.hidden, cfg.intermediate, cfg.experts
+        self.layout = abi.q4_layout_fixed(H, I, cfg.group, cfg.sb_dtype)
+        self.slots = ctx.array(E * self.layout.expert_bytes, np.uint8)
+        abi.check(abi.lib().pbmoe_synth_fill_q4(ctx.handle, self.slots.ptr, C.byref(self.layout), H, I, SEED,
+                                                synth.T_EXPERT, layer, 0, E))
+        self.host = synth.make_layer(cfg, SEED, layer, abi.q4_layout_fixed, with_slots=False)
+        h = self.host
+        self.router = ctx.to_device(h.router_f16)
+        self.bias = ctx.to_device(h.selection_bias) if h.selection_bias is not None else None
+        self.shared = ctx.to_device(h.shared_slot) if cfg.shared_intermediate else None
+        self.gate = ctx.to_device(h.shared_gate_f16) if h.shared_gate_f16 is not None else None
+        self.moe = MoeLayer(ctx, layer if index is None else index, cfg, self.layout, route_order)
+        self.moe.bind_device(self.slots, self.router, self.bias, h.shared_layout, self.shared, self.gate)
+
+    # oracle views ----------------------------------------------------------
+    def oracle_layout(self):
+        cfg, lay = self.cfg, self.layout
+        return orc.make_layout(cfg.hidden, cfg.intermediate, cfg.group, cfg.sb_dtype, lay.offsets,
+                               int(lay.expert_bytes))
+
+    def oracle_shared_layout(self):
+        cfg, sl = self.cfg, self.host.shared_layout
+        if sl is None:
+            return None
+        return orc.make_layout(cfg.hidden, cfg.shared_intermediate, cfg.group, cfg.sb_dtype, sl.offsets,
+                               int(sl.expert_bytes))
+
+    def compact_slots(self, ids: np.ndarray):
+        """Host slots of just the experts in `ids`, and ids remapped onto them."""
+        uniq = sorted(set(int(e) for e in ids.ravel()))
+        lay, cfg = self.layout, self.cfg
+        parts = [synth.q4_experts(SEED, synth.T_EXPERT, self.layer, e, 1, cfg.hidden, cfg.intermediate, cfg.group,
+                                  cfg.sb_dtype, lay.offsets, int(lay.expert_bytes)) for e in uniq]
+        remap = {e: i for i, e in enumerate(uniq)}
+        return np.concatenate(parts), np.vectorize(remap.get)(ids).astype(np.int32), len(uniq)
+
+    def oracle_block(self, x, residual, ids, weights, next_norm=None, threads=8):
+        slots, rid, n = self.compact_slots(ids)
+        h = self.host
+        return orc.moe_block(self.oracle_layout(), slots, n, x, residual, rid, weights,
+                             shared_layout=self.oracle_shared_layout(), shared_slot=h.shared_slot,
+                             shared_gate_w=h.shared_gate_f16, shared_gate_dtype=orc.DT_F16,
+                             next_norm_w=next_norm, threads=threads)
+
+    def oracle_logits(self, x):
+        return np.stack([orc.router_logits(self.host.router_f16, x[t], orc.DT_F16) for t in range(x.shape[0])])

@@ -1,0 +1,259 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle on the
+same seeded inputs.  Integer/index/byte results are bit-exact; layer outputs
+meet max-abs <= 1e-2 and relative L2 <= 2e-3 against the fp32 oracle."""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from pb_amd import abi, synth
+from pb_amd.configs import C1, C2, C3, C5
+from pb_amd.flashmoe import dispatch_plan
+from tests.gpu_common import SEED, DeviceLayer, assert_layer_tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = abi.Context(0)
+    yield c
+    c.close()
+
+
+_layers: dict = {}
+
+
+def _layer(ctx, cfg, layer, order=abi.ORDER_CANONICAL):
+    key = (cfg.name, layer, order)
+    if key not in _layers:
+        _say(f"[setup] binding {cfg.name} layer {layer} order {order}")
+        _layers[key] = DeviceLayer(ctx, cfg, layer, order, index=len(_layers))
+    return _layers[key]
+
+
+def _route(ctx, dl, x_host):
+    T = x_host.shape[0]
+    x = ctx.to_device(x_host)
+    ids = ctx.array((T, dl.cfg.k), np.uint32)
+    w = ctx.array((T, dl.cfg.k), np.float32)
+    logits = ctx.array((T, dl.cfg.experts), np.float32)
+    dl.moe.route(x, ids, w, logits)
+    ctx.sync()
+    return x, ids, w, logits
+
+
+# ------------------------------------------------------------ bytes exact ---
+@pytest.mark.parametrize("dtype", [abi.DTYPE_F16, abi.DTYPE_BF16])
+def test_device_fill_matches_host_generator(ctx, dtype):
+    _say(f"[test] device fill dtype={dtype}")
+    H, I = 2048, 512
+    lay = abi.q4_layout_fixed(H, I, 64, dtype)
+    dev = ctx.array(3 * lay.expert_bytes, np.uint8)
+    abi.check(abi.lib().pbmoe_synth_fill_q4(ctx.handle, dev.ptr, C.byref(lay), H, I, SEED, synth.T_EXPERT, 7, 5, 3))
+    ctx.sync()
+    host = synth.q4_experts(SEED, synth.T_EXPERT, 7, 5, 3, H, I, 64, dtype, lay.offsets, lay.expert_bytes)
+    np.testing.assert_array_equal(dev.download(), host)
+
+
+@pytest.mark.parametrize("dtype", [abi.DTYPE_F16, abi.DTYPE_BF16])
+def test_dequantized_weights_bit_exact(ctx, dtype):
+    _say(f"[test] dequant dtype={dtype}")
+    H, I = 2048, 768
+    lay = abi.q4_layout_fixed(H, I, 64, dtype)
+    slot = synth.q4_experts(SEED, synth.T_EXPERT, 0, 3, 1, H, I, 64, dtype, lay.offsets, lay.expert_bytes)
+    o = lay.offsets
+    for p, (rows, cols) in enumerate([(I, H), (I, H), (H, I)]):
+        packed, sc, bi = slot[o[3 * p]:o[3 * p + 1]], slot[o[3 * p + 1]:o[3 * p + 2]], slot[o[3 * p + 2]:(o[3 * p + 3] if p < 2 else lay.expert_bytes)]
+        dp, ds, db = ctx.to_device(packed), ctx.to_device(sc), ctx.to_device(bi)
+        out = ctx.array((rows, cols), np.float32)
+        abi.check(abi.lib().pbmoe_q4_dequantize(ctx.handle, dp.ptr, ds.ptr, db.ptr, dtype, rows, cols, 64, out.ptr))
+        ctx.sync()
+        ref = orc.q4_dequantize_rows(packed, sc.view(np.uint16), bi.view(np.uint16), rows, cols, 64, dtype)
+        np.testing.assert_array_equal(out.download(), ref)
+
+
+# ----------------------------------------------------------------- router ---
+@pytest.mark.parametrize("cfg,T", [(C1, 1), (C2, 8)])
+def test_router_logits_within_summation_bound(ctx, cfg, T):
+    _say(f"[test] router logits {cfg.name} T={T}")
+    dl = _layer(ctx, cfg, 0)
+    xh, _ = synth.activations(SEED, 0, T, cfg.hidden)
+    _, _, _, logits = _route(ctx, dl, xh)
+    got = logits.download()
+    ref = dl.oracle_logits(xh)
+    w = synth.f16_to_f32(dl.host.router_f16)
+    mag = np.abs(xh) @ np.abs(w).T
+    bound = (cfg.hidden + 64) * 2.0**-24 * mag
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+@pytest.mark.parametrize("cfg,T,order", [(C2, 8, abi.ORDER_CANONICAL), (C1, 8, abi.ORDER_REFERENCE_SLOT),
+                                         (C2, 4, abi.ORDER_REFERENCE_SLOT)])
+def test_topk_bit_exact_on_device_logits(ctx, cfg, T, order):
+    _say(f"[test] topk exact {cfg.name} T={T} order={order}")
+    dl = _layer(ctx, cfg, 0, order)
+    xh, _ = synth.activations(SEED, 1, T, cfg.hidden)
+    _, ids, w, logits = _route(ctx, dl, xh)
+    l = logits.download()
+    ref_ids, ref_w = orc.route_rows(l, cfg.k, orc.ROUTING_SOFTMAX, order)
+    np.testing.assert_array_equal(ids.download().astype(np.int32), ref_ids)
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6, atol=0)
+
+
+def test_topk_ties_follow_lower_index_rule(ctx):
+    _say("[test] topk ties")
+    dl = _layer(ctx, C1, 0)
+    T, E = 4, C1.experts
+    l = np.zeros((T, E), np.float32)
+    l[:, ::3] = 1.0            # many exact ties at the K boundary
+    l[1, 100] = 2.0
+    l[2, :] = -3.0
+    d = ctx.to_device(l)
+    ids = ctx.array((T, C1.k), np.uint32)
+    w = ctx.array((T, C1.k), np.float32)
+    dl.moe.route_logits(d, ids, w)
+    ctx.sync()
+    ref_ids, ref_w = orc.route_rows(l, C1.k, orc.ROUTING_SOFTMAX, orc.ORDER_CANONICAL)
+    np.testing.assert_array_equal(ids.download().astype(np.int32), ref_ids)
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6)
+    dl2 = _layer(ctx, C1, 0, abi.ORDER_REFERENCE_SLOT)
+    dl2.moe.route_logits(d, ids, w)
+    ctx.sync()
+    ref_ids, _ = orc.route_rows(l, C1.k, orc.ROUTING_SOFTMAX, orc.ORDER_REFERENCE_SLOT)
+    np.testing.assert_array_equal(ids.download().astype(np.int32), ref_ids)
+
+
+@pytest.mark.parametrize("cfg,T", [(C1, 8), (C2, 8)])
+def test_routes_end_to_end_match_oracle(ctx, cfg, T):
+    """Expert indices from x: the GPU router (tree sum) against the oracle's
+    sequential logits.  Tokens whose K/K+1 logit gap is below the summation
+    error bound are reported, not compared; the seeded data has none."""
+    _say(f"[test] routes e2e {cfg.name} T={T}")
+    dl = _layer(ctx, cfg, 0, abi.ORDER_REFERENCE_SLOT)
+    xh, _ = synth.activations(SEED, 2, T, cfg.hidden)
+    _, ids, _, _ = _route(ctx, dl, xh)
+    ref_l = dl.oracle_logits(xh)
+    ref_ids, _ = orc.route_rows(ref_l, cfg.k, orc.ROUTING_SOFTMAX, orc.ORDER_REFERENCE_SLOT)
+    w = synth.f16_to_f32(dl.host.router_f16)
+    bound = 2 * (cfg.hidden + 64) * 2.0**-24 * (np.abs(xh) @ np.abs(w).T)
+    got = ids.download().astype(np.int32)
+    close = 0
+    for t in range(T):
+        srt = np.sort(ref_l[t])[::-1]
+        if srt[cfg.k - 1] - srt[cfg.k] <= bound[t].max():
+            close += 1
+            continue
+        np.testing.assert_array_equal(got[t], ref_ids[t])
+    assert close == 0
+
+
+def test_grouped_sigmoid_routing_c5(ctx):
+    _say("[test] grouped sigmoid routing C5")
+    dl = _layer(ctx, C5, 0)
+    T = 8
+    xh, _ = synth.activations(SEED, 3, T, C5.hidden)
+    _, ids, w, logits = _route(ctx, dl, xh)
+    l = logits.download()
+    ref_ids, ref_w = orc.route_rows(l, C5.k, orc.ROUTING_SIGMOID_GROUPED, orc.ORDER_CANONICAL,
+                                    bias=dl.host.selection_bias, n_group=C5.n_group, topk_group=C5.topk_group,
+                                    routed_scale=C5.routed_scale)
+    np.testing.assert_array_equal(ids.download().astype(np.int32), ref_ids)
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6)
+
+
+# ------------------------------------------------------------ expert phase ---
+@pytest.mark.parametrize("cfg,T", [(C1, 1), (C2, 1), (C2, 4), (C2, 8), (C1, 16), (C5, 1)])
+def test_decode_layer_matches_oracle(ctx, cfg, T):
+    _say(f"[test] decode layer {cfg.name} T={T}")
+    dl = _layer(ctx, cfg, 0)
+    xh, rh = synth.activations(SEED, 10 + T, T, cfg.hidden)
+    x, ids, w, _ = _route(ctx, dl, xh)
+    res = ctx.to_device(rh)
+    nw_h = synth.uniform_f32(SEED, 99, 0, 0, 0, cfg.hidden, 0.5, 1.0)
+    nw = ctx.to_device(nw_h)
+    out = ctx.array((T, cfg.hidden), np.float32)
+    nn = ctx.array((T, cfg.hidden), np.float32)
+    dl.moe.submit_scheduled_expert_command(x, res, ids, w, out, nw, nn)
+    ctx.sync()
+    ids_h = ids.download().astype(np.int32)
+    w_h = w.download()
+    ref_h, ref_n = dl.oracle_block(xh, rh, ids_h, w_h, next_norm=nw_h)
+    mx, rel = assert_layer_tolerance(out.download(), ref_h)
+    _say(f"[result] {cfg.name} T={T} hidden max_abs={mx:.3e} rel_l2={rel:.3e}")
+    assert_layer_tolerance(nn.download(), ref_n, "next_normed")
+
+
+def test_one_row_prefill_is_bitwise_decode(ctx):
+    _say("[test] one-row parity")
+    dl = _layer(ctx, C2, 0)
+    xh, rh = synth.activations(SEED, 40, 1, C2.hidden)
+    x, ids, w, _ = _route(ctx, dl, xh)
+    res = ctx.to_device(rh)
+    a = ctx.array((1, C2.hidden), np.float32)
+    b = ctx.array((1, C2.hidden), np.float32)
+    dl.moe.submit_scheduled_expert_command(x, res, ids, w, a)
+    dl.moe.qwen_layer_major_experts(x, res, ids, w, b)
+    ctx.sync()
+    np.testing.assert_array_equal(a.download().view(np.uint32), b.download().view(np.uint32))
+
+
+def test_out_of_range_route_is_reported(ctx):
+    _say("[test] bad route reported")
+    dl = _layer(ctx, C1, 0)
+    xh, rh = synth.activations(SEED, 41, 2, C1.hidden)
+    x, res = ctx.to_device(xh), ctx.to_device(rh)
+    ids_h = np.tile(np.arange(C1.k, dtype=np.uint32), (2, 1))
+    ids_h[1, 3] = C1.experts + 5
+    ids = ctx.to_device(ids_h)
+    w = ctx.to_device(np.full((2, C1.k), 1.0 / C1.k, np.float32))
+    out = ctx.array((2, C1.hidden), np.float32)
+    dl.moe.submit_scheduled_expert_command(x, res, ids, w, out)
+    with pytest.raises(abi.PbmoeError) as e:
+        ctx.sync()
+    assert e.value.status == abi.ERR_ROUTE
+    ctx.sync()  # status word was cleared
+
+
+# --------------------------------------------------------------- dispatch ---
+def _plan_ref(ids, E):
+    uniq, slots = orc.layer_major_union(ids.astype(np.int32), E)
+    src, out, groups = orc.group_plan(slots, len(uniq), ids.shape[1])
+    return uniq, slots, src, out, groups
+
+
+@pytest.mark.parametrize("T,K,E,seed", [(1, 8, 128, 0), (7, 10, 512, 1), (16, 10, 512, 2), (300, 6, 64, 3),
+                                        (1000, 16, 1024, 4)])
+def test_dispatch_plan_bit_exact_random(ctx, T, K, E, seed):
+    _say(f"[test] plan random T={T} K={K} E={E}")
+    rng = np.random.default_rng(seed)
+    ids_h = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.uint32)
+    got = dispatch_plan(ctx, ctx.to_device(ids_h), E)
+    ref = _plan_ref(ids_h, E)
+    np.testing.assert_array_equal(got[0], ref[0])
+    np.testing.assert_array_equal(got[1].astype(np.int32), ref[1])
+    np.testing.assert_array_equal(got[2], ref[2])
+    np.testing.assert_array_equal(got[3], ref[3])
+    assert got[4] == ref[4]
+
+
+def test_dispatch_plan_bit_exact_zipf_prefill(ctx):
+    _say("[test] plan zipf C3")
+    logits, hist = synth.drawn_logits_zipf(SEED, 0, C3.tokens, C3.experts, C3.k, 1.1)
+    ids_ref, _ = orc.route_rows(logits, C3.k, orc.ROUTING_SOFTMAX, orc.ORDER_CANONICAL)
+    got = dispatch_plan(ctx, ctx.to_device(ids_ref.astype(np.uint32)), C3.experts)
+    ref = _plan_ref(ids_ref, C3.experts)
+    for g, r in zip(got[:4], ref[:4]):
+        np.testing.assert_array_equal(np.asarray(g).astype(np.int64), np.asarray(r).astype(np.int64))
+    assert got[4] == ref[4]
+    counts = [c for _, c in got[4]]
+    assert sorted(counts) == sorted(int(h) for h in hist if h)
