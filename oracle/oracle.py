@@ -286,6 +286,29 @@ def moe_block(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarray, 
     return out, nn
 
 
+def moe_block_f64(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarray, residual: np.ndarray,
+                  ids: np.ndarray, weights: np.ndarray, shared_layout: Q4Layout | None = None,
+                  shared_slot: np.ndarray | None = None, shared_gate_w: np.ndarray | None = None,
+                  shared_gate_dtype: int = DT_F16, threads: int = 1) -> np.ndarray:
+    """fp64 evaluation of the block (the exact value the f32 paths round)."""
+    xx = _f32(x)
+    rr = _f32(residual)
+    rows, hidden = xx.shape
+    ii = np.ascontiguousarray(ids, dtype=np.int32)
+    ww = _f32(weights)
+    out = np.empty((rows, hidden), np.float64)
+    sg = np.ascontiguousarray(shared_gate_w) if shared_gate_w is not None else None
+    rc = lib().or_moe_block_f64(
+        C.byref(layout), _p(slots), C.c_int(experts),
+        C.byref(shared_layout) if shared_layout is not None else None,
+        _p(shared_slot) if shared_slot is not None else None,
+        _p(sg) if sg is not None else None, C.c_int(shared_gate_dtype),
+        _p(xx), _p(rr), C.c_int(rows), C.c_int(ii.shape[1]), _p(ii), _p(ww), _p(out), C.c_int(threads))
+    if rc:
+        raise ValueError(f"oracle moe_block_f64 failed: {rc}")
+    return out
+
+
 def route_rows(logits: np.ndarray, k: int, kind: int = ROUTING_SOFTMAX, order: int = ORDER_REFERENCE_SLOT,
                bias: np.ndarray | None = None, n_group: int = 1, topk_group: int = 1,
                policy: int = NORM_RENORMALIZE, routed_scale: float = 1.0):

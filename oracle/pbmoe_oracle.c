@@ -669,3 +669,89 @@ int or_route_rows(const float* logits, const float* bias, int rows, int experts,
     }
     return OR_OK;
 }
+
+/* ------------------------------------------------------------------------
+ * fp64 evaluation of the same block (not a reference restatement: the exact
+ * value the f32 paths approximate).  Used to measure the reference's own
+ * f32 rounding error where outputs are large enough that a fixed absolute
+ * tolerance falls below f32 resolution.
+ * ---------------------------------------------------------------------- */
+static void or_projection_f64(const or_q4_layout* l, const uint8_t* slot, int proj,
+                              const double* x, double* out)
+{
+    int rows = proj == 2 ? (int)l->hidden : (int)l->intermediate;
+    int cols = proj == 2 ? (int)l->intermediate : (int)l->hidden;
+    int g = (int)l->group_size, gpr = cols / g;
+    const uint8_t* packed = slot + l->offset[3 * proj];
+    const void* sc = slot + l->offset[3 * proj + 1];
+    const void* bi = slot + l->offset[3 * proj + 2];
+    size_t stride = (size_t)(cols + 1) / 2;
+    for (int r = 0; r < rows; ++r) {
+        double acc = 0.0;
+        for (int c = 0; c < cols; ++c) {
+            double s = or_load(sc, (int)l->sb_dtype, (size_t)r * gpr + c / g);
+            double b = or_load(bi, (int)l->sb_dtype, (size_t)r * gpr + c / g);
+            acc += ((double)or_nibble(packed, stride, r, c) * s + b) * x[c];
+        }
+        out[r] = acc;
+    }
+}
+
+static void or_expert_f64(const or_q4_layout* l, const uint8_t* slot, const double* x, double* y)
+{
+    int I = (int)l->intermediate;
+    double* g = (double*)malloc(sizeof(double) * 3 * (size_t)I);
+    double* u = g + I;
+    double* a = g + 2 * I;
+    or_projection_f64(l, slot, 0, x, g);
+    or_projection_f64(l, slot, 1, x, u);
+    for (int i = 0; i < I; ++i)
+        a[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
+    or_projection_f64(l, slot, 2, a, y);
+    free(g);
+}
+
+int or_moe_block_f64(const or_q4_layout* lay, const uint8_t* slots, int experts,
+                     const or_q4_layout* shared_lay, const uint8_t* shared_slot,
+                     const void* shared_gate_w, int shared_gate_dtype, const float* x,
+                     const float* residual, int rows, int k, const int32_t* ids,
+                     const float* weights, double* hidden, int threads)
+{
+    int H = (int)lay->hidden;
+    for (int i = 0; i < rows * k; ++i)
+        if (ids[i] < 0 || ids[i] >= experts)
+            return OR_ERR_ROUTE;
+    (void)threads;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(dynamic, 1)
+#endif
+    for (int t = 0; t < rows; ++t) {
+        double* xd = (double*)malloc(sizeof(double) * (size_t)H);
+        double* y = (double*)malloc(sizeof(double) * (size_t)H);
+        double* h = hidden + (size_t)t * H;
+        for (int c = 0; c < H; ++c) {
+            xd[c] = x[(size_t)t * H + c];
+            h[c] = residual[(size_t)t * H + c];
+        }
+        for (int j = 0; j < k; ++j) {
+            or_expert_f64(lay, slots + (size_t)ids[t * k + j] * lay->expert_bytes, xd, y);
+            for (int c = 0; c < H; ++c)
+                h[c] += (double)weights[t * k + j] * y[c];
+        }
+        if (shared_lay) {
+            or_expert_f64(shared_lay, shared_slot, xd, y);
+            double g = 80.0;
+            if (shared_gate_w) {
+                g = 0.0;
+                for (int c = 0; c < H; ++c)
+                    g += (double)or_load(shared_gate_w, shared_gate_dtype, (size_t)c) * xd[c];
+            }
+            double sw = 1.0 / (1.0 + exp(-g));
+            for (int c = 0; c < H; ++c)
+                h[c] += sw * y[c];
+        }
+        free(xd);
+        free(y);
+    }
+    return OR_OK;
+}

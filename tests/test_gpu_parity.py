@@ -136,8 +136,11 @@ def test_topk_ties_follow_lower_index_rule(ctx):
 @pytest.mark.parametrize("cfg,T", [(C1, 8), (C2, 8)])
 def test_routes_end_to_end_match_oracle(ctx, cfg, T):
     """Expert indices from x: the GPU router (tree sum) against the oracle's
-    sequential logits.  Tokens whose K/K+1 logit gap is below the summation
-    error bound are reported, not compared; the seeded data has none."""
+    sequential logits.  Every token must give identical ids; a difference is
+    tolerated only for a token whose K/K+1 logit gap lies inside the rigorous
+    error bound of the two summation orders (none occurs on the seeded data,
+    but the worst-case bound is loose enough that some tokens fall inside it,
+    so those are counted and still compared)."""
     _say(f"[test] routes e2e {cfg.name} T={T}")
     dl = _layer(ctx, cfg, 0, abi.ORDER_REFERENCE_SLOT)
     xh, _ = synth.activations(SEED, 2, T, cfg.hidden)
@@ -147,14 +150,16 @@ def test_routes_end_to_end_match_oracle(ctx, cfg, T):
     w = synth.f16_to_f32(dl.host.router_f16)
     bound = 2 * (cfg.hidden + 64) * 2.0**-24 * (np.abs(xh) @ np.abs(w).T)
     got = ids.download().astype(np.int32)
-    close = 0
+    close, mismatched = 0, 0
     for t in range(T):
         srt = np.sort(ref_l[t])[::-1]
-        if srt[cfg.k - 1] - srt[cfg.k] <= bound[t].max():
-            close += 1
-            continue
-        np.testing.assert_array_equal(got[t], ref_ids[t])
-    assert close == 0
+        inside = srt[cfg.k - 1] - srt[cfg.k] <= bound[t].max()
+        close += int(inside)
+        if not np.array_equal(got[t], ref_ids[t]):
+            mismatched += 1
+            assert inside, f"token {t}: ids differ outside the summation bound"
+    _say(f"[result] {cfg.name}: {close}/{T} tokens inside the bound, {mismatched} mismatched")
+    assert mismatched == 0
 
 
 def test_grouped_sigmoid_routing_c5(ctx):
@@ -188,7 +193,8 @@ def test_decode_layer_matches_oracle(ctx, cfg, T):
     ids_h = ids.download().astype(np.int32)
     w_h = w.download()
     ref_h, ref_n = dl.oracle_block(xh, rh, ids_h, w_h, next_norm=nw_h)
-    mx, rel = assert_layer_tolerance(out.download(), ref_h)
+    exact = dl.exact_block(xh, rh, ids_h, w_h) if np.max(np.abs(ref_h)) > 1e3 else None
+    mx, rel = assert_layer_tolerance(out.download(), ref_h, exact=exact)
     _say(f"[result] {cfg.name} T={T} hidden max_abs={mx:.3e} rel_l2={rel:.3e}")
     assert_layer_tolerance(nn.download(), ref_n, "next_normed")
 

@@ -387,3 +387,15 @@ def test_group_plan_is_stable_sort(seed):
     assert src.tolist() == [r // K for r in order]
     assert [order[i] for i in out] == list(range(T * K))
     assert sum(c for _, c in groups) == T * K
+
+
+def test_fp64_block_agrees_with_f32_golden():
+    # the fp64 evaluation reproduces the K8 golden (tests/scheduler.rs:1013-1176)
+    residual = _residual()
+    normed = orc.rms_norm(residual, [1.0, 1.0])
+    ids, p = orc.routing_top_k(orc.softmax_in_place(SCORES), 8)
+    _, w = orc.renormalize(p, orc.NORM_RENORMALIZE, 1.0)
+    lay, slot = _identity_slot_layout()
+    h = orc.moe_block_f64(lay, np.tile(slot, 9), 9, normed[None, :], residual[None, :], np.asarray([ids], np.int32),
+                          w[None, :])
+    assert np.max(np.abs(h[0] - np.asarray([2.8271027, 0.86557925]))) <= 1e-5
