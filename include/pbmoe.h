@@ -227,6 +227,14 @@ int pbmoe_route_logits(pbmoe_ctx* ctx, uint32_t layer, const float* logits, uint
 int pbmoe_moe_decode(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                      uint32_t tokens, const uint32_t* ids, const float* weights,
                      const float* next_norm_weight, float* hidden_out, float* next_normed_out);
+/* Whole MoE block for a decode batch (tokens <= 16): router projection,
+ * routing stage and expert phase of pbmoe_route + pbmoe_moe_decode in one
+ * call (CMD2 routing then CMD3, metal/mod.rs:2864-3036 and :3252-3332).
+ * ids_out/weights_out ([tokens][K], device) receive the routes, or are both
+ * NULL. */
+int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
+                    uint32_t tokens, uint32_t* ids_out, float* weights_out,
+                    const float* next_norm_weight, float* hidden_out, float* next_normed_out);
 /* Layer-major prefill (qwen_layer_major_experts): any tokens >= 1.  Builds
  * the dispatch plan on the device, runs the grouped expert GEMMs and the
  * fused combine.  Same arguments and result contract as pbmoe_moe_decode;

@@ -101,6 +101,7 @@ _SIG = {
     "pbmoe_route": ([_P, _U32, _P, _U32, _P, _P, _P], C.c_int),
     "pbmoe_route_logits": ([_P, _U32, _P, _U32, _P, _P], C.c_int),
     "pbmoe_moe_decode": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
+    "pbmoe_moe_layer": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_moe_prefill": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_dispatch_plan": ([_P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_q4_dequantize": ([_P, _P, _P, _P, _U32, _U32, _U32, _U32, _P], C.c_int),

@@ -691,12 +691,8 @@ PBMOE_API int pbmoe_unbind_layer(pbmoe_ctx* ctx, uint32_t layer)
     return ok();
 }
 
-static int route_common(pbmoe_ctx* ctx, LayerBinding* b, const float* logits, uint32_t tokens,
-                        uint32_t* ids, float* weights)
+static pbmoe::RouteParams route_params(const pbmoe_layer_desc& d)
 {
-    const pbmoe_layer_desc& d = b->desc;
-    if (d.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
-        return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
     pbmoe::RouteParams p{};
     p.experts = d.experts;
     p.k = d.active_experts;
@@ -706,8 +702,70 @@ static int route_common(pbmoe_ctx* ctx, LayerBinding* b, const float* logits, ui
     p.n_group = d.routing == PBMOE_ROUTING_SIGMOID_GROUPED ? d.n_group : 1;
     p.topk_group = d.routing == PBMOE_ROUTING_SIGMOID_GROUPED ? d.topk_group : 1;
     p.routed_scale = d.routed_scale;
-    HIP_TRY(pbmoe::launch_route_topk(ctx->stream, logits, b->sel_bias, tokens, p, ids, weights,
-                                     ctx->status));
+    return p;
+}
+
+static int route_many(pbmoe_ctx* ctx, LayerBinding* b, const float* logits, uint32_t tokens,
+                      uint32_t* ids, float* weights)
+{
+    if (b->desc.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+        return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
+    HIP_TRY(pbmoe::launch_route_topk(ctx->stream, logits, b->sel_bias, tokens, route_params(b->desc),
+                                     ids, weights, ctx->status));
+    return ok();
+}
+
+// Fill the decode launch description for a bound layer; sizes the scratch.
+static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const float* residual,
+                       uint32_t tokens, uint32_t* ids, float* weights, const float* next_norm_weight,
+                       float* hidden_out, float* next_normed_out, pbmoe::ExpertSet* sh,
+                       pbmoe::DecodeArgs* a)
+{
+    const pbmoe_layer_desc& d = b->desc;
+    const uint32_t K = d.active_experts, H = d.hidden, I = d.intermediate;
+    const uint32_t routes = tokens * K;
+    int rc;
+    if ((rc = ensure(ctx, ctx->logits, (size_t)tokens * d.experts * 4)))
+        return rc;
+    if ((rc = ensure(ctx, ctx->act, (size_t)routes * I * 4)))
+        return rc;
+    if ((rc = ensure(ctx, ctx->act_shared, (size_t)tokens * (d.shared_intermediate + 1) * 4)))
+        return rc;
+    if ((rc = ensure(ctx, ctx->shared_weight, (size_t)tokens * 4)))
+        return rc;
+    pbmoe::Plan plan{};
+    if ((rc = plan_buffers(ctx, d.experts, routes, &plan)))
+        return rc;
+    *a = pbmoe::DecodeArgs{};
+    a->router_w = b->router;
+    a->router_dtype = b->router_dtype;
+    a->sel_bias = b->sel_bias;
+    a->rp = route_params(d);
+    a->logits = static_cast<float*>(ctx->logits.ptr);
+    a->ids = ids;
+    a->weights = weights;
+    a->ex = make_set(b->slots, b->layout, d.experts, H, I);
+    a->shared = nullptr;
+    if (b->has_shared) {
+        *sh = make_set(b->shared_slot, b->shared_layout, 1, H, d.shared_intermediate);
+        a->shared = sh;
+    }
+    a->sgate_w = b->shared_gate;
+    a->sgate_dtype = b->shared_gate_dtype;
+    a->x = x;
+    a->residual = residual;
+    a->tokens = tokens;
+    a->hidden = H;
+    a->act = static_cast<float*>(ctx->act.ptr);
+    a->act_shared = static_cast<float*>(ctx->act_shared.ptr);
+    a->shared_weight = static_cast<float*>(ctx->shared_weight.ptr);
+    a->hidden_out = hidden_out;
+    a->next_norm_w = next_norm_weight;
+    a->eps = d.norm_epsilon > 0.0f ? d.norm_epsilon : 1e-6f;
+    a->next_normed = next_normed_out;
+    a->plan = plan;
+    a->ticket = ctx->status + 32;
+    a->status = ctx->status;
     return ok();
 }
 
@@ -724,9 +782,23 @@ PBMOE_API int pbmoe_route(pbmoe_ctx* ctx, uint32_t layer, const float* x, uint32
         return rc;
     if (!b->router)
         return fail(PBMOE_ERR_NOT_BOUND, "layer %u has no bound router projection", layer);
+    if (b->desc.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+        return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
+    if (!aligned(x, 16))
+        return fail(PBMOE_ERR_ALIGNMENT, "x must be 16-byte aligned");
     rc = set_device(ctx);
     if (rc)
         return rc;
+    if (tokens <= MAX_DECODE_TOKENS) {
+        pbmoe::DecodeArgs a;
+        pbmoe::ExpertSet sh;
+        if ((rc = decode_args(ctx, b, x, nullptr, tokens, ids, weights, nullptr, nullptr, nullptr, &sh, &a)))
+            return rc;
+        if (logits_out)
+            a.logits = logits_out;
+        HIP_TRY(pbmoe::launch_decode_layer(ctx->stream, a, pbmoe::DECODE_ROUTE_ONLY));
+        return ok();
+    }
     float* logits = logits_out;
     if (!logits) {
         rc = ensure(ctx, ctx->logits, (size_t)tokens * b->desc.experts * 4);
@@ -736,7 +808,7 @@ PBMOE_API int pbmoe_route(pbmoe_ctx* ctx, uint32_t layer, const float* x, uint32
     }
     HIP_TRY(pbmoe::launch_router_logits(ctx->stream, b->router, b->router_dtype, x, tokens,
                                         b->desc.experts, b->desc.hidden, logits));
-    return route_common(ctx, b, logits, tokens, ids, weights);
+    return route_many(ctx, b, logits, tokens, ids, weights);
 }
 
 PBMOE_API int pbmoe_route_logits(pbmoe_ctx* ctx, uint32_t layer, const float* logits,
@@ -753,14 +825,15 @@ PBMOE_API int pbmoe_route_logits(pbmoe_ctx* ctx, uint32_t layer, const float* lo
     rc = set_device(ctx);
     if (rc)
         return rc;
-    return route_common(ctx, b, logits, tokens, ids, weights);
+    return route_many(ctx, b, logits, tokens, ids, weights);
 }
 
 static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
-                        uint32_t tokens, const uint32_t* ids, const float* weights,
-                        const float* next_norm_weight, float* hidden_out, float* next_normed_out)
+                        uint32_t tokens, uint32_t* ids, float* weights,
+                        const float* next_norm_weight, float* hidden_out, float* next_normed_out,
+                        uint32_t mode)
 {
-    if (!ctx || !x || !residual || !ids || !weights || !hidden_out)
+    if (!ctx || !x || !residual || !hidden_out || (mode == pbmoe::DECODE_EXPERTS && (!ids || !weights)))
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
     if (tokens == 0)
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "expert phase requires at least one token row");
@@ -775,6 +848,15 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
     if (d.shared_intermediate && !b->has_shared)
         return fail(PBMOE_ERR_NOT_BOUND, "layer %u declares a shared expert that is not bound",
                     layer);
+    if (mode == pbmoe::DECODE_FULL_LAYER) {
+        if (!b->router)
+            return fail(PBMOE_ERR_NOT_BOUND, "layer %u has no bound router projection", layer);
+        if (b->shared_gate && b->shared_gate_dtype != b->router_dtype)
+            return fail(PBMOE_ERR_UNSUPPORTED,
+                        "the fused layer needs the shared gate and router in one dtype");
+        if (d.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+            return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
+    }
     if (tokens > MAX_DECODE_TOKENS)
         return fail(PBMOE_ERR_UNSUPPORTED, "decode expert phase supports at most %u tokens, got %u",
                     MAX_DECODE_TOKENS, tokens);
@@ -784,33 +866,20 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
     rc = set_device(ctx);
     if (rc)
         return rc;
-    const uint32_t K = d.active_experts, H = d.hidden, I = d.intermediate;
-    const uint32_t routes = tokens * K;
-    if ((rc = ensure(ctx, ctx->act, (size_t)routes * I * 4)))
-        return rc;
-    if ((rc = ensure(ctx, ctx->act_shared, (size_t)tokens * (d.shared_intermediate + 1) * 4)))
-        return rc;
-    if ((rc = ensure(ctx, ctx->shared_weight, (size_t)tokens * 4)))
-        return rc;
-    pbmoe::ExpertSet ex = make_set(b->slots, b->layout, d.experts, H, I);
-    pbmoe::ExpertSet sh{};
-    if (b->has_shared)
-        sh = make_set(b->shared_slot, b->shared_layout, 1, H, d.shared_intermediate);
-    pbmoe::Plan plan{};
-    pbmoe::Plan* planp = nullptr;
-    if (tokens > 1) {
-        if ((rc = plan_buffers(ctx, d.experts, routes, &plan)))
+    if (mode == pbmoe::DECODE_FULL_LAYER && (!ids || !weights)) {
+        if ((rc = ensure(ctx, ctx->route_ids, (size_t)tokens * d.active_experts * 4)))
             return rc;
-        HIP_TRY(pbmoe::launch_dispatch_plan(ctx->stream, ids, routes, d.experts, K, plan,
-                                            ctx->status));
-        planp = &plan;
+        if ((rc = ensure(ctx, ctx->route_w, (size_t)tokens * d.active_experts * 4)))
+            return rc;
+        ids = static_cast<uint32_t*>(ctx->route_ids.ptr);
+        weights = static_cast<float*>(ctx->route_w.ptr);
     }
-    HIP_TRY(pbmoe::launch_decode_experts(
-        ctx->stream, ex, b->has_shared ? &sh : nullptr, b->shared_gate, b->shared_gate_dtype, x,
-        residual, tokens, K, H, ids, weights, planp, static_cast<float*>(ctx->act.ptr),
-        static_cast<float*>(ctx->act_shared.ptr), static_cast<float*>(ctx->shared_weight.ptr),
-        hidden_out, next_norm_weight, d.norm_epsilon > 0.0f ? d.norm_epsilon : 1e-6f,
-        next_normed_out, ctx->status));
+    pbmoe::DecodeArgs a;
+    pbmoe::ExpertSet sh;
+    if ((rc = decode_args(ctx, b, x, residual, tokens, ids, weights, next_norm_weight, hidden_out,
+                          next_normed_out, &sh, &a)))
+        return rc;
+    HIP_TRY(pbmoe::launch_decode_layer(ctx->stream, a, mode));
     return ok();
 }
 
@@ -819,8 +888,23 @@ PBMOE_API int pbmoe_moe_decode(pbmoe_ctx* ctx, uint32_t layer, const float* x,
                                const float* weights, const float* next_norm_weight,
                                float* hidden_out, float* next_normed_out)
 {
-    return expert_phase(ctx, layer, x, residual, tokens, ids, weights, next_norm_weight,
-                        hidden_out, next_normed_out);
+    return expert_phase(ctx, layer, x, residual, tokens, const_cast<uint32_t*>(ids),
+                        const_cast<float*>(weights), next_norm_weight, hidden_out, next_normed_out,
+                        pbmoe::DECODE_EXPERTS);
+}
+
+// Router + routing + expert phase of one layer in one call (CMD2 routing
+// followed by CMD3, metal/mod.rs:2864-3036 then :3252-3332).  ids/weights
+// receive the routes when not NULL.
+PBMOE_API int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x,
+                              const float* residual, uint32_t tokens, uint32_t* ids_out,
+                              float* weights_out, const float* next_norm_weight, float* hidden_out,
+                              float* next_normed_out)
+{
+    if ((ids_out == nullptr) != (weights_out == nullptr))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ids_out and weights_out must be given together");
+    return expert_phase(ctx, layer, x, residual, tokens, ids_out, weights_out, next_norm_weight,
+                        hidden_out, next_normed_out, pbmoe::DECODE_FULL_LAYER);
 }
 
 PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
@@ -831,8 +915,9 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     if (tokens > MAX_DECODE_TOKENS)
         return fail(PBMOE_ERR_UNSUPPORTED,
                     "grouped prefill GEMM path for %u tokens is not built yet", tokens);
-    return expert_phase(ctx, layer, x, residual, tokens, ids, weights, next_norm_weight,
-                        hidden_out, next_normed_out);
+    return expert_phase(ctx, layer, x, residual, tokens, const_cast<uint32_t*>(ids),
+                        const_cast<float*>(weights), next_norm_weight, hidden_out, next_normed_out,
+                        pbmoe::DECODE_EXPERTS);
 }
 
 PBMOE_API int pbmoe_dispatch_plan(pbmoe_ctx* ctx, uint32_t experts, uint32_t active_experts,

@@ -1,0 +1,772 @@
+// Decode path of the MoE block on gfx950: three kernels per layer.
+//
+//  1. stage: router rows (W_r . x), shared-expert gate/up rows and the
+//     shared sigmoid gate, spread one task per wave over the whole chip;
+//     the last workgroup to finish (atomic ticket) runs the routing stage
+//     for every token (selection, softmax/sigmoid, renormalisation) and the
+//     dispatch plan of the batch.
+//  2. gate/up: routed experts, SiLU(g)*u formed in registers.
+//  3. down + combine: down projection of every routed and shared item for a
+//     block of output rows, then h = (r + sum_k w_k y_k) + sw * S per token
+//     in route order.
+// Every wave issues all of its weight loads before it consumes any of them:
+// at batch 1 the layer is latency-bound, so the number of dependent memory
+// round trips, not instruction count, sets the time.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "pbmoe_device.h"
+#include "pbmoe_internal.h"
+
+namespace pbmoe {
+
+constexpr int DEC_T = 16;                 // max tokens of the decode path
+constexpr int DEC_ROUTES = DEC_T * MAX_K; // max routes
+
+// ---------------------------------------------------------------------------
+// kernel 1: router rows (W_r . x), shared gate/up rows and the shared sigmoid
+// gate, one task per wave.  No cross-workgroup synchronisation: the kernel
+// boundary publishes the logits to kernel 2.
+// ---------------------------------------------------------------------------
+struct RouterArgs {
+    const void* router_w;
+    uint32_t experts;     // 0: no router rows
+    ExpertSet sh;
+    uint32_t shared_rows; // 0: no shared expert
+    const void* sgate_w;
+    uint32_t sgate_dtype;
+    const float* x;
+    uint32_t tokens, hidden;
+    float* logits;        // [T][E]
+    float* act_shared;    // [T][Is]
+    float* shared_weight; // [T]
+};
+
+template <int WDT>
+__device__ __forceinline__ void load_dense8(const void* w, uint64_t off, float (&v)[8])
+{
+    if constexpr (WDT == 0) {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + off);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+        uint4 raw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + off);
+        const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (WDT == 2) {
+                v[2 * i] = __uint_as_float(r4[i] << 16);
+                v[2 * i + 1] = __uint_as_float(r4[i] & 0xFFFF0000u);
+            } else {
+                v[2 * i] = __half2float(__ushort_as_half((uint16_t)(r4[i] & 0xFFFFu)));
+                v[2 * i + 1] = __half2float(__ushort_as_half((uint16_t)(r4[i] >> 16)));
+            }
+        }
+    }
+}
+
+// dense row . x for every token (8 columns per lane per chunk of 512)
+template <int WDT, int CR>
+__device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, const float* x,
+                                               uint32_t T, uint32_t H, float* out, uint32_t out_stride)
+{
+    const int lane = threadIdx.x & 63;
+    float wv[CR][8];
+#pragma unroll
+    for (int c = 0; c < CR; ++c) {
+        const uint32_t col = (uint32_t)lane * 8 + c * 512;
+        if (col < H) {
+            load_dense8<WDT>(w, row_off + col, wv[c]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                wv[c][i] = 0.0f;
+        }
+    }
+    for (uint32_t t = 0; t < T; ++t) {
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CR; ++c) {
+            const uint32_t col = (uint32_t)lane * 8 + c * 512;
+            if (col < H) {
+                const float4* xp = reinterpret_cast<const float4*>(x + (uint64_t)t * H + col);
+                const float4 u = xp[0], v = xp[1];
+                acc0 = fmaf(wv[c][0], u.x, acc0);
+                acc1 = fmaf(wv[c][1], u.y, acc1);
+                acc0 = fmaf(wv[c][2], u.z, acc0);
+                acc1 = fmaf(wv[c][3], u.w, acc1);
+                acc0 = fmaf(wv[c][4], v.x, acc0);
+                acc1 = fmaf(wv[c][5], v.y, acc1);
+                acc0 = fmaf(wv[c][6], v.z, acc0);
+                acc1 = fmaf(wv[c][7], v.w, acc1);
+            }
+        }
+        const float s = wave_sum(acc0 + acc1);
+        if (lane == 0)
+            out[(uint64_t)t * out_stride] = s;
+    }
+}
+
+template <int WDT, int GDT, int SBT, int CR, int CS>
+__global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t H = a.hidden, T = a.tokens;
+    const uint32_t n_router = a.experts;
+    const uint32_t Is = a.shared_rows;
+    const uint32_t n_tasks = n_router + (Is ? Is + 1u : 0u);
+    const uint32_t wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t n_waves = gridDim.x * 4;
+    for (uint32_t task = wave_id; task < n_tasks; task += n_waves) {
+        if (task < n_router) {
+            dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, a.x, T, H, a.logits + task, n_router);
+        } else if (task < n_router + Is) {
+            const uint32_t i = task - n_router;
+            const ExpertSet& s = a.sh;
+            const uint32_t chunks = H / 32, gpr = H / s.group;
+            const uint4* gw = reinterpret_cast<const uint4*>(s.base + s.gate.w_off + (uint64_t)i * (H / 2));
+            const uint4* uw = reinterpret_cast<const uint4*>(s.base + s.up.w_off + (uint64_t)i * (H / 2));
+            uint4 wg[CS], wu[CS];
+            float sg[CS], bg[CS], su[CS], bu[CS];
+#pragma unroll
+            for (int c = 0; c < CS; ++c) {
+                const uint32_t ch = lane + WAVE * c;
+                if (ch < chunks) {
+                    wg[c] = gw[ch];
+                    wu[c] = uw[ch];
+                    const uint64_t gi = (uint64_t)i * gpr + (ch * 32u) / s.group;
+                    sg[c] = sb_at<SBT>(s.base + s.gate.s_off, gi);
+                    bg[c] = sb_at<SBT>(s.base + s.gate.b_off, gi);
+                    su[c] = sb_at<SBT>(s.base + s.up.s_off, gi);
+                    bu[c] = sb_at<SBT>(s.base + s.up.b_off, gi);
+                }
+            }
+            for (uint32_t t = 0; t < T; ++t) {
+                float pg = 0.0f, pu = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CS; ++c) {
+                    const uint32_t ch = lane + WAVE * c;
+                    if (ch < chunks) {
+                        float xs;
+                        const float* xp = a.x + (uint64_t)t * H + ch * 32;
+                        const float qg = q4_chunk_qx(wg[c], xp, xs);
+                        float xs2;
+                        const float qu = q4_chunk_qx(wu[c], xp, xs2);
+                        pg = fmaf(sg[c], qg, fmaf(bg[c], xs, pg));
+                        pu = fmaf(su[c], qu, fmaf(bu[c], xs, pu));
+                    }
+                }
+                const float g = wave_sum(pg);
+                const float u = wave_sum(pu);
+                if (lane == 0)
+                    a.act_shared[(uint64_t)t * Is + i] = (g / (1.0f + expf(-g))) * u;
+            }
+        } else if (a.sgate_w) {
+            dense_row_dots<GDT, CR>(a.sgate_w, 0, a.x, T, H, a.shared_weight, 1);
+            // sigma applied by the consumer: shared_weight holds the gate logit
+        } else if (lane == 0) {
+            for (uint32_t t = 0; t < T; ++t)
+                a.shared_weight[t] = 80.0f; // sigma(80) = 1 (metal/mod.rs:4666-4669)
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Routing + plan in LDS, redone by every workgroup of kernel 2 from the
+// published logits (or loaded when the caller gave the routes).
+// ---------------------------------------------------------------------------
+struct RouteLds {
+    uint32_t ids[DEC_ROUTES];
+    float w[DEC_ROUTES];
+    uint32_t unique_ids[DEC_ROUTES];
+    uint32_t groups[2 * DEC_ROUTES];
+    uint32_t src_rows[DEC_ROUTES];
+    uint32_t out_idx[DEC_ROUTES];
+    uint32_t count[1024];
+    uint32_t start[1024];
+    uint32_t unique_count;
+    uint32_t sel[4][MAX_K];
+    float grp[4][1024];
+};
+
+// Stable plan of `routes` routes from s.ids (block-wide, routes <= 256):
+// sorted unique union and stable grouping by expert, the definition of the
+// standalone plan kernel (metal/mod.rs:3197-3233, scheduler/mod.rs:685-769).
+__device__ void lds_plan(RouteLds& s, uint32_t routes, uint32_t experts, uint32_t k, uint32_t* status)
+{
+    const int tid = threadIdx.x;
+    for (uint32_t e = tid; e < 1024; e += blockDim.x)
+        s.count[e] = 0;
+    __syncthreads();
+    for (uint32_t r = tid; r < routes; r += blockDim.x) {
+        const uint32_t e = s.ids[r];
+        if (e < experts)
+            atomicAdd(&s.count[e], 1u);
+        else
+            atomicOr(status, ST_ROUTE_RANGE);
+    }
+    __syncthreads();
+    if (tid < 64) { // one wave scans the 1024 counters, 16 per lane
+        uint32_t c[16], run_c = 0, run_f = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            c[j] = s.count[tid * 16 + j];
+            run_c += c[j];
+            run_f += c[j] ? 1u : 0u;
+        }
+        uint32_t inc_c = run_c, inc_f = run_f;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t x = __shfl_up(inc_c, o);
+            const uint32_t y = __shfl_up(inc_f, o);
+            if (tid >= o) {
+                inc_c += x;
+                inc_f += y;
+            }
+        }
+        uint32_t base_c = inc_c - run_c, base_f = inc_f - run_f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t e = tid * 16 + j;
+            s.start[e] = base_c;
+            if (c[j] && e < experts) {
+                s.unique_ids[base_f] = e;
+                s.groups[2 * base_f] = base_c;
+                s.groups[2 * base_f + 1] = c[j];
+            }
+            base_c += c[j];
+            base_f += c[j] ? 1u : 0u;
+        }
+        if (tid == 63)
+            s.unique_count = inc_f;
+    }
+    __syncthreads();
+    for (uint32_t r = tid; r < routes; r += blockDim.x) {
+        const uint32_t e = s.ids[r];
+        if (e >= experts) {
+            s.out_idx[r] = 0xFFFFFFFFu;
+            continue;
+        }
+        uint32_t rank = 0;
+        for (uint32_t q = 0; q < r; ++q)
+            rank += s.ids[q] == e ? 1u : 0u;
+        const uint32_t pos = s.start[e] + rank;
+        s.src_rows[pos] = r / k;
+        s.out_idx[r] = pos;
+    }
+    __syncthreads();
+}
+
+struct ExpertArgs {
+    ExpertSet ex;
+    const float* logits;      // route from these when route_here
+    const float* sel_bias;
+    RouteParams rp;
+    bool route_here;          // false: ids/weights given
+    uint32_t* ids;            // [T][K]
+    float* weights;           // [T][K]
+    Plan plan;                // global copy for kernel 3 (tokens > 1)
+    const float* x;
+    uint32_t tokens, hidden;
+    float* act;               // [T*K][I]
+    uint32_t* status;
+};
+
+template <int EPL>
+__device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s)
+{
+    const int wv = threadIdx.x >> 6;
+    const uint32_t K = a.rp.k;
+    for (uint32_t t = wv; t < a.tokens; t += 4)
+        route_token_wave<EPL>(a.logits + (uint64_t)t * a.rp.experts, a.sel_bias, a.rp, s.ids + t * K,
+                              s.w + t * K, s.sel[wv], s.grp[wv], a.status);
+}
+
+// ---------------------------------------------------------------------------
+// kernel 2: routing (every workgroup) + routed gate/up with SiLU(g)*u.
+// Task = (work item, RPW consecutive rows) per wave.
+// ---------------------------------------------------------------------------
+template <int SBT, int CPL, int RPW, int EPL>
+__global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
+{
+    __shared__ RouteLds s;
+    const int lane = threadIdx.x & 63;
+    const uint32_t T = a.tokens, K = a.rp.k, H = a.hidden, I = a.ex.gate.rows;
+    const uint32_t routes = T * K;
+    const bool use_plan = T > 1;
+
+    if (a.route_here) {
+        route_all_tokens<EPL>(a, s);
+    } else {
+        for (uint32_t r = threadIdx.x; r < routes; r += blockDim.x) {
+            s.ids[r] = a.ids[r];
+            s.w[r] = a.weights[r];
+        }
+    }
+    __syncthreads();
+    if (use_plan)
+        lds_plan(s, routes, a.rp.experts, K, a.status);
+    if (blockIdx.x == 0) { // publish routes and plan for kernel 3 and the caller
+        for (uint32_t r = threadIdx.x; r < routes; r += blockDim.x) {
+            if (a.route_here) {
+                a.ids[r] = s.ids[r];
+                a.weights[r] = s.w[r];
+            }
+            if (use_plan) {
+                a.plan.src_rows[r] = s.src_rows[r];
+                a.plan.out_idx[r] = s.out_idx[r];
+            }
+        }
+        if (use_plan) {
+            for (uint32_t u = threadIdx.x; u < s.unique_count; u += blockDim.x) {
+                a.plan.unique_ids[u] = s.unique_ids[u];
+                a.plan.groups[2 * u] = s.groups[2 * u];
+                a.plan.groups[2 * u + 1] = s.groups[2 * u + 1];
+            }
+            if (threadIdx.x == 0)
+                a.plan.unique_count[0] = s.unique_count;
+        }
+    }
+
+    const uint32_t row_tasks = I / RPW;
+    const uint32_t wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t item = wave_id / row_tasks;
+    const uint32_t row0 = (wave_id % row_tasks) * RPW;
+    const uint32_t n_items = use_plan ? s.unique_count : routes;
+    if (item >= n_items)
+        return;
+    uint32_t e, g0, n;
+    if (use_plan) {
+        e = s.unique_ids[item];
+        g0 = s.groups[2 * item];
+        n = s.groups[2 * item + 1];
+    } else {
+        e = s.ids[item];
+        g0 = item;
+        n = 1;
+    }
+    if (e >= a.ex.count) {
+        if (lane == 0)
+            atomicOr(a.status, ST_ROUTE_RANGE);
+        return;
+    }
+    const ExpertSet& ex = a.ex;
+    const uint8_t* slot = ex.base + (uint64_t)e * ex.stride;
+    const uint32_t chunks = H / 32, gpr = H / ex.group;
+    uint4 wg[RPW][CPL], wu[RPW][CPL];
+    float sg[RPW][CPL], bg[RPW][CPL], su[RPW][CPL], bu[RPW][CPL];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const uint32_t row = row0 + r;
+        const uint4* gw = reinterpret_cast<const uint4*>(slot + ex.gate.w_off + (uint64_t)row * (H / 2));
+        const uint4* uw = reinterpret_cast<const uint4*>(slot + ex.up.w_off + (uint64_t)row * (H / 2));
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lane + WAVE * c;
+            if (ch < chunks) {
+                wg[r][c] = gw[ch];
+                wu[r][c] = uw[ch];
+                const uint64_t gi = (uint64_t)row * gpr + (ch * 32u) / ex.group;
+                sg[r][c] = sb_at<SBT>(slot + ex.gate.s_off, gi);
+                bg[r][c] = sb_at<SBT>(slot + ex.gate.b_off, gi);
+                su[r][c] = sb_at<SBT>(slot + ex.up.s_off, gi);
+                bu[r][c] = sb_at<SBT>(slot + ex.up.b_off, gi);
+            }
+        }
+    }
+    for (uint32_t j = 0; j < n; ++j) {
+        const uint32_t gidx = g0 + j;
+        const uint32_t tok = use_plan ? s.src_rows[gidx] : gidx / K;
+        const float* xt = a.x + (uint64_t)tok * H;
+        float pg[RPW], pu[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            pg[r] = 0.0f, pu[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lane + WAVE * c;
+            if (ch < chunks) {
+                const float4* x4 = reinterpret_cast<const float4*>(xt + ch * 32);
+                float xv[32];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float4 v = x4[q];
+                    xv[4 * q] = v.x, xv[4 * q + 1] = v.y, xv[4 * q + 2] = v.z, xv[4 * q + 3] = v.w;
+                }
+                float xs = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 32; q += 4)
+                    xs += (xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3]);
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float qg = q4_chunk_qx_reg(wg[r][c], xv);
+                    const float qu = q4_chunk_qx_reg(wu[r][c], xv);
+                    pg[r] = fmaf(sg[r][c], qg, fmaf(bg[r][c], xs, pg[r]));
+                    pu[r] = fmaf(su[r][c], qu, fmaf(bu[r][c], xs, pu[r]));
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const float g = wave_sum(pg[r]);
+            const float u = wave_sum(pu[r]);
+            if (lane == r)
+                a.act[(uint64_t)gidx * I + row0 + r] = (g / (1.0f + expf(-g))) * u;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// kernel 3: down projection + combine for R output rows per workgroup.
+// Unit = (item, row) handled by LPR lanes with CPL chunks each.  With one
+// token (direct routes) the activations of every route are staged in LDS by
+// loads that do not wait for the routes; with more tokens they are read from
+// L2 per unit.
+// ---------------------------------------------------------------------------
+constexpr int DOWN_R = 8;
+constexpr uint32_t STAGE_FLOATS = 12288; // 48 KB of staged activations
+
+struct DownArgs {
+    ExpertSet ex, sh;
+    bool has_shared;
+    const float* act;
+    const float* act_shared;
+    const float* shared_logit; // sigma applied here
+    uint32_t tokens, k, hidden;
+    const uint32_t* ids;
+    const float* weights;
+    Plan plan;
+    bool use_plan;
+    bool stage; // activations fit STAGE_FLOATS (direct mode)
+    const float* residual;
+    float* hidden_out;
+    uint32_t* status;
+};
+
+template <int SBT, int LPR, int CPL, int MAXR>
+__global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
+{
+    constexpr int R = DOWN_R;
+    constexpr int SLOTS = 256 / LPR;
+    __shared__ float ylds[DEC_ROUTES][R];
+    __shared__ float yshl[DEC_T][R];
+    __shared__ float astage[STAGE_FLOATS];
+    const int gl = threadIdx.x % LPR;
+    const int slot_id = threadIdx.x / LPR;
+    const uint32_t row_base = blockIdx.x * R;
+    const uint32_t T = a.tokens, K = a.k;
+    const uint32_t I = a.ex.down.cols;
+    const uint32_t gpr = I / a.ex.group;
+    const uint32_t routes = T * K;
+
+    // loads that do not depend on the routes: residual for the combine and
+    // (direct mode) every route's activations
+    float res_v = 0.0f;
+    if (threadIdx.x < T * R)
+        res_v = a.residual[(uint64_t)(threadIdx.x / R) * a.hidden + row_base + threadIdx.x % R];
+    if (a.stage) {
+        const uint32_t n4 = (routes * I) / 4;
+        const float4* src = reinterpret_cast<const float4*>(a.act);
+        float4* dst = reinterpret_cast<float4*>(astage);
+        for (uint32_t i = threadIdx.x; i < n4; i += 256)
+            dst[i] = src[i];
+        if (a.has_shared) {
+            const uint32_t m4 = (T * I) / 4;
+            const float4* s2 = reinterpret_cast<const float4*>(a.act_shared);
+            for (uint32_t i = threadIdx.x; i < m4; i += 256)
+                dst[n4 + i] = s2[i];
+        }
+    }
+    const uint32_t n_routed = a.use_plan ? a.plan.unique_count[0] : routes;
+    const uint32_t n_items = n_routed + (a.has_shared ? 1u : 0u);
+    const uint32_t n_units = n_items * R;
+
+    for (uint32_t u0 = 0; u0 < n_units; u0 += SLOTS * MAXR) {
+        uint4 w[MAXR][CPL];
+        float sc[MAXR][CPL], bi[MAXR][CPL];
+        uint32_t it[MAXR], rw[MAXR];
+        bool live[MAXR];
+#pragma unroll
+        for (int m = 0; m < MAXR; ++m) {
+            const uint32_t unit = u0 + slot_id + SLOTS * m;
+            live[m] = unit < n_units;
+            it[m] = unit / R;
+            rw[m] = unit % R;
+            if (!live[m])
+                continue;
+            const bool shared = a.has_shared && it[m] == n_routed;
+            const ExpertSet& set = shared ? a.sh : a.ex;
+            const uint8_t* slot;
+            if (shared) {
+                slot = a.sh.base;
+            } else {
+                const uint32_t e = a.use_plan ? a.plan.unique_ids[it[m]] : a.ids[it[m]];
+                if (e >= a.ex.count) {
+                    live[m] = false;
+                    continue;
+                }
+                slot = a.ex.base + (uint64_t)e * a.ex.stride;
+            }
+            const uint32_t row = row_base + rw[m];
+            const uint4* dw = reinterpret_cast<const uint4*>(slot + set.down.w_off + (uint64_t)row * (I / 2));
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t ch = gl + LPR * c;
+                w[m][c] = dw[ch];
+                const uint64_t gi = (uint64_t)row * gpr + (ch * 32u) / set.group;
+                sc[m][c] = sb_at<SBT>(slot + set.down.s_off, gi);
+                bi[m][c] = sb_at<SBT>(slot + set.down.b_off, gi);
+            }
+        }
+        if (a.stage && u0 == 0)
+            __syncthreads(); // staged activations visible
+#pragma unroll
+        for (int m = 0; m < MAXR; ++m) {
+            const uint32_t unit = u0 + slot_id + SLOTS * m;
+            if (unit >= n_units)
+                continue;
+            const bool shared = a.has_shared && it[m] == n_routed;
+            uint32_t g0 = 0, n = 0;
+            if (shared) {
+                n = T;
+            } else if (a.use_plan) {
+                g0 = a.plan.groups[2 * it[m]];
+                n = a.plan.groups[2 * it[m] + 1];
+            } else {
+                g0 = it[m];
+                n = 1;
+            }
+            for (uint32_t j = 0; j < n; ++j) {
+                float part = 0.0f;
+                if (live[m]) {
+                    const float* av;
+                    if (a.stage)
+                        av = shared ? astage + (uint64_t)(routes + j) * I : astage + (uint64_t)(g0 + j) * I;
+                    else
+                        av = shared ? a.act_shared + (uint64_t)j * I : a.act + (uint64_t)(g0 + j) * I;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        const uint32_t ch = gl + LPR * c;
+                        float xs;
+                        const float qx = q4_chunk_qx(w[m][c], av + ch * 32, xs);
+                        part = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs, part));
+                    }
+                }
+                const float y = group_sum<LPR>(part);
+                if (gl == 0) {
+                    if (shared)
+                        yshl[j][rw[m]] = y;
+                    else
+                        ylds[g0 + j][rw[m]] = y;
+                }
+            }
+        }
+    }
+    if (a.stage && n_units == 0)
+        __syncthreads();
+    __syncthreads();
+    if (threadIdx.x < T * R) {
+        const uint32_t t = threadIdx.x / R, r = threadIdx.x % R;
+        float moe = 0.0f;
+        for (uint32_t kk = 0; kk < K; ++kk) {
+            const uint32_t route = t * K + kk;
+            const uint32_t gi = a.use_plan ? a.plan.out_idx[route] : route;
+            const float y = gi < DEC_ROUTES ? ylds[gi][r] : 0.0f;
+            moe = moe + a.weights[route] * y;
+        }
+        const float rm = res_v + moe;
+        const float sw = a.has_shared ? sigmoidf_(a.shared_logit[t]) : 0.0f;
+        const float sv = a.has_shared ? yshl[t][r] : 0.0f;
+        a.hidden_out[(uint64_t)t * a.hidden + row_base + r] = rm + sw * sv;
+    }
+}
+
+// next-layer RMSNorm: one block per token (rms_norm_reduced)
+__global__ __launch_bounds__(256) void next_norm_kernel(const float* __restrict__ h,
+                                                        const float* __restrict__ w,
+                                                        uint32_t width, float eps,
+                                                        float* __restrict__ out)
+{
+    __shared__ float part[4];
+    const float* row = h + (uint64_t)blockIdx.x * width;
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < width; i += 256)
+        s = fmaf(row[i], row[i], s);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0)
+        part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float ms = ((part[0] + part[1]) + (part[2] + part[3])) / (float)(width > 1 ? width : 1);
+    const float scale = 1.0f / sqrtf(ms + eps);
+    for (uint32_t i = threadIdx.x; i < width; i += 256)
+        out[(uint64_t)blockIdx.x * width + i] = (row[i] * scale) * w[i];
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool do_router,
+                                      bool do_shared)
+{
+    RouterArgs a{};
+    a.router_w = d.router_w;
+    a.experts = do_router ? d.rp.experts : 0u;
+    if (do_shared && d.shared)
+        a.sh = *d.shared;
+    a.shared_rows = do_shared && d.shared ? d.shared->gate.rows : 0u;
+    a.sgate_w = do_shared ? d.sgate_w : nullptr;
+    a.sgate_dtype = d.sgate_dtype;
+    a.x = d.x;
+    a.tokens = d.tokens;
+    a.hidden = d.hidden;
+    a.logits = d.logits;
+    a.act_shared = d.act_shared;
+    a.shared_weight = d.shared_weight;
+    const uint32_t tasks = a.experts + (a.shared_rows ? a.shared_rows + 1u : 0u);
+    if (tasks == 0)
+        return hipSuccess;
+    const uint32_t blocks = (tasks + 3) / 4;
+    const uint32_t cr = (d.hidden + 511) / 512;
+    const uint32_t cs = (d.hidden / 32 + 63) / 64;
+    if (cr > 16 || cs > 4)
+        return hipErrorInvalidValue;
+    // router/gate dtypes: the BASELINE layers use f16 for both; other
+    // combinations share the f16 gate path only when the gate is f16
+    const uint32_t gdt = a.sgate_w ? d.sgate_dtype : d.router_dtype;
+    const uint32_t wdt = a.experts ? d.router_dtype : gdt;
+    const uint32_t sbt = a.shared_rows ? a.sh.sb_dtype : 1u;
+#define PBM_RS(W, G, S, CRV, CSV) router_stage_kernel<W, G, S, CRV, CSV><<<blocks, 256, 0, st>>>(a)
+#define PBM_RS_CS(W, G, S, CRV)                                                                \
+    do {                                                                                       \
+        if (cs <= 1) PBM_RS(W, G, S, CRV, 1);                                                  \
+        else if (cs <= 2) PBM_RS(W, G, S, CRV, 2);                                             \
+        else PBM_RS(W, G, S, CRV, 4);                                                          \
+    } while (0)
+#define PBM_RS_CR(W, G, S)                                                                     \
+    do {                                                                                       \
+        if (cr <= 4) PBM_RS_CS(W, G, S, 4);                                                    \
+        else if (cr <= 8) PBM_RS_CS(W, G, S, 8);                                               \
+        else PBM_RS_CS(W, G, S, 16);                                                           \
+    } while (0)
+    if (wdt != gdt)
+        return hipErrorInvalidValue; // bind validates matching dtypes
+    if (sbt == 2) {
+        if (wdt == 0) PBM_RS_CR(0, 0, 2);
+        else if (wdt == 2) PBM_RS_CR(2, 2, 2);
+        else PBM_RS_CR(1, 1, 2);
+    } else {
+        if (wdt == 0) PBM_RS_CR(0, 0, 1);
+        else if (wdt == 2) PBM_RS_CR(2, 2, 1);
+        else PBM_RS_CR(1, 1, 1);
+    }
+#undef PBM_RS
+#undef PBM_RS_CS
+#undef PBM_RS_CR
+    return hipGetLastError();
+}
+
+template <int SBT>
+static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool route_here)
+{
+    const ExpertSet& ex = d.ex;
+    const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = ex.gate.rows;
+    const bool use_plan = T > 1;
+    const uint32_t max_items = use_plan ? std::min(ex.count, T * K) : T * K;
+    ExpertArgs ea{};
+    ea.ex = ex;
+    ea.logits = d.logits;
+    ea.sel_bias = d.sel_bias;
+    ea.rp = d.rp;
+    ea.route_here = route_here;
+    ea.ids = d.ids;
+    ea.weights = d.weights;
+    ea.plan = d.plan;
+    ea.x = d.x;
+    ea.tokens = T;
+    ea.hidden = H;
+    ea.act = d.act;
+    ea.status = d.status;
+    constexpr int RPW = 4;
+    const uint32_t waves = max_items * (I / RPW);
+    const uint32_t cpl = (H / 32 + 63) / 64;
+    const uint32_t epl = (d.rp.experts + 63) / 64;
+    dim3 g1((waves + 3) / 4);
+#define PBM_GU(C, EP) route_gateup_kernel<SBT, C, RPW, EP><<<g1, 256, 0, st>>>(ea)
+#define PBM_GU_E(C)                                                                            \
+    do {                                                                                       \
+        if (epl <= 2) PBM_GU(C, 2);                                                            \
+        else if (epl <= 4) PBM_GU(C, 4);                                                       \
+        else if (epl <= 8) PBM_GU(C, 8);                                                       \
+        else PBM_GU(C, 16);                                                                    \
+    } while (0)
+    if (cpl <= 1) PBM_GU_E(1);
+    else if (cpl <= 2) PBM_GU_E(2);
+    else if (cpl <= 4) PBM_GU_E(4);
+    else return hipErrorInvalidValue;
+#undef PBM_GU
+#undef PBM_GU_E
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return err;
+
+    DownArgs da{};
+    da.ex = ex;
+    da.has_shared = d.shared != nullptr;
+    if (da.has_shared)
+        da.sh = *d.shared;
+    da.act = d.act;
+    da.act_shared = d.act_shared;
+    da.shared_logit = d.shared_weight;
+    da.tokens = T;
+    da.k = K;
+    da.hidden = H;
+    da.ids = d.ids;
+    da.weights = d.weights;
+    da.plan = d.plan;
+    da.use_plan = use_plan;
+    da.stage = !use_plan && (uint64_t)(T * K + (da.has_shared ? T : 0u)) * I <= STAGE_FLOATS;
+    da.residual = d.residual;
+    da.hidden_out = d.hidden_out;
+    da.status = d.status;
+    dim3 g2(H / DOWN_R);
+#define PBM_DN(L, C, M) down_combine_kernel<SBT, L, C, M><<<g2, 256, 0, st>>>(da)
+    switch (I) {
+    case 256: PBM_DN(8, 1, 4); break;
+    case 512: PBM_DN(8, 2, 4); break;
+    case 768: PBM_DN(8, 3, 4); break;
+    case 1024: PBM_DN(16, 2, 4); break;
+    case 1536: PBM_DN(16, 3, 4); break;
+    case 2048: PBM_DN(16, 4, 4); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef PBM_DN
+    err = hipGetLastError();
+    if (err != hipSuccess)
+        return err;
+    if (d.next_norm_w && d.next_normed) {
+        next_norm_kernel<<<T, 256, 0, st>>>(d.hidden_out, d.next_norm_w, H, d.eps, d.next_normed);
+        err = hipGetLastError();
+    }
+    return err;
+}
+
+hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mode)
+{
+    hipError_t err;
+    if (mode == DECODE_ROUTE_ONLY) {
+        // router rows, then the routing stage of one wave per token
+        err = launch_router_stage(st, d, true, false);
+        if (err != hipSuccess)
+            return err;
+        return launch_route_topk(st, d.logits, d.sel_bias, d.tokens, d.rp, d.ids, d.weights, d.status);
+    }
+    const bool full = mode == DECODE_FULL_LAYER;
+    err = launch_router_stage(st, d, full, d.shared != nullptr);
+    if (err != hipSuccess)
+        return err;
+    if (d.ex.sb_dtype == 2)
+        return launch_experts_typed<2>(st, d, full);
+    return launch_experts_typed<1>(st, d, full);
+}
+
+} // namespace pbmoe

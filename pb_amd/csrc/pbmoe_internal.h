@@ -57,16 +57,38 @@ hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bi
 hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t routes,
                                 uint32_t experts, uint32_t k, const Plan& plan,
                                 uint32_t* status);
-// Decode expert phase.  plan == nullptr selects direct mode (tokens == 1:
-// one work item per route).  act: [routes][I], act_shared: [tokens][Is].
-hipError_t launch_decode_experts(hipStream_t s, const ExpertSet& ex, const ExpertSet* shared,
-                                 const void* shared_gate_w, uint32_t shared_gate_dtype,
-                                 const float* x, const float* residual, uint32_t tokens,
-                                 uint32_t k, uint32_t hidden, const uint32_t* ids,
-                                 const float* weights, const Plan* plan, float* act,
-                                 float* act_shared, float* shared_weight, float* hidden_out,
-                                 const float* next_norm_w, float eps, float* next_normed,
-                                 uint32_t* status);
+// Decode path (tokens <= 16).  Modes: the full layer (router + routing +
+// experts), the expert phase for given routes, or routing only.
+enum : uint32_t { DECODE_FULL_LAYER = 0, DECODE_EXPERTS = 1, DECODE_ROUTE_ONLY = 2 };
+
+struct DecodeArgs {
+    const void* router_w;      // null: route from the given logits
+    uint32_t router_dtype;
+    const float* sel_bias;     // [E] for sigmoid routing
+    RouteParams rp;
+    float* logits;             // [T][E]
+    uint32_t* ids;             // [T][K]
+    float* weights;            // [T][K]
+    ExpertSet ex;              // routed experts
+    const ExpertSet* shared;   // host pointer, null without a shared expert
+    const void* sgate_w;       // shared gate row [H], null: sigma = 1
+    uint32_t sgate_dtype;
+    const float* x;            // [T][H]
+    const float* residual;     // [T][H]
+    uint32_t tokens, hidden;
+    float* act;                // [T*K][I]
+    float* act_shared;         // [T][Is]
+    float* shared_weight;      // [T]
+    float* hidden_out;         // [T][H]
+    const float* next_norm_w;  // [H] or null
+    float eps;
+    float* next_normed;        // [T][H] or null
+    Plan plan;                 // scratch plan (tokens > 1)
+    uint32_t* ticket;          // zeroed counter for last-workgroup election
+    uint32_t* status;
+};
+
+hipError_t launch_decode_layer(hipStream_t s, const DecodeArgs& d, uint32_t mode);
 hipError_t launch_q4_dequantize(hipStream_t s, const uint8_t* packed, const void* scales,
                                 const void* biases, uint32_t sb_dtype, uint32_t rows,
                                 uint32_t cols, uint32_t group, float* out);

@@ -1,116 +1,22 @@
-// gfx950 (MI355X) kernels for the FlashMoE MoE block.
+// gfx950 (MI355X) kernels of the MoE block outside the decode path: router
+// logits and routing for many tokens (prefill router matrix), the standalone
+// deterministic dispatch plan, dequantisation and the seeded weight fill.
 //
-// Wave64 throughout.  Weights are streamed from HBM once per call with
-// 16-byte loads (32 nibbles per lane); activations stay in registers, LDS or
-// L2.  Every kernel bounds-checks route ids against the expert count and
-// reports problems through a device status word instead of reading out of
-// range.
-//
-// Reference kernels these replace (src/inference/flashmoe/metal/qwen/
-// shaders.metal of Jc2k/pb): dense_mmap_fma_matvec_* (router, :1059-1111),
-// q4_fma_matvec_bf16_scale_bias (:97-199), silu_product (:1699-1708),
-// shared_expert_activation (:1710-1721), qwen_layer_major_combine
-// (:1756-1786), rms_norm_reduced (:1176-1213); the CPU routing stage
-// math.rs:746-819 and scheduler/expert_access.rs:80-135; the group plan
-// metal/mod.rs:3197-3233.
-#include <hip/hip_fp16.h>
+// Reference counterparts (src/inference/flashmoe/ of Jc2k/pb):
+// dense_mmap_fma_matvec_* (metal/qwen/shaders.metal:1059-1111), the CPU
+// routing stage (math.rs:746-819, scheduler/expert_access.rs:80-135), the
+// group plan (metal/mod.rs:3197-3233), q4_dequantize_rows_with_group_size
+// (math.rs:913-954).
 #include <hip/hip_runtime.h>
 #include <math.h>
 
 #include <algorithm>
 
+#include "pbmoe_device.h"
 #include "pbmoe_internal.h"
 #include "pbmoe_synth.h"
 
 namespace pbmoe {
-
-constexpr int WAVE = 64;
-
-// ---------------------------------------------------------------------------
-// small helpers
-// ---------------------------------------------------------------------------
-template <int SBT>
-__device__ __forceinline__ float sb_at(const uint8_t* base, uint64_t i)
-{
-    uint16_t v = reinterpret_cast<const uint16_t*>(base)[i];
-    if constexpr (SBT == 2)
-        return __uint_as_float((uint32_t)v << 16);
-    else
-        return __half2float(__ushort_as_half(v));
-}
-
-__device__ __forceinline__ float wave_sum(float v)
-{
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1)
-        v += __shfl_xor(v, o);
-    return v;
-}
-
-template <int W>
-__device__ __forceinline__ float group_sum(float v)
-{
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1)
-        v += __shfl_xor(v, o);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1)
-        v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
-{
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)v, o);
-        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o);
-        uint64_t w = ((uint64_t)hi << 32) | lo;
-        v = w > v ? w : v;
-    }
-    return v;
-}
-
-// f32 total order (Rust f32::total_cmp) mapped onto unsigned order.
-__device__ __forceinline__ uint32_t total_key(float f)
-{
-    uint32_t b = __float_as_uint(f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ float sigmoidf_(float l) { return 1.0f / (1.0f + expf(-l)); }
-
-// Dot of one 16-byte chunk (32 nibbles, columns col0..col0+31) with x.
-// Returns sum(q*x); xs receives sum(x).  Factored affine form:
-// row = sum_g s_g * sum(q*x) + b_g * sum(x).
-__device__ __forceinline__ float q4_chunk_qx(uint4 w, const float* __restrict__ x, float& xs)
-{
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    float qx = 0.0f, sx = 0.0f;
-    uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float4 a = x4[2 * i];
-        float4 b = x4[2 * i + 1];
-        uint32_t q = words[i];
-        qx = fmaf((float)(q & 15u), a.x, qx);
-        qx = fmaf((float)((q >> 4) & 15u), a.y, qx);
-        qx = fmaf((float)((q >> 8) & 15u), a.z, qx);
-        qx = fmaf((float)((q >> 12) & 15u), a.w, qx);
-        qx = fmaf((float)((q >> 16) & 15u), b.x, qx);
-        qx = fmaf((float)((q >> 20) & 15u), b.y, qx);
-        qx = fmaf((float)((q >> 24) & 15u), b.z, qx);
-        qx = fmaf((float)(q >> 28), b.w, qx);
-        sx += (a.x + a.y) + (a.z + a.w) + ((b.x + b.y) + (b.z + b.w));
-    }
-    xs = sx;
-    return qx;
-}
 
 // ---------------------------------------------------------------------------
 // router logits: one wave per expert row, all tokens (tokens <= 16)
@@ -202,12 +108,8 @@ hipError_t launch_router_logits(hipStream_t s, const void* w, uint32_t w_dtype, 
 }
 
 // ---------------------------------------------------------------------------
-// routing: one wave per token.  Selection (canonical: score desc / index asc,
-// or the reference replacement-slot scan), softmax or sigmoid weights, and
-// renormalisation — math.rs:746-819, expert_access.rs:80-135.
+// routing for many tokens: one wave per token (see route_token_wave)
 // ---------------------------------------------------------------------------
-constexpr int MAX_K = 16;
-
 template <int EPL>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
                                                          const float* __restrict__ bias,
@@ -216,193 +118,14 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                                                          float* __restrict__ weights,
                                                          uint32_t* __restrict__ status)
 {
-    __shared__ float group_buf[4][EPL * WAVE];
-    const int lane = threadIdx.x & 63;
+    __shared__ float grp[4][EPL * WAVE];
+    __shared__ uint32_t sel[4][MAX_K];
     const int wv = threadIdx.x >> 6;
     const uint32_t t = blockIdx.x * 4 + wv;
     if (t >= tokens)
         return;
-    const uint32_t E = p.experts, K = p.k;
-    const float* l = logits + (uint64_t)t * E;
-
-    float raw[EPL], sel[EPL];
-    bool bad = false;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-        uint32_t e = lane + WAVE * j;
-        raw[j] = e < E ? l[e] : 0.0f;
-        if (e < E && !isfinite(raw[j]))
-            bad = true;
-    }
-    if (__ballot(bad) != 0ull && lane == 0)
-        atomicOr(status, ST_NONFINITE);
-
-    float mx = 0.0f, inv_sum = 0.0f;
-    bool have_inv = false;
-    if (p.kind == 0) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j)
-            if (lane + WAVE * j < E)
-                m = fmaxf(m, raw[j]);
-        mx = wave_max(m);
-        float sm = 0.0f;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j)
-            if (lane + WAVE * j < E)
-                sm += expf(raw[j] - mx);
-        float sum = wave_sum(sm);
-        have_inv = sum > 0.0f && isfinite(sum);
-        inv_sum = have_inv ? 1.0f / sum : 0.0f;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j)
-            sel[j] = raw[j];
-    } else {
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            uint32_t e = lane + WAVE * j;
-            sel[j] = e < E ? sigmoidf_(raw[j]) + bias[e] : 0.0f;
-        }
-    }
-
-    // group-limited selection mask (DeepSeek-V3 noaux_tc)
-    uint64_t group_keep = ~0ull;
-    uint32_t per = E / (p.n_group ? p.n_group : 1);
-    if (p.kind == 2 && p.n_group > 1) {
-        float* buf = group_buf[wv];
-#pragma unroll
-        for (int j = 0; j < EPL; ++j)
-            if (lane + WAVE * j < E)
-                buf[lane + WAVE * j] = sel[j];
-        // the buffer is private to this wave: a wave-scope fence orders the
-        // LDS stores before the reads below
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        // lane g scores group g: sum of the two largest biased scores
-        uint64_t gkey = 0;
-        if ((uint32_t)lane < p.n_group) {
-            float a = -INFINITY, b = -INFINITY;
-            uint32_t ka = 0, kb = 0;
-            for (uint32_t i = 0; i < per; ++i) {
-                float v = buf[lane * per + i];
-                uint32_t kv = total_key(v);
-                if (kv > ka) {
-                    kb = ka, b = a;
-                    ka = kv, a = v;
-                } else if (kv > kb) {
-                    kb = kv, b = v;
-                }
-            }
-            float gs = per >= 2 ? a + b : a;
-            gkey = ((uint64_t)total_key(gs) << 32) | (0xFFFFFFFFu - (uint32_t)lane);
-        }
-        group_keep = 0ull;
-        for (uint32_t r = 0; r < p.topk_group; ++r) {
-            uint64_t best = wave_max_u64(gkey);
-            uint32_t g = 0xFFFFFFFFu - (uint32_t)best;
-            group_keep |= 1ull << g;
-            if ((uint32_t)lane == g)
-                gkey = 0;
-        }
-    }
-
-    // per-lane candidate keys
-    uint64_t key[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-        uint32_t e = lane + WAVE * j;
-        bool ok = e < E && ((group_keep >> (e / (per ? per : 1))) & 1ull);
-        key[j] = ok ? (((uint64_t)total_key(sel[j]) << 32) | (0xFFFFFFFFu - e)) : 0ull;
-    }
-
-    uint32_t out_e[MAX_K];
-    float out_v[MAX_K]; // raw logit (softmax) or unbiased sigmoid
-    if (p.order == 0) {
-        for (uint32_t r = 0; r < K; ++r) {
-            uint64_t mine = 0;
-#pragma unroll
-            for (int j = 0; j < EPL; ++j)
-                mine = key[j] > mine ? key[j] : mine;
-            uint64_t best = wave_max_u64(mine);
-            uint32_t e = 0xFFFFFFFFu - (uint32_t)best;
-            out_e[r] = e;
-#pragma unroll
-            for (int j = 0; j < EPL; ++j)
-                if (key[j] == best)
-                    key[j] = 0;
-        }
-    } else {
-        // replacement-slot scan (routing_top_k_iter): state is wave-uniform
-        float sv[MAX_K];
-        uint32_t se[MAX_K];
-        for (uint32_t s = 0; s < K; ++s)
-            sv[s] = -INFINITY, se[s] = 0;
-        uint32_t mi = 0;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            uint32_t e = lane + WAVE * j;
-            uint64_t cand = __ballot(e < E && sel[j] > sv[mi]);
-            while (cand) {
-                int src = __ffsll((unsigned long long)cand) - 1;
-                cand &= cand - 1ull;
-                float s = __shfl(sel[j], src);
-                if (s > sv[mi]) {
-                    sv[mi] = s;
-                    se[mi] = (uint32_t)src + WAVE * j;
-                    mi = 0;
-                    for (uint32_t c = 1; c < K; ++c)
-                        if (sv[c] < sv[mi])
-                            mi = c;
-                }
-            }
-        }
-        for (uint32_t s = 0; s < K; ++s)
-            out_e[s] = se[s];
-    }
-    // gather the value behind each selected id
-    for (uint32_t r = 0; r < K; ++r) {
-        uint32_t e = out_e[r];
-        int src = (int)(e & 63u);
-        int jj = (int)(e >> 6);
-        float v = 0.0f;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j)
-            if (j == jj)
-                v = raw[j];
-        v = __shfl(v, src);
-        out_v[r] = p.kind == 0 ? v : sigmoidf_(v);
-    }
-    if (lane == 0) {
-        float prob[MAX_K];
-        for (uint32_t r = 0; r < K; ++r) {
-            if (p.kind == 0) {
-                float v = expf(out_v[r] - mx);
-                prob[r] = have_inv ? v * inv_sum : v;
-            } else {
-                prob[r] = out_v[r];
-            }
-        }
-        float sum = -0.0f;
-        for (uint32_t r = 0; r < K; ++r)
-            sum = sum + prob[r];
-        float inv;
-        if (p.norm == 1) {
-            if (!(isfinite(sum) && sum >= 0.0f))
-                atomicOr(status, ST_BAD_SUM);
-            inv = 1.0f / fmaxf(sum, 6.103515625e-5f);
-        } else {
-            if (!(isfinite(sum) && sum > 0.0f))
-                atomicOr(status, ST_BAD_SUM);
-            inv = 1.0f / sum;
-        }
-        for (uint32_t r = 0; r < K; ++r) {
-            if (prob[r] < 0.0f)
-                atomicOr(status, ST_NEGATIVE);
-            float wgt = prob[r] * inv;
-            ids[(uint64_t)t * K + r] = out_e[r];
-            weights[(uint64_t)t * K + r] = wgt * p.routed_scale;
-        }
-    }
+    route_token_wave<EPL>(logits + (uint64_t)t * p.experts, bias, p, ids + (uint64_t)t * p.k,
+                          weights + (uint64_t)t * p.k, sel[wv], grp[wv], status);
 }
 
 hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bias, uint32_t tokens,
@@ -555,365 +278,6 @@ hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t rou
 {
     dispatch_plan_kernel<<<1, PLAN_WAVES * 64, 0, s>>>(ids, routes, experts, k, plan, status);
     return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// decode expert phase 1: gate/up projections + SiLU(g)*u for every work
-// item (unique expert with its routed tokens, or the shared expert with all
-// tokens).  One wave per intermediate row; the gate and up rows of the same
-// index are read together so the activation is formed in registers.
-// ---------------------------------------------------------------------------
-struct ItemRef {
-    const uint8_t* slot;
-    uint32_t g0, n;   // grouped route range (or token range for shared)
-    bool shared;
-};
-
-template <int SBT, int CPL>
-__global__ __launch_bounds__(256) void decode_gateup_kernel(
-    ExpertSet ex, ExpertSet sh, bool has_shared, const void* __restrict__ sgate_w,
-    uint32_t sgate_dtype, const float* __restrict__ x, uint32_t tokens, uint32_t k,
-    uint32_t hidden, const uint32_t* __restrict__ ids, Plan plan, bool use_plan,
-    float* __restrict__ act, float* __restrict__ act_shared, float* __restrict__ shared_weight,
-    uint32_t* __restrict__ status)
-{
-    const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const uint32_t item = blockIdx.y;
-    const uint32_t routed_items = use_plan ? plan.unique_count[0] : tokens * k;
-    const uint32_t max_routed = gridDim.y - (has_shared ? 1u : 0u);
-
-    const uint8_t* slot;
-    uint32_t g0, n, I;
-    bool shared = false;
-    if (has_shared && item == max_routed) {
-        shared = true;
-        slot = sh.base;
-        g0 = 0;
-        n = tokens;
-        I = sh.gate.rows;
-    } else {
-        if (item >= routed_items)
-            return;
-        uint32_t e;
-        if (use_plan) {
-            e = plan.unique_ids[item];
-            g0 = plan.groups[2 * item];
-            n = plan.groups[2 * item + 1];
-        } else {
-            e = ids[item];
-            g0 = item;
-            n = 1;
-        }
-        if (e >= ex.count) {
-            if (lane == 0 && wv == 0 && blockIdx.x == 0)
-                atomicOr(status, ST_ROUTE_RANGE);
-            return;
-        }
-        slot = ex.base + (uint64_t)e * ex.stride;
-        I = ex.gate.rows;
-    }
-    const ExpertSet& set = shared ? sh : ex;
-    const uint32_t row = blockIdx.x * 4 + wv;
-
-    // shared-expert sigmoid gate: sigma(W_sg . x_t), or 1 without a gate
-    if (shared && blockIdx.x == 0 && wv == 0) {
-        for (uint32_t t = 0; t < tokens; ++t) {
-            float g = 80.0f;
-            if (sgate_w) {
-                float a = 0.0f;
-                for (uint32_t c = lane; c < hidden; c += WAVE) {
-                    float wvv;
-                    if (sgate_dtype == 0)
-                        wvv = reinterpret_cast<const float*>(sgate_w)[c];
-                    else if (sgate_dtype == 2)
-                        wvv = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(sgate_w)[c] << 16);
-                    else
-                        wvv = __half2float(__ushort_as_half(reinterpret_cast<const uint16_t*>(sgate_w)[c]));
-                    a = fmaf(wvv, x[(uint64_t)t * hidden + c], a);
-                }
-                g = wave_sum(a);
-            }
-            if (lane == 0)
-                shared_weight[t] = sigmoidf_(g);
-        }
-    }
-    if (row >= I)
-        return;
-
-    const uint32_t chunks = hidden / 32; // 16-byte chunks per row
-    const uint32_t gpr = hidden / set.group;
-    const uint8_t* gw = slot + set.gate.w_off + (uint64_t)row * (hidden / 2);
-    const uint8_t* uw = slot + set.up.w_off + (uint64_t)row * (hidden / 2);
-    const uint8_t* gs = slot + set.gate.s_off;
-    const uint8_t* gb = slot + set.gate.b_off;
-    const uint8_t* us = slot + set.up.s_off;
-    const uint8_t* ub = slot + set.up.b_off;
-
-    uint4 wg[CPL], wu[CPL];
-    float sg[CPL], bg[CPL], su[CPL], bu[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        uint32_t c = lane + WAVE * j;
-        if (c < chunks) {
-            wg[j] = reinterpret_cast<const uint4*>(gw)[c];
-            wu[j] = reinterpret_cast<const uint4*>(uw)[c];
-            uint64_t gi = (uint64_t)row * gpr + (c * 32u) / set.group;
-            sg[j] = sb_at<SBT>(gs, gi);
-            bg[j] = sb_at<SBT>(gb, gi);
-            su[j] = sb_at<SBT>(us, gi);
-            bu[j] = sb_at<SBT>(ub, gi);
-        }
-    }
-    for (uint32_t j = 0; j < n; ++j) {
-        uint32_t gidx = g0 + j;
-        uint32_t tok = shared ? j : (use_plan ? plan.src_rows[gidx] : gidx / k);
-        const float* xt = x + (uint64_t)tok * hidden;
-        float pg = 0.0f, pu = 0.0f;
-#pragma unroll
-        for (int jj = 0; jj < CPL; ++jj) {
-            uint32_t c = lane + WAVE * jj;
-            if (c < chunks) {
-                float xs;
-                float qg = q4_chunk_qx(wg[jj], xt + c * 32, xs);
-                float xs2;
-                float qu = q4_chunk_qx(wu[jj], xt + c * 32, xs2);
-                pg = fmaf(sg[jj], qg, fmaf(bg[jj], xs, pg));
-                pu = fmaf(su[jj], qu, fmaf(bu[jj], xs, pu));
-            }
-        }
-        float g = wave_sum(pg);
-        float u = wave_sum(pu);
-        if (lane == 0) {
-            float a = (g / (1.0f + expf(-g))) * u;
-            if (shared)
-                act_shared[(uint64_t)j * I + row] = a;
-            else
-                act[(uint64_t)gidx * I + row] = a;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// decode expert phase 2: down projection fused with the weighted combine and
-// the shared-expert add.  A block owns R = 64/LPR output rows; its 4 waves
-// split the work items; y values meet in LDS and one thread per (token, row)
-// forms  h = (r + sum_k w_k y_k) + sw * S  in route order.
-// ---------------------------------------------------------------------------
-constexpr int DEC_MAX_T = 16;
-constexpr int DEC_MAX_ROUTES = DEC_MAX_T * MAX_K;
-
-template <int SBT, int LPR, int CPL>
-__global__ __launch_bounds__(256) void decode_down_combine_kernel(
-    ExpertSet ex, ExpertSet sh, bool has_shared, const float* __restrict__ act,
-    const float* __restrict__ act_shared, const float* __restrict__ shared_weight,
-    uint32_t tokens, uint32_t k, uint32_t hidden, const uint32_t* __restrict__ ids,
-    const float* __restrict__ weights, Plan plan, bool use_plan,
-    const float* __restrict__ residual, float* __restrict__ hidden_out,
-    uint32_t* __restrict__ status)
-{
-    constexpr int R = 64 / LPR;
-    __shared__ float ylds[DEC_MAX_ROUTES][R];
-    __shared__ float yshl[DEC_MAX_T][R];
-    const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const int gl = lane % LPR;      // lane within the row group
-    const int rr = lane / LPR;      // row within the block
-    const uint32_t row = blockIdx.x * R + rr;
-    const uint32_t routed_items = use_plan ? plan.unique_count[0] : tokens * k;
-    const uint32_t items = routed_items + (has_shared ? 1u : 0u);
-
-    for (uint32_t item = wv; item < items; item += 4) {
-        const bool shared = has_shared && item == routed_items;
-        const ExpertSet& set = shared ? sh : ex;
-        const uint8_t* slot;
-        uint32_t g0, n;
-        if (shared) {
-            slot = sh.base;
-            g0 = 0;
-            n = tokens;
-        } else {
-            uint32_t e;
-            if (use_plan) {
-                e = plan.unique_ids[item];
-                g0 = plan.groups[2 * item];
-                n = plan.groups[2 * item + 1];
-            } else {
-                e = ids[item];
-                g0 = item;
-                n = 1;
-            }
-            if (e >= ex.count) {
-                for (uint32_t j = 0; j < n; ++j)
-                    if (gl == 0)
-                        ylds[g0 + j][rr] = 0.0f;
-                continue;
-            }
-            slot = ex.base + (uint64_t)e * ex.stride;
-        }
-        const uint32_t I = set.down.cols;
-        const uint32_t chunks = I / 32;
-        const uint32_t gpr = I / set.group;
-        const uint8_t* dw = slot + set.down.w_off + (uint64_t)row * (I / 2);
-        uint4 w[CPL];
-        float s[CPL], b[CPL];
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            uint32_t c = gl + LPR * j;
-            if (c < chunks) {
-                w[j] = reinterpret_cast<const uint4*>(dw)[c];
-                uint64_t gi = (uint64_t)row * gpr + (c * 32u) / set.group;
-                s[j] = sb_at<SBT>(slot + set.down.s_off, gi);
-                b[j] = sb_at<SBT>(slot + set.down.b_off, gi);
-            }
-        }
-        for (uint32_t j = 0; j < n; ++j) {
-            const float* a = shared ? act_shared + (uint64_t)j * I : act + (uint64_t)(g0 + j) * I;
-            float part = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < CPL; ++jj) {
-                uint32_t c = gl + LPR * jj;
-                if (c < chunks) {
-                    float xs;
-                    float qx = q4_chunk_qx(w[jj], a + c * 32, xs);
-                    part = fmaf(s[jj], qx, fmaf(b[jj], xs, part));
-                }
-            }
-            float y = group_sum<LPR>(part);
-            if (gl == 0) {
-                if (shared)
-                    yshl[j][rr] = y;
-                else
-                    ylds[g0 + j][rr] = y;
-            }
-        }
-    }
-    __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < tokens * R; idx += 256) {
-        uint32_t t = idx / R, r = idx % R;
-        float moe = 0.0f;
-        for (uint32_t kk = 0; kk < k; ++kk) {
-            uint32_t route = t * k + kk;
-            uint32_t gi = use_plan ? plan.out_idx[route] : route;
-            float y = gi < DEC_MAX_ROUTES ? ylds[gi][r] : 0.0f;
-            moe = moe + weights[route] * y;
-        }
-        uint64_t o = (uint64_t)t * hidden + blockIdx.x * R + r;
-        float rm = residual[o] + moe;
-        float sw = has_shared ? shared_weight[t] : 0.0f;
-        float sv = has_shared ? yshl[t][r] : 0.0f;
-        hidden_out[o] = rm + sw * sv;
-    }
-}
-
-// next-layer RMSNorm: one block per token (rms_norm_reduced)
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ h,
-                                                       const float* __restrict__ w,
-                                                       uint32_t width, float eps,
-                                                       float* __restrict__ out)
-{
-    __shared__ float part[4];
-    const float* row = h + (uint64_t)blockIdx.x * width;
-    float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < width; i += 256)
-        s = fmaf(row[i], row[i], s);
-    s = wave_sum(s);
-    if ((threadIdx.x & 63) == 0)
-        part[threadIdx.x >> 6] = s;
-    __syncthreads();
-    float ms = ((part[0] + part[1]) + (part[2] + part[3])) / (float)(width > 1 ? width : 1);
-    float scale = 1.0f / sqrtf(ms + eps);
-    for (uint32_t i = threadIdx.x; i < width; i += 256)
-        out[(uint64_t)blockIdx.x * width + i] = (row[i] * scale) * w[i];
-}
-
-template <int SBT>
-static hipError_t launch_decode_typed(hipStream_t s, const ExpertSet& ex, const ExpertSet* shared,
-                                      const void* sgw, uint32_t sgdt, const float* x,
-                                      const float* residual, uint32_t tokens, uint32_t k,
-                                      uint32_t hidden, const uint32_t* ids, const float* weights,
-                                      const Plan* plan, float* act, float* act_shared,
-                                      float* shared_weight, float* hidden_out,
-                                      const float* next_norm_w, float eps, float* next_normed,
-                                      uint32_t* status)
-{
-    const bool has_shared = shared != nullptr;
-    ExpertSet sh = has_shared ? *shared : ExpertSet{};
-    Plan pl = plan ? *plan : Plan{};
-    const bool use_plan = plan != nullptr;
-    uint32_t routed_items = use_plan ? std::min(ex.count, tokens * k) : tokens * k;
-    uint32_t I = ex.gate.rows;
-    uint32_t Imax = has_shared && sh.gate.rows > I ? sh.gate.rows : I;
-    dim3 g1((Imax + 3) / 4, routed_items + (has_shared ? 1u : 0u));
-    uint32_t cpl = (hidden / 32 + WAVE - 1) / WAVE;
-#define PBM_GU(C)                                                                              \
-    decode_gateup_kernel<SBT, C><<<g1, 256, 0, s>>>(ex, sh, has_shared, sgw, sgdt, x, tokens, k, \
-                                                    hidden, ids, pl, use_plan, act, act_shared, \
-                                                    shared_weight, status)
-    if (cpl <= 1)
-        PBM_GU(1);
-    else if (cpl <= 2)
-        PBM_GU(2);
-    else if (cpl <= 4)
-        PBM_GU(4);
-    else
-        return hipErrorInvalidValue;
-#undef PBM_GU
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess)
-        return err;
-
-    // down: LPR = 8 lanes per row, CPL2 = I / 256 chunks per lane
-    uint32_t Id = I;
-    if (has_shared && sh.down.cols != Id)
-        return hipErrorInvalidValue; // shared and routed intermediates must match here
-    uint32_t cpl2 = Id / 256;
-    dim3 g2(hidden / 8);
-#define PBM_DN(C)                                                                              \
-    decode_down_combine_kernel<SBT, 8, C><<<g2, 256, 0, s>>>(                                  \
-        ex, sh, has_shared, act, act_shared, shared_weight, tokens, k, hidden, ids, weights,    \
-        pl, use_plan, residual, hidden_out, status)
-    if (cpl2 == 1)
-        PBM_DN(1);
-    else if (cpl2 == 2)
-        PBM_DN(2);
-    else if (cpl2 == 3)
-        PBM_DN(3);
-    else if (cpl2 == 4)
-        PBM_DN(4);
-    else if (cpl2 <= 8)
-        PBM_DN(8);
-    else
-        return hipErrorInvalidValue;
-#undef PBM_DN
-    err = hipGetLastError();
-    if (err != hipSuccess)
-        return err;
-    if (next_norm_w && next_normed) {
-        rms_norm_kernel<<<tokens, 256, 0, s>>>(hidden_out, next_norm_w, hidden, eps, next_normed);
-        err = hipGetLastError();
-    }
-    return err;
-}
-
-hipError_t launch_decode_experts(hipStream_t s, const ExpertSet& ex, const ExpertSet* shared,
-                                 const void* shared_gate_w, uint32_t shared_gate_dtype,
-                                 const float* x, const float* residual, uint32_t tokens,
-                                 uint32_t k, uint32_t hidden, const uint32_t* ids,
-                                 const float* weights, const Plan* plan, float* act,
-                                 float* act_shared, float* shared_weight, float* hidden_out,
-                                 const float* next_norm_w, float eps, float* next_normed,
-                                 uint32_t* status)
-{
-    if (ex.sb_dtype == 2)
-        return launch_decode_typed<2>(s, ex, shared, shared_gate_w, shared_gate_dtype, x,
-                                      residual, tokens, k, hidden, ids, weights, plan, act,
-                                      act_shared, shared_weight, hidden_out, next_norm_w, eps,
-                                      next_normed, status);
-    return launch_decode_typed<1>(s, ex, shared, shared_gate_w, shared_gate_dtype, x, residual,
-                                  tokens, k, hidden, ids, weights, plan, act, act_shared,
-                                  shared_weight, hidden_out, next_norm_w, eps, next_normed,
-                                  status);
 }
 
 // ---------------------------------------------------------------------------

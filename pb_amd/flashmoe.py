@@ -87,6 +87,16 @@ class MoeLayer:
                                      weights.ptr, next_norm.ptr if next_norm is not None else None, hidden_out.ptr,
                                      next_normed.ptr if next_normed is not None else None))
 
+    # -- whole block: routing stage + CMD3 in one call ------------------------
+    def forward(self, x: DeviceArray, residual: DeviceArray, hidden_out: DeviceArray,
+                ids: DeviceArray | None = None, weights: DeviceArray | None = None,
+                next_norm: DeviceArray | None = None, next_normed: DeviceArray | None = None):
+        check(lib().pbmoe_moe_layer(self.ctx.handle, self.index, x.ptr, residual.ptr, x.shape[0],
+                                    ids.ptr if ids is not None else None,
+                                    weights.ptr if weights is not None else None,
+                                    next_norm.ptr if next_norm is not None else None, hidden_out.ptr,
+                                    next_normed.ptr if next_normed is not None else None))
+
     # -- layer-major prefill (qwen_layer_major_experts) -----------------------
     def qwen_layer_major_experts(self, x: DeviceArray, residual: DeviceArray, ids: DeviceArray,
                                  weights: DeviceArray, hidden_out: DeviceArray,

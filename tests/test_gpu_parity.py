@@ -263,3 +263,47 @@ def test_dispatch_plan_bit_exact_zipf_prefill(ctx):
     assert got[4] == ref[4]
     counts = [c for _, c in got[4]]
     assert sorted(counts) == sorted(int(h) for h in hist if h)
+
+
+# ------------------------------------------------------------ fused layer ---
+@pytest.mark.parametrize("cfg,T,order", [(C1, 1, abi.ORDER_CANONICAL), (C2, 1, abi.ORDER_CANONICAL),
+                                         (C2, 4, abi.ORDER_REFERENCE_SLOT), (C2, 8, abi.ORDER_CANONICAL),
+                                         (C5, 1, abi.ORDER_CANONICAL), (C5, 2, abi.ORDER_CANONICAL)])
+def test_fused_layer_matches_split_and_oracle(ctx, cfg, T, order):
+    """pbmoe_moe_layer (router + routing + experts in one call) gives the same
+    routes as pbmoe_route and a hidden state within the bar of the oracle."""
+    _say(f"[test] fused layer {cfg.name} T={T} order={order}")
+    dl = _layer(ctx, cfg, 0, order)
+    xh, rh = synth.activations(SEED, 50 + T, T, cfg.hidden)
+    x, ids_split, w_split, _ = _route(ctx, dl, xh)
+    res = ctx.to_device(rh)
+    ids = ctx.array((T, cfg.k), np.uint32)
+    w = ctx.array((T, cfg.k), np.float32)
+    out = ctx.array((T, cfg.hidden), np.float32)
+    dl.moe.forward(x, res, out, ids, w)
+    ctx.sync()
+    ids_h = ids.download().astype(np.int32)
+    np.testing.assert_array_equal(ids_h, ids_split.download().astype(np.int32))
+    np.testing.assert_array_equal(w.download(), w_split.download())
+    ref_h, _ = dl.oracle_block(xh, rh, ids_h, w.download())
+    exact = dl.exact_block(xh, rh, ids_h, w.download()) if np.max(np.abs(ref_h)) > 1e3 else None
+    mx, rel = assert_layer_tolerance(out.download(), ref_h, exact=exact)
+    _say(f"[result] fused {cfg.name} T={T}: max_abs={mx:.3e} rel_l2={rel:.3e}")
+
+
+def test_fused_layer_repeated_calls_are_deterministic(ctx):
+    """The last-workgroup ticket resets itself: many back-to-back calls give
+    bitwise identical results."""
+    _say("[test] fused determinism")
+    dl = _layer(ctx, C2, 0)
+    xh, rh = synth.activations(SEED, 77, 1, C2.hidden)
+    x, res = ctx.to_device(xh), ctx.to_device(rh)
+    outs = []
+    for _ in range(3):
+        out = ctx.array((1, C2.hidden), np.float32)
+        for _ in range(50):
+            dl.moe.forward(x, res, out)
+        ctx.sync()
+        outs.append(out.download())
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint32), outs[0].view(np.uint32))
