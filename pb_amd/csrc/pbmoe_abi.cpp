@@ -205,6 +205,7 @@ pbmoe::ExpertSet make_set(const uint8_t* base, const pbmoe_q4_layout& l, uint32_
     s.stride = l.expert_bytes;
     s.count = count;
     s.group = l.group_size;
+    s.group_shift = l.group_size == 32 ? 5u : (l.group_size == 64 ? 6u : 7u);
     s.sb_dtype = l.scale_bias_dtype;
     auto proj = [&](int p) {
         pbmoe::Q4Proj q{};

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
         } else if (task < n_router + Is) {
             const uint32_t i = task - n_router;
             const ExpertSet& s = a.sh;
-            const uint32_t chunks = H / 32, gpr = H / s.group;
+            const uint32_t chunks = H / 32, gpr = H >> s.group_shift;
             const uint4* gw = reinterpret_cast<const uint4*>(s.base + s.gate.w_off + (uint64_t)i * (H / 2));
             const uint4* uw = reinterpret_cast<const uint4*>(s.base + s.up.w_off + (uint64_t)i * (H / 2));
             uint4 wg[CS], wu[CS];
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
                 if (ch < chunks) {
                     wg[c] = gw[ch];
                     wu[c] = uw[ch];
-                    const uint64_t gi = (uint64_t)i * gpr + (ch * 32u) / s.group;
+                    const uint64_t gi = (uint64_t)i * gpr + ((ch * 32u) >> s.group_shift);
                     sg[c] = sb_at<SBT>(s.base + s.gate.s_off, gi);
                     bg[c] = sb_at<SBT>(s.base + s.gate.b_off, gi);
                     su[c] = sb_at<SBT>(s.base + s.up.s_off, gi);
@@ -187,7 +187,7 @@ struct RouteLds {
     uint32_t start[1024];
     uint32_t unique_count;
     uint32_t sel[4][MAX_K];
-    float grp[4][1024];
+    float grp[4][2048 + 192];
 };
 
 // Stable plan of `routes` routes from s.ids (block-wide, routes <= 256):
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
     }
     const ExpertSet& ex = a.ex;
     const uint8_t* slot = ex.base + (uint64_t)e * ex.stride;
-    const uint32_t chunks = H / 32, gpr = H / ex.group;
+    const uint32_t chunks = H / 32, gpr = H >> ex.group_shift;
     uint4 wg[RPW][CPL], wu[RPW][CPL];
     float sg[RPW][CPL], bg[RPW][CPL], su[RPW][CPL], bu[RPW][CPL];
 #pragma unroll
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
             if (ch < chunks) {
                 wg[r][c] = gw[ch];
                 wu[r][c] = uw[ch];
-                const uint64_t gi = (uint64_t)row * gpr + (ch * 32u) / ex.group;
+                const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> ex.group_shift);
                 sg[r][c] = sb_at<SBT>(slot + ex.gate.s_off, gi);
                 bg[r][c] = sb_at<SBT>(slot + ex.gate.b_off, gi);
                 su[r][c] = sb_at<SBT>(slot + ex.up.s_off, gi);
@@ -451,12 +451,13 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     __shared__ float ylds[DEC_ROUTES][R];
     __shared__ float yshl[DEC_T][R];
     __shared__ float astage[STAGE_FLOATS];
+    __shared__ float xsl[STAGE_FLOATS / 32]; // per-chunk sums of the staged activations
     const int gl = threadIdx.x % LPR;
     const int slot_id = threadIdx.x / LPR;
     const uint32_t row_base = blockIdx.x * R;
     const uint32_t T = a.tokens, K = a.k;
     const uint32_t I = a.ex.down.cols;
-    const uint32_t gpr = I / a.ex.group;
+    const uint32_t gpr = I >> a.ex.group_shift;
     const uint32_t routes = T * K;
 
     // loads that do not depend on the routes: residual for the combine and
@@ -513,13 +514,26 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             for (int c = 0; c < CPL; ++c) {
                 const uint32_t ch = gl + LPR * c;
                 w[m][c] = dw[ch];
-                const uint64_t gi = (uint64_t)row * gpr + (ch * 32u) / set.group;
+                const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> set.group_shift);
                 sc[m][c] = sb_at<SBT>(slot + set.down.s_off, gi);
                 bi[m][c] = sb_at<SBT>(slot + set.down.b_off, gi);
             }
         }
-        if (a.stage && u0 == 0)
+        if (a.stage && u0 == 0) {
             __syncthreads(); // staged activations visible
+            const uint32_t n_chunks = (routes + (a.has_shared ? T : 0u)) * (I / 32);
+            for (uint32_t q = threadIdx.x; q < n_chunks; q += 256) {
+                const float4* c4 = reinterpret_cast<const float4*>(astage + q * 32);
+                float sum = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const float4 f = c4[v];
+                    sum += (f.x + f.y) + (f.z + f.w);
+                }
+                xsl[q] = sum;
+            }
+            __syncthreads();
+        }
 #pragma unroll
         for (int m = 0; m < MAXR; ++m) {
             const uint32_t unit = u0 + slot_id + SLOTS * m;
@@ -539,17 +553,25 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             for (uint32_t j = 0; j < n; ++j) {
                 float part = 0.0f;
                 if (live[m]) {
-                    const float* av;
-                    if (a.stage)
-                        av = shared ? astage + (uint64_t)(routes + j) * I : astage + (uint64_t)(g0 + j) * I;
-                    else
-                        av = shared ? a.act_shared + (uint64_t)j * I : a.act + (uint64_t)(g0 + j) * I;
+                    if (a.stage) {
+                        const uint32_t rt = shared ? routes + j : g0 + j;
+                        const float* av = astage + (uint64_t)rt * I;
+                        const float* xs = xsl + rt * (I / 32);
 #pragma unroll
-                    for (int c = 0; c < CPL; ++c) {
-                        const uint32_t ch = gl + LPR * c;
-                        float xs;
-                        const float qx = q4_chunk_qx(w[m][c], av + ch * 32, xs);
-                        part = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs, part));
+                        for (int c = 0; c < CPL; ++c) {
+                            const uint32_t ch = gl + LPR * c;
+                            const float qx = q4_chunk_q(w[m][c], av + ch * 32);
+                            part = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs[ch], part));
+                        }
+                    } else {
+                        const float* av = shared ? a.act_shared + (uint64_t)j * I : a.act + (uint64_t)(g0 + j) * I;
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) {
+                            const uint32_t ch = gl + LPR * c;
+                            float xs;
+                            const float qx = q4_chunk_qx(w[m][c], av + ch * 32, xs);
+                            part = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs, part));
+                        }
                     }
                 }
                 const float y = group_sum<LPR>(part);
@@ -562,8 +584,10 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
         }
     }
-    if (a.stage && n_units == 0)
+    if (a.stage && n_units == 0) {
         __syncthreads();
+        __syncthreads();
+    }
     __syncthreads();
     if (threadIdx.x < T * R) {
         const uint32_t t = threadIdx.x / R, r = threadIdx.x % R;
@@ -750,8 +774,15 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     return err;
 }
 
+static bool set_ok(const ExpertSet& s)
+{
+    return (1u << s.group_shift) == s.group && s.group >= 32 && s.group <= 128;
+}
+
 hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mode)
 {
+    if (mode != DECODE_ROUTE_ONLY && (!set_ok(d.ex) || (d.shared && !set_ok(*d.shared))))
+        return hipErrorInvalidValue; // the kernels index scales with group_shift
     hipError_t err;
     if (mode == DECODE_ROUTE_ONLY) {
         // router rows, then the routing stage of one wave per token

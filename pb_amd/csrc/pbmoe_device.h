@@ -82,6 +82,19 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
     return max(max(a, b), max(c, d));
 }
 
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
+{
+    v = min(v, dpp_u<DPP_QUAD_1032>(v));
+    v = min(v, dpp_u<DPP_QUAD_2301>(v));
+    v = min(v, dpp_u<DPP_ROW_HALF_MIRROR>(v));
+    v = min(v, dpp_u<DPP_ROW_MIRROR>(v));
+    uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return min(min(a, b), min(c, d));
+}
+
 // f32 total order (Rust f32::total_cmp) mapped onto unsigned order.
 __device__ __forceinline__ uint32_t total_key(float f)
 {
@@ -90,6 +103,7 @@ __device__ __forceinline__ uint32_t total_key(float f)
 }
 
 __device__ __forceinline__ float sigmoidf_(float l) { return 1.0f / (1.0f + expf(-l)); }
+__device__ __forceinline__ float fast_sigmoid(float l) { return 1.0f / (1.0f + __expf(-l)); }
 
 template <int SBT>
 __device__ __forceinline__ float sb_at(const uint8_t* base, uint64_t i)
@@ -125,6 +139,29 @@ __device__ __forceinline__ float q4_chunk_qx(uint4 w, const float* __restrict__ 
         sx += ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
     }
     xs = sx;
+    return qx0 + qx1;
+}
+
+// sum(q * x) only (the sum of x is known).
+__device__ __forceinline__ float q4_chunk_q(uint4 w, const float* __restrict__ x)
+{
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float qx0 = 0.0f, qx1 = 0.0f;
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 a = x4[2 * i];
+        const float4 b = x4[2 * i + 1];
+        const uint32_t q = words[i];
+        qx0 = fmaf((float)(q & 15u), a.x, qx0);
+        qx1 = fmaf((float)((q >> 4) & 15u), a.y, qx1);
+        qx0 = fmaf((float)((q >> 8) & 15u), a.z, qx0);
+        qx1 = fmaf((float)((q >> 12) & 15u), a.w, qx1);
+        qx0 = fmaf((float)((q >> 16) & 15u), b.x, qx0);
+        qx1 = fmaf((float)((q >> 20) & 15u), b.y, qx1);
+        qx0 = fmaf((float)((q >> 24) & 15u), b.z, qx0);
+        qx1 = fmaf((float)(q >> 28), b.w, qx1);
+    }
     return qx0 + qx1;
 }
 
@@ -188,24 +225,92 @@ __device__ __forceinline__ void wave_topk_canonical(uint32_t (&key)[EPL], uint32
         }
         const uint32_t best = wave_max_u32(hk);
         const uint64_t tied = __ballot(hk == best);
-        uint32_t win_lane = (uint32_t)(__ffsll((unsigned long long)tied) - 1);
-        uint32_t win_e = (uint32_t)__builtin_amdgcn_readlane((int)hi, (int)win_lane);
-        if (__popcll(tied) > 1) { // exact tie across lanes: lowest index wins
-            uint64_t rest = tied & (tied - 1ull);
-            while (rest) {
-                uint32_t l2 = (uint32_t)(__ffsll((unsigned long long)rest) - 1);
-                rest &= rest - 1ull;
-                uint32_t e2 = (uint32_t)__builtin_amdgcn_readlane((int)hi, (int)l2);
-                if (e2 < win_e) {
-                    win_e = e2;
-                    win_lane = l2;
-                }
-            }
+        uint32_t win_e;
+        if (__popcll(tied) == 1) {
+            win_e = (uint32_t)__builtin_amdgcn_readlane((int)hi, __ffsll((unsigned long long)tied) - 1);
+        } else { // exact tie across lanes: lowest index wins (constant time)
+            win_e = wave_min_u32(hk == best ? hi : 0xFFFFFFFFu);
         }
-        if ((uint32_t)lane == win_lane)
+        if ((uint32_t)lane == (win_e & 63u))
             ++p;
         out_e[r] = win_e;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Faster canonical top-k for the common case.  The K-th largest lane maximum
+// is a lower bound of the K-th largest element, so every member of the top-k
+// has a key >= that bound.  When at most 64 elements pass the bound they are
+// compacted one per lane (through LDS scratch of 64 entries) and K rounds of
+// a wave max pick them in canonical order; otherwise the sorted-list
+// selection above runs.  Both return the same ids.
+// ---------------------------------------------------------------------------
+template <int EPL>
+__device__ __forceinline__ void wave_topk_filtered(uint32_t (&key)[EPL], uint32_t k, uint32_t* out_e,
+                                                   uint32_t* scratch128)
+{
+    const int lane = threadIdx.x & 63;
+    uint32_t head = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+        head = max(head, key[j]);
+    // K-th largest lane head, by parallel ranking against broadcast LDS
+    // reads: lane l holds it when #(heads > h_l) <= K-1 < #(heads >= h_l)
+    scratch128[128 + lane] = head;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    uint32_t gt = 0, ge = 0;
+    const uint4* hv4 = reinterpret_cast<const uint4*>(scratch128 + 128);
+#pragma unroll
+    for (int j = 0; j < WAVE / 4; ++j) {
+        const uint4 h4 = hv4[j];
+        gt += (h4.x > head ? 1u : 0u) + (h4.y > head ? 1u : 0u) + (h4.z > head ? 1u : 0u) + (h4.w > head ? 1u : 0u);
+        ge += (h4.x >= head ? 1u : 0u) + (h4.y >= head ? 1u : 0u) + (h4.z >= head ? 1u : 0u) + (h4.w >= head ? 1u : 0u);
+    }
+    const uint64_t holds = __ballot(gt <= k - 1 && k - 1 < ge);
+    const uint32_t bound = (uint32_t)__builtin_amdgcn_readlane((int)head, __ffsll((unsigned long long)holds) - 1);
+    uint32_t total = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+        total += (uint32_t)__popcll(__ballot(key[j] >= bound && key[j] != 0u));
+    if (total > 64u || bound == 0u || holds == 0ull) {
+        wave_topk_canonical<EPL>(key, k, out_e);
+        return;
+    }
+    // compact candidates one per lane
+    uint32_t base = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const bool c = key[j] >= bound && key[j] != 0u;
+        const uint64_t b = __ballot(c);
+        if (c) {
+            const uint32_t pos = base + (uint32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            scratch128[pos] = key[j];
+            scratch128[64 + pos] = (uint32_t)lane + WAVE * j;
+        }
+        base += (uint32_t)__popcll(b);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t ck = (uint32_t)lane < total ? scratch128[lane] : 0u;
+    const uint32_t ci = (uint32_t)lane < total ? scratch128[64 + lane] : 0xFFFFFFFFu;
+    // canonical rank among the candidates (score desc, then lower index),
+    // candidates read back as broadcast LDS vectors
+    uint32_t rank = 0;
+    const uint4* k4 = reinterpret_cast<const uint4*>(scratch128);
+    const uint4* i4 = reinterpret_cast<const uint4*>(scratch128 + 64);
+    const uint32_t n4 = (total + 3) / 4;
+    for (uint32_t j = 0; j < n4; ++j) {
+        const uint4 kk = k4[j], ii = i4[j];
+        const uint32_t kv[4] = {kk.x, kk.y, kk.z, kk.w}, iv[4] = {ii.x, ii.y, ii.z, ii.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (4 * j + q < total)
+                rank += (kv[q] > ck || (kv[q] == ck && iv[q] < ci)) ? 1u : 0u;
+    }
+    if ((uint32_t)lane < total && rank < k)
+        out_e[rank] = ci;
 }
 
 // ---------------------------------------------------------------------------
@@ -229,6 +334,11 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
     if (__ballot(bad) != 0ull && lane == 0)
         atomicOr(status, ST_NONFINITE);
 
+    // raw logits of this token, for the value lookup after selection
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+        if (lane + WAVE * j < E)
+            lds_grp[lane + WAVE * j] = raw[j];
     float mx = 0.0f, inv_sum = 0.0f;
     bool have_inv = false;
     float sel[EPL];
@@ -243,7 +353,7 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
 #pragma unroll
         for (int j = 0; j < EPL; ++j)
             if (lane + WAVE * j < E)
-                sm += expf(raw[j] - mx);
+                sm += __expf(raw[j] - mx);
         float sum = wave_sum(sm);
         have_inv = sum > 0.0f && isfinite(sum);
         inv_sum = have_inv ? 1.0f / sum : 0.0f;
@@ -260,11 +370,12 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
 
     uint64_t keep = ~0ull;
     const uint32_t per = E / (p.n_group ? p.n_group : 1);
+    float* grp_sel = lds_grp + E; // lds_grp holds 2*E floats
     if (p.kind == 2 && p.n_group > 1) {
 #pragma unroll
         for (int j = 0; j < EPL; ++j)
             if (lane + WAVE * j < E)
-                lds_grp[lane + WAVE * j] = sel[j];
+                grp_sel[lane + WAVE * j] = sel[j];
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
         uint32_t gkey = 0;
@@ -272,7 +383,7 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
             uint32_t ka = 0, kb = 0;
             float a = -INFINITY, b = -INFINITY;
             for (uint32_t i = 0; i < per; ++i) {
-                float v = lds_grp[lane * per + i];
+                float v = grp_sel[lane * per + i];
                 uint32_t kv = total_key(v);
                 if (kv > ka) {
                     kb = ka, b = a;
@@ -294,15 +405,18 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
     }
 
     uint32_t key[EPL];
+    const bool grouped = p.kind == 2 && p.n_group > 1;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
-        uint32_t e = lane + WAVE * j;
-        bool ok = e < E && ((keep >> (e / (per ? per : 1))) & 1ull);
+        const uint32_t e = lane + WAVE * j;
+        bool ok = e < E;
+        if (grouped)
+            ok = ok && ((keep >> (e / per)) & 1ull);
         key[j] = ok ? total_key(sel[j]) : 0u;
     }
 
     if (p.order == 0) {
-        wave_topk_canonical<EPL>(key, K, lds_e);
+        wave_topk_filtered<EPL>(key, K, lds_e, reinterpret_cast<uint32_t*>(lds_grp) + 2 * E);
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
     } else {
@@ -352,7 +466,7 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
 
     // value behind each selected id: lane r fetches route r's logit
     uint32_t myid = (uint32_t)lane < K ? lds_e[lane] : 0u;
-    float v = (uint32_t)lane < K && myid < E ? l[myid] : 0.0f;
+    float v = (uint32_t)lane < K && myid < E ? lds_grp[myid] : 0.0f;
     float prob;
     if (p.kind == 0) {
         float ev = expf(v - mx);
@@ -360,10 +474,8 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
     } else {
         prob = sigmoidf_(v);
     }
-    // sequential renormalisation in route order (lane 0 sums like the CPU)
-    float sum = -0.0f;
-    for (uint32_t r = 0; r < K; ++r)
-        sum = sum + readlane_f(prob, (int)r);
+    // renormalisation over the K selected probabilities (lanes < K)
+    const float sum = wave_sum((uint32_t)lane < K ? prob : 0.0f);
     float inv;
     if (p.norm == 1) {
         if (lane == 0 && !(isfinite(sum) && sum >= 0.0f))

@@ -29,6 +29,7 @@ struct ExpertSet {
     uint64_t stride;     // expert_bytes
     uint32_t count;      // number of slots
     uint32_t group;      // quantisation group size (32, 64 or 128)
+    uint32_t group_shift; // log2(group)
     uint32_t sb_dtype;   // 1 = f16, 2 = bf16
     Q4Proj gate, up, down;
 };

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                                                          float* __restrict__ weights,
                                                          uint32_t* __restrict__ status)
 {
-    __shared__ float grp[4][EPL * WAVE];
+    __shared__ float grp[4][2 * EPL * WAVE + 192];
     __shared__ uint32_t sel[4][MAX_K];
     const int wv = threadIdx.x >> 6;
     const uint32_t t = blockIdx.x * 4 + wv;
