@@ -54,6 +54,7 @@ int ok()
 constexpr uint32_t MAX_EXPERTS = 1024;
 constexpr uint32_t MAX_K = 16;
 constexpr uint32_t MAX_DECODE_TOKENS = 16;
+constexpr uint32_t MAX_PREFILL_TOKENS = 32768;
 constexpr uint32_t MAX_HIDDEN = 8192;
 constexpr uint32_t MAX_INTERMEDIATE = 2048;
 
@@ -91,6 +92,7 @@ struct pbmoe_ctx {
     uint32_t* status = nullptr; // device status word
     DeviceBuf logits, act, act_shared, shared_weight, plan;
     DeviceBuf route_ids, route_w;
+    DeviceBuf prefill; // prefill scratch (operand splits, activations, y)
 };
 
 namespace {
@@ -464,6 +466,9 @@ PBMOE_API int pbmoe_sync(pbmoe_ctx* ctx)
         if (st & (pbmoe::ST_BAD_SUM | pbmoe::ST_NEGATIVE))
             return fail(PBMOE_ERR_ROUTE,
                         "selected expert probabilities must have a positive finite sum");
+        if (st & pbmoe::ST_F16_RANGE)
+            return fail(PBMOE_ERR_NONFINITE,
+                        "a prefill SwiGLU activation exceeded the f16 operand range (|a| > 65504)");
         return fail(PBMOE_ERR_DEVICE, "device status 0x%x", st);
     }
     return ok();
@@ -908,17 +913,106 @@ PBMOE_API int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x,
                         hidden_out, next_normed_out, pbmoe::DECODE_FULL_LAYER);
 }
 
+static size_t align256(size_t v)
+{
+    return (v + 255) & ~(size_t)255;
+}
+
+// Layer-major prefill (qwen_layer_major_experts, runtime/mod.rs:1151-1161;
+// metal/mod.rs:3583-4106).  Up to 16 tokens run through the decode kernels
+// (the same arithmetic as pbmoe_moe_decode); larger chunks run the grouped
+// GEMM on the matrix cores.
 PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
                                 const float* residual, uint32_t tokens, const uint32_t* ids,
                                 const float* weights, const float* next_norm_weight,
                                 float* hidden_out, float* next_normed_out)
 {
-    if (tokens > MAX_DECODE_TOKENS)
+    if (tokens <= MAX_DECODE_TOKENS)
+        return expert_phase(ctx, layer, x, residual, tokens, const_cast<uint32_t*>(ids),
+                            const_cast<float*>(weights), next_norm_weight, hidden_out,
+                            next_normed_out, pbmoe::DECODE_EXPERTS);
+    if (!ctx || !x || !residual || !hidden_out || !ids || !weights)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if ((next_norm_weight == nullptr) != (next_normed_out == nullptr))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT,
+                    "next_norm_weight and next_normed_out must be given together");
+    if (tokens > MAX_PREFILL_TOKENS)
+        return fail(PBMOE_ERR_UNSUPPORTED, "prefill chunk of %u tokens exceeds %u", tokens,
+                    MAX_PREFILL_TOKENS);
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    const pbmoe_layer_desc& d = b->desc;
+    if (d.shared_intermediate && !b->has_shared)
+        return fail(PBMOE_ERR_NOT_BOUND, "layer %u declares a shared expert that is not bound",
+                    layer);
+    if (b->has_shared && b->shared_layout.group_size != b->layout.group_size)
         return fail(PBMOE_ERR_UNSUPPORTED,
-                    "grouped prefill GEMM path for %u tokens is not built yet", tokens);
-    return expert_phase(ctx, layer, x, residual, tokens, const_cast<uint32_t*>(ids),
-                        const_cast<float*>(weights), next_norm_weight, hidden_out, next_normed_out,
-                        pbmoe::DECODE_EXPERTS);
+                    "prefill needs the shared expert in the routed experts' group size");
+    if (b->has_shared && b->shared_layout.scale_bias_dtype != b->layout.scale_bias_dtype)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "prefill needs the shared expert in the routed experts' scale/bias dtype");
+    for (const void* p : {(const void*)x, (const void*)residual, (const void*)hidden_out,
+                          (const void*)next_norm_weight, (const void*)next_normed_out})
+        if (p && !aligned(p, 16))
+            return fail(PBMOE_ERR_ALIGNMENT, "activation buffers must be 16-byte aligned");
+    if ((rc = set_device(ctx)))
+        return rc;
+    const uint32_t K = d.active_experts, H = d.hidden, I = d.intermediate;
+    const size_t T = tokens, routes = T * K, rows = routes + T;
+    pbmoe::Plan plan{};
+    if ((rc = plan_buffers(ctx, d.experts, (uint32_t)routes, &plan)))
+        return rc;
+    const uint32_t max_tiles = pbmoe::prefill_max_tiles(tokens, K, d.experts, b->has_shared);
+    // scratch layout, each part 256-byte aligned
+    size_t off[12], total = 0;
+    const size_t part[12] = {
+        (size_t)max_tiles * 8, 4,      T * H * 2, T * H * 2, T * (H / 32) * 4, T * 4, T * 4,
+        rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, 0};
+    for (int i = 0; i < 12; ++i) {
+        off[i] = total;
+        total += align256(part[i]);
+    }
+    if ((rc = ensure(ctx, ctx->prefill, total)))
+        return rc;
+    uint8_t* base = static_cast<uint8_t*>(ctx->prefill.ptr);
+    pbmoe::ExpertSet sh;
+    pbmoe::PrefillArgs a{};
+    a.ex = make_set(b->slots, b->layout, d.experts, H, I);
+    a.shared = nullptr;
+    if (b->has_shared) {
+        sh = make_set(b->shared_slot, b->shared_layout, 1, H, d.shared_intermediate);
+        a.shared = &sh;
+    }
+    a.sgate_w = b->has_shared ? b->shared_gate : nullptr;
+    a.sgate_dtype = b->shared_gate_dtype;
+    a.ids = ids;
+    a.weights = weights;
+    a.x = x;
+    a.residual = residual;
+    a.tokens = tokens;
+    a.k = K;
+    a.hidden = H;
+    a.hidden_out = hidden_out;
+    a.next_norm_w = next_norm_weight;
+    a.eps = d.norm_epsilon > 0.0f ? d.norm_epsilon : 1e-6f;
+    a.next_normed = next_normed_out;
+    a.plan = plan;
+    a.tiles = reinterpret_cast<uint32_t*>(base + off[0]);
+    a.tile_count = reinterpret_cast<uint32_t*>(base + off[1]);
+    a.x_hi = reinterpret_cast<uint16_t*>(base + off[2]);
+    a.x_lo = reinterpret_cast<uint16_t*>(base + off[3]);
+    a.x_sum32 = reinterpret_cast<float*>(base + off[4]);
+    a.rowscale = reinterpret_cast<float*>(base + off[5]);
+    a.shared_logit = reinterpret_cast<float*>(base + off[6]);
+    a.act_hi = reinterpret_cast<uint16_t*>(base + off[7]);
+    a.act_lo = reinterpret_cast<uint16_t*>(base + off[8]);
+    a.act_sum32 = reinterpret_cast<float*>(base + off[9]);
+    a.y = reinterpret_cast<float*>(base + off[10]);
+    a.status = ctx->status;
+    HIP_TRY(pbmoe::launch_prefill(ctx->stream, a));
+    return ok();
 }
 
 PBMOE_API int pbmoe_dispatch_plan(pbmoe_ctx* ctx, uint32_t experts, uint32_t active_experts,

@@ -14,7 +14,8 @@ enum : uint32_t {
     ST_NONFINITE = 1u << 1,    // non-finite router logit
     ST_BAD_SUM = 1u << 2,      // renormalisation sum not positive/finite
     ST_NEGATIVE = 1u << 3,     // negative selected probability
-    ST_PLAN_OVERFLOW = 1u << 4 // more routes than the plan buffers hold
+    ST_PLAN_OVERFLOW = 1u << 4, // more routes than the plan buffers hold
+    ST_F16_RANGE = 1u << 5      // prefill activation outside the f16 operand range
 };
 
 // One projection inside a fixed expert slot.
@@ -90,6 +91,40 @@ struct DecodeArgs {
 };
 
 hipError_t launch_decode_layer(hipStream_t s, const DecodeArgs& d, uint32_t mode);
+// Prefill path (grouped GEMM on the matrix cores, any token count).
+struct PrefillArgs {
+    ExpertSet ex;              // routed experts
+    const ExpertSet* shared;   // host pointer, null without a shared expert
+    const void* sgate_w;       // shared gate row [H], null: sigma(80) = 1
+    uint32_t sgate_dtype;
+    const uint32_t* ids;       // [T][K]
+    const float* weights;      // [T][K]
+    const float* x;            // [T][H]
+    const float* residual;     // [T][H]
+    uint32_t tokens, k, hidden;
+    float* hidden_out;         // [T][H]
+    const float* next_norm_w;  // [H] or null
+    float eps;
+    float* next_normed;        // [T][H] or null
+    Plan plan;                 // [routes] plan scratch
+    // scratch (sizes from prefill_scratch_bytes)
+    uint32_t* tiles;           // [max_tiles][2]
+    uint32_t* tile_count;      // [1]
+    uint16_t* x_hi;            // [T][H] f16
+    uint16_t* x_lo;            // [T][H] f16
+    float* x_sum32;            // [T][H/32]
+    float* rowscale;           // [T]
+    float* shared_logit;       // [T]
+    uint16_t* act_hi;          // [T*K + T][I] f16
+    uint16_t* act_lo;          // [T*K + T][I] f16
+    float* act_sum32;          // [T*K + T][I/32]
+    float* y;                  // [T*K + T][H]
+    uint32_t* status;
+};
+
+uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared);
+hipError_t launch_prefill(hipStream_t s, const PrefillArgs& p);
+
 hipError_t launch_q4_dequantize(hipStream_t s, const uint8_t* packed, const void* scales,
                                 const void* biases, uint32_t sb_dtype, uint32_t rows,
                                 uint32_t cols, uint32_t group, float* out);

@@ -1,0 +1,704 @@
+// Layer-major prefill of the MoE block on gfx950: a grouped Q4 GEMM on the
+// matrix cores (v_mfma_f32_16x16x32_f16).  It replaces the reference's
+// per-expert batched matvecs for many-token chunks
+// (q4_mmap_fma_matvec_batch_*, metal/qwen/shaders.metal:973-1057, driven by
+// qwen_layer_major_experts, metal/mod.rs:3583-4106).
+//
+// Arithmetic.  The 4-bit codes q in [0, 15] enter the MFMA as exact f16
+// values (0x6400 | q is the f16 number 1024 + q; subtracting 1024 is exact),
+// and each 32-wide K-step of an MFMA lies inside one quantisation group.  A
+// group's partial product P = sum(q * x) is therefore formed in f32 and the
+// group scale and bias are applied outside the MFMA:
+//     row . x = sum_g  s_g * P_g + b_g * sum_{c in g} x_c
+// which is the factored form of fma(q, s, b) . x.  Activations enter as two
+// f16 parts, x = hi + lo (about 22 significant bits), so a product keeps
+// f32-level accuracy; token rows of x are first scaled by a power of two so
+// that hi stays inside the f16 range.  Rounding activations to one f16 (or
+// the weights to bf16) would put errors of several 1e-2 on layer outputs
+// whose magnitude is in the tens to hundreds.
+//
+// K order.  Inside every 8-column block the operands are stored in the
+// order (c0 c4 c1 c5 c2 c6 c3 c7): the nibble unpack then yields f16 pairs
+// without any shuffling.  Activation buffers written here use that order.
+//
+// Kernels (one layer, T tokens, K routes per token, U used experts):
+//   tile_table: per used expert ceil(count / 64) tiles (+ shared expert)
+//   split:      x [T][H] f32 -> hi, lo f16 (K order above), sums per 32
+//               columns, row scale
+//   gemm<gate/up>: per (tile, 128-row block of I): gate and up, SiLU(g)*u,
+//               act hi/lo f16 (K order) + sums per 32 rows
+//   gemm<down>: per (tile, 128-row block of H): y [route][H] f32
+//   combine:    h = (r + sum_k w_k y_k) + sw * S in route order, optional
+//               next-layer RMSNorm
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "pbmoe_device.h"
+#include "pbmoe_internal.h"
+
+namespace pbmoe {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int TOK = 64;              // tokens per tile (4 MFMA fragments of 16)
+constexpr int WG_ROWS = 128;         // weight rows per GEMM workgroup (4 waves x 32)
+constexpr float F16_SAFE = 16384.0f; // |hi| bound after the row scale
+
+// position of column c (0..7) inside an 8-column block in the K order
+__device__ __forceinline__ uint32_t kpos(uint32_t c) { return c < 4 ? 2 * c : 2 * (c - 4) + 1; }
+
+// 8 nibbles of one word as exact f16 codes, in K order
+__device__ __forceinline__ half8_t unpack8(uint32_t w)
+{
+    uint32_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        v[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+    half8_t r = __builtin_bit_cast(half8_t, v);
+    return r - (_Float16)1024.0f;
+}
+
+// ---------------------------------------------------------------------------
+// tile table: for every used expert ceil(count / 64) tiles (item, start);
+// the shared expert, when present, is item U with all T tokens.  One wave:
+// a scan of per-item tile counts, then each lane writes its item's tiles.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void tile_table_kernel(const uint32_t* __restrict__ unique_count,
+                                                       const uint32_t* __restrict__ groups,
+                                                       uint32_t has_shared, uint32_t tokens,
+                                                       uint32_t* __restrict__ tiles,
+                                                       uint32_t* __restrict__ tile_count)
+{
+    const uint32_t lane = threadIdx.x;
+    const uint32_t U = unique_count[0];
+    const uint32_t items = U + has_shared;
+    uint32_t base = 0;
+    for (uint32_t u0 = 0; u0 < items; u0 += 64) {
+        const uint32_t u = u0 + lane;
+        uint32_t cnt = 0;
+        if (u < U)
+            cnt = groups[2 * u + 1];
+        else if (u < items)
+            cnt = tokens;
+        const uint32_t nt = (cnt + TOK - 1) / TOK;
+        uint32_t inc = nt; // inclusive scan over the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t v = __shfl_up(inc, o);
+            if ((int)lane >= o)
+                inc += v;
+        }
+        const uint32_t first = base + inc - nt;
+        for (uint32_t j = 0; j < nt; ++j) {
+            tiles[2 * (first + j)] = u;
+            tiles[2 * (first + j) + 1] = j * TOK;
+        }
+        base += __shfl(inc, 63);
+    }
+    if (lane == 0)
+        tile_count[0] = base;
+}
+
+// ---------------------------------------------------------------------------
+// split: one workgroup per token row.  hi/lo f16 of x * 2^-e in K order,
+// sums of x * 2^-e per 32 columns, rowscale = 2^e (e > 0 only for rows
+// whose magnitude would leave the f16 range).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, uint32_t cols,
+                                                         uint16_t* __restrict__ hi,
+                                                         uint16_t* __restrict__ lo,
+                                                         float* __restrict__ sum32,
+                                                         float* __restrict__ rowscale)
+{
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const float* xr = x + (uint64_t)t * cols;
+    float amax = 0.0f;
+    for (uint32_t c = threadIdx.x; c < cols; c += 256)
+        amax = fmaxf(amax, fabsf(xr[c]));
+    amax = wave_max(amax);
+    if (lane == 0)
+        red[wv] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (amax > F16_SAFE)
+        (void)frexpf(amax / F16_SAFE, &e); // amax * 2^-e <= F16_SAFE
+    const float f = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0)
+        rowscale[t] = ldexpf(1.0f, e);
+    // each wave handles 64-column groups; lane = column within the group
+    for (uint32_t g = wv; g < cols / 64; g += 4) {
+        const uint32_t c = g * 64 + lane;
+        const float v = xr[c] * f;
+        const _Float16 h = (_Float16)v;
+        const _Float16 l = (_Float16)(v - (float)h);
+        const uint64_t o = (uint64_t)t * cols + (c & ~7u) + kpos(c & 7u);
+        hi[o] = __builtin_bit_cast(uint16_t, h);
+        lo[o] = __builtin_bit_cast(uint16_t, l);
+        float s = v; // sums per 32 columns: lanes 0..31 and 32..63
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        s += __shfl_xor(s, 8);
+        s += __shfl_xor(s, 16);
+        if ((lane & 31) == 0)
+            sum32[(uint64_t)t * (cols / 32) + g * 2 + (lane >> 5)] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grouped GEMM
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+    ExpertSet ex, sh;
+    uint32_t has_shared;
+    const uint32_t* unique_ids;
+    const uint32_t* unique_count;
+    const uint32_t* groups;   // [items][2] (start, count) in grouped order
+    const uint32_t* src_rows; // grouped route -> token
+    const uint32_t* tiles;    // [n][2] (item, first token of the item)
+    const uint32_t* tile_count;
+    uint32_t routes;          // T*K: grouped rows of the routed experts
+    uint32_t tokens;
+    // B operand rows (hi/lo f16 in K order + sums per 32 columns)
+    const uint16_t* b_hi;
+    const uint16_t* b_lo;
+    const float* b_sum32;
+    const float* rowscale;    // gate/up: per token; down: unused
+    uint32_t kdim;            // H (gate/up) or I (down)
+    // outputs
+    uint16_t* act_hi;         // [routes + T][I]
+    uint16_t* act_lo;
+    float* act_sum32;         // [routes + T][I/32]
+    float* y;                 // [routes + T][H]
+    uint32_t* status;
+};
+
+// LDS plan of one GEMM workgroup.  Staging: two buffers of the activation
+// tile of one quantisation group, [TOK tokens][hi 32KS | lo 32KS | pad 8]
+// halfs (the pad spreads the 16 token rows a fragment read touches over
+// distinct banks).  Epilogues reuse the same bytes for the output tile.
+template <int KS>
+struct GemmLds {
+    static constexpr int XPITCH = 64 * KS + 8;             // halfs per token row
+    static constexpr int STAGE_HALFS = TOK * XPITCH;       // one buffer
+    static constexpr int ACT_PITCH = 2 * WG_ROWS + 8;      // halfs: hi | lo | pad
+    static constexpr int Y_PITCH = WG_ROWS + 4;            // floats
+    static constexpr int STAGE_BYTES = 2 * STAGE_HALFS * 2;
+    static constexpr int ACT_BYTES = TOK * ACT_PITCH * 2;
+    static constexpr int Y_BYTES = TOK * Y_PITCH * 4;
+    static constexpr int EPI_BYTES = ACT_BYTES > Y_BYTES ? ACT_BYTES : Y_BYTES;
+    static constexpr int BYTES = STAGE_BYTES > EPI_BYTES ? STAGE_BYTES : EPI_BYTES;
+};
+
+template <int N>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&w)[N])
+{
+    if constexpr (N == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+    } else if constexpr (N == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        w[0] = v.x, w[1] = v.y;
+    } else {
+        w[0] = p[0];
+    }
+}
+
+// One workgroup: TOK tokens of one item x WG_ROWS weight rows.  The
+// activation tile is the MFMA A operand (16 tokens x 32 K per fragment),
+// the weights the B operand (32 K x 16 rows); wave w owns rows
+// 32w .. 32w+31 of the block (two 16-row fragments) and all 4 token
+// fragments.  Lane (i16 = lane & 15, kb = lane >> 4) supplies the KS words
+// of K columns [g*32KS + 8KS*kb, +8KS) of its row: the 4 kb lanes of one
+// K-step (columns 8s + j of each lane's run) stay inside quantisation group
+// g.  The accumulator element (token 4kb + r of the fragment, row i16) gets
+// s[row][g] * P + b[row][g] * sum_g(x) after each group.
+//
+// Work mapping: the flat list (row block major, tile minor) is cut into 8
+// contiguous ranges, one per XCD (workgroup ids are dealt to the XCDs
+// round-robin), so workgroups that share an expert's row block run on one
+// XCD and share its L2.
+template <int SBT, bool GATEUP, int KS>
+__global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
+{
+    using L = GemmLds<KS>;
+    constexpr int NMAT = GATEUP ? 2 : 1;
+    __shared__ __align__(16) uint8_t lds[L::BYTES];
+    __shared__ __align__(16) float xs_lds[2][TOK];
+    __shared__ float rs_lds[TOK];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+
+    // ---- work item ----
+    const uint32_t ntiles = a.tile_count[0];
+    const uint32_t rows_total = GATEUP ? a.ex.gate.rows : a.ex.down.rows;
+    const uint32_t RB = rows_total / WG_ROWS;
+    const uint32_t total = ntiles * RB;
+    const uint32_t chunk = (total + 7) / 8;
+    const uint32_t j = blockIdx.x >> 3, xcd = blockIdx.x & 7;
+    if (j >= chunk)
+        return;
+    const uint32_t widx = xcd * chunk + j;
+    if (widx >= total)
+        return;
+    const uint32_t rb = widx / ntiles, tile = widx % ntiles;
+    const uint32_t item = a.tiles[2 * tile], n0 = a.tiles[2 * tile + 1];
+    const bool shared = a.has_shared && item == a.unique_count[0];
+    uint32_t g0, cnt;
+    const uint8_t* slot;
+    if (shared) {
+        g0 = a.routes;
+        cnt = a.tokens;
+        slot = a.sh.base;
+    } else {
+        const uint32_t e = a.unique_ids[item];
+        g0 = a.groups[2 * item];
+        cnt = a.groups[2 * item + 1];
+        if (e >= a.ex.count) {
+            if (tid == 0)
+                atomicOr(a.status, ST_ROUTE_RANGE);
+            return;
+        }
+        slot = a.ex.base + (uint64_t)e * a.ex.stride;
+    }
+    const ExpertSet& set = shared ? a.sh : a.ex;
+    const Q4Proj p0 = GATEUP ? set.gate : set.down;
+    const Q4Proj p1 = set.up;
+    const uint32_t K = a.kdim;
+    const uint32_t G = K / (32 * KS), C32 = K / 32, WPR = K / 8;
+
+    // ---- staging role: thread -> (token, quarter of the group's columns) ----
+    const uint32_t s_tok = tid >> 2, s_part = tid & 3;
+    const uint32_t s_n = n0 + s_tok;
+    const bool s_valid = s_n < cnt;
+    uint32_t s_row = 0;
+    if (s_valid)
+        s_row = GATEUP ? (shared ? s_n : a.src_rows[g0 + s_n]) : g0 + s_n;
+    const uint16_t* s_hi = a.b_hi + (uint64_t)s_row * K + s_part * 8 * KS;
+    const uint16_t* s_lo = a.b_lo + (uint64_t)s_row * K + s_part * 8 * KS;
+    const float* s_sum = a.b_sum32 + (uint64_t)s_row * C32;
+    if (GATEUP && s_part == 0)
+        rs_lds[s_tok] = s_valid ? a.rowscale[s_row] : 1.0f;
+    uint4 st_hi[KS], st_lo[KS];
+    float st_sum = 0.0f;
+    auto stage_load = [&](uint32_t g) {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            if (s_valid) {
+                st_hi[k] = reinterpret_cast<const uint4*>(s_hi + g * 32 * KS)[k];
+                st_lo[k] = reinterpret_cast<const uint4*>(s_lo + g * 32 * KS)[k];
+            } else {
+                st_hi[k] = make_uint4(0, 0, 0, 0);
+                st_lo[k] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        if (s_part == 0) {
+            float s = 0.0f;
+            if (s_valid) {
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                    s += s_sum[g * KS + k];
+            }
+            st_sum = s;
+        }
+    };
+    auto stage_store = [&](int buf) {
+        uint16_t* row = reinterpret_cast<uint16_t*>(lds) + buf * L::STAGE_HALFS + s_tok * L::XPITCH;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            reinterpret_cast<uint4*>(row + s_part * 8 * KS)[k] = st_hi[k];
+            reinterpret_cast<uint4*>(row + 32 * KS + s_part * 8 * KS)[k] = st_lo[k];
+        }
+        if (s_part == 0)
+            xs_lds[buf][s_tok] = st_sum;
+    };
+
+    // ---- compute role ----
+    const uint32_t i16 = lane & 15, kb = lane >> 4;
+    const uint32_t row_base = rb * WG_ROWS + wv * 32;
+    const uint32_t* wp[2][NMAT];
+    const uint8_t* sbase[2][NMAT];
+    const uint8_t* bbase[2][NMAT];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const uint32_t row = row_base + 16 * rt + i16;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const Q4Proj& p = m == 0 ? p0 : p1;
+            wp[rt][m] = reinterpret_cast<const uint32_t*>(slot + p.w_off) + (uint64_t)row * WPR + KS * kb;
+            sbase[rt][m] = slot + p.s_off + (uint64_t)row * G * 2;
+            bbase[rt][m] = slot + p.b_off + (uint64_t)row * G * 2;
+        }
+    }
+    uint32_t wcur[2][NMAT][KS], wnext[2][NMAT][KS];
+    float sc[2][NMAT], bi[2][NMAT], sc_n[2][NMAT], bi_n[2][NMAT];
+    auto w_load = [&](uint32_t g, uint32_t (&w)[2][NMAT][KS], float (&s)[2][NMAT], float (&b)[2][NMAT]) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                load_words<KS>(wp[rt][m] + g * 4 * KS, w[rt][m]);
+                s[rt][m] = sb_at<SBT>(sbase[rt][m], g);
+                b[rt][m] = sb_at<SBT>(bbase[rt][m], g);
+            }
+    };
+
+    float4_t acc[2][NMAT][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc[rt][m][st] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    stage_load(0);
+    w_load(0, wcur, sc, bi);
+    stage_store(0);
+    __syncthreads();
+
+    for (uint32_t g = 0; g < G; ++g) {
+        const int buf = g & 1;
+        const bool more = g + 1 < G;
+        if (more) {
+            stage_load(g + 1);
+            w_load(g + 1, wnext, sc_n, bi_n);
+        }
+        half8_t wf[2][NMAT][KS];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                    wf[rt][m][k] = unpack8(wcur[rt][m][k]);
+        const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + buf * L::STAGE_HALFS;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const uint16_t* xr = xb + (16 * st + i16) * L::XPITCH + 8 * KS * kb;
+            half8_t ah[KS], al[KS];
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                ah[k] = *reinterpret_cast<const half8_t*>(xr + 8 * k);
+                al[k] = *reinterpret_cast<const half8_t*>(xr + 32 * KS + 8 * k);
+            }
+            const float4 xs4 = *reinterpret_cast<const float4*>(&xs_lds[buf][16 * st + 4 * kb]);
+            const float xsv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    float4_t p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int k = 0; k < KS; ++k) {
+                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[k], wf[rt][m][k], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[k], wf[rt][m][k], p, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[rt][m][st][r] =
+                            fmaf(sc[rt][m], p[r], fmaf(bi[rt][m], xsv[r], acc[rt][m][st][r]));
+                }
+        }
+        if (more)
+            stage_store(buf ^ 1);
+        __syncthreads();
+        if (more) {
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+#pragma unroll
+                    for (int k = 0; k < KS; ++k)
+                        wcur[rt][m][k] = wnext[rt][m][k];
+                    sc[rt][m] = sc_n[rt][m];
+                    bi[rt][m] = bi_n[rt][m];
+                }
+        }
+    }
+
+    // ---- epilogue: accumulator element (token 16st + 4kb + r, row
+    //      row_base + 16rt + i16); the output tile goes through LDS so that
+    //      global stores are whole rows ----
+    const uint32_t tok_c = s_tok, part_c = s_part; // copy-out role = staging role
+    if constexpr (GATEUP) {
+        const uint32_t I = rows_total;
+        uint16_t* at = reinterpret_cast<uint16_t*>(lds);
+        bool overflow = false;
+        float csum[4][4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tk = 16 * st + 4 * kb + r;
+                const float rs = rs_lds[tk];
+                float s = 0.0f;
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const float gg = acc[rt][0][st][r] * rs, uu = acc[rt][1][st][r] * rs;
+                    const float v = (gg / (1.0f + expf(-gg))) * uu;
+                    s += v;
+                    const uint32_t il = 32 * wv + 16 * rt + i16;
+                    const uint32_t pos = (il & ~7u) + kpos(il & 7u);
+                    overflow |= !(fabsf(v) <= 65504.0f);
+                    const _Float16 h = (_Float16)v;
+                    const _Float16 l = (_Float16)(v - (float)h);
+                    at[tk * L::ACT_PITCH + pos] = __builtin_bit_cast(uint16_t, h);
+                    at[tk * L::ACT_PITCH + WG_ROWS + pos] = __builtin_bit_cast(uint16_t, l);
+                }
+                csum[st][r] = s;
+            }
+        // sums over the wave's 32 rows (one 32-row chunk of I): the 16 i16
+        // lanes hold 16 rows each for rt = 0, 1
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = csum[st][r];
+                v += __shfl_xor(v, 1);
+                v += __shfl_xor(v, 2);
+                v += __shfl_xor(v, 4);
+                v += __shfl_xor(v, 8);
+                const uint32_t n = n0 + 16 * st + 4 * kb + r;
+                if (i16 == 0 && n < cnt)
+                    a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + (row_base >> 5)] = v;
+            }
+        if (__ballot(overflow) != 0ull && lane == 0)
+            atomicOr(a.status, ST_F16_RANGE);
+        __syncthreads();
+        const uint32_t n = n0 + tok_c;
+        if (n < cnt) {
+            const uint16_t* src = at + tok_c * L::ACT_PITCH + part_c * 32;
+            uint16_t* dh = a.act_hi + (uint64_t)(g0 + n) * I + rb * WG_ROWS + part_c * 32;
+            uint16_t* dl = a.act_lo + (uint64_t)(g0 + n) * I + rb * WG_ROWS + part_c * 32;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                reinterpret_cast<uint4*>(dh)[k] = reinterpret_cast<const uint4*>(src)[k];
+                reinterpret_cast<uint4*>(dl)[k] = reinterpret_cast<const uint4*>(src + WG_ROWS)[k];
+            }
+        }
+    } else {
+        const uint32_t H = rows_total;
+        float* yt = reinterpret_cast<float*>(lds);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    yt[(16 * st + 4 * kb + r) * L::Y_PITCH + 32 * wv + 16 * rt + i16] = acc[rt][0][st][r];
+        __syncthreads();
+        const uint32_t n = n0 + tok_c;
+        if (n < cnt) {
+            const float* src = yt + tok_c * L::Y_PITCH + part_c * 32;
+            float* dst = a.y + (uint64_t)(g0 + n) * H + rb * WG_ROWS + part_c * 32;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                reinterpret_cast<float4*>(dst)[k] = reinterpret_cast<const float4*>(src)[k];
+        }
+    }
+}
+
+// shared-expert gate logit per token: one wave per token, f32 accumulation
+template <int WDT>
+__global__ __launch_bounds__(256) void gate_row_kernel(const void* __restrict__ w, const float* __restrict__ x,
+                                                      uint32_t tokens, uint32_t hidden, float* __restrict__ out)
+{
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= tokens)
+        return;
+    const float* xr = x + (uint64_t)t * hidden;
+    float acc = 0.0f;
+    for (uint32_t c = lane; c < hidden; c += 64) {
+        float wv;
+        if constexpr (WDT == 0)
+            wv = reinterpret_cast<const float*>(w)[c];
+        else
+            wv = sb_at<WDT>(reinterpret_cast<const uint8_t*>(w), c);
+        acc = fmaf(wv, xr[c], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0)
+        out[t] = acc;
+}
+
+// h[t][c] = (r + sum_k w[t,k] y[out_idx[t,k]][c]) + sw_t * S[t][c], then
+// the optional next-layer RMSNorm.  One workgroup per token.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(
+    const float* __restrict__ y, const float* __restrict__ ysh, const float* __restrict__ shared_logit,
+    uint32_t has_shared, const uint32_t* __restrict__ out_idx, const float* __restrict__ weights,
+    const float* __restrict__ residual, uint32_t k, uint32_t hidden, float* __restrict__ out,
+    const float* __restrict__ norm_w, float eps, float* __restrict__ normed)
+{
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    float sw = 0.0f;
+    if (has_shared)
+        sw = sigmoidf_(shared_logit ? shared_logit[t] : 80.0f);
+    float ss = 0.0f;
+    for (uint32_t c = threadIdx.x * 4; c < hidden; c += 1024) {
+        float4 moe = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t kk = 0; kk < k; ++kk) {
+            const uint32_t route = t * k + kk;
+            const uint32_t gi = out_idx[route];
+            if (gi == 0xFFFFFFFFu)
+                continue;
+            const float w = weights[route];
+            const float4 v = *reinterpret_cast<const float4*>(y + (uint64_t)gi * hidden + c);
+            moe.x = moe.x + w * v.x;
+            moe.y = moe.y + w * v.y;
+            moe.z = moe.z + w * v.z;
+            moe.w = moe.w + w * v.w;
+        }
+        const uint64_t o = (uint64_t)t * hidden + c;
+        const float4 r = *reinterpret_cast<const float4*>(residual + o);
+        float4 h = make_float4(r.x + moe.x, r.y + moe.y, r.z + moe.z, r.w + moe.w);
+        if (has_shared) {
+            const float4 s = *reinterpret_cast<const float4*>(ysh + o);
+            h.x = h.x + sw * s.x;
+            h.y = h.y + sw * s.y;
+            h.z = h.z + sw * s.z;
+            h.w = h.w + sw * s.w;
+        }
+        *reinterpret_cast<float4*>(out + o) = h;
+        ss += h.x * h.x + h.y * h.y + h.z * h.z + h.w * h.w;
+    }
+    if (!norm_w)
+        return;
+    ss = wave_sum(ss);
+    if (lane == 0)
+        red[wv] = ss;
+    __syncthreads();
+    const float ms = ((red[0] + red[1]) + (red[2] + red[3])) / (float)hidden;
+    const float scale = 1.0f / sqrtf(ms + eps);
+    for (uint32_t c = threadIdx.x * 4; c < hidden; c += 1024) {
+        const uint64_t o = (uint64_t)t * hidden + c;
+        const float4 h = *reinterpret_cast<const float4*>(out + o);
+        const float4 w = *reinterpret_cast<const float4*>(norm_w + c);
+        *reinterpret_cast<float4*>(normed + o) =
+            make_float4(h.x * scale * w.x, h.y * scale * w.y, h.z * scale * w.z, h.w * scale * w.w);
+    }
+}
+
+uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared)
+{
+    const uint32_t routes = tokens * k;
+    return routes / TOK + std::min(experts, routes) +
+           (has_shared ? (tokens + TOK - 1) / TOK : 0u) + 1;
+}
+
+// 8 x ceil(work / 8) workgroups for the XCD-split work list (see the kernel)
+static dim3 gemm_grid(uint32_t max_tiles, uint32_t rows)
+{
+    const uint64_t work = (uint64_t)max_tiles * (rows / WG_ROWS);
+    return dim3((uint32_t)(8 * ((work + 7) / 8)));
+}
+
+template <int SBT, int KS>
+static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
+{
+    const ExpertSet& ex = p.ex;
+    const uint32_t T = p.tokens, K = p.k, H = p.hidden, I = ex.gate.rows;
+    const uint32_t routes = T * K;
+    const uint32_t has_shared = p.shared ? 1u : 0u;
+    hipError_t err = launch_dispatch_plan(st, p.ids, routes, ex.count, K, p.plan, p.status);
+    if (err != hipSuccess)
+        return err;
+    tile_table_kernel<<<1, 64, 0, st>>>(p.plan.unique_count, p.plan.groups, has_shared, T, p.tiles,
+                                        p.tile_count);
+    if ((err = hipGetLastError()) != hipSuccess)
+        return err;
+    split_rows_kernel<<<T, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale);
+    if ((err = hipGetLastError()) != hipSuccess)
+        return err;
+    if (has_shared && p.sgate_w) {
+        const dim3 gg((T + 3) / 4);
+        if (p.sgate_dtype == 0)
+            gate_row_kernel<0><<<gg, 256, 0, st>>>(p.sgate_w, p.x, T, H, p.shared_logit);
+        else if (p.sgate_dtype == 2)
+            gate_row_kernel<2><<<gg, 256, 0, st>>>(p.sgate_w, p.x, T, H, p.shared_logit);
+        else
+            gate_row_kernel<1><<<gg, 256, 0, st>>>(p.sgate_w, p.x, T, H, p.shared_logit);
+        if ((err = hipGetLastError()) != hipSuccess)
+            return err;
+    }
+    GemmArgs a{};
+    a.ex = ex;
+    a.has_shared = has_shared;
+    if (has_shared)
+        a.sh = *p.shared;
+    a.unique_ids = p.plan.unique_ids;
+    a.unique_count = p.plan.unique_count;
+    a.groups = p.plan.groups;
+    a.src_rows = p.plan.src_rows;
+    a.tiles = p.tiles;
+    a.tile_count = p.tile_count;
+    a.routes = routes;
+    a.tokens = T;
+    a.status = p.status;
+    const uint32_t max_tiles = prefill_max_tiles(T, K, ex.count, has_shared != 0);
+    a.b_hi = p.x_hi;
+    a.b_lo = p.x_lo;
+    a.b_sum32 = p.x_sum32;
+    a.rowscale = p.rowscale;
+    a.kdim = H;
+    a.act_hi = p.act_hi;
+    a.act_lo = p.act_lo;
+    a.act_sum32 = p.act_sum32;
+    q4_group_gemm_kernel<SBT, true, KS><<<gemm_grid(max_tiles, I), 256, 0, st>>>(a);
+    if ((err = hipGetLastError()) != hipSuccess)
+        return err;
+    a.b_hi = p.act_hi;
+    a.b_lo = p.act_lo;
+    a.b_sum32 = p.act_sum32;
+    a.rowscale = nullptr;
+    a.kdim = I;
+    a.y = p.y;
+    q4_group_gemm_kernel<SBT, false, KS><<<gemm_grid(max_tiles, H), 256, 0, st>>>(a);
+    if ((err = hipGetLastError()) != hipSuccess)
+        return err;
+    prefill_combine_kernel<<<T, 256, 0, st>>>(p.y, p.y + (uint64_t)routes * H,
+                                              p.sgate_w ? p.shared_logit : nullptr, has_shared,
+                                              p.plan.out_idx, p.weights, p.residual, K, H,
+                                              p.hidden_out, p.next_norm_w, p.eps, p.next_normed);
+    return hipGetLastError();
+}
+
+template <int SBT>
+static hipError_t launch_prefill_sb(hipStream_t st, const PrefillArgs& p)
+{
+    switch (p.ex.group) {
+    case 32:
+        return launch_prefill_typed<SBT, 1>(st, p);
+    case 64:
+        return launch_prefill_typed<SBT, 2>(st, p);
+    case 128:
+        return launch_prefill_typed<SBT, 4>(st, p);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prefill(hipStream_t st, const PrefillArgs& p)
+{
+    // shapes the kernels assume: 128-row blocks of H and I, group = 2^shift,
+    // a shared expert in the routed experts' format
+    if ((1u << p.ex.group_shift) != p.ex.group || p.hidden % WG_ROWS || p.ex.gate.rows % WG_ROWS ||
+        p.ex.gate.cols != p.hidden || p.ex.down.rows != p.hidden)
+        return hipErrorInvalidValue;
+    if (p.shared && (p.shared->group != p.ex.group || p.shared->sb_dtype != p.ex.sb_dtype ||
+                     p.shared->gate.rows != p.ex.gate.rows || p.shared->down.rows != p.hidden))
+        return hipErrorInvalidValue;
+    if (p.ex.sb_dtype == 2)
+        return launch_prefill_sb<2>(st, p);
+    return launch_prefill_sb<1>(st, p);
+}
+
+} // namespace pbmoe
