@@ -93,6 +93,7 @@ struct pbmoe_ctx {
     DeviceBuf logits, act, act_shared, shared_weight, plan;
     DeviceBuf route_ids, route_w;
     DeviceBuf prefill; // prefill scratch (operand splits, activations, y)
+    DeviceBuf plan_work; // multi-workgroup plan scratch of pbmoe_dispatch_plan
 };
 
 namespace {
@@ -236,7 +237,8 @@ int get_layer(pbmoe_ctx* ctx, uint32_t layer, LayerBinding** out)
 int plan_buffers(pbmoe_ctx* ctx, uint32_t experts, uint32_t routes, pbmoe::Plan* plan)
 {
     size_t words = (size_t)experts * 3 + 1 + (size_t)routes * 3;
-    int rc = ensure(ctx, ctx->plan, words * 4);
+    const size_t work = pbmoe::plan_work_words(routes, experts);
+    int rc = ensure(ctx, ctx->plan, (words + work) * 4);
     if (rc)
         return rc;
     uint32_t* p = static_cast<uint32_t*>(ctx->plan.ptr);
@@ -246,6 +248,7 @@ int plan_buffers(pbmoe_ctx* ctx, uint32_t experts, uint32_t routes, pbmoe::Plan*
     plan->route_slots = p + experts * 3 + 1;
     plan->src_rows = plan->route_slots + routes;
     plan->out_idx = plan->src_rows + routes;
+    plan->work = plan->out_idx + routes;
     return ok();
 }
 
@@ -420,7 +423,8 @@ PBMOE_API int pbmoe_ctx_destroy(pbmoe_ctx* ctx)
         free_buf(kv.second.gate_owned);
     }
     for (DeviceBuf* b : {&ctx->logits, &ctx->act, &ctx->act_shared, &ctx->shared_weight,
-                         &ctx->plan, &ctx->route_ids, &ctx->route_w})
+                         &ctx->plan, &ctx->route_ids, &ctx->route_w, &ctx->prefill,
+                         &ctx->plan_work})
         free_buf(*b);
     (void)hipFree(ctx->status);
     (void)hipStreamDestroy(ctx->stream);
@@ -1039,7 +1043,11 @@ PBMOE_API int pbmoe_dispatch_plan(pbmoe_ctx* ctx, uint32_t experts, uint32_t act
     p.src_rows = grouped_source_rows;
     p.out_idx = grouped_output_indices;
     p.groups = groups;
-    HIP_TRY(pbmoe::launch_dispatch_plan(ctx->stream, ids, tokens * active_experts, experts,
+    const uint32_t routes = tokens * active_experts;
+    if ((rc = ensure(ctx, ctx->plan_work, (size_t)pbmoe::plan_work_words(routes, experts) * 4)))
+        return rc;
+    p.work = static_cast<uint32_t*>(ctx->plan_work.ptr);
+    HIP_TRY(pbmoe::launch_dispatch_plan(ctx->stream, ids, routes, experts,
                                         active_experts, p, ctx->status));
     return ok();
 }

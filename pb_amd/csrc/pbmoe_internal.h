@@ -49,6 +49,7 @@ struct Plan {
     uint32_t* src_rows;    // [routes]
     uint32_t* out_idx;     // [routes]
     uint32_t* groups;      // [experts][2]
+    uint32_t* work;        // multi-workgroup scratch (plan_work_words), or null
 };
 
 hipError_t launch_router_logits(hipStream_t s, const void* w, uint32_t w_dtype, const float* x,
@@ -56,6 +57,8 @@ hipError_t launch_router_logits(hipStream_t s, const void* w, uint32_t w_dtype, 
 hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bias, uint32_t tokens,
                              const RouteParams& p, uint32_t* ids, float* weights,
                              uint32_t* status);
+// words of Plan::work needed for the multi-workgroup plan of `routes`
+uint32_t plan_work_words(uint32_t routes, uint32_t experts);
 hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t routes,
                                 uint32_t experts, uint32_t k, const Plan& plan,
                                 uint32_t* status);

@@ -273,10 +273,171 @@ __global__ __launch_bounds__(PLAN_WAVES * 64) void dispatch_plan_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// multi-workgroup plan for long route lists (prefill): the same stable order
+// as dispatch_plan_kernel.  Routes are cut into blocks of PLAN_CHUNK;
+//   count: per block, per expert route counts;
+//   scan:  per expert the exclusive prefix over blocks, then the sorted union
+//          (unique ids, group starts/counts, slots) over experts;
+//   place: per block the single-workgroup placement with absolute bases.
+// ---------------------------------------------------------------------------
+constexpr uint32_t PLAN_CHUNK = PLAN_WAVES * 256;
+
+__global__ __launch_bounds__(PLAN_WAVES * 64) void plan_count_kernel(
+    const uint32_t* __restrict__ ids, uint32_t routes, uint32_t experts, uint32_t* __restrict__ cnt,
+    uint32_t* __restrict__ status)
+{
+    __shared__ uint32_t c[PLAN_MAX_E];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int nthr = PLAN_WAVES * 64;
+    for (int i = tid; i < PLAN_MAX_E; i += nthr)
+        c[i] = 0;
+    __syncthreads();
+    const uint32_t r0 = blockIdx.x * PLAN_CHUNK;
+    const uint32_t r1 = min(routes, r0 + PLAN_CHUNK);
+    bool bad = false;
+    for (uint32_t r = r0 + tid; r < r1; r += nthr) {
+        const uint32_t e = ids[r];
+        if (e < experts)
+            atomicAdd(&c[e], 1u);
+        else
+            bad = true;
+    }
+    if (__ballot(bad) != 0ull && lane == 0)
+        atomicOr(status, ST_ROUTE_RANGE);
+    __syncthreads();
+    for (uint32_t e = tid; e < experts; e += nthr)
+        cnt[(uint64_t)blockIdx.x * experts + e] = c[e];
+}
+
+__global__ __launch_bounds__(PLAN_MAX_E) void plan_scan_kernel(const uint32_t* __restrict__ cnt,
+                                                              uint32_t nblk, uint32_t experts, Plan plan,
+                                                              uint32_t* __restrict__ base,
+                                                              uint32_t* __restrict__ slot_of)
+{
+    __shared__ uint32_t sa[PLAN_MAX_E], sb[PLAN_MAX_E];
+    const uint32_t e = threadIdx.x;
+    uint32_t run = 0;
+    if (e < experts) {
+        for (uint32_t b = 0; b < nblk; ++b) {
+            const uint32_t v = cnt[(uint64_t)b * experts + e];
+            base[(uint64_t)b * experts + e] = run;
+            run += v;
+        }
+    }
+    sa[e] = run;
+    sb[e] = run > 0 ? 1u : 0u;
+    __syncthreads();
+    for (uint32_t off = 1; off < PLAN_MAX_E; off <<= 1) {
+        const uint32_t va = sa[e] + (e >= off ? sa[e - off] : 0u);
+        const uint32_t vb = sb[e] + (e >= off ? sb[e - off] : 0u);
+        __syncthreads();
+        sa[e] = va;
+        sb[e] = vb;
+        __syncthreads();
+    }
+    const uint32_t start = sa[e] - run;
+    if (e < experts) {
+        uint32_t sl = 0xFFFFFFFFu;
+        if (run > 0) {
+            sl = sb[e] - 1u;
+            plan.unique_ids[sl] = e;
+            plan.groups[2 * sl] = start;
+            plan.groups[2 * sl + 1] = run;
+        }
+        slot_of[e] = sl;
+        for (uint32_t b = 0; b < nblk; ++b)
+            base[(uint64_t)b * experts + e] += start;
+    }
+    if (e == 0)
+        plan.unique_count[0] = sb[PLAN_MAX_E - 1];
+}
+
+__global__ __launch_bounds__(PLAN_WAVES * 64) void plan_place_kernel(
+    const uint32_t* __restrict__ ids, uint32_t routes, uint32_t experts, uint32_t k, Plan plan,
+    const uint32_t* __restrict__ base, const uint32_t* __restrict__ slot_of)
+{
+    __shared__ uint32_t wcnt[PLAN_WAVES][PLAN_MAX_E];
+    __shared__ uint32_t slt[PLAN_MAX_E];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nthr = PLAN_WAVES * 64;
+    for (int i = tid; i < PLAN_WAVES * PLAN_MAX_E; i += nthr)
+        (&wcnt[0][0])[i] = 0;
+    for (uint32_t e = tid; e < experts; e += nthr)
+        slt[e] = slot_of[e];
+    __syncthreads();
+    const uint32_t r_begin = blockIdx.x * PLAN_CHUNK + wv * (PLAN_CHUNK / PLAN_WAVES);
+    const uint32_t r_end = min(routes, r_begin + PLAN_CHUNK / PLAN_WAVES);
+    for (uint32_t r = r_begin + lane; r < r_end; r += 64) {
+        const uint32_t e = ids[r];
+        if (e < experts)
+            atomicAdd(&wcnt[wv][e], 1u);
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < experts; e += nthr) {
+        uint32_t run = base[(uint64_t)blockIdx.x * experts + e];
+        for (int w = 0; w < PLAN_WAVES; ++w) {
+            const uint32_t c = wcnt[w][e];
+            wcnt[w][e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (uint32_t r0 = r_begin; r0 < r_end; r0 += 64) {
+        const uint32_t r = r0 + lane;
+        const bool valid = r < r_end;
+        const uint32_t e = valid ? ids[r] : 0xFFFFFFFFu;
+        const bool in_range = valid && e < experts;
+        uint64_t remaining = __ballot(in_range);
+        uint64_t peers = 0;
+        while (remaining) {
+            const int leader = __ffsll((unsigned long long)remaining) - 1;
+            const uint32_t le = __shfl(e, leader);
+            const uint64_t m = __ballot(in_range && e == le);
+            if (in_range && e == le)
+                peers = m;
+            remaining &= ~m;
+        }
+        if (in_range) {
+            const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+            const uint32_t pos = wcnt[wv][e] + __popcll(peers & below);
+            plan.src_rows[pos] = r / k;
+            plan.out_idx[r] = pos;
+            plan.route_slots[r] = slt[e];
+        } else if (valid) {
+            plan.out_idx[r] = 0xFFFFFFFFu;
+            plan.route_slots[r] = 0xFFFFFFFFu;
+        }
+        if (in_range) {
+            const int top = 63 - __clzll((long long)peers);
+            if (top == lane)
+                wcnt[wv][e] += __popcll(peers);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    }
+}
+
+uint32_t plan_work_words(uint32_t routes, uint32_t experts)
+{
+    const uint32_t nblk = (routes + PLAN_CHUNK - 1) / PLAN_CHUNK;
+    return 2 * nblk * experts + experts;
+}
+
 hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t routes,
                                 uint32_t experts, uint32_t k, const Plan& plan, uint32_t* status)
 {
-    dispatch_plan_kernel<<<1, PLAN_WAVES * 64, 0, s>>>(ids, routes, experts, k, plan, status);
+    if (routes <= PLAN_CHUNK || plan.work == nullptr) {
+        dispatch_plan_kernel<<<1, PLAN_WAVES * 64, 0, s>>>(ids, routes, experts, k, plan, status);
+        return hipGetLastError();
+    }
+    const uint32_t nblk = (routes + PLAN_CHUNK - 1) / PLAN_CHUNK;
+    uint32_t* cnt = plan.work;
+    uint32_t* base = cnt + (uint64_t)nblk * experts;
+    uint32_t* slot_of = base + (uint64_t)nblk * experts;
+    plan_count_kernel<<<nblk, PLAN_WAVES * 64, 0, s>>>(ids, routes, experts, cnt, status);
+    plan_scan_kernel<<<1, PLAN_MAX_E, 0, s>>>(cnt, nblk, experts, plan, base, slot_of);
+    plan_place_kernel<<<nblk, PLAN_WAVES * 64, 0, s>>>(ids, routes, experts, k, plan, base, slot_of);
     return hipGetLastError();
 }
 

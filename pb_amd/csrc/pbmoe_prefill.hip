@@ -50,13 +50,22 @@ constexpr float F16_SAFE = 16384.0f; // |hi| bound after the row scale
 // position of column c (0..7) inside an 8-column block in the K order
 __device__ __forceinline__ uint32_t kpos(uint32_t c) { return c < 4 ? 2 * c : 2 * (c - 4) + 1; }
 
-// 8 nibbles of one word as exact f16 codes, in K order
-__device__ __forceinline__ half8_t unpack8(uint32_t w)
+// (x & mask) | orv in one VALU op (the compiler splits it when both
+// constants would need the scalar constant bus)
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv)
+{
+    return (x & mask) | orv;
+}
+
+// 8 nibbles of one word as exact f16 codes, in K order; `magic` is
+// 0x64006400 (f16 pair 1024, 1024) kept in a vector register
+__device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 {
     uint32_t v[4];
+    v[0] = and_or(w, 0x000F000Fu, magic);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        v[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+    for (int i = 1; i < 4; ++i)
+        v[i] = and_or(w >> (4 * i), 0x000F000Fu, magic);
     half8_t r = __builtin_bit_cast(half8_t, v);
     return r - (_Float16)1024.0f;
 }
@@ -171,6 +180,7 @@ struct GemmArgs {
     const float* b_sum32;
     const float* rowscale;    // gate/up: per token; down: unused
     uint32_t kdim;            // H (gate/up) or I (down)
+    uint32_t b_rows;          // rows of the B operand buffers
     // outputs
     uint16_t* act_hi;         // [routes + T][I]
     uint16_t* act_lo;
@@ -180,9 +190,10 @@ struct GemmArgs {
 };
 
 // LDS plan of one GEMM workgroup.  Staging: two buffers of the activation
-// tile of one quantisation group, [TOK tokens][hi 32KS | lo 32KS | pad 8]
-// halfs (the pad spreads the 16 token rows a fragment read touches over
-// distinct banks).  Epilogues reuse the same bytes for the output tile.
+// tile of one quantisation group, [TOK tokens][64KS halfs + pad 8], the row
+// holding the hi and lo 16-byte chunks interleaved (the pad spreads the 16
+// token rows a fragment read touches over distinct banks).  Epilogues reuse
+// the same bytes for the output tile.
 template <int KS>
 struct GemmLds {
     static constexpr int XPITCH = 64 * KS + 8;             // halfs per token row
@@ -196,18 +207,39 @@ struct GemmLds {
     static constexpr int BYTES = STAGE_BYTES > EPI_BYTES ? STAGE_BYTES : EPI_BYTES;
 };
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// raw buffer resource over [p, p + bytes): 32-bit offsets, loads past the
+// end return zero
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 template <int N>
-__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&w)[N])
+__device__ __forceinline__ void load_words(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&w)[N])
 {
     if constexpr (N == 4) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
-        w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+        w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
     } else if constexpr (N == 2) {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        w[0] = v.x, w[1] = v.y;
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+        w[0] = v[0], w[1] = v[1];
     } else {
-        w[0] = p[0];
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
     }
+}
+
+template <int SBT>
+__device__ __forceinline__ float sb_buf(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    const uint16_t v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    if constexpr (SBT == 2)
+        return __uint_as_float((uint32_t)v << 16);
+    else
+        return __half2float(__ushort_as_half(v));
 }
 
 // One workgroup: TOK tokens of one item x WG_ROWS weight rows.  The
@@ -220,17 +252,18 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&w)[N])
 // g.  The accumulator element (token 4kb + r of the fragment, row i16) gets
 // s[row][g] * P + b[row][g] * sum_g(x) after each group.
 //
-// Work mapping: the flat list (row block major, tile minor) is cut into 8
-// contiguous ranges, one per XCD (workgroup ids are dealt to the XCDs
-// round-robin), so workgroups that share an expert's row block run on one
-// XCD and share its L2.
+// Work mapping: the flat list (tile major, row block minor; tiles are grouped
+// by expert) is cut into 8 contiguous ranges, one per XCD (workgroup ids are
+// dealt to the XCDs round-robin): the row blocks of one token tile run back
+// to back on one XCD and share the activation tile in its L2, and the next
+// tiles of the same expert find the expert's weights there.
 template <int SBT, bool GATEUP, int KS>
 __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
 {
     using L = GemmLds<KS>;
     constexpr int NMAT = GATEUP ? 2 : 1;
     __shared__ __align__(16) uint8_t lds[L::BYTES];
-    __shared__ __align__(16) float xs_lds[2][TOK];
+    __shared__ uint32_t row_lds[TOK];
     __shared__ float rs_lds[TOK];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
 
@@ -246,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
     const uint32_t widx = xcd * chunk + j;
     if (widx >= total)
         return;
-    const uint32_t rb = widx / ntiles, tile = widx % ntiles;
+    const uint32_t tile = widx / RB, rb = widx % RB;
     const uint32_t item = a.tiles[2 * tile], n0 = a.tiles[2 * tile + 1];
     const bool shared = a.has_shared && item == a.unique_count[0];
     uint32_t g0, cnt;
@@ -279,73 +312,85 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
     uint32_t s_row = 0;
     if (s_valid)
         s_row = GATEUP ? (shared ? s_n : a.src_rows[g0 + s_n]) : g0 + s_n;
-    const uint16_t* s_hi = a.b_hi + (uint64_t)s_row * K + s_part * 8 * KS;
-    const uint16_t* s_lo = a.b_lo + (uint64_t)s_row * K + s_part * 8 * KS;
-    const float* s_sum = a.b_sum32 + (uint64_t)s_row * C32;
-    if (GATEUP && s_part == 0)
-        rs_lds[s_tok] = s_valid ? a.rowscale[s_row] : 1.0f;
-    uint4 st_hi[KS], st_lo[KS];
-    float st_sum = 0.0f;
-    auto stage_load = [&](uint32_t g) {
+    const rsrc_t r_hi = make_rsrc(a.b_hi, a.b_rows * K * 2);
+    const rsrc_t r_lo = make_rsrc(a.b_lo, a.b_rows * K * 2);
+    const uint32_t s_off = s_row * K * 2;
+    if (s_part == 0) {
+        row_lds[s_tok] = s_valid ? s_row : 0xFFFFFFFFu;
+        if (GATEUP)
+            rs_lds[s_tok] = s_valid ? a.rowscale[s_row] : 1.0f;
+    }
+    // The 4 threads of a token each move 2KS of the token's 8KS 16-byte
+    // chunks; LDS chunk 2j holds hi chunk j and 2j + 1 lo chunk j, and the
+    // chunk numbering c = 4 part + (k & 3) + 16 (k >> 2) makes the 16 lanes
+    // of a store hit 16 distinct bank groups of the padded rows.
+    auto chunk_of = [&](int k) -> uint32_t {
+        if constexpr (KS == 1)
+            return 2 * s_part + k;
+        else
+            return 4 * s_part + (k & 3) + 16 * (k >> 2);
+    };
+    typedef uint4 Stage[2 * KS];
+    Stage st_a, st_b;
+    auto stage_load = [&](uint32_t g, Stage& st) {
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
+        for (int k = 0; k < 2 * KS; ++k) {
+            const uint32_t c = chunk_of(k);
             if (s_valid) {
-                st_hi[k] = reinterpret_cast<const uint4*>(s_hi + g * 32 * KS)[k];
-                st_lo[k] = reinterpret_cast<const uint4*>(s_lo + g * 32 * KS)[k];
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((k & 1) ? r_lo : r_hi,
+                                                                      s_off + (c >> 1) * 16, g * 64 * KS, 0);
+                st[k] = make_uint4(v[0], v[1], v[2], v[3]);
             } else {
-                st_hi[k] = make_uint4(0, 0, 0, 0);
-                st_lo[k] = make_uint4(0, 0, 0, 0);
+                st[k] = make_uint4(0, 0, 0, 0);
             }
-        }
-        if (s_part == 0) {
-            float s = 0.0f;
-            if (s_valid) {
-#pragma unroll
-                for (int k = 0; k < KS; ++k)
-                    s += s_sum[g * KS + k];
-            }
-            st_sum = s;
         }
     };
-    auto stage_store = [&](int buf) {
+    auto stage_store = [&](int buf, const Stage& st) {
         uint16_t* row = reinterpret_cast<uint16_t*>(lds) + buf * L::STAGE_HALFS + s_tok * L::XPITCH;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            reinterpret_cast<uint4*>(row + s_part * 8 * KS)[k] = st_hi[k];
-            reinterpret_cast<uint4*>(row + 32 * KS + s_part * 8 * KS)[k] = st_lo[k];
-        }
-        if (s_part == 0)
-            xs_lds[buf][s_tok] = st_sum;
+        for (int k = 0; k < 2 * KS; ++k)
+            reinterpret_cast<uint4*>(row)[chunk_of(k)] = st[k];
     };
 
     // ---- compute role ----
     const uint32_t i16 = lane & 15, kb = lane >> 4;
     const uint32_t row_base = rb * WG_ROWS + wv * 32;
-    const uint32_t* wp[2][NMAT];
-    const uint8_t* sbase[2][NMAT];
-    const uint8_t* bbase[2][NMAT];
+    // per lane byte offsets inside the expert slot (the component offsets and
+    // the group go into the scalar offset)
+    const rsrc_t wr = make_rsrc(slot, (uint32_t)set.stride);
+    uint32_t w_voff[2], sb_voff[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
         const uint32_t row = row_base + 16 * rt + i16;
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            const Q4Proj& p = m == 0 ? p0 : p1;
-            wp[rt][m] = reinterpret_cast<const uint32_t*>(slot + p.w_off) + (uint64_t)row * WPR + KS * kb;
-            sbase[rt][m] = slot + p.s_off + (uint64_t)row * G * 2;
-            bbase[rt][m] = slot + p.b_off + (uint64_t)row * G * 2;
-        }
+        w_voff[rt] = row * WPR * 4 + KS * kb * 4;
+        sb_voff[rt] = row * G * 2;
     }
-    uint32_t wcur[2][NMAT][KS], wnext[2][NMAT][KS];
-    float sc[2][NMAT], bi[2][NMAT], sc_n[2][NMAT], bi_n[2][NMAT];
-    auto w_load = [&](uint32_t g, uint32_t (&w)[2][NMAT][KS], float (&s)[2][NMAT], float (&b)[2][NMAT]) {
+    const uint32_t w_soff[2] = {(uint32_t)p0.w_off, (uint32_t)p1.w_off};
+    const uint32_t s_soff[2] = {(uint32_t)p0.s_off, (uint32_t)p1.s_off};
+    const uint32_t b_soff[2] = {(uint32_t)p0.b_off, (uint32_t)p1.b_off};
+    const uint32_t magic = 0x64006400u; // held in a VGPR for v_and_or_b32
+    uint32_t wa[2][NMAT][KS], wb[2][NMAT][KS];
+    auto w_load = [&](uint32_t g, uint32_t (&w)[2][NMAT][KS]) {
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-                load_words<KS>(wp[rt][m] + g * 4 * KS, w[rt][m]);
-                s[rt][m] = sb_at<SBT>(sbase[rt][m], g);
-                b[rt][m] = sb_at<SBT>(bbase[rt][m], g);
-            }
+            for (int m = 0; m < NMAT; ++m)
+                load_words<KS>(wr, w_voff[rt], w_soff[m] + g * 16 * KS, w[rt][m]);
+    };
+    // scales of a pair of groups (g even, G is even) in one 32-bit load
+    auto s_load = [&](uint32_t g, uint32_t (&sp)[2][NMAT]) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+                sp[rt][m] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff[rt], s_soff[m] + g * 2, 0);
+    };
+    auto s_of = [&](uint32_t pair, uint32_t g) -> float {
+        const uint16_t v = (uint16_t)(pair >> ((g & 1) * 16));
+        if constexpr (SBT == 2)
+            return __uint_as_float((uint32_t)v << 16);
+        else
+            return __half2float(__ushort_as_half(v));
     };
 
     float4_t acc[2][NMAT][4];
@@ -357,18 +402,36 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
             for (int st = 0; st < 4; ++st)
                 acc[rt][m][st] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    stage_load(0);
-    w_load(0, wcur, sc, bi);
-    stage_store(0);
+    // two-deep prefetch: at the top of step g the loads for g + 2 are
+    // issued (registers st_a / wc), the tile for g + 1 (st_b, loaded one
+    // step earlier) is stored into the other LDS buffer at its end
+    uint32_t wc[2][NMAT][KS];
+    uint32_t spa[2][NMAT], spb[2][NMAT]; // scale pairs: current, next
+    stage_load(0, st_a);
+    w_load(0, wa);
+    s_load(0, spa);
+    stage_store(0, st_a);
+    if (G > 1) {
+        stage_load(1, st_b);
+        w_load(1, wb);
+    }
     __syncthreads();
-
     for (uint32_t g = 0; g < G; ++g) {
         const int buf = g & 1;
         const bool more = g + 1 < G;
-        if (more) {
-            stage_load(g + 1);
-            w_load(g + 1, wnext, sc_n, bi_n);
+        const bool more2 = g + 2 < G;
+        if (more2) {
+            stage_load(g + 2, st_a);
+            w_load(g + 2, wc);
+            if ((g & 1) == 0)
+                s_load(g + 2, spb);
         }
+        float sa[2][NMAT];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+                sa[rt][m] = s_of(spa[rt][m], g);
         half8_t wf[2][NMAT][KS];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
@@ -376,49 +439,102 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
             for (int m = 0; m < NMAT; ++m)
 #pragma unroll
                 for (int k = 0; k < KS; ++k)
-                    wf[rt][m][k] = unpack8(wcur[rt][m][k]);
+                    wf[rt][m][k] = unpack8(wa[rt][m][k], magic);
         const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + buf * L::STAGE_HALFS;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            const uint16_t* xr = xb + (16 * st + i16) * L::XPITCH + 8 * KS * kb;
+            const uint16_t* xr = xb + (16 * st + i16) * L::XPITCH + 16 * KS * kb;
             half8_t ah[KS], al[KS];
 #pragma unroll
             for (int k = 0; k < KS; ++k) {
-                ah[k] = *reinterpret_cast<const half8_t*>(xr + 8 * k);
-                al[k] = *reinterpret_cast<const half8_t*>(xr + 32 * KS + 8 * k);
+                ah[k] = *reinterpret_cast<const half8_t*>(xr + 16 * k);
+                al[k] = *reinterpret_cast<const half8_t*>(xr + 16 * k + 8);
             }
-            const float4 xs4 = *reinterpret_cast<const float4*>(&xs_lds[buf][16 * st + 4 * kb]);
-            const float xsv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+            // the 2 x NMAT partial chains are interleaved step by step so
+            // that no MFMA waits on the one just issued
+            float4_t p[2][NMAT];
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                        for (int m = 0; m < NMAT; ++m) {
+                            const float4_t c = (k == 0 && hl == 0) ? float4_t{0.0f, 0.0f, 0.0f, 0.0f} : p[rt][m];
+                            p[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hl ? al[k] : ah[k], wf[rt][m][k], c,
+                                                                            0, 0, 0);
+                        }
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-                for (int m = 0; m < NMAT; ++m) {
-                    float4_t p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int k = 0; k < KS; ++k) {
-                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[k], wf[rt][m][k], p, 0, 0, 0);
-                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[k], wf[rt][m][k], p, 0, 0, 0);
-                    }
+                for (int m = 0; m < NMAT; ++m)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[rt][m][st][r] =
-                            fmaf(sc[rt][m], p[r], fmaf(bi[rt][m], xsv[r], acc[rt][m][st][r]));
-                }
+                        acc[rt][m][st][r] = fmaf(sa[rt][m], p[rt][m][r], acc[rt][m][st][r]);
         }
         if (more)
-            stage_store(buf ^ 1);
+            stage_store(buf ^ 1, st_b);
         __syncthreads();
-        if (more) {
+#pragma unroll
+        for (int k = 0; k < 2 * KS; ++k)
+            st_b[k] = st_a[k];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+#pragma unroll
+                for (int k = 0; k < KS; ++k) {
+                    wa[rt][m][k] = wb[rt][m][k];
+                    wb[rt][m][k] = wc[rt][m][k];
+                }
+                if (g & 1)
+                    spa[rt][m] = spb[rt][m];
+            }
+    }
+
+    // ---- bias term on the matrix cores: acc += sum_g b[row][g] * xsum[token][g],
+    //      K' = groups, the group sums split into f16 hi + lo ----
+    {
+        for (uint32_t k0 = 0; k0 < G; k0 += 32) {
+            half8_t bw[2][NMAT];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-                for (int m = 0; m < NMAT; ++m) {
+                for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-                    for (int k = 0; k < KS; ++k)
-                        wcur[rt][m][k] = wnext[rt][m][k];
-                    sc[rt][m] = sc_n[rt][m];
-                    bi[rt][m] = bi_n[rt][m];
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t gg = k0 + 8 * kb + j;
+                        bw[rt][m][j] = gg < G ? (_Float16)sb_buf<SBT>(wr, sb_voff[rt], b_soff[m] + gg * 2)
+                                              : (_Float16)0.0f;
+                    }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t brow = row_lds[16 * st + i16];
+                half8_t xh, xl;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t gg = k0 + 8 * kb + j;
+                    float v = 0.0f;
+                    if (brow != 0xFFFFFFFFu && gg < G) {
+#pragma unroll
+                        for (int c = 0; c < KS; ++c)
+                            v += a.b_sum32[(uint64_t)brow * C32 + gg * KS + c];
+                    }
+                    const _Float16 h = (_Float16)v;
+                    xh[j] = h;
+                    xl[j] = (_Float16)(v - (float)h);
                 }
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int m = 0; m < NMAT; ++m) {
+                        float4_t p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[rt][m], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[rt][m], p, 0, 0, 0);
+                        acc[rt][m][st] += p;
+                    }
+            }
         }
     }
 
@@ -649,6 +765,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.b_sum32 = p.x_sum32;
     a.rowscale = p.rowscale;
     a.kdim = H;
+    a.b_rows = T;
     a.act_hi = p.act_hi;
     a.act_lo = p.act_lo;
     a.act_sum32 = p.act_sum32;
@@ -660,6 +777,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.b_sum32 = p.act_sum32;
     a.rowscale = nullptr;
     a.kdim = I;
+    a.b_rows = routes + T;
     a.y = p.y;
     q4_group_gemm_kernel<SBT, false, KS><<<gemm_grid(max_tiles, H), 256, 0, st>>>(a);
     if ((err = hipGetLastError()) != hipSuccess)
