@@ -146,6 +146,161 @@ def cpu_baseline(cfg, host_layers, tokens: int, budget_s: float, threads: int):
                       f"({t_total:.1f} s, oracle router+routing+experts+combine)"}
 
 
+KERNEL_NAMES = {"stage": "router_stage_kernel", "gateup": "route_gateup_kernel", "down": "down_combine_kernel"}
+
+
+def load_traffic(phase: str, workload: str):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the plain-copy
+    calibration), or None when no summary covers this kernel/workload."""
+    path = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        ent = rec[workload][KERNEL_NAMES[phase]]
+        return int(ent["traffic_bytes"]), "profiles/decode_traffic.json"
+    except (OSError, KeyError, ValueError, TypeError):
+        return None, None
+
+
+def copy_calibration(ctx, mb: int, reps: int) -> None:
+    """A plain device-to-device copy of known size on the library stream
+    (the runtime's copy kernel): the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters of a PMC run to bytes."""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    n = mb << 20
+    src, dst = ctx.array(n, np.uint8), ctx.array(n, np.uint8)
+    for _ in range(reps):
+        assert hip.hipMemcpyAsync(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), n, 3, C.c_void_p(ctx.stream())) == 0
+    ctx.sync()
+    print(f"[bench] copy calibration: {reps} x {n} bytes device-to-device", file=sys.stderr, flush=True)
+
+
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16
+
+
+def prefill_flops(cfg, tokens: int, routes: int) -> dict:
+    """Algorithmic flops of the grouped prefill GEMMs (2 per multiply-add):
+    gate/up 2 x 2*H*I per routed row (+ shared rows), down 2*H*I per row."""
+    H, I, Is = cfg.hidden, cfg.intermediate, cfg.shared_intermediate
+    rows_sh = tokens if Is else 0
+    gateup = 2 * 2 * H * (routes * I + rows_sh * Is)
+    down = 2 * H * (routes * I + rows_sh * Is)
+    return {"gateup": gateup, "down": down}
+
+
+def bench_prefill(args, cfg, ctx, ev) -> dict:
+    """Layer-major prefill of T tokens through one MoE layer per step
+    (pbmoe_moe_prefill: dispatch plan, grouped gate/up GEMM + SwiGLU,
+    grouped down GEMM, combine).  C3 routes come from Zipf(1.1)-drawn router
+    logits; other configs route x through the bound router."""
+    from pb_amd import abi, synth
+    T = args.tokens if args.tokens > 1 else cfg.tokens
+    stream = ctx.stream()
+    L = max(1, min(args.layers, 4))
+    lay, layers = build_layers(ctx, cfg, L, T)
+    xh, rh = synth.activations(SEED, 303, T, cfg.hidden)
+    x, res = ctx.to_device(xh), ctx.to_device(rh)
+    ids = ctx.array((T, cfg.k), np.uint32)
+    w = ctx.array((T, cfg.k), np.float32)
+    out = ctx.array((T, cfg.hidden), np.float32)
+    if cfg.name.startswith("c3"):
+        logits_h, _ = synth.drawn_logits_zipf(SEED, 0, T, cfg.experts, cfg.k, 1.1)
+        layers[0][0].route_logits(ctx.to_device(logits_h), ids, w)
+    else:
+        layers[0][0].route(x, ids, w)
+    ctx.sync()
+
+    def step(i):
+        layers[i % L][0].qwen_layer_major_experts(x, res, ids, w, out)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.sync()
+    a, b = ev.create(), ev.create()
+    ev.record(a, stream)
+    for i in range(args.steps):
+        step(i)
+    ev.record(b, stream)
+    us_step = ev.elapsed_ms(a, b) * 1e3 / args.steps
+    ctx.sync()
+    n_ph = min(args.steps, 64)
+    evs = [[ev.create() for _ in range(6)] for _ in range(n_ph)]
+    for i in range(n_ph):
+        arr = (C.c_void_p * 6)(*[e.value for e in evs[i]])
+        abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 6))
+        step(i)
+    abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, None, 0))
+    ctx.sync()
+    names = ("gateup", "down", "combine")
+    phase_us = {nm: float(np.mean([ev.elapsed_ms(e[2 * j], e[2 * j + 1]) * 1e3 for e in evs]))
+                for j, nm in enumerate(names)}
+    fl = prefill_flops(cfg, T, T * cfg.k)
+    kernels = {nm: {"us": round(phase_us[nm], 3)} for nm in names}
+    for nm in ("gateup", "down"):
+        tf = fl[nm] / (phase_us[nm] * 1e-6) / 1e12
+        kernels[nm].update({"flops": fl[nm], "TFLOPs": round(tf, 1), "mfma_issued_TFLOPs": round(2 * tf, 1)})
+    total_tf = (fl["gateup"] + fl["down"]) / (us_step * 1e-6) / 1e12
+    print(f"[bench] prefill {cfg.name} T={T}: {us_step:.1f} us/layer, {total_tf:.1f} TFLOP/s; kernels (us): "
+          + ", ".join(f"{k} {v:.1f}" for k, v in phase_us.items()), file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_prefill_baseline(cfg, layers[0][1], xh, rh, ids.download().astype(np.int32), w.download(),
+                                   args.cpu_seconds)
+    g = kernels["gateup"]
+    return {
+        "metric": "MoE layer prefill µs/token + MFMA utilisation",
+        "value": round(us_step / T, 4),
+        "unit": "us/token/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA (exact 4-bit codes x f16 hi+lo activations), f32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden, "experts": cfg.experts, "k": cfg.k,
+                   "intermediate": cfg.intermediate, "shared_intermediate": cfg.shared_intermediate,
+                   "quant": f"q4 affine g{cfg.group}", "layers_cycled": L},
+        "tokens_per_s": round(T / (us_step * 1e-6), 1),
+        "expert_TFLOPs": round(total_tf, 1),
+        "roofline": {"bound": "mfma", "achieved": g["TFLOPs"], "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(g["TFLOPs"] / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "q4_group_gemm_kernel (gate/up)", "flops_per_launch": g["flops"],
+                     "launch_us": g["us"], "mfma_issued_frac": round(g["mfma_issued_TFLOPs"] / MFMA_PEAK_TFLOPS, 4)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_prefill_baseline(cfg, host, xh, rh, ids_h, w_h, budget_s: float):
+    """The oracle's expert phase for a bounded sample of the same routed
+    tokens (one thread), per token."""
+    from oracle import oracle as orc
+    from pb_amd import abi, synth
+    lay = abi.q4_layout_fixed(cfg.hidden, cfg.intermediate, cfg.group, cfg.sb_dtype)
+    olay = orc.make_layout(cfg.hidden, cfg.intermediate, cfg.group, cfg.sb_dtype, lay.offsets, int(lay.expert_bytes))
+    slots = synth.q4_experts(SEED, synth.T_EXPERT, host.layer, 0, cfg.experts, cfg.hidden, cfg.intermediate, cfg.group,
+                             cfg.sb_dtype, lay.offsets, int(lay.expert_bytes))
+    sl = None
+    if host.shared_layout is not None:
+        sl = orc.make_layout(cfg.hidden, cfg.shared_intermediate, cfg.group, cfg.sb_dtype,
+                             host.shared_layout.offsets, int(host.shared_layout.expert_bytes))
+    done, t_total, chunk = 0, 0.0, 8
+    while t_total < budget_s and done + chunk <= xh.shape[0]:
+        r = slice(done, done + chunk)
+        t0 = time.perf_counter()
+        orc.moe_block(olay, slots, cfg.experts, xh[r], rh[r], ids_h[r], w_h[r], shared_layout=sl,
+                      shared_slot=host.shared_slot, shared_gate_w=host.shared_gate_f16, threads=1)
+        t_total += time.perf_counter() - t0
+        done += chunk
+    return {"value": round(t_total / done * 1e6, 1), "unit": "us/token/layer", "cores": 1, "kind": "port",
+            "sample": f"{done} tokens of the same routed chunk through the oracle expert phase ({t_total:.1f} s)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,6 +311,12 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill", action="store_true",
+                    help="layer-major prefill of --tokens (default: the config's) instead of decode")
+    ap.add_argument("--expert-phase", action="store_true",
+                    help="also time pbmoe_moe_decode alone (routes fixed)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="also run a plain device copy of this size (PMC calibration runs)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -164,13 +325,18 @@ def main() -> int:
         return 2
 
     from pb_amd import abi
-    from pb_amd.configs import CONFIGS, algorithmic_bytes
+    from pb_amd.configs import CONFIGS, algorithmic_bytes, decode_phase_bytes
 
     cfg = CONFIGS[args.config]
     T = args.tokens
     ctx = abi.Context(0)
     stream = ctx.stream()
     ev = HipEvents()
+    if args.prefill or cfg.name.startswith("c3"):
+        rec = bench_prefill(args, cfg, ctx, ev)
+        print(json.dumps(rec))
+        ctx.close()
+        return 0
     t_setup = time.perf_counter()
     lay, layers = build_layers(ctx, cfg, args.layers, T)
     from pb_amd import synth
@@ -213,18 +379,36 @@ def main() -> int:
     ctx.sync()
     steps_timed = reps * L
 
-    # expert phase alone (routes fixed): its share of the layer
-    for i in range(L):
-        layers[i][0].route(x, ids, w)
-    ctx.sync()
-    ev.record(a, stream)
-    for i in range(args.steps):
-        layers[i % L][0].submit_scheduled_expert_command(x, res, ids, w, out)
-    ev.record(b, stream)
-    us_expert = ev.elapsed_ms(a, b) * 1e3 / args.steps
-    ctx.sync()
+    us_expert = None
+    if args.expert_phase:
+        # expert phase alone (routes fixed, pbmoe_moe_decode)
+        for i in range(L):
+            layers[i][0].route(x, ids, w)
+        ctx.sync()
+        ev.record(a, stream)
+        for i in range(args.steps):
+            layers[i % L][0].submit_scheduled_expert_command(x, res, ids, w, out)
+        ev.record(b, stream)
+        us_expert = round(ev.elapsed_ms(a, b) * 1e3 / args.steps, 3)
+        ctx.sync()
     print(f"[bench] {us_step:.2f} us/layer (graph), {us_stream:.2f} us/layer (stream), "
-          f"expert phase {us_expert:.2f} us", file=sys.stderr, flush=True)
+          f"expert phase {us_expert} us", file=sys.stderr, flush=True)
+
+    # per-kernel durations of the same steps (stream mode): the library
+    # records hipEvents between its three kernels (pbmoe_set_phase_events)
+    # (start/stop events attached to each kernel's dispatch packet)
+    n_ph = min(args.steps, 512)
+    evs = [[ev.create() for _ in range(6)] for _ in range(n_ph)]
+    for i in range(n_ph):
+        arr = (C.c_void_p * 6)(*[e.value for e in evs[i]])
+        abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 6))
+        step(i)
+    abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, None, 0))
+    ctx.sync()
+    phase_us = {name: float(np.mean([ev.elapsed_ms(e[2 * j], e[2 * j + 1]) * 1e3 for e in evs]))
+                for j, name in enumerate(("stage", "gateup", "down"))}
+    print(f"[bench] phases (us): " + ", ".join(f"{k} {v:.2f}" for k, v in phase_us.items()), file=sys.stderr,
+          flush=True)
 
     # unique experts per step (decode: distinct ids of the batch)
     uniq = []
@@ -235,6 +419,12 @@ def main() -> int:
     u_mean = float(np.mean(uniq))
     bytes_layer = algorithmic_bytes(cfg, int(round(u_mean)), T)
     gbps = bytes_layer / (us_step * 1e-6) / 1e9
+    ph_bytes = decode_phase_bytes(cfg, int(round(u_mean)), T)
+    kernels = {k: {"us": round(phase_us[k], 3), "bytes": ph_bytes[k],
+                   "GBps": round(ph_bytes[k] / (phase_us[k] * 1e-6) / 1e9, 1)} for k in phase_us}
+    dominant = max(phase_us, key=phase_us.get)
+    dom_gbps = kernels[dominant]["GBps"]
+    traffic, traffic_src = load_traffic(dominant, cfg.name)
 
     cpu = None
     if not args.no_cpu:
@@ -260,14 +450,18 @@ def main() -> int:
         "tokens_per_s": round(T / (us_step * 1e-6), 1),
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "expert_phase_us": round(us_expert, 3),
+        "expert_phase_us": us_expert,
         "stream_us_per_layer": round(us_stream, 3),
         "timing": "hipGraph replay of the per-layer launches (stream_us_per_layer: one ABI call per step)",
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "whole MoE layer (pbmoe_moe_layer: stage, gate/up, down+combine)", "bytes_per_launch": bytes_layer},
+        "roofline": {"bound": "hbm", "achieved": dom_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": KERNEL_NAMES[dominant], "bytes_per_launch": ph_bytes[dominant],
+                     "launch_us": kernels[dominant]["us"], "traffic_source": traffic_src},
+        "kernels": kernels,
         "cpu_baseline": cpu,
     }
+    if args.copy_calibration_mb:
+        copy_calibration(ctx, args.copy_calibration_mb, 3)
     print(json.dumps(rec))
     ctx.close()
     return 0

@@ -176,6 +176,13 @@ int pbmoe_ctx_stream(pbmoe_ctx* ctx, void** stream);
  * with the 120 s limit of metal/mod.rs:539-540) and report deferred device
  * errors.  Returns PBMOE_ERR_ROUTE if a kernel saw an out-of-range route. */
 int pbmoe_sync(pbmoe_ctx* ctx);
+/* Per-kernel device timing (FlashMoeTimingBuckets / record_detailed_timing,
+ * types.rs:600-619, runtime/mod.rs:1470): with count == 6, the expert-phase
+ * calls attach events[2i] / events[2i+1] (hipEvent_t) as the start / stop
+ * events of kernel i's dispatch packet.  Decode and whole-layer calls:
+ * 0 router stage, 1 gate/up, 2 down + combine.  Grouped prefill (more than
+ * 16 tokens): 0 gate/up GEMM, 1 down GEMM, 2 combine.  count == 0 disables. */
+int pbmoe_set_phase_events(pbmoe_ctx* ctx, void* const* events, uint32_t count);
 int pbmoe_device_alloc(pbmoe_ctx* ctx, size_t bytes, void** dptr);
 int pbmoe_device_free(pbmoe_ctx* ctx, void* dptr);
 int pbmoe_upload(pbmoe_ctx* ctx, void* dst_device, const void* src_host, size_t bytes);
@@ -235,11 +242,16 @@ int pbmoe_moe_decode(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float
 int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                     uint32_t tokens, uint32_t* ids_out, float* weights_out,
                     const float* next_norm_weight, float* hidden_out, float* next_normed_out);
-/* Layer-major prefill (qwen_layer_major_experts): any tokens >= 1.  Builds
- * the dispatch plan on the device, runs the grouped expert GEMMs and the
- * fused combine.  Same arguments and result contract as pbmoe_moe_decode;
- * for tokens == 1 the result is bitwise equal to pbmoe_moe_decode
- * (one-row parity, metal/mod.rs:4015-4079). */
+/* Layer-major prefill (qwen_layer_major_experts, runtime/mod.rs:1151-1161,
+ * metal/mod.rs:3583-4106): 1 <= tokens <= 32768.  Same arguments and result
+ * contract as pbmoe_moe_decode.  Up to 16 tokens run the decode kernels, so
+ * tokens == 1 is bitwise equal to pbmoe_moe_decode (one-row parity,
+ * metal/mod.rs:4015-4079).  Larger chunks build the dispatch plan on the
+ * device and run the grouped expert GEMMs on the matrix cores (exact 4-bit
+ * codes, activations as f16 hi + lo pairs), then the combine in route
+ * order.  A SwiGLU activation beyond the f16 range (|a| > 65504) is
+ * reported by pbmoe_sync as PBMOE_ERR_NONFINITE; the shared expert must
+ * use the routed experts' group size and scale/bias dtype. */
 int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                       uint32_t tokens, const uint32_t* ids, const float* weights,
                       const float* next_norm_weight, float* hidden_out, float* next_normed_out);

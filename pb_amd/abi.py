@@ -90,6 +90,7 @@ _SIG = {
     "pbmoe_ctx_destroy": ([_P], C.c_int),
     "pbmoe_ctx_stream": ([_P, C.POINTER(_P)], C.c_int),
     "pbmoe_sync": ([_P], C.c_int),
+    "pbmoe_set_phase_events": ([_P, C.POINTER(_P), _U32], C.c_int),
     "pbmoe_device_alloc": ([_P, C.c_size_t, C.POINTER(_P)], C.c_int),
     "pbmoe_device_free": ([_P, _P], C.c_int),
     "pbmoe_upload": ([_P, _P, _P, C.c_size_t], C.c_int),

@@ -42,3 +42,29 @@ def algorithmic_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:
     b += cfg.experts * cfg.hidden * 2
     b += tokens * cfg.hidden * 4 * 3
     return b
+
+
+def q4_proj_bytes(rows: int, cols: int, group: int) -> int:
+    """Bytes of one Q4 projection: packed nibbles + 2-byte scale and bias."""
+    return rows * cols // 2 + 2 * (rows * cols // group) * 2
+
+
+def decode_phase_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> dict:
+    """Algorithmic HBM bytes of each decode kernel (pbmoe_moe_layer):
+    stage   router rows (f16), shared gate/up + gate row, x in, logits and
+            shared activations out;
+    gateup  gate/up of the selected experts, logits and x in, act out;
+    down    down of the selected experts + shared down, act in, residual
+            in, hidden out."""
+    H, I, Is, E, K, g, T = (cfg.hidden, cfg.intermediate, cfg.shared_intermediate, cfg.experts, cfg.k,
+                            cfg.group, tokens)
+    stage = E * H * 2 + T * H * 4 + T * E * 4
+    if Is:
+        stage += 2 * q4_proj_bytes(Is, H, g) + T * Is * 4
+        if cfg.shared_gated:
+            stage += H * 2
+    gateup = unique_experts * 2 * q4_proj_bytes(I, H, g) + T * E * 4 + T * H * 4 + T * K * I * 4
+    down = unique_experts * q4_proj_bytes(H, I, g) + T * K * I * 4 + 2 * T * H * 4
+    if Is:
+        down += q4_proj_bytes(H, Is, g) + T * Is * 4
+    return {"stage": stage, "gateup": gateup, "down": down}

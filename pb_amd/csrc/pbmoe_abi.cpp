@@ -94,6 +94,8 @@ struct pbmoe_ctx {
     DeviceBuf route_ids, route_w;
     DeviceBuf prefill; // prefill scratch (operand splits, activations, y)
     DeviceBuf plan_work; // multi-workgroup plan scratch of pbmoe_dispatch_plan
+    hipEvent_t phase_ev[6] = {};
+    bool phase_timing = false;
 };
 
 namespace {
@@ -478,6 +480,30 @@ PBMOE_API int pbmoe_sync(pbmoe_ctx* ctx)
     return ok();
 }
 
+// Per-kernel device timing of the decode launches (the counterpart of the
+// reference's FlashMoeTimingBuckets / record_detailed_timing, types.rs:600-619,
+// runtime/mod.rs:1470): events (hipEvent_t) 2i / 2i+1 are the start / stop
+// events of kernel i (router stage, gate/up, down+combine), attached to the
+// dispatch packets.
+PBMOE_API int pbmoe_set_phase_events(pbmoe_ctx* ctx, void* const* events, uint32_t count)
+{
+    if (!ctx)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
+    if (count == 0) {
+        ctx->phase_timing = false;
+        return ok();
+    }
+    if (count != 6 || !events)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "phase timing takes exactly 6 events (or 0 to disable)");
+    for (uint32_t i = 0; i < 6; ++i) {
+        if (!events[i])
+            return fail(PBMOE_ERR_INVALID_ARGUMENT, "phase event %u is null", i);
+        ctx->phase_ev[i] = static_cast<hipEvent_t>(events[i]);
+    }
+    ctx->phase_timing = true;
+    return ok();
+}
+
 PBMOE_API int pbmoe_device_alloc(pbmoe_ctx* ctx, size_t bytes, void** dptr)
 {
     if (!ctx || !dptr)
@@ -776,6 +802,9 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     a->plan = plan;
     a->ticket = ctx->status + 32;
     a->status = ctx->status;
+    a->phase_timing = ctx->phase_timing;
+    for (int i = 0; i < 6; ++i)
+        a->phase_ev[i] = ctx->phase_ev[i];
     return ok();
 }
 
@@ -1015,6 +1044,9 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     a.act_sum32 = reinterpret_cast<float*>(base + off[9]);
     a.y = reinterpret_cast<float*>(base + off[10]);
     a.status = ctx->status;
+    a.phase_timing = ctx->phase_timing;
+    for (int i = 0; i < 6; ++i)
+        a.phase_ev[i] = ctx->phase_ev[i];
     HIP_TRY(pbmoe::launch_prefill(ctx->stream, a));
     return ok();
 }

@@ -12,6 +12,7 @@
 // Every wave issues all of its weight loads before it consumes any of them:
 // at batch 1 the layer is latency-bound, so the number of dependent memory
 // round trips, not instruction count, sets the time.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -629,6 +630,14 @@ __global__ __launch_bounds__(256) void next_norm_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+// start/stop events of kernel phase i/2 when the caller asked for phase
+// timing: attached to the dispatch packet itself, so they bracket exactly
+// the kernel's execution
+static inline hipEvent_t phase_event(const DecodeArgs& d, int i)
+{
+    return d.phase_timing ? d.phase_ev[i] : nullptr;
+}
+
 static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool do_router,
                                       bool do_shared)
 {
@@ -647,8 +656,15 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     a.act_shared = d.act_shared;
     a.shared_weight = d.shared_weight;
     const uint32_t tasks = a.experts + (a.shared_rows ? a.shared_rows + 1u : 0u);
-    if (tasks == 0)
+    if (tasks == 0) {
+        if (d.phase_timing) {
+            hipError_t e = hipEventRecord(d.phase_ev[0], st);
+            if (e == hipSuccess)
+                e = hipEventRecord(d.phase_ev[1], st);
+            return e;
+        }
         return hipSuccess;
+    }
     const uint32_t blocks = (tasks + 3) / 4;
     const uint32_t cr = (d.hidden + 511) / 512;
     const uint32_t cs = (d.hidden / 32 + 63) / 64;
@@ -659,7 +675,9 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     const uint32_t gdt = a.sgate_w ? d.sgate_dtype : d.router_dtype;
     const uint32_t wdt = a.experts ? d.router_dtype : gdt;
     const uint32_t sbt = a.shared_rows ? a.sh.sb_dtype : 1u;
-#define PBM_RS(W, G, S, CRV, CSV) router_stage_kernel<W, G, S, CRV, CSV><<<blocks, 256, 0, st>>>(a)
+#define PBM_RS(W, G, S, CRV, CSV)                                                              \
+    hipExtLaunchKernelGGL((router_stage_kernel<W, G, S, CRV, CSV>), dim3(blocks), dim3(256), 0, st, \
+                          phase_event(d, 0), phase_event(d, 1), 0, a)
 #define PBM_RS_CS(W, G, S, CRV)                                                                \
     do {                                                                                       \
         if (cs <= 1) PBM_RS(W, G, S, CRV, 1);                                                  \
@@ -715,7 +733,9 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     const uint32_t cpl = (H / 32 + 63) / 64;
     const uint32_t epl = (d.rp.experts + 63) / 64;
     dim3 g1((waves + 3) / 4);
-#define PBM_GU(C, EP) route_gateup_kernel<SBT, C, RPW, EP><<<g1, 256, 0, st>>>(ea)
+#define PBM_GU(C, EP)                                                                          \
+    hipExtLaunchKernelGGL((route_gateup_kernel<SBT, C, RPW, EP>), g1, dim3(256), 0, st, phase_event(d, 2), \
+                          phase_event(d, 3), 0, ea)
 #define PBM_GU_E(C)                                                                            \
     do {                                                                                       \
         if (epl <= 2) PBM_GU(C, 2);                                                            \
@@ -753,7 +773,9 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     da.hidden_out = d.hidden_out;
     da.status = d.status;
     dim3 g2(H / DOWN_R);
-#define PBM_DN(L, C, M) down_combine_kernel<SBT, L, C, M><<<g2, 256, 0, st>>>(da)
+#define PBM_DN(L, C, M)                                                                        \
+    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M>), g2, dim3(256), 0, st, phase_event(d, 4), \
+                          phase_event(d, 5), 0, da)
     switch (I) {
     case 256: PBM_DN(8, 1, 4); break;
     case 512: PBM_DN(8, 2, 4); break;
@@ -796,8 +818,10 @@ hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mod
     if (err != hipSuccess)
         return err;
     if (d.ex.sb_dtype == 2)
-        return launch_experts_typed<2>(st, d, full);
-    return launch_experts_typed<1>(st, d, full);
+        err = launch_experts_typed<2>(st, d, full);
+    else
+        err = launch_experts_typed<1>(st, d, full);
+    return err;
 }
 
 } // namespace pbmoe

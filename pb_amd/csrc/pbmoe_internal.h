@@ -90,6 +90,8 @@ struct DecodeArgs {
     float* next_normed;        // [T][H] or null
     Plan plan;                 // scratch plan (tokens > 1)
     uint32_t* ticket;          // zeroed counter for last-workgroup election
+    hipEvent_t phase_ev[6];    // start/stop per kernel when phase_timing
+    bool phase_timing;
     uint32_t* status;
 };
 
@@ -123,6 +125,8 @@ struct PrefillArgs {
     float* act_sum32;          // [T*K + T][I/32]
     float* y;                  // [T*K + T][H]
     uint32_t* status;
+    hipEvent_t phase_ev[6];    // start/stop of gate/up, down, combine
+    bool phase_timing;
 };
 
 uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared);

@@ -30,6 +30,7 @@
 //   gemm<down>: per (tile, 128-row block of H): y [route][H] f32
 //   combine:    h = (r + sum_k w_k y_k) + sw * S in route order, optional
 //               next-layer RMSNorm
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -710,6 +711,13 @@ uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool h
            (has_shared ? (tokens + TOK - 1) / TOK : 0u) + 1;
 }
 
+// start/stop events of kernel i/2 (gate/up GEMM, down GEMM, combine) when
+// the caller asked for per-kernel timing; attached to the dispatch packets
+static inline hipEvent_t phase_event(const PrefillArgs& p, int i)
+{
+    return p.phase_timing ? p.phase_ev[i] : nullptr;
+}
+
 // 8 x ceil(work / 8) workgroups for the XCD-split work list (see the kernel)
 static dim3 gemm_grid(uint32_t max_tiles, uint32_t rows)
 {
@@ -769,7 +777,8 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.act_hi = p.act_hi;
     a.act_lo = p.act_lo;
     a.act_sum32 = p.act_sum32;
-    q4_group_gemm_kernel<SBT, true, KS><<<gemm_grid(max_tiles, I), 256, 0, st>>>(a);
+    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(256), 0, st,
+                          phase_event(p, 0), phase_event(p, 1), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     a.b_hi = p.act_hi;
@@ -779,13 +788,15 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.kdim = I;
     a.b_rows = routes + T;
     a.y = p.y;
-    q4_group_gemm_kernel<SBT, false, KS><<<gemm_grid(max_tiles, H), 256, 0, st>>>(a);
+    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(256), 0, st,
+                          phase_event(p, 2), phase_event(p, 3), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
-    prefill_combine_kernel<<<T, 256, 0, st>>>(p.y, p.y + (uint64_t)routes * H,
-                                              p.sgate_w ? p.shared_logit : nullptr, has_shared,
-                                              p.plan.out_idx, p.weights, p.residual, K, H,
-                                              p.hidden_out, p.next_norm_w, p.eps, p.next_normed);
+    hipExtLaunchKernelGGL(prefill_combine_kernel, dim3(T), dim3(256), 0, st, phase_event(p, 4), phase_event(p, 5), 0,
+                          (const float*)p.y, (const float*)(p.y + (uint64_t)routes * H),
+                          (const float*)(p.sgate_w ? p.shared_logit : nullptr), has_shared,
+                          (const uint32_t*)p.plan.out_idx, p.weights, p.residual, K, H, p.hidden_out,
+                          p.next_norm_w, p.eps, p.next_normed);
     return hipGetLastError();
 }
 
