@@ -278,6 +278,18 @@ __device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s)
 {
     const int wv = threadIdx.x >> 6;
     const uint32_t K = a.rp.k;
+    const bool grouped = a.rp.kind == 2 && a.rp.n_group > 1;
+    if (a.tokens < 4 && a.rp.order == 0 && !grouped) {
+        // few tokens: all four waves route each token in turn
+        constexpr int EPT = EPL <= 4 ? 1 : (EPL <= 8 ? 2 : 4); // ceil(E / 256) bucket
+        for (uint32_t t = 0; t < a.tokens; ++t) {
+            if (t)
+                __syncthreads(); // scratch reuse
+            route_token_block<EPT>(a.logits + (uint64_t)t * a.rp.experts, a.sel_bias, a.rp, s.ids + t * K,
+                                   s.w + t * K, &s.grp[0][0], a.status);
+        }
+        return;
+    }
     for (uint32_t t = wv; t < a.tokens; t += 4)
         route_token_wave<EPL>(a.logits + (uint64_t)t * a.rp.experts, a.sel_bias, a.rp, s.ids + t * K,
                               s.w + t * K, s.sel[wv], s.grp[wv], a.status);
@@ -379,6 +391,16 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
         const uint32_t gidx = g0 + j;
         const uint32_t tok = use_plan ? s.src_rows[gidx] : gidx / K;
         const float* xt = a.x + (uint64_t)tok * H;
+        // the nibble conversions below do not depend on the token; without
+        // this opaque step the compiler hoists all of them out of the loop
+        // (hundreds of registers, one wave per SIMD)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                asm volatile("" : "+v"(wg[r][c].x), "+v"(wg[r][c].y), "+v"(wg[r][c].z), "+v"(wg[r][c].w));
+                asm volatile("" : "+v"(wu[r][c].x), "+v"(wu[r][c].y), "+v"(wu[r][c].z), "+v"(wu[r][c].w));
+            }
         float pg[RPW], pu[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; ++r)

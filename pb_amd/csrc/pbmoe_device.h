@@ -494,4 +494,161 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
     }
 }
 
+// ---------------------------------------------------------------------------
+// routing of one token by a whole 256-thread workgroup (canonical order,
+// softmax or ungrouped sigmoid): each wave takes the canonical top-K of its
+// quarter of the experts (K rounds of a wave max over per-thread sorted
+// heads), then wave 0 merges the <= 4K candidates, one per lane.  Same
+// selection rule (score desc, lower index) and value arithmetic as
+// route_token_wave; every thread of the workgroup must call it.
+// lds: >= 1024 + 8 + 144 floats of workgroup scratch.
+// ---------------------------------------------------------------------------
+template <int EPT>
+__device__ inline void route_token_block(const float* __restrict__ l, const float* __restrict__ bias,
+                                         const RouteParams& p, uint32_t* ids_out, float* w_out, float* lds,
+                                         uint32_t* status)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t E = p.experts, K = p.k;
+    float* raw_l = lds;                                         // [E <= 1024]
+    float* red = lds + 1024;                                    // [8]
+    uint32_t* cand_k = reinterpret_cast<uint32_t*>(lds + 1032); // [4][16]
+    uint32_t* cand_i = cand_k + 64;                             // [4][16]
+    float raw[EPT];
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const uint32_t e = tid + 256 * j;
+        raw[j] = e < E ? l[e] : 0.0f;
+        bad |= e < E && !isfinite(raw[j]);
+        if (e < E)
+            raw_l[e] = raw[j];
+    }
+    if (__ballot(bad) != 0ull && lane == 0)
+        atomicOr(status, ST_NONFINITE);
+    float mx = 0.0f;
+    float sel[EPT];
+    if (p.kind == 0) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (tid + 256 * j < E)
+                m = fmaxf(m, raw[j]);
+        m = wave_max(m);
+        if (lane == 0)
+            red[wv] = m;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        float sm = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (tid + 256 * j < E)
+                sm += __expf(raw[j] - mx);
+        sm = wave_sum(sm);
+        if (lane == 0)
+            red[4 + wv] = sm;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            sel[j] = raw[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const uint32_t e = tid + 256 * j;
+            sel[j] = e < E ? sigmoidf_(raw[j]) + bias[e] : 0.0f;
+        }
+    }
+    // per-thread keys sorted descending (ascending index on equal keys)
+    uint32_t key[EPT], idx[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const uint32_t e = tid + 256 * j;
+        key[j] = e < E ? total_key(sel[j]) : 0u;
+        idx[j] = e;
+    }
+#pragma unroll
+    for (int i = 1; i < EPT; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            const bool sw = key[j] > key[j - 1];
+            const uint32_t ka = key[j - 1], kb2 = key[j], ia = idx[j - 1], ib = idx[j];
+            key[j - 1] = sw ? kb2 : ka, key[j] = sw ? ka : kb2;
+            idx[j - 1] = sw ? ib : ia, idx[j] = sw ? ia : ib;
+        }
+    // K rounds per wave over the heads
+    uint32_t ptr = 0;
+    for (uint32_t r = 0; r < K; ++r) {
+        uint32_t hk = 0, hi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if ((uint32_t)j == ptr)
+                hk = key[j], hi = idx[j];
+        const uint32_t best = wave_max_u32(hk);
+        const uint64_t tied = __ballot(hk == best);
+        uint32_t win;
+        if (__popcll(tied) == 1)
+            win = (uint32_t)__builtin_amdgcn_readlane((int)hi, __ffsll((unsigned long long)tied) - 1);
+        else // exact tie between heads: the lower index first
+            win = wave_min_u32(hk == best ? hi : 0xFFFFFFFFu);
+        if (hk == best && hi == win)
+            ++ptr;
+        if (lane == 0) {
+            cand_k[wv * 16 + r] = best;
+            cand_i[wv * 16 + r] = win;
+        }
+    }
+    __syncthreads();
+    if (wv != 0)
+        return;
+    // merge: candidate (wave w, rank r) on lane w * K + r
+    const uint32_t n = 4 * K;
+    uint32_t ck = 0, ci = 0xFFFFFFFFu;
+    if ((uint32_t)lane < n) {
+        const uint32_t w = (uint32_t)lane / K, r = (uint32_t)lane % K;
+        ck = cand_k[w * 16 + r];
+        ci = cand_i[w * 16 + r];
+    }
+    uint32_t myid = 0;
+    for (uint32_t r = 0; r < K; ++r) {
+        const uint32_t best = wave_max_u32(ck);
+        const uint64_t tied = __ballot(ck == best);
+        uint32_t win;
+        if (__popcll(tied) == 1)
+            win = (uint32_t)__builtin_amdgcn_readlane((int)ci, __ffsll((unsigned long long)tied) - 1);
+        else
+            win = wave_min_u32(ck == best ? ci : 0xFFFFFFFFu);
+        if (ck == best && ci == win)
+            ck = 0u;
+        if ((uint32_t)lane == r)
+            myid = win;
+    }
+    // value behind each selected id, renormalisation (as route_token_wave)
+    const float v = (uint32_t)lane < K && myid < E ? raw_l[myid] : 0.0f;
+    float prob;
+    if (p.kind == 0) {
+        const float sum = (red[4] + red[5]) + (red[6] + red[7]);
+        const bool have_inv = sum > 0.0f && isfinite(sum);
+        const float ev = expf(v - mx);
+        prob = have_inv ? ev * (1.0f / sum) : ev;
+    } else {
+        prob = sigmoidf_(v);
+    }
+    const float sum = wave_sum((uint32_t)lane < K ? prob : 0.0f);
+    float inv;
+    if (p.norm == 1) {
+        if (lane == 0 && !(isfinite(sum) && sum >= 0.0f))
+            atomicOr(status, ST_BAD_SUM);
+        inv = 1.0f / fmaxf(sum, 6.103515625e-5f);
+    } else {
+        if (lane == 0 && !(isfinite(sum) && sum > 0.0f))
+            atomicOr(status, ST_BAD_SUM);
+        inv = 1.0f / sum;
+    }
+    if ((uint32_t)lane < K) {
+        if (prob < 0.0f)
+            atomicOr(status, ST_NEGATIVE);
+        ids_out[lane] = myid;
+        w_out[lane] = (prob * inv) * p.routed_scale;
+    }
+}
+
 } // namespace pbmoe

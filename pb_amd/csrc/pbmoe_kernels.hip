@@ -128,9 +128,33 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                           weights + (uint64_t)t * p.k, sel[wv], grp[wv], status);
 }
 
+// few tokens: one workgroup per token (route_token_block), the same routing
+// the fused decode layer performs, so both entry points agree bitwise
+template <int EPT>
+__global__ __launch_bounds__(256) void route_block_kernel(const float* __restrict__ logits,
+                                                         const float* __restrict__ bias, RouteParams p,
+                                                         uint32_t* __restrict__ ids,
+                                                         float* __restrict__ weights,
+                                                         uint32_t* __restrict__ status)
+{
+    __shared__ float scratch[1024 + 8 + 144];
+    const uint32_t t = blockIdx.x;
+    route_token_block<EPT>(logits + (uint64_t)t * p.experts, bias, p, ids + (uint64_t)t * p.k,
+                           weights + (uint64_t)t * p.k, scratch, status);
+}
+
 hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bias, uint32_t tokens,
                              const RouteParams& p, uint32_t* ids, float* weights, uint32_t* status)
 {
+    if (tokens < 4 && p.order == 0 && !(p.kind == 2 && p.n_group > 1)) {
+        if (p.experts <= 256)
+            route_block_kernel<1><<<tokens, 256, 0, s>>>(logits, bias, p, ids, weights, status);
+        else if (p.experts <= 512)
+            route_block_kernel<2><<<tokens, 256, 0, s>>>(logits, bias, p, ids, weights, status);
+        else
+            route_block_kernel<4><<<tokens, 256, 0, s>>>(logits, bias, p, ids, weights, status);
+        return hipGetLastError();
+    }
     dim3 grid((tokens + 3) / 4), block(256);
     uint32_t epl = (p.experts + WAVE - 1) / WAVE;
     if (epl <= 2)
