@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 // loads that do not wait for the routes; with more tokens they are read from
 // L2 per unit.
 // ---------------------------------------------------------------------------
-constexpr int DOWN_R = 8;
+constexpr int DOWN_R = 4;
 constexpr uint32_t STAGE_FLOATS = 12288; // 48 KB of staged activations
 
 struct DownArgs {
@@ -750,7 +750,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     ea.hidden = H;
     ea.act = d.act;
     ea.status = d.status;
-    constexpr int RPW = 4;
+    constexpr int RPW = 2;
     const uint32_t waves = max_items * (I / RPW);
     const uint32_t cpl = (H / 32 + 63) / 64;
     const uint32_t epl = (d.rp.experts + 63) / 64;
