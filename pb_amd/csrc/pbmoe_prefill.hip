@@ -43,9 +43,10 @@ namespace pbmoe {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int TOK = 64;              // tokens per tile (4 MFMA fragments of 16)
-constexpr int WG_ROWS = 128;         // weight rows per GEMM workgroup (4 waves x 32)
+constexpr int WG_ROWS = 256;         // weight rows per GEMM workgroup (8 waves x 32)
 constexpr float F16_SAFE = 16384.0f; // |hi| bound after the row scale
 
 // position of column c (0..7) inside an 8-column block in the K order
@@ -192,20 +193,18 @@ struct GemmArgs {
 
 // LDS plan of one GEMM workgroup.  Staging: two buffers of the activation
 // tile of one quantisation group, [TOK tokens][64KS halfs + pad 8], the row
-// holding the hi and lo 16-byte chunks interleaved (the pad spreads the 16
-// token rows a fragment read touches over distinct banks).  Epilogues reuse
-// the same bytes for the output tile.
+// holding the group's hi and lo 16-byte chunks interleaved (chunk 2c = hi
+// chunk c, 2c + 1 = lo chunk c); the pad spreads the 16 token rows of a
+// fragment read over distinct banks.  The epilogue reuses the bytes for the
+// f32 output tile [TOK][256 + 4].
 template <int KS>
 struct GemmLds {
-    static constexpr int XPITCH = 64 * KS + 8;             // halfs per token row
-    static constexpr int STAGE_HALFS = TOK * XPITCH;       // one buffer
-    static constexpr int ACT_PITCH = 2 * WG_ROWS + 8;      // halfs: hi | lo | pad
-    static constexpr int Y_PITCH = WG_ROWS + 4;            // floats
+    static constexpr int XPITCH = 64 * KS + 8;
+    static constexpr int STAGE_HALFS = TOK * XPITCH;
     static constexpr int STAGE_BYTES = 2 * STAGE_HALFS * 2;
-    static constexpr int ACT_BYTES = TOK * ACT_PITCH * 2;
-    static constexpr int Y_BYTES = TOK * Y_PITCH * 4;
-    static constexpr int EPI_BYTES = ACT_BYTES > Y_BYTES ? ACT_BYTES : Y_BYTES;
-    static constexpr int BYTES = STAGE_BYTES > EPI_BYTES ? STAGE_BYTES : EPI_BYTES;
+    static constexpr int OPITCH = WG_ROWS + 4;
+    static constexpr int OUT_BYTES = TOK * OPITCH * 4;
+    static constexpr int BYTES = STAGE_BYTES > OUT_BYTES ? STAGE_BYTES : OUT_BYTES;
 };
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -222,7 +221,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes)
 template <int N>
 __device__ __forceinline__ void load_words(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&w)[N])
 {
-    if constexpr (N == 4) {
+    if constexpr (N == 8) {
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+        w[0] = v0[0], w[1] = v0[1], w[2] = v0[2], w[3] = v0[3];
+        w[4] = v1[0], w[5] = v1[1], w[6] = v1[2], w[7] = v1[3];
+    } else if constexpr (N == 4) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
         w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
     } else if constexpr (N == 2) {
@@ -243,15 +247,17 @@ __device__ __forceinline__ float sb_buf(rsrc_t r, uint32_t voff, uint32_t soff)
         return __half2float(__ushort_as_half(v));
 }
 
-// One workgroup: TOK tokens of one item x WG_ROWS weight rows.  The
-// activation tile is the MFMA A operand (16 tokens x 32 K per fragment),
-// the weights the B operand (32 K x 16 rows); wave w owns rows
-// 32w .. 32w+31 of the block (two 16-row fragments) and all 4 token
-// fragments.  Lane (i16 = lane & 15, kb = lane >> 4) supplies the KS words
-// of K columns [g*32KS + 8KS*kb, +8KS) of its row: the 4 kb lanes of one
-// K-step (columns 8s + j of each lane's run) stay inside quantisation group
-// g.  The accumulator element (token 4kb + r of the fragment, row i16) gets
-// s[row][g] * P + b[row][g] * sum_g(x) after each group.
+// One workgroup: TOK tokens of one item x WG_ROWS weight rows, 8 waves.
+// MFMA 32x32x16 f16: the activation tile is the A operand (32 tokens x 16 K
+// per fragment), the weights the B operand (16 K x 32 rows); wave w owns
+// rows 32w .. 32w+31 of the block, one row per lane (lane & 31), and both
+// 32-token fragments.  Lane half h = lane >> 5 supplies, for quantisation
+// group g, the 2KS words (16KS columns) [g*32KS + 16KS*h, +16KS) of its
+// row; word s is K-step s, so each K-step stays inside group g and a
+// lane's group of weights is one 4KS-byte load.  The accumulator element
+// (token 8(j/4) + 4h + (j%4) of the fragment, the lane's row) gets
+// s[row][g] * P after each group; the bias term sum_g b[row][g] * xsum_g
+// runs on the matrix cores after the loop.
 //
 // Work mapping: the flat list (tile major, row block minor; tiles are grouped
 // by expert) is cut into 8 contiguous ranges, one per XCD (workgroup ids are
@@ -259,10 +265,11 @@ __device__ __forceinline__ float sb_buf(rsrc_t r, uint32_t voff, uint32_t soff)
 // to back on one XCD and share the activation tile in its L2, and the next
 // tiles of the same expert find the expert's weights there.
 template <int SBT, bool GATEUP, int KS>
-__global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
+__global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
 {
     using L = GemmLds<KS>;
     constexpr int NMAT = GATEUP ? 2 : 1;
+    constexpr int NSTEP = 2 * KS; // 16-column K-steps per quantisation group
     __shared__ __align__(16) uint8_t lds[L::BYTES];
     __shared__ uint32_t row_lds[TOK];
     __shared__ float rs_lds[TOK];
@@ -274,10 +281,10 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
     const uint32_t RB = rows_total / WG_ROWS;
     const uint32_t total = ntiles * RB;
     const uint32_t chunk = (total + 7) / 8;
-    const uint32_t j = blockIdx.x >> 3, xcd = blockIdx.x & 7;
-    if (j >= chunk)
+    const uint32_t j8 = blockIdx.x >> 3, xcd = blockIdx.x & 7;
+    if (j8 >= chunk)
         return;
-    const uint32_t widx = xcd * chunk + j;
+    const uint32_t widx = xcd * chunk + j8;
     if (widx >= total)
         return;
     const uint32_t tile = widx / RB, rb = widx % RB;
@@ -306,85 +313,67 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
     const uint32_t K = a.kdim;
     const uint32_t G = K / (32 * KS), C32 = K / 32, WPR = K / 8;
 
-    // ---- staging role: thread -> (token, quarter of the group's columns) ----
-    const uint32_t s_tok = tid >> 2, s_part = tid & 3;
+    // ---- staging role: 8 threads per token, KS of the token's 8KS chunks each ----
+    const uint32_t s_tok = tid >> 3, s_part = tid & 7;
     const uint32_t s_n = n0 + s_tok;
     const bool s_valid = s_n < cnt;
     uint32_t s_row = 0;
     if (s_valid)
         s_row = GATEUP ? (shared ? s_n : a.src_rows[g0 + s_n]) : g0 + s_n;
-    const rsrc_t r_hi = make_rsrc(a.b_hi, a.b_rows * K * 2);
-    const rsrc_t r_lo = make_rsrc(a.b_lo, a.b_rows * K * 2);
-    const uint32_t s_off = s_row * K * 2;
+    const uint16_t* s_hi = a.b_hi + (uint64_t)s_row * K;
+    const uint16_t* s_lo = a.b_lo + (uint64_t)s_row * K;
     if (s_part == 0) {
         row_lds[s_tok] = s_valid ? s_row : 0xFFFFFFFFu;
         if (GATEUP)
             rs_lds[s_tok] = s_valid ? a.rowscale[s_row] : 1.0f;
     }
-    // The 4 threads of a token each move 2KS of the token's 8KS 16-byte
-    // chunks; LDS chunk 2j holds hi chunk j and 2j + 1 lo chunk j, and the
-    // chunk numbering c = 4 part + (k & 3) + 16 (k >> 2) makes the 16 lanes
-    // of a store hit 16 distinct bank groups of the padded rows.
+    // chunk numbering: the 16 lanes of a store (2 tokens x 8 parts) hit 16
+    // distinct bank groups of the padded rows
     auto chunk_of = [&](int k) -> uint32_t {
         if constexpr (KS == 1)
-            return 2 * s_part + k;
+            return s_part;
         else
-            return 4 * s_part + (k & 3) + 16 * (k >> 2);
+            return 2 * s_part + (k & 1) + 16 * (k >> 1);
     };
-    typedef uint4 Stage[2 * KS];
+    typedef uint4 Stage[KS];
     Stage st_a, st_b;
     auto stage_load = [&](uint32_t g, Stage& st) {
 #pragma unroll
-        for (int k = 0; k < 2 * KS; ++k) {
+        for (int k = 0; k < KS; ++k) {
             const uint32_t c = chunk_of(k);
-            if (s_valid) {
-                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128((k & 1) ? r_lo : r_hi,
-                                                                      s_off + (c >> 1) * 16, g * 64 * KS, 0);
-                st[k] = make_uint4(v[0], v[1], v[2], v[3]);
-            } else {
-                st[k] = make_uint4(0, 0, 0, 0);
-            }
+            const uint16_t* src = ((c & 1) ? s_lo : s_hi) + g * 32 * KS + (c >> 1) * 8;
+            st[k] = s_valid ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
         }
     };
     auto stage_store = [&](int buf, const Stage& st) {
         uint16_t* row = reinterpret_cast<uint16_t*>(lds) + buf * L::STAGE_HALFS + s_tok * L::XPITCH;
 #pragma unroll
-        for (int k = 0; k < 2 * KS; ++k)
+        for (int k = 0; k < KS; ++k)
             reinterpret_cast<uint4*>(row)[chunk_of(k)] = st[k];
     };
 
     // ---- compute role ----
-    const uint32_t i16 = lane & 15, kb = lane >> 4;
-    const uint32_t row_base = rb * WG_ROWS + wv * 32;
-    // per lane byte offsets inside the expert slot (the component offsets and
-    // the group go into the scalar offset)
+    const uint32_t n32 = lane & 31, h = lane >> 5;
+    const uint32_t row = rb * WG_ROWS + wv * 32 + n32; // this lane's weight row
     const rsrc_t wr = make_rsrc(slot, (uint32_t)set.stride);
-    uint32_t w_voff[2], sb_voff[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const uint32_t row = row_base + 16 * rt + i16;
-        w_voff[rt] = row * WPR * 4 + KS * kb * 4;
-        sb_voff[rt] = row * G * 2;
-    }
+    const uint32_t w_voff = (row * WPR + h * 2 * KS) * 4;
+    const uint32_t sb_voff = row * G * 2;
     const uint32_t w_soff[2] = {(uint32_t)p0.w_off, (uint32_t)p1.w_off};
     const uint32_t s_soff[2] = {(uint32_t)p0.s_off, (uint32_t)p1.s_off};
     const uint32_t b_soff[2] = {(uint32_t)p0.b_off, (uint32_t)p1.b_off};
-    const uint32_t magic = 0x64006400u; // held in a VGPR for v_and_or_b32
-    uint32_t wa[2][NMAT][KS], wb[2][NMAT][KS];
-    auto w_load = [&](uint32_t g, uint32_t (&w)[2][NMAT][KS]) {
+    const uint32_t magic = 0x64006400u;
+    uint32_t wa[NMAT][2 * KS], wb[NMAT][2 * KS], wc[NMAT][2 * KS];
+    auto w_load = [&](uint32_t g, uint32_t (&w)[NMAT][2 * KS]) {
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-                load_words<KS>(wr, w_voff[rt], w_soff[m] + g * 16 * KS, w[rt][m]);
+        for (int m = 0; m < NMAT; ++m)
+            load_words<2 * KS>(wr, w_voff, w_soff[m] + g * 16 * KS, w[m]);
     };
-    // scales of a pair of groups (g even, G is even) in one 32-bit load
-    auto s_load = [&](uint32_t g, uint32_t (&sp)[2][NMAT]) {
+    // scales of a pair of groups (g even; G is even) in one 32-bit load
+    uint32_t spa[NMAT], spb[NMAT];
+    auto s_load = [&](uint32_t g, uint32_t (&sp)[NMAT]) {
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-                sp[rt][m] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff[rt], s_soff[m] + g * 2, 0);
+        for (int m = 0; m < NMAT; ++m)
+            sp[m] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff, s_soff[m] + g * 2, 0);
     };
     auto s_of = [&](uint32_t pair, uint32_t g) -> float {
         const uint16_t v = (uint16_t)(pair >> ((g & 1) * 16));
@@ -394,20 +383,18 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
             return __half2float(__ushort_as_half(v));
     };
 
-    float4_t acc[2][NMAT][4];
+    float16_t acc[2][NMAT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
-                acc[rt][m][st] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < 16; ++j)
+                acc[tf][m][j] = 0.0f;
 
-    // two-deep prefetch: at the top of step g the loads for g + 2 are
-    // issued (registers st_a / wc), the tile for g + 1 (st_b, loaded one
-    // step earlier) is stored into the other LDS buffer at its end
-    uint32_t wc[2][NMAT][KS];
-    uint32_t spa[2][NMAT], spb[2][NMAT]; // scale pairs: current, next
+    // two-deep prefetch: at the top of step g the loads for g + 2 are issued
+    // (st_a, wc), the tile for g + 1 (st_b, one step old) is stored into the
+    // other LDS buffer at its end
     stage_load(0, st_a);
     w_load(0, wa);
     s_load(0, spa);
@@ -419,204 +406,187 @@ __global__ __launch_bounds__(256, 2) void q4_group_gemm_kernel(GemmArgs a)
     __syncthreads();
     for (uint32_t g = 0; g < G; ++g) {
         const int buf = g & 1;
-        const bool more = g + 1 < G;
-        const bool more2 = g + 2 < G;
-        if (more2) {
+        if (g + 2 < G) {
             stage_load(g + 2, st_a);
             w_load(g + 2, wc);
             if ((g & 1) == 0)
                 s_load(g + 2, spb);
         }
-        float sa[2][NMAT];
+        float sa[NMAT];
+        half8_t wf[NMAT][NSTEP];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int m = 0; m < NMAT; ++m) {
+            sa[m] = s_of(spa[m], g);
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-                sa[rt][m] = s_of(spa[rt][m], g);
-        half8_t wf[2][NMAT][KS];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-                for (int k = 0; k < KS; ++k)
-                    wf[rt][m][k] = unpack8(wa[rt][m][k], magic);
+            for (int k = 0; k < NSTEP; ++k)
+                wf[m][k] = unpack8(wa[m][k], magic);
+        }
         const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + buf * L::STAGE_HALFS;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const uint16_t* xr = xb + (16 * st + i16) * L::XPITCH + 16 * KS * kb;
-            half8_t ah[KS], al[KS];
+        for (int tf = 0; tf < 2; ++tf) {
+            const uint16_t* xr = xb + (32 * tf + n32) * L::XPITCH + 16 * (h * NSTEP);
+            half8_t ah[NSTEP], al[NSTEP];
 #pragma unroll
-            for (int k = 0; k < KS; ++k) {
+            for (int k = 0; k < NSTEP; ++k) {
                 ah[k] = *reinterpret_cast<const half8_t*>(xr + 16 * k);
                 al[k] = *reinterpret_cast<const half8_t*>(xr + 16 * k + 8);
             }
-            // the 2 x NMAT partial chains are interleaved step by step so
-            // that no MFMA waits on the one just issued
-            float4_t p[2][NMAT];
+            float16_t p[NMAT];
 #pragma unroll
-            for (int k = 0; k < KS; ++k)
+            for (int k = 0; k < NSTEP; ++k)
 #pragma unroll
                 for (int hl = 0; hl < 2; ++hl)
 #pragma unroll
-                    for (int rt = 0; rt < 2; ++rt)
+                    for (int m = 0; m < NMAT; ++m) {
+                        float16_t c;
+                        if (k == 0 && hl == 0) {
 #pragma unroll
-                        for (int m = 0; m < NMAT; ++m) {
-                            const float4_t c = (k == 0 && hl == 0) ? float4_t{0.0f, 0.0f, 0.0f, 0.0f} : p[rt][m];
-                            p[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hl ? al[k] : ah[k], wf[rt][m][k], c,
-                                                                            0, 0, 0);
+                            for (int j = 0; j < 16; ++j)
+                                c[j] = 0.0f;
+                        } else {
+                            c = p[m];
                         }
+                        p[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(hl ? al[k] : ah[k], wf[m][k], c, 0, 0, 0);
+                    }
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-                for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[rt][m][st][r] = fmaf(sa[rt][m], p[rt][m][r], acc[rt][m][st][r]);
+                for (int j = 0; j < 16; ++j)
+                    acc[tf][m][j] = fmaf(sa[m], p[m][j], acc[tf][m][j]);
         }
-        if (more)
+        if (g + 1 < G)
             stage_store(buf ^ 1, st_b);
         __syncthreads();
 #pragma unroll
-        for (int k = 0; k < 2 * KS; ++k)
+        for (int k = 0; k < KS; ++k)
             st_b[k] = st_a[k];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int m = 0; m < NMAT; ++m) {
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-#pragma unroll
-                for (int k = 0; k < KS; ++k) {
-                    wa[rt][m][k] = wb[rt][m][k];
-                    wb[rt][m][k] = wc[rt][m][k];
-                }
-                if (g & 1)
-                    spa[rt][m] = spb[rt][m];
+            for (int k = 0; k < 2 * KS; ++k) {
+                wa[m][k] = wb[m][k];
+                wb[m][k] = wc[m][k];
             }
+            if (g & 1)
+                spa[m] = spb[m];
+        }
     }
 
     // ---- bias term on the matrix cores: acc += sum_g b[row][g] * xsum[token][g],
-    //      K' = groups, the group sums split into f16 hi + lo ----
-    {
-        for (uint32_t k0 = 0; k0 < G; k0 += 32) {
-            half8_t bw[2][NMAT];
+    //      K' = groups in steps of 16 (lane half h: groups k0 + 8h .. +8),
+    //      the group sums split into f16 hi + lo ----
+    for (uint32_t k0 = 0; k0 < G; k0 += 16) {
+        half8_t bw[NMAT];
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+        for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-                for (int m = 0; m < NMAT; ++m)
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t gg = k0 + 8 * h + j;
+                bw[m][j] = gg < G ? (_Float16)sb_buf<SBT>(wr, sb_voff, b_soff[m] + gg * 2) : (_Float16)0.0f;
+            }
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const uint32_t gg = k0 + 8 * kb + j;
-                        bw[rt][m][j] = gg < G ? (_Float16)sb_buf<SBT>(wr, sb_voff[rt], b_soff[m] + gg * 2)
-                                              : (_Float16)0.0f;
-                    }
+        for (int tf = 0; tf < 2; ++tf) {
+            const uint32_t brow = row_lds[32 * tf + n32];
+            half8_t xh, xl;
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const uint32_t brow = row_lds[16 * st + i16];
-                half8_t xh, xl;
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t gg = k0 + 8 * h + j;
+                float v = 0.0f;
+                if (brow != 0xFFFFFFFFu && gg < G) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t gg = k0 + 8 * kb + j;
-                    float v = 0.0f;
-                    if (brow != 0xFFFFFFFFu && gg < G) {
-#pragma unroll
-                        for (int c = 0; c < KS; ++c)
-                            v += a.b_sum32[(uint64_t)brow * C32 + gg * KS + c];
-                    }
-                    const _Float16 h = (_Float16)v;
-                    xh[j] = h;
-                    xl[j] = (_Float16)(v - (float)h);
+                    for (int c = 0; c < KS; ++c)
+                        v += a.b_sum32[(uint64_t)brow * C32 + gg * KS + c];
                 }
+                const _Float16 hv = (_Float16)v;
+                xh[j] = hv;
+                xl[j] = (_Float16)(v - (float)hv);
+            }
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
+            for (int m = 0; m < NMAT; ++m) {
+                float16_t c;
 #pragma unroll
-                    for (int m = 0; m < NMAT; ++m) {
-                        float4_t p = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[rt][m], p, 0, 0, 0);
-                        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[rt][m], p, 0, 0, 0);
-                        acc[rt][m][st] += p;
-                    }
+                for (int j = 0; j < 16; ++j)
+                    c[j] = 0.0f;
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, bw[m], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, bw[m], c, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    acc[tf][m][j] += c[j];
             }
         }
     }
 
-    // ---- epilogue: accumulator element (token 16st + 4kb + r, row
-    //      row_base + 16rt + i16); the output tile goes through LDS so that
-    //      global stores are whole rows ----
-    const uint32_t tok_c = s_tok, part_c = s_part; // copy-out role = staging role
-    if constexpr (GATEUP) {
-        const uint32_t I = rows_total;
-        uint16_t* at = reinterpret_cast<uint16_t*>(lds);
-        bool overflow = false;
-        float csum[4][4];
+    // ---- epilogue: accumulator element (token 32tf + 8(j/4) + 4h + (j%4),
+    //      row wv*32 + n32 of the block) -> f32 tile in LDS -> each thread
+    //      (token, 32-row chunk) writes whole rows ----
+    float* ot = reinterpret_cast<float*>(lds);
+    const uint32_t col = wv * 32 + n32;
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
+    for (int tf = 0; tf < 2; ++tf)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t tk = 16 * st + 4 * kb + r;
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t tk = 32 * tf + 8 * (j / 4) + 4 * h + (j % 4);
+            float v;
+            if constexpr (GATEUP) {
                 const float rs = rs_lds[tk];
-                float s = 0.0f;
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const float gg = acc[rt][0][st][r] * rs, uu = acc[rt][1][st][r] * rs;
-                    const float v = (gg / (1.0f + expf(-gg))) * uu;
-                    s += v;
-                    const uint32_t il = 32 * wv + 16 * rt + i16;
-                    const uint32_t pos = (il & ~7u) + kpos(il & 7u);
-                    overflow |= !(fabsf(v) <= 65504.0f);
-                    const _Float16 h = (_Float16)v;
-                    const _Float16 l = (_Float16)(v - (float)h);
-                    at[tk * L::ACT_PITCH + pos] = __builtin_bit_cast(uint16_t, h);
-                    at[tk * L::ACT_PITCH + WG_ROWS + pos] = __builtin_bit_cast(uint16_t, l);
-                }
-                csum[st][r] = s;
+                const float gg = acc[tf][0][j] * rs, uu = acc[tf][1][j] * rs;
+                v = (gg / (1.0f + expf(-gg))) * uu;
+            } else {
+                v = acc[tf][0][j];
             }
-        // sums over the wave's 32 rows (one 32-row chunk of I): the 16 i16
-        // lanes hold 16 rows each for rt = 0, 1
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = csum[st][r];
-                v += __shfl_xor(v, 1);
-                v += __shfl_xor(v, 2);
-                v += __shfl_xor(v, 4);
-                v += __shfl_xor(v, 8);
-                const uint32_t n = n0 + 16 * st + 4 * kb + r;
-                if (i16 == 0 && n < cnt)
-                    a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + (row_base >> 5)] = v;
-            }
-        if (__ballot(overflow) != 0ull && lane == 0)
-            atomicOr(a.status, ST_F16_RANGE);
-        __syncthreads();
-        const uint32_t n = n0 + tok_c;
-        if (n < cnt) {
-            const uint16_t* src = at + tok_c * L::ACT_PITCH + part_c * 32;
-            uint16_t* dh = a.act_hi + (uint64_t)(g0 + n) * I + rb * WG_ROWS + part_c * 32;
-            uint16_t* dl = a.act_lo + (uint64_t)(g0 + n) * I + rb * WG_ROWS + part_c * 32;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                reinterpret_cast<uint4*>(dh)[k] = reinterpret_cast<const uint4*>(src)[k];
-                reinterpret_cast<uint4*>(dl)[k] = reinterpret_cast<const uint4*>(src + WG_ROWS)[k];
-            }
+            ot[tk * L::OPITCH + col] = v;
         }
-    } else {
-        const uint32_t H = rows_total;
-        float* yt = reinterpret_cast<float*>(lds);
+    __syncthreads();
+    const uint32_t c_tok = tid >> 3, c_chunk = tid & 7; // rows 32 c_chunk .. +32
+    const uint32_t n = n0 + c_tok;
+    if (n < cnt) {
+        const float* src = ot + c_tok * L::OPITCH + 32 * c_chunk;
+        if constexpr (GATEUP) {
+            const uint32_t I = rows_total;
+            float v[32];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = reinterpret_cast<const float4*>(src)[q];
+                v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+            }
+            float sum = 0.0f;
+            bool overflow = false;
+            uint16_t hv[32], lv[32];
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
+            for (int q = 0; q < 32; ++q) {
+                // K order inside every 8-row block: c0 c4 c1 c5 c2 c6 c3 c7
+                const int cb = (q & ~7) + ((q & 1) ? 4 + ((q & 7) >> 1) : ((q & 7) >> 1));
+                const float x = v[cb];
+                sum += v[q];
+                overflow |= !(fabsf(x) <= 65504.0f);
+                const _Float16 hh = (_Float16)x;
+                hv[q] = __builtin_bit_cast(uint16_t, hh);
+                lv[q] = __builtin_bit_cast(uint16_t, (_Float16)(x - (float)hh));
+            }
+            if (overflow)
+                atomicOr(a.status, ST_F16_RANGE);
+            const uint64_t o = (uint64_t)(g0 + n) * I + rb * WG_ROWS + 32 * c_chunk;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    yt[(16 * st + 4 * kb + r) * L::Y_PITCH + 32 * wv + 16 * rt + i16] = acc[rt][0][st][r];
-        __syncthreads();
-        const uint32_t n = n0 + tok_c;
-        if (n < cnt) {
-            const float* src = yt + tok_c * L::Y_PITCH + part_c * 32;
-            float* dst = a.y + (uint64_t)(g0 + n) * H + rb * WG_ROWS + part_c * 32;
+            for (int q = 0; q < 4; ++q) {
+                uint4 hq, lq;
+                hq.x = hv[8 * q] | ((uint32_t)hv[8 * q + 1] << 16);
+                hq.y = hv[8 * q + 2] | ((uint32_t)hv[8 * q + 3] << 16);
+                hq.z = hv[8 * q + 4] | ((uint32_t)hv[8 * q + 5] << 16);
+                hq.w = hv[8 * q + 6] | ((uint32_t)hv[8 * q + 7] << 16);
+                lq.x = lv[8 * q] | ((uint32_t)lv[8 * q + 1] << 16);
+                lq.y = lv[8 * q + 2] | ((uint32_t)lv[8 * q + 3] << 16);
+                lq.z = lv[8 * q + 4] | ((uint32_t)lv[8 * q + 5] << 16);
+                lq.w = lv[8 * q + 6] | ((uint32_t)lv[8 * q + 7] << 16);
+                reinterpret_cast<uint4*>(a.act_hi + o)[q] = hq;
+                reinterpret_cast<uint4*>(a.act_lo + o)[q] = lq;
+            }
+            a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + rb * (WG_ROWS / 32) + c_chunk] = sum;
+        } else {
+            const uint32_t H = rows_total;
+            float* dst = a.y + (uint64_t)(g0 + n) * H + rb * WG_ROWS + 32 * c_chunk;
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                reinterpret_cast<float4*>(dst)[k] = reinterpret_cast<const float4*>(src)[k];
+            for (int q = 0; q < 8; ++q)
+                reinterpret_cast<float4*>(dst)[q] = reinterpret_cast<const float4*>(src)[q];
         }
     }
 }
@@ -777,7 +747,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.act_hi = p.act_hi;
     a.act_lo = p.act_lo;
     a.act_sum32 = p.act_sum32;
-    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(256), 0, st,
+    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(512), 0, st,
                           phase_event(p, 0), phase_event(p, 1), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
@@ -788,7 +758,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.kdim = I;
     a.b_rows = routes + T;
     a.y = p.y;
-    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(256), 0, st,
+    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(512), 0, st,
                           phase_event(p, 2), phase_event(p, 3), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
@@ -817,7 +787,7 @@ static hipError_t launch_prefill_sb(hipStream_t st, const PrefillArgs& p)
 
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs& p)
 {
-    // shapes the kernels assume: 128-row blocks of H and I, group = 2^shift,
+    // shapes the kernels assume: 256-row blocks of H and I, group = 2^shift,
     // a shared expert in the routed experts' format
     if ((1u << p.ex.group_shift) != p.ex.group || p.hidden % WG_ROWS || p.ex.gate.rows % WG_ROWS ||
         p.ex.gate.cols != p.hidden || p.ex.down.rows != p.hidden)
