@@ -1002,7 +1002,7 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     size_t off[12], total = 0;
     const size_t part[12] = {
         (size_t)max_tiles * 8, 4,      T * H * 2, T * H * 2, T * (H / 32) * 4, T * 4, T * 4,
-        rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, 0};
+        rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, T * 4};
     for (int i = 0; i < 12; ++i) {
         off[i] = total;
         total += align256(part[i]);
@@ -1043,6 +1043,7 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     a.act_lo = reinterpret_cast<uint16_t*>(base + off[8]);
     a.act_sum32 = reinterpret_cast<float*>(base + off[9]);
     a.y = reinterpret_cast<float*>(base + off[10]);
+    a.x_lo_any = reinterpret_cast<uint32_t*>(base + off[11]);
     a.status = ctx->status;
     a.phase_timing = ctx->phase_timing;
     for (int i = 0; i < 6; ++i)

@@ -119,6 +119,7 @@ struct PrefillArgs {
     uint16_t* x_lo;            // [T][H] f16
     float* x_sum32;            // [T][H/32]
     float* rowscale;           // [T]
+    uint32_t* x_lo_any;        // [T] nonzero when the row's lo part is not all zero
     float* shared_logit;       // [T]
     uint16_t* act_hi;          // [T*K + T][I] f16
     uint16_t* act_lo;          // [T*K + T][I] f16

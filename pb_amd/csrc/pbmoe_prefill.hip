@@ -34,6 +34,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "pbmoe_device.h"
 #include "pbmoe_internal.h"
@@ -46,30 +47,50 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int TOK = 64;              // tokens per tile (4 MFMA fragments of 16)
-constexpr int WG_ROWS = 256;         // weight rows per GEMM workgroup (8 waves x 32)
+#ifndef PBMOE_GEMM_WAVES
+#define PBMOE_GEMM_WAVES 4
+#endif
+constexpr int GEMM_WAVES = PBMOE_GEMM_WAVES; // waves per GEMM workgroup
+constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
+constexpr int WG_ROWS = 32 * GEMM_WAVES;      // weight rows per GEMM workgroup (32 per wave)
 constexpr float F16_SAFE = 16384.0f; // |hi| bound after the row scale
 
 // position of column c (0..7) inside an 8-column block in the K order
 __device__ __forceinline__ uint32_t kpos(uint32_t c) { return c < 4 ? 2 * c : 2 * (c - 4) + 1; }
 
-// (x & mask) | orv in one VALU op (the compiler splits it when both
-// constants would need the scalar constant bus)
+// (x & mask) | orv in one VALU op; written out because the compiler splits
+// it into two instructions with literal operands
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv)
 {
-    return (x & mask) | orv;
+    uint32_t d;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(x), "s"(mask), "v"(orv));
+    return d;
 }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
 // 8 nibbles of one word as exact f16 codes, in K order; `magic` is
-// 0x64006400 (f16 pair 1024, 1024) kept in a vector register
+// 0x64006400 (f16 pair 1024, 1024) kept in a vector register.  Nibbles
+// 0/4 and 2/6 (after one shift by 8) land in mantissa bits 0-3 (1024 + q,
+// minus 1024); nibbles 1/5 and 3/7 are masked in place into bits 4-7
+// (1024 + 16q) and recovered as (1024 + 16q) / 16 - 64 = q by one packed
+// FMA.  Every step is exact.
 __device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 {
-    uint32_t v[4];
-    v[0] = and_or(w, 0x000F000Fu, magic);
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        v[i] = and_or(w >> (4 * i), 0x000F000Fu, magic);
-    half8_t r = __builtin_bit_cast(half8_t, v);
-    return r - (_Float16)1024.0f;
+    const uint32_t w8 = w >> 8;
+    const half2_t off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2_t off16 = {(_Float16)-64.0f, (_Float16)-64.0f};
+    const half2_t v0 = __builtin_bit_cast(half2_t, and_or(w, 0x000F000Fu, magic)) + off;
+    const half2_t v1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, and_or(w, 0x00F000F0u, magic)),
+                                                 sixteenth, off16);
+    const half2_t v2 = __builtin_bit_cast(half2_t, and_or(w8, 0x000F000Fu, magic)) + off;
+    const half2_t v3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, and_or(w8, 0x00F000F0u, magic)),
+                                                 sixteenth, off16);
+    half8_t r;
+    r[0] = v0[0], r[1] = v0[1], r[2] = v1[0], r[3] = v1[1];
+    r[4] = v2[0], r[5] = v2[1], r[6] = v3[0], r[7] = v3[1];
+    return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -116,13 +137,16 @@ __global__ __launch_bounds__(64) void tile_table_kernel(const uint32_t* __restri
 // ---------------------------------------------------------------------------
 // split: one workgroup per token row.  hi/lo f16 of x * 2^-e in K order,
 // sums of x * 2^-e per 32 columns, rowscale = 2^e (e > 0 only for rows
-// whose magnitude would leave the f16 range).
+// whose magnitude would leave the f16 range), and whether any lo is nonzero
+// (rows of f16-valued inputs have lo == 0 throughout; the gate/up GEMM then
+// skips the lo products, which would add exact zeros).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, uint32_t cols,
                                                          uint16_t* __restrict__ hi,
                                                          uint16_t* __restrict__ lo,
                                                          float* __restrict__ sum32,
-                                                         float* __restrict__ rowscale)
+                                                         float* __restrict__ rowscale,
+                                                         uint32_t* __restrict__ lo_any)
 {
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
@@ -143,6 +167,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     if (threadIdx.x == 0)
         rowscale[t] = ldexpf(1.0f, e);
     // each wave handles 64-column groups; lane = column within the group
+    int any_lo = 0;
     for (uint32_t g = wv; g < cols / 64; g += 4) {
         const uint32_t c = g * 64 + lane;
         const float v = xr[c] * f;
@@ -151,6 +176,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
         const uint64_t o = (uint64_t)t * cols + (c & ~7u) + kpos(c & 7u);
         hi[o] = __builtin_bit_cast(uint16_t, h);
         lo[o] = __builtin_bit_cast(uint16_t, l);
+        any_lo |= l != (_Float16)0.0f;
         float s = v; // sums per 32 columns: lanes 0..31 and 32..63
         s += __shfl_xor(s, 1);
         s += __shfl_xor(s, 2);
@@ -160,6 +186,9 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
         if ((lane & 31) == 0)
             sum32[(uint64_t)t * (cols / 32) + g * 2 + (lane >> 5)] = s;
     }
+    any_lo = __syncthreads_or(any_lo);
+    if (threadIdx.x == 0)
+        lo_any[t] = any_lo ? 1u : 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -181,6 +210,7 @@ struct GemmArgs {
     const uint16_t* b_lo;
     const float* b_sum32;
     const float* rowscale;    // gate/up: per token; down: unused
+    const uint32_t* b_lo_any; // per B row: lo part not all zero (null: assume it is not)
     uint32_t kdim;            // H (gate/up) or I (down)
     uint32_t b_rows;          // rows of the B operand buffers
     // outputs
@@ -191,17 +221,21 @@ struct GemmArgs {
     uint32_t* status;
 };
 
-// LDS plan of one GEMM workgroup.  Staging: two buffers of the activation
-// tile of one quantisation group, [TOK tokens][64KS halfs + pad 8], the row
-// holding the group's hi and lo 16-byte chunks interleaved (chunk 2c = hi
-// chunk c, 2c + 1 = lo chunk c); the pad spreads the 16 token rows of a
-// fragment read over distinct banks.  The epilogue reuses the bytes for the
-// f32 output tile [TOK][256 + 4].
+// LDS plan of one GEMM workgroup.  Staging: NBUF buffers, each the
+// activation tile of one quantisation group, [TOK tokens][CH 16-byte
+// chunks], the group's hi and lo chunks interleaved (chunk 2c = hi chunk c,
+// 2c + 1 = lo chunk c) and chunk c of token row r stored at position
+// c ^ (r % CH), so that the rows of a fragment read fall on distinct bank
+// groups.  The tiles are written by direct global->LDS loads (one wave
+// instruction fills 1 KB, lane i bytes 16i .. 16i + 15), which is why the
+// layout is swizzled rather than padded.  The epilogue reuses the bytes for
+// the f32 output tile [TOK][WG_ROWS + 4].
 template <int KS>
 struct GemmLds {
-    static constexpr int XPITCH = 64 * KS + 8;
-    static constexpr int STAGE_HALFS = TOK * XPITCH;
-    static constexpr int STAGE_BYTES = 2 * STAGE_HALFS * 2;
+    static constexpr int CH = 8 * KS;            // 16-byte chunks per token row
+    static constexpr int NBUF = KS >= 4 ? 2 : 4; // groups resident (staged ahead: NBUF - 1)
+    static constexpr int TILE_BYTES = TOK * CH * 16;
+    static constexpr int STAGE_BYTES = NBUF * TILE_BYTES;
     static constexpr int OPITCH = WG_ROWS + 4;
     static constexpr int OUT_BYTES = TOK * OPITCH * 4;
     static constexpr int BYTES = STAGE_BYTES > OUT_BYTES ? STAGE_BYTES : OUT_BYTES;
@@ -247,7 +281,10 @@ __device__ __forceinline__ float sb_buf(rsrc_t r, uint32_t voff, uint32_t soff)
         return __half2float(__ushort_as_half(v));
 }
 
-// One workgroup: TOK tokens of one item x WG_ROWS weight rows, 8 waves.
+// One workgroup: TOK tokens of one item x WG_ROWS weight rows, GEMM_WAVES
+// waves; two workgroups per CU, so that the two waves sharing a SIMD belong
+// to different workgroups and their barriers do not lock them into the same
+// phase (one wave's VALU work then overlaps the other's MFMAs).
 // MFMA 32x32x16 f16: the activation tile is the A operand (32 tokens x 16 K
 // per fragment), the weights the B operand (16 K x 32 rows); wave w owns
 // rows 32w .. 32w+31 of the block, one row per lane (lane & 31), and both
@@ -265,7 +302,7 @@ __device__ __forceinline__ float sb_buf(rsrc_t r, uint32_t voff, uint32_t soff)
 // to back on one XCD and share the activation tile in its L2, and the next
 // tiles of the same expert find the expert's weights there.
 template <int SBT, bool GATEUP, int KS>
-__global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
+__global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs a)
 {
     using L = GemmLds<KS>;
     constexpr int NMAT = GATEUP ? 2 : 1;
@@ -313,43 +350,43 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
     const uint32_t K = a.kdim;
     const uint32_t G = K / (32 * KS), C32 = K / 32, WPR = K / 8;
 
-    // ---- staging role: 8 threads per token, KS of the token's 8KS chunks each ----
-    const uint32_t s_tok = tid >> 3, s_part = tid & 7;
-    const uint32_t s_n = n0 + s_tok;
-    const bool s_valid = s_n < cnt;
-    uint32_t s_row = 0;
-    if (s_valid)
-        s_row = GATEUP ? (shared ? s_n : a.src_rows[g0 + s_n]) : g0 + s_n;
-    const uint16_t* s_hi = a.b_hi + (uint64_t)s_row * K;
-    const uint16_t* s_lo = a.b_lo + (uint64_t)s_row * K;
-    if (s_part == 0) {
-        row_lds[s_tok] = s_valid ? s_row : 0xFFFFFFFFu;
+    // ---- staging: direct global->LDS loads, DW wave instructions per group;
+    //      instruction j fills chunk positions 64j .. 64j + 63 of the tile ----
+    constexpr int CH = L::CH, NBUF = L::NBUF, PF = NBUF - 1;
+    constexpr int DW = TOK * CH / 64 / GEMM_WAVES;
+    auto tok_row = [&](uint32_t n) -> uint32_t {
+        return GATEUP ? (shared ? n : a.src_rows[g0 + n]) : g0 + n;
+    };
+    int lo_flag = 0;
+    if (tid < TOK) {
+        const uint32_t n = n0 + tid;
+        const bool v = n < cnt;
+        const uint32_t r = v ? tok_row(n) : 0u;
+        row_lds[tid] = v ? r : 0xFFFFFFFFu;
         if (GATEUP)
-            rs_lds[s_tok] = s_valid ? a.rowscale[s_row] : 1.0f;
+            rs_lds[tid] = v ? a.rowscale[r] : 1.0f;
+        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[r] != 0u);
     }
-    // chunk numbering: the 16 lanes of a store (2 tokens x 8 parts) hit 16
-    // distinct bank groups of the padded rows
-    auto chunk_of = [&](int k) -> uint32_t {
-        if constexpr (KS == 1)
-            return s_part;
-        else
-            return 2 * s_part + (k & 1) + 16 * (k >> 1);
-    };
-    typedef uint4 Stage[KS];
-    Stage st_a, st_b;
-    auto stage_load = [&](uint32_t g, Stage& st) {
+    // whether any token row of the tile has a nonzero lo part; if none has,
+    // the lo products would all be exact zeros and are skipped
+    const bool tile_lo = __syncthreads_or(lo_flag) != 0;
+    const uint32_t first_row = tok_row(n0); // n0 < cnt
+    const uint16_t* dsrc[DW];               // this lane's chunk of each instruction, group 0
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const uint32_t c = chunk_of(k);
-            const uint16_t* src = ((c & 1) ? s_lo : s_hi) + g * 32 * KS + (c >> 1) * 8;
-            st[k] = s_valid ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto stage_store = [&](int buf, const Stage& st) {
-        uint16_t* row = reinterpret_cast<uint16_t*>(lds) + buf * L::STAGE_HALFS + s_tok * L::XPITCH;
+    for (int i = 0; i < DW; ++i) {
+        const uint32_t pos = 64 * (wv + GEMM_WAVES * i) + lane;
+        const uint32_t r = pos / CH, c = (pos % CH) ^ (r % CH);
+        const uint32_t n = n0 + r;
+        const uint32_t trow = n < cnt ? tok_row(n) : first_row; // rows past the item: any valid row
+        dsrc[i] = ((c & 1) ? a.b_lo : a.b_hi) + (uint64_t)trow * K + (c >> 1) * 8;
+    }
+    auto stage = [&](uint32_t g, int buf) {
 #pragma unroll
-        for (int k = 0; k < KS; ++k)
-            reinterpret_cast<uint4*>(row)[chunk_of(k)] = st[k];
+        for (int i = 0; i < DW; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(dsrc[i] + g * 32 * KS),
+                (__attribute__((address_space(3))) void*)(lds + buf * L::TILE_BYTES + 1024 * (wv + GEMM_WAVES * i)),
+                16, 0, 0);
     };
 
     // ---- compute role ----
@@ -362,8 +399,10 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
     const uint32_t s_soff[2] = {(uint32_t)p0.s_off, (uint32_t)p1.s_off};
     const uint32_t b_soff[2] = {(uint32_t)p0.b_off, (uint32_t)p1.b_off};
     const uint32_t magic = 0x64006400u;
-    uint32_t wa[NMAT][2 * KS], wb[NMAT][2 * KS], wc[NMAT][2 * KS];
-    auto w_load = [&](uint32_t g, uint32_t (&w)[NMAT][2 * KS]) {
+    typedef uint32_t Words[NMAT][2 * KS];
+    Words w0, w1; // codes of the even / odd group in flight
+    constexpr int WL = 2 * KS == 8 ? 2 : 1; // load instructions per w_load matrix
+    auto w_load = [&](uint32_t g, Words& w) {
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
             load_words<2 * KS>(wr, w_voff, w_soff[m] + g * 16 * KS, w[m]);
@@ -382,6 +421,14 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
         else
             return __half2float(__ushort_as_half(v));
     };
+    // fragment reads: row 32tf + n32 of the tile, chunk c = 2(h NSTEP + k) + hl
+    // at position c ^ (n32 % CH) (32tf is a multiple of CH)
+    uint32_t rd_off[NSTEP][2];
+#pragma unroll
+    for (int k = 0; k < NSTEP; ++k)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+            rd_off[k][hl] = (n32 * CH + ((2 * (h * NSTEP + k) + hl) ^ (n32 % CH))) * 16;
 
     float16_t acc[2][NMAT];
 #pragma unroll
@@ -392,26 +439,24 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
             for (int j = 0; j < 16; ++j)
                 acc[tf][m][j] = 0.0f;
 
-    // two-deep prefetch: at the top of step g the loads for g + 2 are issued
-    // (st_a, wc), the tile for g + 1 (st_b, one step old) is stored into the
-    // other LDS buffer at its end
-    stage_load(0, st_a);
-    w_load(0, wa);
-    s_load(0, spa);
-    stage_store(0, st_a);
-    if (G > 1) {
-        stage_load(1, st_b);
-        w_load(1, wb);
-    }
-    __syncthreads();
-    for (uint32_t g = 0; g < G; ++g) {
-        const int buf = g & 1;
-        if (g + 2 < G) {
-            stage_load(g + 2, st_a);
-            w_load(g + 2, wc);
-            if ((g & 1) == 0)
-                s_load(g + 2, spb);
-        }
+    // Pipeline (the loop is unrolled by NBUF, so buffers and registers have
+    // fixed roles).  Step g, buffer g % NBUF: stage group g + PF into buffer
+    // (g + PF) % NBUF, which held group g - 1 (read before the last barrier);
+    // unpack group g's codes from w[g & 1], then load group g + 2's codes into
+    // those registers; the MFMAs; wait until this wave's loads of group
+    // g + 1's tile have landed and meet the other waves at the barrier.
+    // Loads past the last group fetch group G - 1 again (never read), so
+    // every step issues the same instructions and the wait count below is
+    // exact: the instructions of steps g - 1 and g follow the staging of
+    // group g + 1.
+    auto clampg = [&](uint32_t g) -> uint32_t { return g < G ? g : G - 1; };
+    constexpr int VMW = (PF - 1) * (DW + NMAT * WL) + (PF >= 2 ? NMAT : 0);
+    auto step = [&](auto lo_tag, uint32_t g, int buf, Words& w) {
+        constexpr bool LO = decltype(lo_tag)::value; // lo products of the activations
+        constexpr int NHL = LO ? 2 : 1;
+        stage(clampg(g + PF), (buf + PF) % NBUF);
+        if ((g & 1) == 0)
+            s_load(g + 2 < G ? g + 2 : G - 2, spb);
         float sa[NMAT];
         half8_t wf[NMAT][NSTEP];
 #pragma unroll
@@ -419,23 +464,24 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
             sa[m] = s_of(spa[m], g);
 #pragma unroll
             for (int k = 0; k < NSTEP; ++k)
-                wf[m][k] = unpack8(wa[m][k], magic);
+                wf[m][k] = unpack8(w[m][k], magic);
         }
-        const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + buf * L::STAGE_HALFS;
+        w_load(clampg(g + 2), w);
+        const uint8_t* xb = lds + buf * L::TILE_BYTES;
 #pragma unroll
         for (int tf = 0; tf < 2; ++tf) {
-            const uint16_t* xr = xb + (32 * tf + n32) * L::XPITCH + 16 * (h * NSTEP);
             half8_t ah[NSTEP], al[NSTEP];
 #pragma unroll
             for (int k = 0; k < NSTEP; ++k) {
-                ah[k] = *reinterpret_cast<const half8_t*>(xr + 16 * k);
-                al[k] = *reinterpret_cast<const half8_t*>(xr + 16 * k + 8);
+                ah[k] = *reinterpret_cast<const half8_t*>(xb + tf * 32 * CH * 16 + rd_off[k][0]);
+                if constexpr (LO)
+                    al[k] = *reinterpret_cast<const half8_t*>(xb + tf * 32 * CH * 16 + rd_off[k][1]);
             }
             float16_t p[NMAT];
 #pragma unroll
             for (int k = 0; k < NSTEP; ++k)
 #pragma unroll
-                for (int hl = 0; hl < 2; ++hl)
+                for (int hl = 0; hl < NHL; ++hl)
 #pragma unroll
                     for (int m = 0; m < NMAT; ++m) {
                         float16_t c;
@@ -454,49 +500,85 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
                 for (int j = 0; j < 16; ++j)
                     acc[tf][m][j] = fmaf(sa[m], p[m][j], acc[tf][m][j]);
         }
-        if (g + 1 < G)
-            stage_store(buf ^ 1, st_b);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VMW) : "memory");
         __syncthreads();
+        if (g & 1) {
 #pragma unroll
-        for (int k = 0; k < KS; ++k)
-            st_b[k] = st_a[k];
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-#pragma unroll
-            for (int k = 0; k < 2 * KS; ++k) {
-                wa[m][k] = wb[m][k];
-                wb[m][k] = wc[m][k];
-            }
-            if (g & 1)
+            for (int m = 0; m < NMAT; ++m)
                 spa[m] = spb[m];
         }
-    }
+    };
+#pragma unroll
+    for (int d = 0; d < PF; ++d)
+        stage(clampg(d), d);
+    w_load(0, w0);
+    s_load(0, spa);
+    w_load(clampg(1), w1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    auto run = [&](auto lo_tag) {
+        for (uint32_t g = 0; g < G; g += NBUF) { // G is a multiple of NBUF
+#pragma unroll
+            for (int b = 0; b < NBUF; ++b)
+                step(lo_tag, g + b, b, (b & 1) ? w1 : w0);
+        }
+    };
+    if (tile_lo)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
+    // staging loads of the clamped tail may still be landing in LDS, which the
+    // epilogue reuses
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
 
     // ---- bias term on the matrix cores: acc += sum_g b[row][g] * xsum[token][g],
     //      K' = groups in steps of 16 (lane half h: groups k0 + 8h .. +8),
-    //      the group sums split into f16 hi + lo ----
+    //      the group sums split into f16 hi + lo.  Vector loads through buffer
+    //      resources (reads past a row are masked, past the buffer return 0) ----
+    const rsrc_t sum_r = make_rsrc(a.b_sum32, a.b_rows * C32 * 4);
     for (uint32_t k0 = 0; k0 < G; k0 += 16) {
+        const uint32_t gb = k0 + 8 * h; // first group of this lane half
         half8_t bw[NMAT];
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
+        for (int m = 0; m < NMAT; ++m) {
+            uint32_t b2[4]; // 8 consecutive 16-bit biases (4-byte aligned: G is even)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                b2[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff, b_soff[m] + gb * 2 + 4 * q, 0);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const uint32_t gg = k0 + 8 * h + j;
-                bw[m][j] = gg < G ? (_Float16)sb_buf<SBT>(wr, sb_voff, b_soff[m] + gg * 2) : (_Float16)0.0f;
+                const uint16_t raw = (uint16_t)(b2[j / 2] >> (16 * (j & 1)));
+                float bv;
+                if constexpr (SBT == 2)
+                    bv = __uint_as_float((uint32_t)raw << 16);
+                else
+                    bv = __half2float(__ushort_as_half(raw));
+                bw[m][j] = gb + j < G ? (_Float16)bv : (_Float16)0.0f;
             }
+        }
 #pragma unroll
         for (int tf = 0; tf < 2; ++tf) {
             const uint32_t brow = row_lds[32 * tf + n32];
+            const bool bvalid = brow != 0xFFFFFFFFu;
+            float sv[8 * KS]; // sums per 32 columns of groups gb .. gb + 7
+#pragma unroll
+            for (int q = 0; q < 2 * KS; ++q) {
+                const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(sum_r, (bvalid ? brow : 0u) * C32 * 4,
+                                                                       (gb * KS + 4 * q) * 4, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sv[4 * q + e] = __uint_as_float(v4[e]);
+            }
             half8_t xh, xl;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const uint32_t gg = k0 + 8 * h + j;
                 float v = 0.0f;
-                if (brow != 0xFFFFFFFFu && gg < G) {
 #pragma unroll
-                    for (int c = 0; c < KS; ++c)
-                        v += a.b_sum32[(uint64_t)brow * C32 + gg * KS + c];
-                }
+                for (int c = 0; c < KS; ++c)
+                    v += sv[j * KS + c];
+                if (!bvalid || gb + j >= G)
+                    v = 0.0f;
                 const _Float16 hv = (_Float16)v;
                 xh[j] = hv;
                 xl[j] = (_Float16)(v - (float)hv);
@@ -530,14 +612,16 @@ __global__ __launch_bounds__(512, 1) void q4_group_gemm_kernel(GemmArgs a)
             if constexpr (GATEUP) {
                 const float rs = rs_lds[tk];
                 const float gg = acc[tf][0][j] * rs, uu = acc[tf][1][j] * rs;
-                v = (gg / (1.0f + expf(-gg))) * uu;
+                // SiLU with the hardware exponential and reciprocal (relative
+                // error ~1e-6, far inside the layer tolerance)
+                v = __fdividef(gg, 1.0f + __expf(-gg)) * uu;
             } else {
                 v = acc[tf][0][j];
             }
             ot[tk * L::OPITCH + col] = v;
         }
     __syncthreads();
-    const uint32_t c_tok = tid >> 3, c_chunk = tid & 7; // rows 32 c_chunk .. +32
+    const uint32_t c_tok = tid / GEMM_WAVES, c_chunk = tid % GEMM_WAVES; // rows 32 c_chunk .. +32
     const uint32_t n = n0 + c_tok;
     if (n < cnt) {
         const float* src = ot + c_tok * L::OPITCH + 32 * c_chunk;
@@ -709,7 +793,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
                                         p.tile_count);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
-    split_rows_kernel<<<T, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale);
+    split_rows_kernel<<<T, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     if (has_shared && p.sgate_w) {
@@ -742,12 +826,13 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.b_lo = p.x_lo;
     a.b_sum32 = p.x_sum32;
     a.rowscale = p.rowscale;
+    a.b_lo_any = p.x_lo_any;
     a.kdim = H;
     a.b_rows = T;
     a.act_hi = p.act_hi;
     a.act_lo = p.act_lo;
     a.act_sum32 = p.act_sum32;
-    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(512), 0, st,
+    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(GEMM_THREADS), 0, st,
                           phase_event(p, 0), phase_event(p, 1), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
@@ -755,10 +840,11 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.b_lo = p.act_lo;
     a.b_sum32 = p.act_sum32;
     a.rowscale = nullptr;
+    a.b_lo_any = nullptr;
     a.kdim = I;
     a.b_rows = routes + T;
     a.y = p.y;
-    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(512), 0, st,
+    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(GEMM_THREADS), 0, st,
                           phase_event(p, 2), phase_event(p, 3), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
@@ -787,9 +873,13 @@ static hipError_t launch_prefill_sb(hipStream_t st, const PrefillArgs& p)
 
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs& p)
 {
-    // shapes the kernels assume: 256-row blocks of H and I, group = 2^shift,
-    // a shared expert in the routed experts' format
+    // shapes the kernels assume: WG_ROWS-row blocks of H and I, a multiple
+    // of NBUF quantisation groups along both (the group loop is unrolled by
+    // the number of staging buffers; 256 columns in every case), group =
+    // 2^shift, a shared expert in the routed experts' format
+    const uint32_t kmul = p.ex.group * (p.ex.group >= 128 ? 2u : 4u);
     if ((1u << p.ex.group_shift) != p.ex.group || p.hidden % WG_ROWS || p.ex.gate.rows % WG_ROWS ||
+        p.hidden % kmul || p.ex.gate.rows % kmul ||
         p.ex.gate.cols != p.hidden || p.ex.down.rows != p.hidden)
         return hipErrorInvalidValue;
     if (p.shared && (p.shared->group != p.ex.group || p.shared->sb_dtype != p.ex.sb_dtype ||
