@@ -444,30 +444,47 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     // (g + PF) % NBUF, which held group g - 1 (read before the last barrier);
     // unpack group g's codes from w[g & 1], then load group g + 2's codes into
     // those registers; the MFMAs; wait until this wave's loads of group
-    // g + 1's tile have landed and meet the other waves at the barrier.
-    // Loads past the last group fetch group G - 1 again (never read), so
-    // every step issues the same instructions and the wait count below is
-    // exact: the instructions of steps g - 1 and g follow the staging of
-    // group g + 1.
-    auto clampg = [&](uint32_t g) -> uint32_t { return g < G ? g : G - 1; };
+    // g + 1's tile have landed and meet the other waves at the barrier.  The
+    // last NBUF steps (TAIL) issue no loads past group G - 1.  Wait counts:
+    // the instructions of steps g - 1 and g were all issued after the
+    // staging of group g + 1 (the order inside one step is the compiler's).
     constexpr int VMW = (PF - 1) * (DW + NMAT * WL) + (PF >= 2 ? NMAT : 0);
-    auto step = [&](auto lo_tag, uint32_t g, int buf, Words& w) {
+    auto step = [&](auto lo_tag, uint32_t g, auto b_tag, auto tail_tag, Words& w) {
         constexpr bool LO = decltype(lo_tag)::value; // lo products of the activations
         constexpr int NHL = LO ? 2 : 1;
-        stage(clampg(g + PF), (buf + PF) % NBUF);
-        if ((g & 1) == 0)
-            s_load(g + 2 < G ? g + 2 : G - 2, spb);
+        constexpr int B = decltype(b_tag)::value;    // g % NBUF
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        constexpr bool ST = !TAIL || B + PF < NBUF;  // stage group g + PF
+        constexpr bool WLD = !TAIL || B + 2 < NBUF;  // codes of group g + 2
+        constexpr bool SLD = B % 2 == 0 && WLD;      // scales of groups g + 2, g + 3
+        // VMEM instructions of tail step b (b = -1: the steady step before)
+        constexpr auto cnt = [](int b) {
+            if (b < 0)
+                return DW + NMAT * WL;
+            return (b + PF < NBUF ? DW : 0) + (b % 2 == 0 && b + 2 < NBUF ? NMAT : 0) +
+                   (b + 2 < NBUF ? NMAT * WL : 0);
+        };
+        constexpr int WAIT = PF < 2 ? 0 : (TAIL ? cnt(B - 1) + cnt(B) : VMW);
+        if constexpr (ST)
+            stage(g + PF, (B + PF) % NBUF);
+        if constexpr (SLD)
+            s_load(g + 2, spb);
         float sa[NMAT];
         half8_t wf[NMAT][NSTEP];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             sa[m] = s_of(spa[m], g);
 #pragma unroll
-            for (int k = 0; k < NSTEP; ++k)
+            for (int k = 0; k < NSTEP; ++k) {
+                // keeps the unpack inside its step: without it the compiler
+                // hoists the unpacks of load-free tail steps and spills
+                asm volatile("" : "+v"(w[m][k]));
                 wf[m][k] = unpack8(w[m][k], magic);
+            }
         }
-        w_load(clampg(g + 2), w);
-        const uint8_t* xb = lds + buf * L::TILE_BYTES;
+        if constexpr (WLD)
+            w_load(g + 2, w);
+        const uint8_t* xb = lds + B * L::TILE_BYTES;
 #pragma unroll
         for (int tf = 0; tf < 2; ++tf) {
             half8_t ah[NSTEP], al[NSTEP];
@@ -500,37 +517,48 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
                 for (int j = 0; j < 16; ++j)
                     acc[tf][m][j] = fmaf(sa[m], p[m][j], acc[tf][m][j]);
         }
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VMW) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
         __syncthreads();
-        if (g & 1) {
+        if constexpr (B % 2 == 1) {
 #pragma unroll
             for (int m = 0; m < NMAT; ++m)
                 spa[m] = spb[m];
         }
     };
+    // prologue: the first PF tiles and two groups of codes (G >= NBUF > PF)
 #pragma unroll
     for (int d = 0; d < PF; ++d)
-        stage(clampg(d), d);
+        stage(d, d);
     w_load(0, w0);
     s_load(0, spa);
-    w_load(clampg(1), w1);
+    w_load(1, w1);
+
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    auto run = [&](auto lo_tag) {
-        for (uint32_t g = 0; g < G; g += NBUF) { // G is a multiple of NBUF
-#pragma unroll
-            for (int b = 0; b < NBUF; ++b)
-                step(lo_tag, g + b, b, (b & 1) ? w1 : w0);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    auto iter = [&](auto lo_tag, uint32_t g, auto tail_tag) {
+        step(lo_tag, g, I0{}, tail_tag, w0);
+        step(lo_tag, g + 1, I1{}, tail_tag, w1);
+        if constexpr (NBUF == 4) {
+            step(lo_tag, g + 2, I2{}, tail_tag, w0);
+            step(lo_tag, g + 3, I3{}, tail_tag, w1);
         }
+    };
+    auto run = [&](auto lo_tag) {
+        uint32_t g = 0;
+        for (; g + NBUF < G; g += NBUF) // G is a multiple of NBUF
+            iter(lo_tag, g, std::false_type{});
+        iter(lo_tag, g, std::true_type{});
     };
     if (tile_lo)
         run(std::true_type{});
     else
         run(std::false_type{});
-    // staging loads of the clamped tail may still be landing in LDS, which the
-    // epilogue reuses
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // the last step waited for every load and met the other waves: the
+    // staging buffers are free for the epilogue
 
     // ---- bias term on the matrix cores: acc += sum_g b[row][g] * xsum[token][g],
     //      K' = groups in steps of 16 (lane half h: groups k0 + 8h .. +8),
