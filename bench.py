@@ -238,9 +238,13 @@ def bench_prefill(args, cfg, ctx, ev) -> dict:
                 for j, nm in enumerate(names)}
     fl = prefill_flops(cfg, T, T * cfg.k)
     kernels = {nm: {"us": round(phase_us[nm], 3)} for nm in names}
+    # the GEMMs issue the activation hi and lo products; the gate/up GEMM skips
+    # the lo products of tiles whose activations are all f16 values (lo == 0)
+    x_f16 = bool(np.array_equal(xh.astype(np.float16).astype(np.float32), xh))
+    issue = {"gateup": 1 if x_f16 else 2, "down": 2}
     for nm in ("gateup", "down"):
         tf = fl[nm] / (phase_us[nm] * 1e-6) / 1e12
-        kernels[nm].update({"flops": fl[nm], "TFLOPs": round(tf, 1), "mfma_issued_TFLOPs": round(2 * tf, 1)})
+        kernels[nm].update({"flops": fl[nm], "TFLOPs": round(tf, 1), "mfma_issued_TFLOPs": round(issue[nm] * tf, 1)})
     total_tf = (fl["gateup"] + fl["down"]) / (us_step * 1e-6) / 1e12
     print(f"[bench] prefill {cfg.name} T={T}: {us_step:.1f} us/layer, {total_tf:.1f} TFLOP/s; kernels (us): "
           + ", ".join(f"{k} {v:.1f}" for k, v in phase_us.items()), file=sys.stderr, flush=True)
@@ -260,7 +264,8 @@ def bench_prefill(args, cfg, ctx, ev) -> dict:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 MFMA (exact 4-bit codes x f16 hi+lo activations), f32 accumulate",
+        "dtype": "f16 MFMA (exact 4-bit codes x f16 hi+lo activations; lo products skipped where the "
+                 "activations are f16 values), f32 accumulate",
         "data": "synthetic",
         "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden, "experts": cfg.experts, "k": cfg.k,
                    "intermediate": cfg.intermediate, "shared_intermediate": cfg.shared_intermediate,
@@ -270,7 +275,8 @@ def bench_prefill(args, cfg, ctx, ev) -> dict:
         "roofline": {"bound": "mfma", "achieved": g["TFLOPs"], "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(g["TFLOPs"] / MFMA_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "q4_group_gemm_kernel (gate/up)", "flops_per_launch": g["flops"],
-                     "launch_us": g["us"], "mfma_issued_frac": round(g["mfma_issued_TFLOPs"] / MFMA_PEAK_TFLOPS, 4)},
+                     "launch_us": g["us"], "mfma_issued_frac": round(g["mfma_issued_TFLOPs"] / MFMA_PEAK_TFLOPS, 4),
+                     "activations_f16_valued": x_f16},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
@@ -325,7 +331,7 @@ def main() -> int:
         return 2
 
     from pb_amd import abi
-    from pb_amd.configs import CONFIGS, algorithmic_bytes, decode_phase_bytes
+    from pb_amd.configs import CONFIGS, algorithmic_bytes, decode_phase_bytes, down_prefetch_bytes
 
     cfg = CONFIGS[args.config]
     T = args.tokens
@@ -425,6 +431,9 @@ def main() -> int:
     dominant = max(phase_us, key=phase_us.get)
     dom_gbps = kernels[dominant]["GBps"]
     traffic, traffic_src = load_traffic(dominant, cfg.name)
+    # route_gateup_kernel also touches the down weights of the selected
+    # experts (prefetch for down_combine_kernel); its traffic includes them
+    pf_bytes = down_prefetch_bytes(cfg, int(round(u_mean)), T) if dominant == "gateup" else 0
 
     cpu = None
     if not args.no_cpu:
@@ -456,7 +465,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": dom_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": KERNEL_NAMES[dominant], "bytes_per_launch": ph_bytes[dominant],
-                     "launch_us": kernels[dominant]["us"], "traffic_source": traffic_src},
+                     "launch_us": kernels[dominant]["us"], "traffic_source": traffic_src,
+                     "prefetch_bytes": pf_bytes},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

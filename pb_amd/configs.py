@@ -68,3 +68,21 @@ def decode_phase_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> dict
     if Is:
         down += q4_proj_bytes(H, Is, g) + T * Is * 4
     return {"stage": stage, "gateup": gateup, "down": down}
+
+
+def down_prefetch_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:
+    """Bytes of down weights (codes, scales, biases) that route_gateup_kernel
+    touches for down_combine_kernel: the selected experts and the shared
+    expert, when they total at most 16 MiB and the gate/up grid leaves room
+    for the prefetch workgroups (the host rule in pbmoe_decode.hip)."""
+    H, I, g = cfg.hidden, cfg.intermediate, cfg.group
+    max_items = min(cfg.experts, tokens * cfg.k) if tokens > 1 else tokens * cfg.k
+    items_bound = max_items + (1 if cfg.shared_intermediate else 0)
+    if items_bound * H * (I // 2 + 4 * (I // g)) > (16 << 20):
+        return 0
+    wgs = ((max_items * (I // 2) + 3) // 4 + 7) // 8 * 8
+    if wgs >= 768:
+        return 0
+    items = unique_experts + (1 if cfg.shared_intermediate else 0)
+    return items * H * (I // 2 + 4 * (I // g))
+
