@@ -1,12 +1,12 @@
 // Layer-major prefill of the MoE block on gfx950: a grouped Q4 GEMM on the
-// matrix cores (v_mfma_f32_16x16x32_f16).  It replaces the reference's
+// matrix cores (v_mfma_f32_32x32x16_f16).  It replaces the reference's
 // per-expert batched matvecs for many-token chunks
 // (q4_mmap_fma_matvec_batch_*, metal/qwen/shaders.metal:973-1057, driven by
 // qwen_layer_major_experts, metal/mod.rs:3583-4106).
 //
 // Arithmetic.  The 4-bit codes q in [0, 15] enter the MFMA as exact f16
 // values (0x6400 | q is the f16 number 1024 + q; subtracting 1024 is exact),
-// and each 32-wide K-step of an MFMA lies inside one quantisation group.  A
+// and each 16-wide K-step of an MFMA lies inside one quantisation group.  A
 // group's partial product P = sum(q * x) is therefore formed in f32 and the
 // group scale and bias are applied outside the MFMA:
 //     row . x = sum_g  s_g * P_g + b_g * sum_{c in g} x_c
@@ -24,9 +24,11 @@
 // Kernels (one layer, T tokens, K routes per token, U used experts):
 //   tile_table: per used expert ceil(count / 64) tiles (+ shared expert)
 //   split:      x [T][H] f32 -> hi, lo f16 (K order above), sums per 32
-//               columns, row scale
+//               columns, row scale, whether the row's lo part is nonzero
 //   gemm<gate/up>: per (tile, 128-row block of I): gate and up, SiLU(g)*u,
-//               act hi/lo f16 (K order) + sums per 32 rows
+//               act hi/lo f16 (K order) + sums per 32 rows; tiles whose
+//               rows all have lo == 0 (f16-valued inputs) skip the lo
+//               products, which would add exact zeros
 //   gemm<down>: per (tile, 128-row block of H): y [route][H] f32
 //   combine:    h = (r + sum_k w_k y_k) + sw * S in route order, optional
 //               next-layer RMSNorm
