@@ -282,6 +282,72 @@ int pbmoe_q4_dequantize(pbmoe_ctx* ctx, const void* packed, const void* scales,
 int pbmoe_synth_fill_q4(pbmoe_ctx* ctx, void* slots_device, const pbmoe_q4_layout* layout,
                         uint32_t hidden, uint32_t intermediate, uint64_t seed, uint32_t tensor,
                         uint32_t layer, uint32_t first_expert, uint32_t count);
+/* Zero-mean variant of the filled slots: bias -= 7.5 * scale for every group
+ * of the three projections (rounded to the scale/bias dtype), as an affine
+ * quantisation of zero-mean weights gives; the multi-layer decode stack uses
+ * it so that its activations stay bounded across layers. */
+int pbmoe_synth_center_q4(pbmoe_ctx* ctx, void* slots_device, const pbmoe_q4_layout* layout,
+                          uint32_t hidden, uint32_t intermediate, uint32_t count);
+
+/* ---- GQA full attention, batch-1 decode (the layer before each MoE block)
+ * Replaces the Qwen full-attention step of the decode loop:
+ * full_attention_output_values (flashmoe/runtime/mod.rs:2215-2367): q/k/v
+ * resident Q4 projections, per-head q/k RMSNorm + split-half RoPE
+ * (apply_optional_per_head_rms_norm_and_split_half_rope, math.rs:252-325),
+ * the KV record of this position (KvCache, state/kv_cache.rs:456-480),
+ * causal attention over positions 0..position (causal_attention,
+ * math.rs:671-707, softmax_in_place math.rs:728-744); then the o_proj
+ * projection and residual add, and the post-attention RMSNorm that feeds the
+ * MoE block (add_in_place + rms_norm_with_model_weight, runtime/mod.rs
+ * :2979-2996; residual_add_rms_norm, metal/qwen/shaders.metal:1239-1283). */
+typedef struct pbmoe_attn_desc {
+    uint32_t hidden;       /* H */
+    uint32_t q_heads;      /* num_attention_heads */
+    uint32_t kv_heads;     /* num_key_value_heads (q_heads multiple, <= 8 q per kv) */
+    uint32_t head_dim;     /* 128 */
+    uint32_t rotary_dim;   /* == head_dim (split-half pairs (i, i + head_dim/2)) */
+    float rope_theta;      /* theta.max(1.0) as f32 (1e6 for Qwen3) */
+    float norm_epsilon;    /* post-attention RMSNorm epsilon; q/k norms use 1e-6 */
+    uint32_t max_context;  /* KV cache positions */
+    uint32_t group_size;   /* Q4 group of the four projections */
+    uint32_t scale_bias_dtype; /* PBMOE_DTYPE_F16 or PBMOE_DTYPE_BF16 */
+} pbmoe_attn_desc;
+
+/* One resident Q4 projection [rows][cols]: codes rows*cols/2 bytes (low
+ * nibble = even column), scale and bias [rows][cols/group] 2-byte each
+ * (the q4_mmap_fma_matvec_bf16_scale_bias operand, shaders.metal:488-660). */
+typedef struct pbmoe_q4_matrix {
+    const void* codes;
+    const void* scales;
+    const void* biases;
+} pbmoe_q4_matrix;
+
+/* q [q_heads*head_dim][H], k and v [kv_heads*head_dim][H], o [H][q_heads*
+ * head_dim]; q_norm / k_norm [head_dim] f32 (self_attn.q_norm / k_norm, both
+ * required as in the reference).  All device memory, referenced. */
+typedef struct pbmoe_attn_weights {
+    pbmoe_q4_matrix q, k, v, o;
+    const float* q_norm;
+    const float* k_norm;
+} pbmoe_attn_weights;
+
+/* Bind attention layer `layer` and allocate its KV cache (f16, keys and
+ * values [max_context][kv_heads][head_dim] each, zeroed). */
+int pbmoe_bind_attention(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_attn_desc* desc,
+                         const pbmoe_attn_weights* weights);
+int pbmoe_unbind_attention(pbmoe_ctx* ctx, uint32_t layer);
+/* Device pointers of the layer's KV cache (keys, values). */
+int pbmoe_attention_kv_cache(pbmoe_ctx* ctx, uint32_t layer, void** keys, void** values);
+/* One token at `position`: normed [H] (x after input_layernorm) -> attention
+ * over positions 0..position (this position's k/v written to the cache
+ * first) -> o_proj; hidden_out [H] = residual + o; when post_norm_weight is
+ * not NULL, post_normed_out [H] = RMSNorm(hidden_out) * post_norm_weight.
+ * attn_out [q_heads*head_dim] (optional, may be NULL) receives the attention
+ * values before o_proj.  All pointers are device memory. */
+int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float* normed,
+                           const float* residual, uint32_t position, float* hidden_out,
+                           const float* post_norm_weight, float* post_normed_out,
+                           float* attn_out);
 
 #ifdef __cplusplus
 }

@@ -327,6 +327,61 @@ def route_rows(logits: np.ndarray, k: int, kind: int = ROUTING_SOFTMAX, order: i
     return ids, w
 
 
+# ---- GQA attention of the decode stack ----------------------------------------
+
+def qk_norm_rope(values, heads: int, head_dim: int, weight, position: int, rotary_dim: int,
+                 theta: float) -> np.ndarray:
+    """apply_optional_per_head_rms_norm_and_split_half_rope (math.rs:252-325)."""
+    v = _f32(values).copy()
+    w = _f32(weight) if weight is not None else None
+    lib().or_qk_norm_rope(_p(v), C.c_int(heads), C.c_int(head_dim), _p(w) if w is not None else None,
+                          C.c_int(position), C.c_int(rotary_dim), C.c_float(theta))
+    return v
+
+
+def causal_attention(q, keys, values, q_heads: int, kv_heads: int, head_dim: int) -> np.ndarray:
+    """causal_attention (math.rs:671-707); keys/values [n][kv_heads*head_dim]."""
+    qq, kk, vv = _f32(q), _f32(keys), _f32(values)
+    n = kk.size // (kv_heads * head_dim) if kv_heads * head_dim else 0
+    out = np.zeros(q_heads * head_dim, np.float32)
+    lib().or_causal_attention(_p(qq), _p(kk), _p(vv), C.c_int(n), C.c_int(q_heads), C.c_int(kv_heads),
+                              C.c_int(head_dim), _p(out))
+    return out
+
+
+class AttnOracle:
+    """One attention layer of the decode stack with its own f32 copy of the
+    f16 KV cache (or_attention_decode: runtime/mod.rs:2215-2367 + o_proj).
+    mats: dict q/k/v/o -> (codes u8, scales u16, biases u16)."""
+
+    def __init__(self, mats: dict, q_norm, k_norm, hidden: int, q_heads: int, kv_heads: int,
+                 head_dim: int, theta: float, group: int, sb_dtype: int, max_context: int):
+        self.mats = {k: tuple(np.ascontiguousarray(a) for a in v) for k, v in mats.items()}
+        self.q_norm, self.k_norm = _f32(q_norm), _f32(k_norm)
+        self.H, self.qh, self.kvh, self.hd = hidden, q_heads, kv_heads, head_dim
+        self.theta, self.group, self.sb = theta, group, sb_dtype
+        self.cache_k = np.zeros((max_context, kv_heads * head_dim), np.float32)
+        self.cache_v = np.zeros((max_context, kv_heads * head_dim), np.float32)
+
+    def decode(self, normed, position: int):
+        """Returns (attention values [q_heads*head_dim], o [H])."""
+        order = ("q", "k", "v", "o")
+        codes = (C.c_void_p * 4)(*[self.mats[n][0].ctypes.data for n in order])
+        scales = (C.c_void_p * 4)(*[self.mats[n][1].ctypes.data for n in order])
+        biases = (C.c_void_p * 4)(*[self.mats[n][2].ctypes.data for n in order])
+        x = _f32(normed)
+        att = np.zeros(self.qh * self.hd, np.float32)
+        o = np.zeros(self.H, np.float32)
+        rc = lib().or_attention_decode(codes, scales, biases, C.c_int(self.sb), C.c_int(self.group),
+                                       _p(self.q_norm), _p(self.k_norm), C.c_int(self.H), C.c_int(self.qh),
+                                       C.c_int(self.kvh), C.c_int(self.hd), C.c_int(self.hd),
+                                       C.c_float(self.theta), C.c_int(position), _p(x), _p(self.cache_k),
+                                       _p(self.cache_v), _p(att), _p(o))
+        if rc != 0:
+            raise RuntimeError(f"or_attention_decode failed ({rc})")
+        return att, o
+
+
 def _declare():
     L = lib()
     L.or_routing_top_k.restype = C.c_int

@@ -17,6 +17,11 @@
  *   routing_top_k_iter / top_k / softmax / sigmoid-noaux / renormalise /
  *   validate / dequant / q4 matvec / swiglu / rms norm / group plan:
  *     reference golden vectors plus brute-force and closed-form checks.
+ *   or_qk_norm_rope / or_causal_attention / or_attention_decode (the GQA
+ *     attention layer of the decode stack): the reference's golden attention
+ *     vector (tests/scheduler.rs:826-860), f64 brute force, RoPE closed forms
+ *     (identity at position 0, norm preservation per pair, the i = 0
+ *     frequency equals the position) and the softmax/GQA invariants.
  *   or_routing_sigmoid_grouped_top_k (DeepSeek-V3 group-limited routing):
  *     no reference implementation exists; pinned only by its n_group=1
  *     reduction to routing_sigmoid_noaux_top_k and by brute-force invariants
@@ -755,3 +760,131 @@ int or_moe_block_f64(const or_q4_layout* lay, const uint8_t* slots, int experts,
     }
     return OR_OK;
 }
+
+/* ---- GQA attention of the decode stack ----------------------------------- */
+
+/* Per-head RMSNorm with weight then split-half RoPE:
+ * apply_optional_per_head_rms_norm_and_split_half_rope (math.rs:252-301)
+ * with the rotations of split_half_rope_rotations (math.rs:303-325):
+ * inv_freq = theta^(-(2i)/rotary_dim) and angle = position * inv_freq in
+ * f32, (sin, cos) of that f32 angle; value *= scale * weight[d] with
+ * scale = 1 / sqrt(mean(v^2) + 1e-6); pairs (i, i + rotary_dim / 2).
+ * weight NULL: no norm. */
+void or_qk_norm_rope(float* v, int heads, int head_dim, const float* weight, int position,
+                     int rotary_dim, float theta)
+{
+    if (theta < 1.0f)
+        theta = 1.0f;
+    if (head_dim < 2)
+        head_dim = 2;
+    int rot = rotary_dim < head_dim ? rotary_dim : head_dim;
+    rot -= rot % 2;
+    const int half = rot / 2;
+    float* sn = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    float* cs = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    for (int i = 0; i < half; ++i) {
+        const float inv = powf(theta, -((float)(2 * i)) / (float)(rot > 0 ? rot : 1));
+        const float ang = (float)position * inv;
+        sn[i] = sinf(ang);
+        cs[i] = cosf(ang);
+    }
+    for (int h = 0; h < heads; ++h) {
+        float* x = v + (size_t)h * head_dim;
+        if (weight) {
+            float ms = 0.0f;
+            for (int d = 0; d < head_dim; ++d)
+                ms = ms + x[d] * x[d];
+            ms = ms / (float)head_dim;
+            const float scale = 1.0f / sqrtf(ms + 1e-6f);
+            for (int d = 0; d < head_dim; ++d)
+                x[d] = x[d] * (scale * weight[d]);
+        }
+        for (int i = 0; i < half; ++i) {
+            const float x0 = x[i], x1 = x[i + half];
+            x[i] = x0 * cs[i] - x1 * sn[i];
+            x[i + half] = x0 * sn[i] + x1 * cs[i];
+        }
+    }
+    free(sn);
+    free(cs);
+}
+
+/* causal_attention (math.rs:671-707): for every q head, scores over the n
+ * rows of keys [n][kv_heads*head_dim] (sum of q*k in order, times
+ * 1/sqrt(head_dim)), softmax_in_place (math.rs:728-744), then the weighted
+ * sum of the value rows; q head h reads kv head h / (q_heads / kv_heads). */
+void or_causal_attention(const float* q, const float* keys, const float* values, int n, int q_heads,
+                         int kv_heads, int head_dim, float* out)
+{
+    const int qw = q_heads * head_dim, kvw = kv_heads * head_dim;
+    for (int i = 0; i < qw; ++i)
+        out[i] = 0.0f;
+    if (n <= 0 || q_heads <= 0 || head_dim <= 0)
+        return;
+    const int groups = q_heads / (kv_heads > 0 ? kv_heads : 1);
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)n);
+    for (int qh = 0; qh < q_heads; ++qh) {
+        const int kh = qh / (groups > 0 ? groups : 1);
+        const float* qs = q + (size_t)qh * head_dim;
+        for (int t = 0; t < n; ++t) {
+            const float* ks = keys + (size_t)t * kvw + (size_t)kh * head_dim;
+            float s = 0.0f;
+            for (int d = 0; d < head_dim; ++d)
+                s = s + qs[d] * ks[d];
+            sc[t] = s * scale;
+        }
+        or_softmax_in_place(sc, n);
+        float* o = out + (size_t)qh * head_dim;
+        for (int t = 0; t < n; ++t) {
+            const float* vs = values + (size_t)t * kvw + (size_t)kh * head_dim;
+            for (int d = 0; d < head_dim; ++d)
+                o[d] = o[d] + sc[t] * vs[d];
+        }
+    }
+    free(sc);
+}
+
+static float or_f16_round(float x)
+{
+    return pbm_f16_to_f32(pbm_f32_to_f16(x));
+}
+
+/* One decode token through the attention layer (full_attention_output_values,
+ * runtime/mod.rs:2215-2367, then the o_proj projection of the decode loop):
+ * q, k, v = Q4 projections of `normed` (q4_fma_matvec form); per-head q/k
+ * norm + RoPE at `position`; k and v rounded to f16 (the KV cache format)
+ * into cache row `position` (the cache holds the f16 values as f32,
+ * [rows][kv_heads*head_dim]); causal attention over rows 0..position;
+ * o_out = W_o . attention.  Matrices: q [qh*hd][H], k/v [kvh*hd][H],
+ * o [H][qh*hd], codes + 2-byte scale/bias (sb_dtype). */
+int or_attention_decode(const uint8_t* const* codes, const void* const* scales, const void* const* biases,
+                        int sb_dtype, int group, const float* q_norm, const float* k_norm, int hidden,
+                        int q_heads, int kv_heads, int head_dim, int rotary_dim, float theta, int position,
+                        const float* normed, float* cache_k, float* cache_v, float* attn_out, float* o_out)
+{
+    const int qw = q_heads * head_dim, kvw = kv_heads * head_dim;
+    float* q = (float*)malloc(sizeof(float) * (size_t)qw);
+    float* k = (float*)malloc(sizeof(float) * (size_t)kvw);
+    float* v = (float*)malloc(sizeof(float) * (size_t)kvw);
+    int rc = or_q4_fma_matvec(codes[0], normed, scales[0], biases[0], sb_dtype, qw, hidden, group, q);
+    if (rc == OR_OK)
+        rc = or_q4_fma_matvec(codes[1], normed, scales[1], biases[1], sb_dtype, kvw, hidden, group, k);
+    if (rc == OR_OK)
+        rc = or_q4_fma_matvec(codes[2], normed, scales[2], biases[2], sb_dtype, kvw, hidden, group, v);
+    if (rc == OR_OK) {
+        or_qk_norm_rope(q, q_heads, head_dim, q_norm, position, rotary_dim, theta);
+        or_qk_norm_rope(k, kv_heads, head_dim, k_norm, position, rotary_dim, theta);
+        for (int i = 0; i < kvw; ++i) {
+            cache_k[(size_t)position * kvw + i] = or_f16_round(k[i]);
+            cache_v[(size_t)position * kvw + i] = or_f16_round(v[i]);
+        }
+        or_causal_attention(q, cache_k, cache_v, position + 1, q_heads, kv_heads, head_dim, attn_out);
+        rc = or_q4_fma_matvec(codes[3], attn_out, scales[3], biases[3], sb_dtype, hidden, qw, group, o_out);
+    }
+    free(q);
+    free(k);
+    free(v);
+    return rc;
+}
+

@@ -79,6 +79,25 @@ class LayerDesc(C.Structure):
 
 _P = C.c_void_p
 _U32 = C.c_uint32
+class AttnDesc(C.Structure):
+    """pbmoe_attn_desc."""
+    _fields_ = [("hidden", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32),
+                ("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32), ("rope_theta", C.c_float),
+                ("norm_epsilon", C.c_float), ("max_context", C.c_uint32), ("group_size", C.c_uint32),
+                ("scale_bias_dtype", C.c_uint32)]
+
+
+class Q4Matrix(C.Structure):
+    """pbmoe_q4_matrix (device pointers)."""
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p)]
+
+
+class AttnWeights(C.Structure):
+    """pbmoe_attn_weights (device pointers)."""
+    _fields_ = [("q", Q4Matrix), ("k", Q4Matrix), ("v", Q4Matrix), ("o", Q4Matrix),
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+
+
 _SIG = {
     "pbmoe_abi_version": ([], C.c_int),
     "pbmoe_last_error": ([], C.c_char_p),
@@ -107,6 +126,11 @@ _SIG = {
     "pbmoe_dispatch_plan": ([_P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_q4_dequantize": ([_P, _P, _P, _P, _U32, _U32, _U32, _U32, _P], C.c_int),
     "pbmoe_synth_fill_q4": ([_P, _P, C.POINTER(Q4Layout), _U32, _U32, C.c_uint64, _U32, _U32, _U32, _U32], C.c_int),
+    "pbmoe_synth_center_q4": ([_P, _P, C.POINTER(Q4Layout), _U32, _U32, _U32], C.c_int),
+    "pbmoe_bind_attention": ([_P, _U32, C.POINTER(AttnDesc), C.POINTER(AttnWeights)], C.c_int),
+    "pbmoe_unbind_attention": ([_P, _U32], C.c_int),
+    "pbmoe_attention_kv_cache": ([_P, _U32, C.POINTER(_P), C.POINTER(_P)], C.c_int),
+    "pbmoe_attention_decode": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P], C.c_int),
 }
 
 _lib: C.CDLL | None = None

@@ -3,6 +3,7 @@
 C1  CPU-runnable single layer: H2048, E128, K8 softmax renormalised, I768.
 C2  Qwen3-Next decode: H2048, E512, K10, I512 + sigmoid-gated shared I512.
 C3  prefill of 2048 tokens through the C1 layer with drawn Zipf(1.1) logits.
+C4  48 decode layers: GQA attention (C4_ATTN) + the C1 MoE layer, context 4096.
 C5  DeepSeek-V3 shape: H7168, E256, K8 sigmoid, 8 groups / topk_group 4,
     per-expert selection bias, I2048 + shared I2048 (ungated), routed
     scale 2.5 (the DeepSeek-V3 routed_scaling_factor; BASELINE leaves it open).
@@ -11,7 +12,7 @@ All: 4-bit affine, group 64, f16 scale/bias.
 from __future__ import annotations
 
 from .abi import (NORM_RENORMALIZE_SELECTED, ROUTING_SIGMOID_GROUPED, ROUTING_SOFTMAX_TOPK, DTYPE_F16)
-from .synth import MoeConfig
+from .synth import AttnConfig, MoeConfig
 
 C1 = MoeConfig("c1_decode", hidden=2048, intermediate=768, experts=128, k=8,
                routing=ROUTING_SOFTMAX_TOPK, normalization=NORM_RENORMALIZE_SELECTED, sb_dtype=DTYPE_F16)
@@ -26,6 +27,13 @@ C5 = MoeConfig("c5_deepseekv3_decode", hidden=7168, intermediate=2048, experts=2
                n_group=8, topk_group=4, shared_intermediate=2048, shared_gated=False, sb_dtype=DTYPE_F16)
 
 CONFIGS = {c.name: c for c in (C1, C2, C3, C5)}
+
+# C4: 48-layer decode stack of C1-shaped MoE layers, each preceded by GQA
+# attention (32 q heads, 4 kv heads, head_dim 128, f16 KV cache, context
+# 4096, RMSNorm eps 1e-6, RoPE theta 1e6), Q4 g64 projections, batch 1.
+C4_ATTN = AttnConfig("c4_attention", hidden=2048, q_heads=32, kv_heads=4, head_dim=128, rope_theta=1e6,
+                     group=64, sb_dtype=DTYPE_F16, max_context=4096)
+C4_LAYERS = 48
 
 
 def algorithmic_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:

@@ -83,17 +83,26 @@ struct LayerBinding {
     DeviceBuf gate_owned;
 };
 
+// Attention layer: weights referenced, KV cache and rotary table owned.
+struct AttnBinding {
+    pbmoe_attn_desc desc{};
+    pbmoe::AttnArgs base{}; // weights, shapes, cache pointers
+    DeviceBuf cache_k, cache_v, inv_freq;
+};
+
 } // namespace
 
 struct pbmoe_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     std::map<uint32_t, LayerBinding> layers;
+    std::map<uint32_t, AttnBinding> attn;
     uint32_t* status = nullptr; // device status word
     DeviceBuf logits, act, act_shared, shared_weight, plan;
     DeviceBuf route_ids, route_w;
     DeviceBuf prefill; // prefill scratch (operand splits, activations, y)
     DeviceBuf plan_work; // multi-workgroup plan scratch of pbmoe_dispatch_plan
+    DeviceBuf attn_scratch; // q/k/v, chunk partials and attention values of one decode step
     hipEvent_t phase_ev[6] = {};
     bool phase_timing = false;
 };
@@ -424,9 +433,14 @@ PBMOE_API int pbmoe_ctx_destroy(pbmoe_ctx* ctx)
         free_buf(kv.second.shared_owned);
         free_buf(kv.second.gate_owned);
     }
+    for (auto& kv : ctx->attn) {
+        free_buf(kv.second.cache_k);
+        free_buf(kv.second.cache_v);
+        free_buf(kv.second.inv_freq);
+    }
     for (DeviceBuf* b : {&ctx->logits, &ctx->act, &ctx->act_shared, &ctx->shared_weight,
                          &ctx->plan, &ctx->route_ids, &ctx->route_w, &ctx->prefill,
-                         &ctx->plan_work})
+                         &ctx->plan_work, &ctx->attn_scratch})
         free_buf(*b);
     (void)hipFree(ctx->status);
     (void)hipStreamDestroy(ctx->stream);
@@ -1130,3 +1144,219 @@ PBMOE_API int pbmoe_synth_fill_q4(pbmoe_ctx* ctx, void* slots_device,
                                      layer, first_expert, count));
     return ok();
 }
+
+PBMOE_API int pbmoe_synth_center_q4(pbmoe_ctx* ctx, void* slots_device, const pbmoe_q4_layout* layout,
+                                    uint32_t hidden, uint32_t intermediate, uint32_t count)
+{
+    if (!ctx || !slots_device || !layout)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_layout(layout, hidden, intermediate);
+    if (rc)
+        return rc;
+    if ((rc = set_device(ctx)))
+        return rc;
+    uint64_t off[9];
+    for (int i = 0; i < 9; ++i)
+        off[i] = layout->components[i].offset;
+    HIP_TRY(pbmoe::launch_synth_center(ctx->stream, static_cast<uint8_t*>(slots_device), layout->expert_bytes,
+                                       off, hidden, intermediate, layout->group_size,
+                                       layout->scale_bias_dtype, count));
+    return ok();
+}
+
+// ---- GQA decode attention --------------------------------------------------
+
+namespace {
+
+constexpr uint32_t ATTN_HEAD_DIM = 128;
+
+int attn_matrix(const pbmoe_q4_matrix& m, uint32_t rows, uint32_t cols, const char* name,
+                pbmoe::Q4Mat* out)
+{
+    if (!m.codes || !m.scales || !m.biases)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "attention %s projection has a null component", name);
+    if (!aligned(m.codes, 16) || !aligned(m.scales, 2) || !aligned(m.biases, 2))
+        return fail(PBMOE_ERR_ALIGNMENT,
+                    "attention %s projection: codes must be 16-byte and scales/biases 2-byte aligned", name);
+    out->codes = static_cast<const uint8_t*>(m.codes);
+    out->scales = static_cast<const uint8_t*>(m.scales);
+    out->biases = static_cast<const uint8_t*>(m.biases);
+    out->rows = rows;
+    out->cols = cols;
+    return ok();
+}
+
+} // namespace
+
+// full_attention_output_values (runtime/mod.rs:2215-2367) state of one
+// layer: FullAttentionLayout shape checks (the kernels' limits explicitly
+// rejected), the KV cache of the layer (KvCache, state/kv_cache.rs) and the
+// rotary table of split_half_rope_rotations (math.rs:303-325).
+PBMOE_API int pbmoe_bind_attention(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_attn_desc* desc,
+                                   const pbmoe_attn_weights* w)
+{
+    if (!ctx || !desc || !w)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    const pbmoe_attn_desc d = *desc;
+    if (d.head_dim != ATTN_HEAD_DIM || d.rotary_dim != d.head_dim)
+        return fail(PBMOE_ERR_UNSUPPORTED, "attention head_dim=%u rotary_dim=%u: head_dim 128 with full "
+                    "split-half rotary is implemented", d.head_dim, d.rotary_dim);
+    if (d.kv_heads == 0 || d.q_heads == 0 || d.q_heads % d.kv_heads)
+        return fail(PBMOE_ERR_SHAPE, "q_heads=%u must be a non-zero multiple of kv_heads=%u", d.q_heads,
+                    d.kv_heads);
+    const uint32_t nq = d.q_heads / d.kv_heads;
+    if (nq != 1 && nq != 2 && nq != 4 && nq != 8)
+        return fail(PBMOE_ERR_UNSUPPORTED, "%u q heads per kv head (1, 2, 4 or 8 implemented)", nq);
+    const uint32_t qw = d.q_heads * d.head_dim, kvw = d.kv_heads * d.head_dim;
+    if (d.hidden == 0 || d.hidden > MAX_HIDDEN || qw > MAX_HIDDEN)
+        return fail(PBMOE_ERR_UNSUPPORTED, "attention hidden=%u, q width=%u (at most %u)", d.hidden, qw,
+                    MAX_HIDDEN);
+    if (d.group_size != 32 && d.group_size != 64 && d.group_size != 128)
+        return fail(PBMOE_ERR_UNSUPPORTED, "attention group size %u (32, 64 or 128)", d.group_size);
+    if (d.hidden % d.group_size || qw % d.group_size || d.hidden % 2)
+        return fail(PBMOE_ERR_SHAPE, "hidden=%u and q width=%u must be multiples of group %u", d.hidden, qw,
+                    d.group_size);
+    if (d.scale_bias_dtype != PBMOE_DTYPE_F16 && d.scale_bias_dtype != PBMOE_DTYPE_BF16)
+        return fail(PBMOE_ERR_DTYPE, "attention scale/bias dtype must be F16 or BF16");
+    if (d.max_context == 0 || !(d.rope_theta > 0.0f))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "max_context and rope_theta must be positive");
+    if (!w->q_norm || !w->k_norm)
+        return fail(PBMOE_ERR_NOT_BOUND, "attention layer %u: self_attn.q_norm / k_norm are required", layer);
+    int rc;
+    pbmoe::AttnArgs a{};
+    if ((rc = attn_matrix(w->q, qw, d.hidden, "q", &a.q)) || (rc = attn_matrix(w->k, kvw, d.hidden, "k", &a.k)) ||
+        (rc = attn_matrix(w->v, kvw, d.hidden, "v", &a.v)) || (rc = attn_matrix(w->o, d.hidden, qw, "o", &a.o)))
+        return rc;
+    if ((rc = set_device(ctx)))
+        return rc;
+    if (ctx->attn.count(layer))
+        if ((rc = pbmoe_unbind_attention(ctx, layer)))
+            return rc;
+    AttnBinding b;
+    b.desc = d;
+    const size_t cache_bytes = (size_t)d.max_context * kvw * 2;
+    HIP_TRY(hipMalloc(&b.cache_k.ptr, cache_bytes));
+    b.cache_k.bytes = cache_bytes;
+    hipError_t e = hipMalloc(&b.cache_v.ptr, cache_bytes);
+    if (e == hipSuccess)
+        b.cache_v.bytes = cache_bytes;
+    if (e == hipSuccess)
+        e = hipMalloc(&b.inv_freq.ptr, 256 * sizeof(float));
+    if (e == hipSuccess) {
+        b.inv_freq.bytes = 256 * sizeof(float);
+        // theta.powf(-(2 i) / rotary_dim) in f32, as the reference computes it
+        float inv[256] = {};
+        const uint32_t half = d.rotary_dim / 2;
+        for (uint32_t i = 0; i < half; ++i)
+            inv[i] = powf(d.rope_theta, -((float)(2 * i)) / (float)d.rotary_dim);
+        e = hipMemcpyAsync(b.inv_freq.ptr, inv, sizeof inv, hipMemcpyHostToDevice, ctx->stream);
+    }
+    if (e == hipSuccess)
+        e = hipMemsetAsync(b.cache_k.ptr, 0, cache_bytes, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(b.cache_v.ptr, 0, cache_bytes, ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        free_buf(b.cache_k);
+        free_buf(b.cache_v);
+        free_buf(b.inv_freq);
+        return fail(e == hipErrorOutOfMemory ? PBMOE_ERR_OUT_OF_MEMORY : PBMOE_ERR_DEVICE,
+                    "attention layer %u setup: %s", layer, hipGetErrorString(e));
+    }
+    a.q_norm = w->q_norm;
+    a.k_norm = w->k_norm;
+    a.group_shift = 0;
+    while ((1u << a.group_shift) < d.group_size)
+        ++a.group_shift;
+    a.sb_dtype = d.scale_bias_dtype;
+    a.hidden = d.hidden;
+    a.q_heads = d.q_heads;
+    a.kv_heads = d.kv_heads;
+    a.head_dim = d.head_dim;
+    a.inv_freq = static_cast<const float*>(b.inv_freq.ptr);
+    a.cache_k = static_cast<uint16_t*>(b.cache_k.ptr);
+    a.cache_v = static_cast<uint16_t*>(b.cache_v.ptr);
+    a.post_eps = d.norm_epsilon > 0.0f ? d.norm_epsilon : 1e-6f;
+    b.base = a;
+    ctx->attn[layer] = b;
+    return ok();
+}
+
+PBMOE_API int pbmoe_unbind_attention(pbmoe_ctx* ctx, uint32_t layer)
+{
+    if (!ctx)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
+    auto it = ctx->attn.find(layer);
+    if (it == ctx->attn.end())
+        return fail(PBMOE_ERR_NOT_BOUND, "attention layer %u is not bound", layer);
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    free_buf(it->second.cache_k);
+    free_buf(it->second.cache_v);
+    free_buf(it->second.inv_freq);
+    ctx->attn.erase(it);
+    return ok();
+}
+
+PBMOE_API int pbmoe_attention_kv_cache(pbmoe_ctx* ctx, uint32_t layer, void** keys, void** values)
+{
+    if (!ctx || !keys || !values)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    auto it = ctx->attn.find(layer);
+    if (it == ctx->attn.end())
+        return fail(PBMOE_ERR_NOT_BOUND, "attention layer %u is not bound", layer);
+    *keys = it->second.cache_k.ptr;
+    *values = it->second.cache_v.ptr;
+    return ok();
+}
+
+PBMOE_API int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float* normed,
+                                     const float* residual, uint32_t position, float* hidden_out,
+                                     const float* post_norm_weight, float* post_normed_out,
+                                     float* attn_out)
+{
+    if (!ctx || !normed || !residual || !hidden_out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if ((post_norm_weight == nullptr) != (post_normed_out == nullptr))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "post_norm_weight and post_normed_out go together");
+    auto it = ctx->attn.find(layer);
+    if (it == ctx->attn.end())
+        return fail(PBMOE_ERR_NOT_BOUND, "attention layer %u is not bound", layer);
+    const AttnBinding& b = it->second;
+    if (position >= b.desc.max_context)
+        return fail(PBMOE_ERR_SHAPE, "position %u beyond the KV cache (%u positions)", position,
+                    b.desc.max_context);
+    for (const void* p : {(const void*)normed, (const void*)residual, (const void*)hidden_out,
+                          (const void*)post_normed_out, (const void*)attn_out})
+        if (p && !aligned(p, 16))
+            return fail(PBMOE_ERR_ALIGNMENT, "activation buffers must be 16-byte aligned");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    const uint32_t qw = b.desc.q_heads * b.desc.head_dim, kvw = b.desc.kv_heads * b.desc.head_dim;
+    // partials sized for the whole cache, so the scratch does not grow with
+    // the position (one allocation before a decode loop or graph capture)
+    const uint32_t chunks = (b.desc.max_context + pbmoe::ATTN_CHUNK - 1) / pbmoe::ATTN_CHUNK;
+    const size_t qkv_bytes = align256((size_t)(qw + 2 * kvw) * 4);
+    const size_t part_bytes = align256((size_t)b.desc.q_heads * chunks * (b.desc.head_dim + 2) * 4);
+    const size_t out_bytes = align256((size_t)qw * 4);
+    if ((rc = ensure(ctx, ctx->attn_scratch, qkv_bytes + part_bytes + out_bytes)))
+        return rc;
+    uint8_t* base = static_cast<uint8_t*>(ctx->attn_scratch.ptr);
+    pbmoe::AttnArgs a = b.base;
+    a.position = position;
+    a.normed = normed;
+    a.residual = residual;
+    a.hidden_out = hidden_out;
+    a.post_norm_w = post_norm_weight;
+    a.post_normed = post_normed_out;
+    a.qkv = reinterpret_cast<float*>(base);
+    a.part = reinterpret_cast<float*>(base + qkv_bytes);
+    a.attn_out = attn_out ? attn_out : reinterpret_cast<float*>(base + qkv_bytes + part_bytes);
+    HIP_TRY(pbmoe::launch_attention_decode(ctx->stream, a));
+    return ok();
+}
+

@@ -1,0 +1,399 @@
+// Batch-1 decode attention of one layer on gfx950 (GQA, head_dim 128):
+// the Qwen full-attention step that precedes every MoE block
+// (full_attention_output_values, flashmoe/runtime/mod.rs:2215-2367).
+//
+//  1. q4_rows_kernel: q, k, v = W . normed (three resident Q4 projections
+//     in one launch, one wave per two rows).
+//  2. attn_chunk_kernel: one workgroup per (64-position chunk, kv head):
+//     per-head q RMSNorm + split-half RoPE for the kv head's q heads; the
+//     chunk holding this position also normalises/rotates the new k, rounds
+//     k and v to f16 and writes them to the cache; scores over the chunk,
+//     softmax partial (max, sum), P.V partial.
+//  3. attn_merge_kernel: log-sum-exp merge of the chunk partials per head.
+//  4. q4_rows_kernel: hidden = residual + W_o . attention.
+//  5. rms_norm_kernel: post-attention RMSNorm (optional).
+// Arithmetic is f32 throughout; keys and values are stored as f16 (the
+// cache format), queries stay f32.
+#include <hip/hip_ext.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "pbmoe_device.h"
+#include "pbmoe_internal.h"
+
+namespace pbmoe {
+
+constexpr int HD = 128;        // head_dim the attention kernels are written for
+constexpr int HALF = HD / 2;   // split-half RoPE pairs (i, i + 64): lane i holds both
+constexpr int KPITCH = HD + 8; // halfs per staged K row: 272 bytes, rows fall on distinct banks
+constexpr int CH = (int)ATTN_CHUNK;
+static_assert(CH == 64, "one position per lane");
+
+// ---------------------------------------------------------------------------
+// Q4 rows . x for up to three matrices with the same column count; output
+// rows are concatenated (matrix i starts at first[i]).  The factored form
+// sum_g s_g * sum(q x) + b_g * sum(x) of the reference's fma(q, s x, b x)
+// (q4_fma_row_bf16_ptrs, shaders.metal:97-199).
+// ---------------------------------------------------------------------------
+struct RowsArgs {
+    Q4Mat m[3];
+    uint32_t n_mat;
+    uint32_t first[4];
+    uint32_t group_shift;
+    const float* x;        // [cols]
+    const float* residual; // null or [total rows]
+    float* y;              // [total rows]
+};
+
+template <int SBT, int CPL>
+__global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
+{
+    constexpr int RPW = 2;
+    const int lane = threadIdx.x & 63;
+    const uint32_t r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    if (r0 >= a.first[a.n_mat])
+        return;
+    uint32_t mi = 0;
+    while (mi + 1 < a.n_mat && r0 >= a.first[mi + 1])
+        ++mi;
+    const Q4Mat m = a.m[mi];
+    const uint32_t row0 = r0 - a.first[mi];
+    const uint32_t chunks = m.cols / 32, gpr = m.cols >> a.group_shift;
+    uint4 w[RPW][CPL];
+    float sc[RPW][CPL], bi[RPW][CPL];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const uint32_t row = row0 + r;
+        const uint4* wp = reinterpret_cast<const uint4*>(m.codes + (uint64_t)row * (m.cols / 2));
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t ch = lane + WAVE * c;
+            if (ch < chunks) {
+                w[r][c] = wp[ch];
+                const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> a.group_shift);
+                sc[r][c] = sb_at<SBT>(m.scales, gi);
+                bi[r][c] = sb_at<SBT>(m.biases, gi);
+            }
+        }
+    }
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+        acc[r] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const uint32_t ch = lane + WAVE * c;
+        if (ch < chunks) {
+            const float4* x4 = reinterpret_cast<const float4*>(a.x + ch * 32);
+            float xv[32];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 v = x4[q];
+                xv[4 * q] = v.x, xv[4 * q + 1] = v.y, xv[4 * q + 2] = v.z, xv[4 * q + 3] = v.w;
+            }
+            float xs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 32; q += 4)
+                xs += (xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3]);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+                acc[r] = fmaf(sc[r][c], q4_chunk_qx_reg(w[r][c], xv), fmaf(bi[r][c], xs, acc[r]));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const float s = wave_sum(acc[r]);
+        if (lane == r) {
+            const uint32_t o = r0 + r;
+            a.y[o] = a.residual ? a.residual[o] + s : s;
+        }
+    }
+}
+
+// Per-head RMSNorm with weight, then the split-half rotation of pair
+// (lane, lane + 64): the order of
+// apply_optional_per_head_rms_norm_and_split_half_rope (math.rs:278-300):
+// value *= (1 / sqrt(mean(v^2) + 1e-6)) * weight, then x0 cos - x1 sin,
+// x0 sin + x1 cos.
+__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const float* w, float sn, float cs)
+{
+    const int lane = threadIdx.x & 63;
+    const float ms = wave_sum(x0 * x0 + x1 * x1) / (float)HD;
+    const float scale = 1.0f / sqrtf(ms + 1e-6f);
+    const float a0 = x0 * (scale * w[lane]);
+    const float a1 = x1 * (scale * w[lane + HALF]);
+    x0 = a0 * cs - a1 * sn;
+    x1 = a0 * sn + a1 * cs;
+}
+
+// ---------------------------------------------------------------------------
+// attention partials: workgroup (chunk c, kv head j), NQ q heads per kv
+// head; wave w handles q heads w, w + 4 (< NQ).  Partial record per (q head,
+// chunk): sum_t exp(s_t - m) v_t [HD], m, sum_t exp(s_t - m).
+// ---------------------------------------------------------------------------
+template <int NQ>
+__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
+{
+    constexpr int NQW = (NQ + 3) / 4; // q heads per wave
+    __shared__ float qs[NQ][HD];
+    __shared__ __align__(16) uint16_t kc[CH][KPITCH];
+    __shared__ __align__(16) uint16_t vc[CH][HD];
+    __shared__ float ps[NQ][CH];
+    __shared__ __align__(16) uint16_t knew[HD];
+    __shared__ __align__(16) uint16_t vnew[HD];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t chunk = blockIdx.x, j = blockIdx.y;
+    const uint32_t n = a.position + 1; // attended positions 0..position
+    const uint32_t t0 = chunk * CH;
+    const uint32_t cnt = min((uint32_t)CH, n - t0);
+    const uint32_t chunks = gridDim.x;
+    const bool has_new = a.position >= t0 && a.position < t0 + CH;
+
+    // rotation of the pair (lane, lane + 64) at this position: the f32 angle
+    // of split_half_rope_rotations (math.rs:303-325)
+    float sn, cs;
+    sincosf((float)a.position * a.inv_freq[lane], &sn, &cs);
+
+#pragma unroll
+    for (int u = 0; u < NQW; ++u) {
+        const int h = wv + 4 * u;
+        if (h < NQ) {
+            const float* qr = a.qkv + (uint64_t)(j * NQ + h) * HD;
+            float x0 = qr[lane], x1 = qr[lane + HALF];
+            norm_rope_pair(x0, x1, a.q_norm, sn, cs);
+            qs[h][lane] = x0;
+            qs[h][lane + HALF] = x1;
+        }
+    }
+    if (has_new && wv == 0) {
+        const float* kr = a.qkv + (uint64_t)a.q_heads * HD + (uint64_t)j * HD;
+        const float* vr = kr + (uint64_t)a.kv_heads * HD;
+        float x0 = kr[lane], x1 = kr[lane + HALF];
+        norm_rope_pair(x0, x1, a.k_norm, sn, cs);
+        const uint16_t k0 = __half_as_ushort(__float2half(x0)), k1 = __half_as_ushort(__float2half(x1));
+        const uint16_t v0 = __half_as_ushort(__float2half(vr[lane]));
+        const uint16_t v1 = __half_as_ushort(__float2half(vr[lane + HALF]));
+        knew[lane] = k0, knew[lane + HALF] = k1;
+        vnew[lane] = v0, vnew[lane + HALF] = v1;
+        const uint64_t o = ((uint64_t)a.position * a.kv_heads + j) * HD;
+        a.cache_k[o + lane] = k0, a.cache_k[o + lane + HALF] = k1;
+        a.cache_v[o + lane] = v0, a.cache_v[o + lane + HALF] = v1;
+    }
+    __syncthreads();
+    // stage the chunk's keys and values (16 bytes per thread per step); this
+    // position's row comes from LDS, not from the cache write above
+    for (uint32_t i = tid; i < (uint32_t)CH * (HD / 8); i += 256) {
+        const uint32_t t = i / (HD / 8), q = i % (HD / 8);
+        uint4 kk = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+        if (t < cnt) {
+            if (t0 + t == a.position) {
+                kk = reinterpret_cast<const uint4*>(knew)[q];
+                vv = reinterpret_cast<const uint4*>(vnew)[q];
+            } else {
+                const uint64_t o = ((uint64_t)(t0 + t) * a.kv_heads + j) * HD;
+                kk = reinterpret_cast<const uint4*>(a.cache_k + o)[q];
+                vv = reinterpret_cast<const uint4*>(a.cache_v + o)[q];
+            }
+        }
+        reinterpret_cast<uint4*>(&kc[t][0])[q] = kk;
+        reinterpret_cast<uint4*>(&vc[t][0])[q] = vv;
+    }
+    __syncthreads();
+
+    // scores: lane = position t of the chunk
+    const float scale = 1.0f / sqrtf((float)HD);
+    float s[NQW];
+#pragma unroll
+    for (int u = 0; u < NQW; ++u)
+        s[u] = 0.0f;
+    const uint16_t* krow = &kc[lane][0];
+#pragma unroll 4
+    for (int d8 = 0; d8 < HD / 8; ++d8) {
+        const uint4 raw = reinterpret_cast<const uint4*>(krow)[d8];
+        const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
+        float kv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kv[2 * e] = __half2float(__ushort_as_half((uint16_t)(r4[e] & 0xFFFFu)));
+            kv[2 * e + 1] = __half2float(__ushort_as_half((uint16_t)(r4[e] >> 16)));
+        }
+#pragma unroll
+        for (int u = 0; u < NQW; ++u) {
+            const int h = wv + 4 * u;
+            if (h < NQ) {
+                const float4 qa = reinterpret_cast<const float4*>(&qs[h][8 * d8])[0];
+                const float4 qb = reinterpret_cast<const float4*>(&qs[h][8 * d8])[1];
+                s[u] = fmaf(qa.x, kv[0], s[u]);
+                s[u] = fmaf(qa.y, kv[1], s[u]);
+                s[u] = fmaf(qa.z, kv[2], s[u]);
+                s[u] = fmaf(qa.w, kv[3], s[u]);
+                s[u] = fmaf(qb.x, kv[4], s[u]);
+                s[u] = fmaf(qb.y, kv[5], s[u]);
+                s[u] = fmaf(qb.z, kv[6], s[u]);
+                s[u] = fmaf(qb.w, kv[7], s[u]);
+            }
+        }
+    }
+    const bool valid = (uint32_t)lane < cnt;
+    float mx[NQW], sum[NQW];
+#pragma unroll
+    for (int u = 0; u < NQW; ++u) {
+        const int h = wv + 4 * u;
+        const float sv = valid ? s[u] * scale : -INFINITY;
+        mx[u] = wave_max(sv);
+        const float p = valid ? expf(sv - mx[u]) : 0.0f;
+        sum[u] = wave_sum(p);
+        if (h < NQ)
+            ps[h][lane] = p;
+    }
+    // P . V: lane holds dims 2 lane, 2 lane + 1 (ps rows were written by this
+    // wave; LDS operations of a wave complete in order)
+    float o0[NQW], o1[NQW];
+#pragma unroll
+    for (int u = 0; u < NQW; ++u)
+        o0[u] = 0.0f, o1[u] = 0.0f;
+    for (uint32_t t = 0; t < cnt; ++t) {
+        const uint32_t vw = reinterpret_cast<const uint32_t*>(&vc[t][0])[lane];
+        const float v0 = __half2float(__ushort_as_half((uint16_t)(vw & 0xFFFFu)));
+        const float v1 = __half2float(__ushort_as_half((uint16_t)(vw >> 16)));
+#pragma unroll
+        for (int u = 0; u < NQW; ++u) {
+            const int h = wv + 4 * u;
+            if (h < NQ) {
+                const float p = ps[h][t];
+                o0[u] = fmaf(p, v0, o0[u]);
+                o1[u] = fmaf(p, v1, o1[u]);
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NQW; ++u) {
+        const int h = wv + 4 * u;
+        if (h < NQ) {
+            float* rec = a.part + ((uint64_t)(j * NQ + h) * chunks + chunk) * (HD + 2);
+            reinterpret_cast<float2*>(rec)[lane] = make_float2(o0[u], o1[u]);
+            if (lane == 0) {
+                rec[HD] = mx[u];
+                rec[HD + 1] = sum[u];
+            }
+        }
+    }
+}
+
+// merge the chunk partials of one q head: out = sum_c e^(m_c - M) o_c /
+// sum_c e^(m_c - M) l_c, i.e. softmax over every position (softmax_in_place,
+// math.rs:728-744) then the weighted sum of values.
+__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part, uint32_t chunks,
+                                                        float* __restrict__ out)
+{
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const float* ph = part + (uint64_t)h * chunks * (HD + 2);
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < chunks; ++c)
+        M = fmaxf(M, ph[(uint64_t)c * (HD + 2) + HD]);
+    float L = 0.0f, acc = 0.0f;
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const float* rec = ph + (uint64_t)c * (HD + 2);
+        const float e = expf(rec[HD] - M);
+        L = fmaf(e, rec[HD + 1], L);
+        acc = fmaf(e, rec[d], acc);
+    }
+    out[(uint64_t)h * HD + d] = acc / L;
+}
+
+// RMSNorm with weight, one workgroup: rms_norm_with_weight_and_epsilon
+// (math.rs:151-167): value *= 1 / sqrt(mean(v^2) + eps); value *= weight.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ h, const float* __restrict__ w,
+                                                       uint32_t width, float eps, float* __restrict__ out)
+{
+    __shared__ float red[4];
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < width; i += 256)
+        s = fmaf(h[i], h[i], s);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float ms = ((red[0] + red[1]) + (red[2] + red[3])) / (float)width;
+    const float scale = 1.0f / sqrtf(ms + eps);
+    for (uint32_t i = threadIdx.x; i < width; i += 256)
+        out[i] = (h[i] * scale) * w[i];
+}
+
+template <int SBT>
+static hipError_t launch_rows(hipStream_t st, const RowsArgs& r)
+{
+    const uint32_t total = r.first[r.n_mat];
+    const uint32_t cols = r.m[0].cols;
+    const uint32_t cpl = (cols / 32 + 63) / 64;
+    const dim3 grid((total / 2 + 3) / 4);
+    if (cpl <= 1)
+        hipLaunchKernelGGL((q4_rows_kernel<SBT, 1>), grid, dim3(256), 0, st, r);
+    else if (cpl <= 2)
+        hipLaunchKernelGGL((q4_rows_kernel<SBT, 2>), grid, dim3(256), 0, st, r);
+    else if (cpl <= 4)
+        hipLaunchKernelGGL((q4_rows_kernel<SBT, 4>), grid, dim3(256), 0, st, r);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
+{
+    if (a.head_dim != HD || a.kv_heads == 0 || a.q_heads % a.kv_heads)
+        return hipErrorInvalidValue;
+    const uint32_t nq = a.q_heads / a.kv_heads;
+    const uint32_t qw = a.q_heads * HD, kvw = a.kv_heads * HD;
+    // 1. q, k, v
+    RowsArgs r{};
+    r.m[0] = a.q, r.m[1] = a.k, r.m[2] = a.v;
+    r.n_mat = 3;
+    r.first[0] = 0, r.first[1] = qw, r.first[2] = qw + kvw, r.first[3] = qw + 2 * kvw;
+    r.group_shift = a.group_shift;
+    r.x = a.normed;
+    r.residual = nullptr;
+    r.y = a.qkv;
+    hipError_t e = a.sb_dtype == 2 ? launch_rows<2>(st, r) : launch_rows<1>(st, r);
+    if (e != hipSuccess)
+        return e;
+    // 2. chunk partials
+    const uint32_t chunks = (a.position + 1 + CH - 1) / CH;
+    const dim3 g2(chunks, a.kv_heads);
+    switch (nq) {
+    case 1: hipLaunchKernelGGL((attn_chunk_kernel<1>), g2, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_chunk_kernel<2>), g2, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_chunk_kernel<4>), g2, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((attn_chunk_kernel<8>), g2, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    if ((e = hipGetLastError()) != hipSuccess)
+        return e;
+    // 3. merge
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads), dim3(HD), 0, st, (const float*)a.part, chunks,
+                       a.attn_out);
+    if ((e = hipGetLastError()) != hipSuccess)
+        return e;
+    // 4. o_proj + residual
+    RowsArgs o{};
+    o.m[0] = a.o;
+    o.n_mat = 1;
+    o.first[0] = 0, o.first[1] = a.hidden;
+    o.group_shift = a.group_shift;
+    o.x = a.attn_out;
+    o.residual = a.residual;
+    o.y = a.hidden_out;
+    e = a.sb_dtype == 2 ? launch_rows<2>(st, o) : launch_rows<1>(st, o);
+    if (e != hipSuccess)
+        return e;
+    // 5. post-attention RMSNorm
+    if (a.post_norm_w) {
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), 0, st, (const float*)a.hidden_out, a.post_norm_w,
+                           a.hidden, a.post_eps, a.post_normed);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+} // namespace pbmoe

@@ -140,6 +140,43 @@ hipError_t launch_synth_fill(hipStream_t s, uint8_t* slots, uint64_t stride,
                              const uint64_t* offsets9, uint32_t hidden, uint32_t intermediate,
                              uint32_t group, uint32_t sb_dtype, uint64_t seed, uint32_t tensor,
                              uint32_t layer, uint32_t first_expert, uint32_t count);
+hipError_t launch_synth_center(hipStream_t s, uint8_t* slots, uint64_t stride, const uint64_t* offsets9,
+                               uint32_t hidden, uint32_t intermediate, uint32_t group, uint32_t sb_dtype,
+                               uint32_t count);
 hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t value, uint64_t n);
+
+// One resident Q4 matrix [rows][cols] (codes, 2-byte scale and bias rows).
+struct Q4Mat {
+    const uint8_t* codes;
+    const uint8_t* scales;
+    const uint8_t* biases;
+    uint32_t rows, cols;
+};
+
+// Batch-1 decode attention of one layer (pbmoe_attention_decode).
+struct AttnArgs {
+    Q4Mat q, k, v, o;
+    const float* q_norm; // [head_dim]
+    const float* k_norm; // [head_dim]
+    uint32_t group_shift, sb_dtype;
+    uint32_t hidden, q_heads, kv_heads, head_dim;
+    const float* inv_freq; // [head_dim / 2] rotary inverse frequencies (f32, host-computed)
+    uint16_t* cache_k;     // [max_context][kv_heads][head_dim] f16
+    uint16_t* cache_v;
+    uint32_t position;
+    const float* normed;   // [H]
+    const float* residual; // [H]
+    float* hidden_out;     // [H]
+    const float* post_norm_w; // null: no post-attention norm
+    float post_eps;
+    float* post_normed;    // [H]
+    float* attn_out;       // [q_heads * head_dim] (scratch or the caller's buffer)
+    // scratch
+    float* qkv;            // [(q_heads + 2 kv_heads) * head_dim]
+    float* part;           // [q_heads][chunks][head_dim + 2]
+};
+
+constexpr uint32_t ATTN_CHUNK = 64; // positions per attention workgroup
+hipError_t launch_attention_decode(hipStream_t s, const AttnArgs& a);
 
 } // namespace pbmoe

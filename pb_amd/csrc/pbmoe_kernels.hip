@@ -568,6 +568,48 @@ hipError_t launch_synth_fill(hipStream_t s, uint8_t* slots, uint64_t stride,
     return hipSuccess;
 }
 
+// zero-mean variant of the seeded weights: bias' = bias - 7.5 scale for every
+// group of the three projections (codes are uniform over 0..15), rounded back
+// to the scale/bias dtype; 7.5 scale is exact in f32, so one rounding.
+__global__ void synth_center_kernel(uint8_t* __restrict__ slots, SynthArgs a)
+{
+    uint8_t* slot = slots + (uint64_t)blockIdx.y * a.stride;
+    const uint64_t gpp = (uint64_t)a.hidden * a.intermediate / a.group;
+    const uint64_t nthreads = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < 3 * gpp; i += nthreads) {
+        const uint32_t p = (uint32_t)(i / gpp);
+        const uint64_t j = i % gpp;
+        const uint16_t sv = reinterpret_cast<const uint16_t*>(slot + a.off[3 * p + 1])[j];
+        uint16_t* bp = reinterpret_cast<uint16_t*>(slot + a.off[3 * p + 2]) + j;
+        if (a.sb_dtype == 2)
+            *bp = pbm_f32_to_bf16(pbm_bf16_to_f32(*bp) - 7.5f * pbm_bf16_to_f32(sv));
+        else
+            *bp = pbm_f32_to_f16(pbm_f16_to_f32(*bp) - 7.5f * pbm_f16_to_f32(sv));
+    }
+}
+
+hipError_t launch_synth_center(hipStream_t s, uint8_t* slots, uint64_t stride, const uint64_t* offsets9,
+                               uint32_t hidden, uint32_t intermediate, uint32_t group, uint32_t sb_dtype,
+                               uint32_t count)
+{
+    SynthArgs a{};
+    for (int i = 0; i < 9; ++i)
+        a.off[i] = offsets9[i];
+    a.stride = stride;
+    a.hidden = hidden;
+    a.intermediate = intermediate;
+    a.group = group;
+    a.sb_dtype = sb_dtype;
+    for (uint32_t done = 0; done < count; done += 65535u) {
+        const uint32_t n = std::min(count - done, 65535u);
+        synth_center_kernel<<<dim3(64, n), 256, 0, s>>>(slots + (uint64_t)done * stride, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return e;
+    }
+    return hipSuccess;
+}
+
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n)
 {
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;

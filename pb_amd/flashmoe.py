@@ -126,3 +126,65 @@ def dispatch_plan(ctx: Context, ids: DeviceArray, experts: int):
     u = int(cnt.download()[0])
     return (uniq.download()[:u], slots.download(), src.download(), out.download(),
             [tuple(int(v) for v in g) for g in groups.download()[:u]])
+
+
+class AttentionLayer:
+    """One bound GQA attention layer of the decode stack with its KV cache:
+    the reference's Qwen full-attention step (full_attention_output_values,
+    runtime/mod.rs:2215-2367) followed by o_proj, the residual add and the
+    post-attention RMSNorm (runtime/mod.rs:2979-2996)."""
+
+    def __init__(self, ctx: Context, index: int, acfg):
+        self.ctx, self.index, self.acfg = ctx, index, acfg
+        d = abi.AttnDesc()
+        d.hidden, d.q_heads, d.kv_heads, d.head_dim = acfg.hidden, acfg.q_heads, acfg.kv_heads, acfg.head_dim
+        d.rotary_dim = acfg.head_dim
+        d.rope_theta = acfg.rope_theta
+        d.norm_epsilon = acfg.eps
+        d.max_context = acfg.max_context
+        d.group_size = acfg.group
+        d.scale_bias_dtype = acfg.sb_dtype
+        self.desc = d
+        self._keep: list = []
+
+    def bind_synth(self, seed: int, layer: int) -> "AttentionLayer":
+        """Seeded Q4 projections (synth.attn_host_mats) and norm weights,
+        uploaded to the device."""
+        from . import synth
+        mats = synth.attn_host_mats(self.acfg, seed, layer, abi.q4_layout_fixed)
+        qn, kn, self.input_norm_h, self.post_norm_h = synth.attn_norms(self.acfg, seed, layer)
+        return self.bind_host(mats, qn, kn)
+
+    def bind_host(self, mats: dict, q_norm: np.ndarray, k_norm: np.ndarray) -> "AttentionLayer":
+        """mats: q/k/v/o -> (codes u8, scales u16, biases u16) host arrays."""
+        ctx = self.ctx
+        keep = []
+        w = abi.AttnWeights()
+        for name in ("q", "k", "v", "o"):
+            parts = [ctx.to_device(np.ascontiguousarray(a)) for a in mats[name]]
+            keep += parts
+            m = abi.Q4Matrix()
+            m.codes, m.scales, m.biases = parts[0].ptr, parts[1].ptr, parts[2].ptr
+            setattr(w, name, m)
+        qn, kn = ctx.to_device(np.asarray(q_norm, np.float32)), ctx.to_device(np.asarray(k_norm, np.float32))
+        keep += [qn, kn]
+        w.q_norm, w.k_norm = qn.ptr, kn.ptr
+        if getattr(self, "input_norm_h", None) is not None:
+            self.input_norm, self.post_norm = ctx.to_device(self.input_norm_h), ctx.to_device(self.post_norm_h)
+        self._keep = keep
+        check(lib().pbmoe_bind_attention(ctx.handle, self.index, C.byref(self.desc), C.byref(w)))
+        return self
+
+    def kv_cache(self):
+        k, v = C.c_void_p(), C.c_void_p()
+        check(lib().pbmoe_attention_kv_cache(self.ctx.handle, self.index, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def decode(self, normed: DeviceArray, residual: DeviceArray, position: int, hidden_out: DeviceArray,
+               post_norm: DeviceArray | None = None, post_normed: DeviceArray | None = None,
+               attn_out: DeviceArray | None = None):
+        check(lib().pbmoe_attention_decode(self.ctx.handle, self.index, normed.ptr, residual.ptr, position,
+                                           hidden_out.ptr, post_norm.ptr if post_norm is not None else None,
+                                           post_normed.ptr if post_normed is not None else None,
+                                           attn_out.ptr if attn_out is not None else None))
+

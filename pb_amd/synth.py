@@ -16,6 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libpbmoe_synth.so")
 
 T_EXPERT, T_ROUTER, T_SHARED, T_SHARED_GATE, T_INPUT, T_RESIDUAL, T_ROUTER_BIAS, T_LOGITS = range(1, 9)
+# attention layer of the decode stack: q and o share one pseudo slot (gate =
+# W_q, down = W_o), k and v another (gate = W_k, up = W_v); norm weights
+T_ATTN_QO, T_ATTN_KV, T_ATTN_NORM, T_LAYER_NORM, T_KV_FILL = range(9, 14)
 
 _lib = None
 
@@ -162,3 +165,100 @@ def activations(seed: int, layer: int, tokens: int, hidden: int):
     x = f16_to_f32(normal_f16(seed, T_INPUT, layer, 0, 0, tokens * hidden, 1.0)).reshape(tokens, hidden)
     r = f16_to_f32(normal_f16(seed, T_RESIDUAL, layer, 0, 0, tokens * hidden, 1.0)).reshape(tokens, hidden)
     return x, r
+
+
+@dataclass
+class AttnConfig:
+    """The GQA attention layer before each MoE block of the decode stack
+    (32 q heads, 4 kv heads, head_dim 128, f16 KV
+    cache, RMSNorm eps 1e-6, RoPE theta 1e6, Q4 projections)."""
+    name: str
+    hidden: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int = 128
+    rope_theta: float = 1e6
+    group: int = 64
+    sb_dtype: int = 1
+    max_context: int = 4096
+    eps: float = 1e-6
+
+    @property
+    def q_width(self) -> int:
+        return self.q_heads * self.head_dim
+
+    @property
+    def kv_width(self) -> int:
+        return self.kv_heads * self.head_dim
+
+
+def attn_pseudo_layouts(acfg: AttnConfig, layout_fn):
+    """(q/o layout, k/v layout): fixed Q4 slots whose gate/down (resp.
+    gate/up) projections hold W_q/W_o (resp. W_k/W_v)."""
+    return (layout_fn(acfg.hidden, acfg.q_width, acfg.group, acfg.sb_dtype),
+            layout_fn(acfg.hidden, acfg.kv_width, acfg.group, acfg.sb_dtype))
+
+
+def attn_norms(acfg: AttnConfig, seed: int, layer: int):
+    """q_norm, k_norm [head_dim] ~ U(0.5, 1.5); input and post-attention
+    RMSNorm weights [hidden] ~ U(0.5, 1.5) (f32)."""
+    hd, H = acfg.head_dim, acfg.hidden
+    return (uniform_f32(seed, T_ATTN_NORM, layer, 0, 0, hd, 0.5, 1.0),
+            uniform_f32(seed, T_ATTN_NORM, layer, 0, 1, hd, 0.5, 1.0),
+            uniform_f32(seed, T_LAYER_NORM, layer, 0, 0, H, 0.5, 1.0),
+            uniform_f32(seed, T_LAYER_NORM, layer, 0, 1, H, 0.5, 1.0))
+
+
+def attn_host_mats(acfg: AttnConfig, seed: int, layer: int, layout_fn) -> dict:
+    """W_q, W_k, W_v, W_o as (codes u8, scales u16, biases u16): the seeded
+    Q4 generator's codes and scales over two pseudo slots, biases centred so
+    that every weight row has mean ~0 (the activations of a decoder layer
+    then stay O(1-10), as in a trained model)."""
+    lqo, lkv = attn_pseudo_layouts(acfg, layout_fn)
+    H = acfg.hidden
+    qo = q4_experts(seed, T_ATTN_QO, layer, 0, 1, H, acfg.q_width, acfg.group, acfg.sb_dtype, lqo.offsets,
+                    int(lqo.expert_bytes))
+    kv = q4_experts(seed, T_ATTN_KV, layer, 0, 1, H, acfg.kv_width, acfg.group, acfg.sb_dtype, lkv.offsets,
+                    int(lkv.expert_bytes))
+
+    def part(slot, lay, comp):
+        c = lay.components[comp]
+        return slot[int(c.offset):int(c.offset) + int(c.bytes)]
+
+    def mat(slot, lay, first):
+        # zero-mean weights, as an affine quantisation of zero-mean tensors
+        # gives: bias' = bias - 7.5 scale (codes uniform over 0..15)
+        scales = part(slot, lay, first + 1).view(np.uint16).copy()
+        biases = part(slot, lay, first + 2).view(np.uint16)
+        return part(slot, lay, first).copy(), scales, centred_bias(biases, scales, acfg.sb_dtype)
+
+    return {"q": mat(qo, lqo, 0), "o": mat(qo, lqo, 6), "k": mat(kv, lkv, 0), "v": mat(kv, lkv, 3)}
+
+
+def _sb_to_f32(a: np.ndarray, sb_dtype: int) -> np.ndarray:
+    if sb_dtype == 2:
+        return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return f16_to_f32(a)
+
+
+def centred_bias(biases: np.ndarray, scales: np.ndarray, sb_dtype: int) -> np.ndarray:
+    """bias - 7.5 scale rounded to the scale/bias dtype (7.5 scale is exact
+    in f32): the host mirror of pbmoe_synth_center_q4."""
+    v = _sb_to_f32(biases, sb_dtype) - np.float32(7.5) * _sb_to_f32(scales, sb_dtype)
+    return f32_to_bf16(v) if sb_dtype == 2 else f32_to_f16(v)
+
+
+def center_q4_slots(slots: np.ndarray, lay, count: int, sb_dtype: int) -> np.ndarray:
+    """Copy of `count` fixed Q4 slots with every projection's biases centred
+    (pbmoe_synth_center_q4 on the host)."""
+    out = np.array(slots, dtype=np.uint8, copy=True)
+    stride = int(lay.expert_bytes)
+    for e in range(count):
+        for p in range(3):
+            cs, cb = lay.components[3 * p + 1], lay.components[3 * p + 2]
+            so, bo = e * stride + int(cs.offset), e * stride + int(cb.offset)
+            sc = out[so:so + int(cs.bytes)].view(np.uint16)
+            bi = out[bo:bo + int(cb.bytes)].view(np.uint16)
+            bi[:] = centred_bias(bi, sc, sb_dtype)
+    return out
+

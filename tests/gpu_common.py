@@ -41,15 +41,19 @@ class DeviceLayer:
     oracle needs (expert slots are regenerated on the host on demand)."""
 
     def __init__(self, ctx: abi.Context, cfg, layer: int, route_order: int = abi.ORDER_CANONICAL,
-                 index: int | None = None):
-        self.ctx, self.cfg, self.layer = ctx, cfg, layer
+                 index: int | None = None, centred: bool = False):
+        self.ctx, self.cfg, self.layer, self.centred = ctx, cfg, layer, centred
         H, I, E = cfg.hidden, cfg.intermediate, cfg.experts
         self.layout = abi.q4_layout_fixed(H, I, cfg.group, cfg.sb_dtype)
         self.slots = ctx.array(E * self.layout.expert_bytes, np.uint8)
         abi.check(abi.lib().pbmoe_synth_fill_q4(ctx.handle, self.slots.ptr, C.byref(self.layout), H, I, SEED,
                                                 synth.T_EXPERT, layer, 0, E))
+        if centred:  # zero-mean experts (the multi-layer stack)
+            abi.check(abi.lib().pbmoe_synth_center_q4(ctx.handle, self.slots.ptr, C.byref(self.layout), H, I, E))
         self.host = synth.make_layer(cfg, SEED, layer, abi.q4_layout_fixed, with_slots=False)
         h = self.host
+        if centred and h.shared_slot is not None:
+            h.shared_slot = synth.center_q4_slots(h.shared_slot, h.shared_layout, 1, cfg.sb_dtype)
         self.router = ctx.to_device(h.router_f16)
         self.bias = ctx.to_device(h.selection_bias) if h.selection_bias is not None else None
         self.shared = ctx.to_device(h.shared_slot) if cfg.shared_intermediate else None
@@ -76,6 +80,8 @@ class DeviceLayer:
         lay, cfg = self.layout, self.cfg
         parts = [synth.q4_experts(SEED, synth.T_EXPERT, self.layer, e, 1, cfg.hidden, cfg.intermediate, cfg.group,
                                   cfg.sb_dtype, lay.offsets, int(lay.expert_bytes)) for e in uniq]
+        if self.centred:
+            parts = [synth.center_q4_slots(p_, lay, 1, cfg.sb_dtype) for p_ in parts]
         remap = {e: i for i, e in enumerate(uniq)}
         return np.concatenate(parts), np.vectorize(remap.get)(ids).astype(np.int32), len(uniq)
 
