@@ -84,7 +84,7 @@ class HipEvents:
         return float(ms.value)
 
 
-def build_layers(ctx, cfg, n_layers: int, tokens: int):
+def build_layers(ctx, cfg, n_layers: int, tokens: int, centred: bool = False):
     from pb_amd import abi, synth
     from pb_amd.flashmoe import MoeLayer
 
@@ -94,6 +94,9 @@ def build_layers(ctx, cfg, n_layers: int, tokens: int):
         slots = ctx.array(cfg.experts * lay.expert_bytes, np.uint8)
         abi.check(abi.lib().pbmoe_synth_fill_q4(ctx.handle, slots.ptr, C.byref(lay), cfg.hidden, cfg.intermediate,
                                                 SEED, synth.T_EXPERT, l, 0, cfg.experts))
+        if centred:
+            abi.check(abi.lib().pbmoe_synth_center_q4(ctx.handle, slots.ptr, C.byref(lay), cfg.hidden,
+                                                      cfg.intermediate, cfg.experts))
         host = synth.make_layer(cfg, SEED, l, abi.q4_layout_fixed, with_slots=False)
         router = ctx.to_device(host.router_f16)
         bias = ctx.to_device(host.selection_bias) if host.selection_bias is not None else None
@@ -307,6 +310,145 @@ def cpu_prefill_baseline(cfg, host, xh, rh, ids_h, w_h, budget_s: float):
             "sample": f"{done} tokens of the same routed chunk through the oracle expert phase ({t_total:.1f} s)"}
 
 
+def stack_bytes_per_token(acfg, mcfg, layers: int, position: int) -> dict:
+    """Algorithmic HBM bytes of one token through the C4 stack: per layer the
+    four attention projections, the KV rows 0..position (f16 keys and
+    values), and the MoE layer (router, the K selected experts)."""
+    from pb_amd.configs import algorithmic_bytes, q4_proj_bytes
+    H, g = acfg.hidden, acfg.group
+    attn = (q4_proj_bytes(acfg.q_width, H, g) + 2 * q4_proj_bytes(acfg.kv_width, H, g)
+            + q4_proj_bytes(H, acfg.q_width, g) + (position + 1) * acfg.kv_width * 2 * 2 + 6 * H * 4)
+    moe = algorithmic_bytes(mcfg, mcfg.k, 1)
+    return {"attention": attn * layers, "moe": moe * layers, "total": (attn + moe) * layers}
+
+
+def bench_stack(args, ctx, ev) -> dict:
+    """one token through the 48-layer decode stack —
+    per layer the GQA attention block (pbmoe_attention_decode: q/k/v, q/k norm
+    + RoPE, f16 KV cache at context 4096, o_proj + residual, post-attention
+    RMSNorm) and the C1 MoE layer (pbmoe_moe_layer, the next layer's input
+    RMSNorm fused).  KV rows 0..4094 hold synthetic f16 values, the timed
+    token is position 4095; expert and attention weights are seeded zero-mean
+    4-bit (the stack's activations stay bounded across 48 layers).  The
+    timed steps replay a hipGraph of one token's launches."""
+    from pb_amd import abi, synth
+    from pb_amd.configs import C1, C4_ATTN, C4_LAYERS
+    from pb_amd.flashmoe import AttentionLayer
+
+    acfg, mcfg, L = C4_ATTN, C1, C4_LAYERS
+    H, pos = acfg.hidden, acfg.max_context - 1
+    stream = ctx.stream()
+    t_setup = time.perf_counter()
+    _, moes = build_layers(ctx, mcfg, L, 1, centred=True)
+    atts = [AttentionLayer(ctx, l, acfg).bind_synth(SEED, l) for l in range(L)]
+    rng = np.random.default_rng(SEED)
+    keys = rng.standard_normal((pos, acfg.kv_width)).astype(np.float16)
+    vals = rng.standard_normal((pos, acfg.kv_width)).astype(np.float16)
+    for a in atts:
+        kp, vp = a.kv_cache()
+        abi.check(abi.lib().pbmoe_upload(ctx.handle, kp, keys.ctypes.data, keys.nbytes))
+        abi.check(abi.lib().pbmoe_upload(ctx.handle, vp, vals.ctypes.data, vals.nbytes))
+    h0, _ = synth.activations(SEED, 4000, 1, H)
+    w0 = atts[0].input_norm_h
+    x0 = (h0 / np.sqrt(np.mean(h0 * h0) + acfg.eps) * w0).astype(np.float32)
+    x_a, h_a = ctx.to_device(x0), ctx.to_device(h0)
+    x_b, h_b = ctx.array((1, H), np.float32), ctx.array((1, H), np.float32)
+    mid, post = ctx.array((1, H), np.float32), ctx.array((1, H), np.float32)
+    ids = ctx.array((1, mcfg.k), np.uint32)
+    wts = ctx.array((1, mcfg.k), np.float32)
+    ctx.sync()
+    print(f"[bench] stack setup {time.perf_counter() - t_setup:.1f} s: {L} layers, context {pos + 1}",
+          file=sys.stderr, flush=True)
+
+    def token(parts=("attn", "moe")):
+        bufs = ((x_a, h_a), (x_b, h_b))
+        for l in range(L):
+            (x, h), (xn, hn) = bufs[l % 2], bufs[(l + 1) % 2]
+            if "attn" in parts:
+                atts[l].decode(x, h, pos, mid, post_norm=atts[l].post_norm, post_normed=post)
+            if "moe" in parts:
+                moes[l][0].forward(post, mid, hn, ids, wts, next_norm=atts[(l + 1) % L].input_norm, next_normed=xn)
+
+    for _ in range(args.warmup):
+        token()
+    ctx.sync()
+    a, b = ev.create(), ev.create()
+    res = {}
+    for name, parts in (("token", ("attn", "moe")), ("attention", ("attn",)), ("moe", ("moe",))):
+        graph = ev.capture(stream, lambda: token(parts))
+        ev.launch_graph(graph, stream)
+        ctx.sync()
+        ev.record(a, stream)
+        for _ in range(args.steps):
+            ev.launch_graph(graph, stream)
+        ev.record(b, stream)
+        res[name] = ev.elapsed_ms(a, b) / args.steps
+        ctx.sync()
+    ms = res["token"]
+    nbytes = stack_bytes_per_token(acfg, mcfg, L, pos)
+    gbps = nbytes["total"] / (ms * 1e-3) / 1e9
+    print(f"[bench] stack: {ms:.3f} ms/token ({1e3 / ms:.1f} tokens/s); attention-only {res['attention']:.3f} ms, "
+          f"MoE-only {res['moe']:.3f} ms; {gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_stack_baseline(acfg, mcfg, [h for _, h in moes[:2]], pos, keys, vals, args.cpu_seconds)
+    return {
+        "metric": "decode stack tokens/s (48 layers: GQA attention + MoE), batch 1",
+        "value": round(1e3 / ms, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (f16 KV cache, 4-bit weights)",
+        "data": "synthetic",
+        "config": {"workload": "c4_stack_decode", "layers": L, "context": pos + 1, "hidden": H,
+                   "q_heads": acfg.q_heads, "kv_heads": acfg.kv_heads, "head_dim": acfg.head_dim,
+                   "experts": mcfg.experts, "k": mcfg.k, "intermediate": mcfg.intermediate,
+                   "quant": "q4 affine g64 f16 scale/bias (zero-mean)"},
+        "tokens_per_s": round(1e3 / ms, 2),
+        "phase_ms": {"attention_only": round(res["attention"], 4), "moe_only": round(res["moe"], 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "whole token (all kernels of the 48 layers)", "bytes_per_token": nbytes["total"],
+                     "bytes_attention": nbytes["attention"], "bytes_moe": nbytes["moe"]},
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_stack_baseline(acfg, mcfg, host_layers, pos: int, keys, vals, budget_s: float):
+    """The oracle on a bounded sample of the stack: attention layers at the
+    same context (or_attention_decode) and MoE layers (router + routing +
+    experts + combine), each timed for about half the budget; the per-token
+    figure is 48 x (attention layer + MoE layer)."""
+    from oracle import oracle as orc
+    from pb_amd import abi, synth
+    from pb_amd.configs import C4_LAYERS
+
+    mats = synth.attn_host_mats(acfg, SEED, 0, abi.q4_layout_fixed)
+    qn, kn, _, _ = synth.attn_norms(acfg, SEED, 0)
+    att = orc.AttnOracle(mats, qn, kn, acfg.hidden, acfg.q_heads, acfg.kv_heads, acfg.head_dim, acfg.rope_theta,
+                         acfg.group, acfg.sb_dtype, acfg.max_context)
+    att.cache_k[:pos] = keys.astype(np.float32)
+    att.cache_v[:pos] = vals.astype(np.float32)
+    x = synth.activations(SEED, 4001, 1, acfg.hidden)[0].ravel()
+    n_att, t_att = 0, 0.0
+    while t_att < budget_s / 2 and n_att < 64:
+        t0 = time.perf_counter()
+        att.decode(x, pos)
+        t_att += time.perf_counter() - t0
+        n_att += 1
+    moe = cpu_baseline(mcfg, host_layers, 1, budget_s / 2, 1)
+    per_layer_us = t_att / n_att * 1e6 + moe["value"]
+    tok_s = 1e6 / (per_layer_us * C4_LAYERS)
+    return {"value": round(tok_s, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n_att} attention layers at context {pos + 1} ({t_att:.1f} s) + MoE: {moe['sample']}; "
+                      f"per token = {C4_LAYERS} x {per_layer_us:.0f} us"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -333,6 +475,12 @@ def main() -> int:
     from pb_amd import abi
     from pb_amd.configs import CONFIGS, algorithmic_bytes, decode_phase_bytes, down_prefetch_bytes
 
+    if args.config in ("c4_stack", "c4_stack_decode"):
+        ctx = abi.Context(0)
+        rec = bench_stack(args, ctx, HipEvents())
+        print(json.dumps(rec))
+        ctx.close()
+        return 0
     cfg = CONFIGS[args.config]
     T = args.tokens
     ctx = abi.Context(0)

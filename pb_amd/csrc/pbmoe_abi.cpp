@@ -1220,6 +1220,8 @@ PBMOE_API int pbmoe_bind_attention(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_a
         return fail(PBMOE_ERR_DTYPE, "attention scale/bias dtype must be F16 or BF16");
     if (d.max_context == 0 || !(d.rope_theta > 0.0f))
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "max_context and rope_theta must be positive");
+    if (d.max_context > 65536)
+        return fail(PBMOE_ERR_UNSUPPORTED, "max_context %u (at most 65536 positions)", d.max_context);
     if (!w->q_norm || !w->k_norm)
         return fail(PBMOE_ERR_NOT_BOUND, "attention layer %u: self_attn.q_norm / k_norm are required", layer);
     int rc;

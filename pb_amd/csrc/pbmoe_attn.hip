@@ -4,8 +4,8 @@
 //
 //  1. q4_rows_kernel: q, k, v = W . normed (three resident Q4 projections
 //     in one launch, one wave per two rows).
-//  2. attn_chunk_kernel: one workgroup per (64-position chunk, kv head):
-//     per-head q RMSNorm + split-half RoPE for the kv head's q heads; the
+//  2. attn_chunk_kernel: one workgroup per (64-position chunk, kv head, up
+//     to 4 of its q heads): per-head q RMSNorm + split-half RoPE; the
 //     chunk holding this position also normalises/rotates the new k, rounds
 //     k and v to f16 and writes them to the cache; scores over the chunk,
 //     softmax partial (max, sum), P.V partial.
@@ -129,43 +129,55 @@ __device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const float
 }
 
 // ---------------------------------------------------------------------------
-// attention partials: workgroup (chunk c, kv head j), NQ q heads per kv
-// head; wave w handles q heads w, w + 4 (< NQ).  Partial record per (q head,
-// chunk): sum_t exp(s_t - m) v_t [HD], m, sum_t exp(s_t - m).
+// attention partials: workgroup (chunk c, kv head j, head group z), NH <= 4
+// q heads per workgroup (heads j*NQ + z*NH .. +NH), wave w handles head w.
+// Partial record per (q head, chunk): sum_t exp(s_t - m) v_t [HD], m,
+// sum_t exp(s_t - m).
 // ---------------------------------------------------------------------------
-template <int NQ>
+template <int NH>
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
 {
-    constexpr int NQW = (NQ + 3) / 4; // q heads per wave
-    __shared__ float qs[NQ][HD];
+    __shared__ float qs[NH][HD];
     __shared__ __align__(16) uint16_t kc[CH][KPITCH];
     __shared__ __align__(16) uint16_t vc[CH][HD];
-    __shared__ float ps[NQ][CH];
+    __shared__ float ps[NH][CH];
     __shared__ __align__(16) uint16_t knew[HD];
     __shared__ __align__(16) uint16_t vnew[HD];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t chunk = blockIdx.x, j = blockIdx.y;
+    const uint32_t nq = a.q_heads / a.kv_heads;
+    const uint32_t qh = j * nq + blockIdx.z * NH + wv; // this wave's q head (wv < NH)
     const uint32_t n = a.position + 1; // attended positions 0..position
     const uint32_t t0 = chunk * CH;
     const uint32_t cnt = min((uint32_t)CH, n - t0);
     const uint32_t chunks = gridDim.x;
     const bool has_new = a.position >= t0 && a.position < t0 + CH;
 
+    // issue the chunk's key/value loads first (16 bytes per thread per step);
+    // this position's row is taken from LDS below, not from the cache
+    constexpr int PIECES = CH * (HD / 8) / 256;
+    uint4 kk[PIECES], vv[PIECES];
+#pragma unroll
+    for (int u = 0; u < PIECES; ++u) {
+        const uint32_t i = tid + 256 * u, t = i / (HD / 8), q = i % (HD / 8);
+        kk[u] = make_uint4(0, 0, 0, 0), vv[u] = make_uint4(0, 0, 0, 0);
+        if (t < cnt && t0 + t != a.position) {
+            const uint64_t o = ((uint64_t)(t0 + t) * a.kv_heads + j) * HD;
+            kk[u] = reinterpret_cast<const uint4*>(a.cache_k + o)[q];
+            vv[u] = reinterpret_cast<const uint4*>(a.cache_v + o)[q];
+        }
+    }
+
     // rotation of the pair (lane, lane + 64) at this position: the f32 angle
     // of split_half_rope_rotations (math.rs:303-325)
     float sn, cs;
     sincosf((float)a.position * a.inv_freq[lane], &sn, &cs);
-
-#pragma unroll
-    for (int u = 0; u < NQW; ++u) {
-        const int h = wv + 4 * u;
-        if (h < NQ) {
-            const float* qr = a.qkv + (uint64_t)(j * NQ + h) * HD;
-            float x0 = qr[lane], x1 = qr[lane + HALF];
-            norm_rope_pair(x0, x1, a.q_norm, sn, cs);
-            qs[h][lane] = x0;
-            qs[h][lane + HALF] = x1;
-        }
+    if (wv < NH) {
+        const float* qr = a.qkv + (uint64_t)qh * HD;
+        float x0 = qr[lane], x1 = qr[lane + HALF];
+        norm_rope_pair(x0, x1, a.q_norm, sn, cs);
+        qs[wv][lane] = x0;
+        qs[wv][lane + HALF] = x1;
     }
     if (has_new && wv == 0) {
         const float* kr = a.qkv + (uint64_t)a.q_heads * HD + (uint64_t)j * HD;
@@ -177,130 +189,116 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
         const uint16_t v1 = __half_as_ushort(__float2half(vr[lane + HALF]));
         knew[lane] = k0, knew[lane + HALF] = k1;
         vnew[lane] = v0, vnew[lane + HALF] = v1;
-        const uint64_t o = ((uint64_t)a.position * a.kv_heads + j) * HD;
-        a.cache_k[o + lane] = k0, a.cache_k[o + lane + HALF] = k1;
-        a.cache_v[o + lane] = v0, a.cache_v[o + lane + HALF] = v1;
-    }
-    __syncthreads();
-    // stage the chunk's keys and values (16 bytes per thread per step); this
-    // position's row comes from LDS, not from the cache write above
-    for (uint32_t i = tid; i < (uint32_t)CH * (HD / 8); i += 256) {
-        const uint32_t t = i / (HD / 8), q = i % (HD / 8);
-        uint4 kk = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-        if (t < cnt) {
-            if (t0 + t == a.position) {
-                kk = reinterpret_cast<const uint4*>(knew)[q];
-                vv = reinterpret_cast<const uint4*>(vnew)[q];
-            } else {
-                const uint64_t o = ((uint64_t)(t0 + t) * a.kv_heads + j) * HD;
-                kk = reinterpret_cast<const uint4*>(a.cache_k + o)[q];
-                vv = reinterpret_cast<const uint4*>(a.cache_v + o)[q];
-            }
+        if (blockIdx.z == 0) { // one writer per kv head
+            const uint64_t o = ((uint64_t)a.position * a.kv_heads + j) * HD;
+            a.cache_k[o + lane] = k0, a.cache_k[o + lane + HALF] = k1;
+            a.cache_v[o + lane] = v0, a.cache_v[o + lane + HALF] = v1;
         }
-        reinterpret_cast<uint4*>(&kc[t][0])[q] = kk;
-        reinterpret_cast<uint4*>(&vc[t][0])[q] = vv;
     }
     __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PIECES; ++u) {
+        const uint32_t i = tid + 256 * u, t = i / (HD / 8), q = i % (HD / 8);
+        if (t0 + t == a.position) {
+            kk[u] = reinterpret_cast<const uint4*>(knew)[q];
+            vv[u] = reinterpret_cast<const uint4*>(vnew)[q];
+        }
+        reinterpret_cast<uint4*>(&kc[t][0])[q] = kk[u];
+        reinterpret_cast<uint4*>(&vc[t][0])[q] = vv[u];
+    }
+    __syncthreads();
+    if (wv >= NH)
+        return;
 
     // scores: lane = position t of the chunk
     const float scale = 1.0f / sqrtf((float)HD);
-    float s[NQW];
-#pragma unroll
-    for (int u = 0; u < NQW; ++u)
-        s[u] = 0.0f;
+    float s = 0.0f;
     const uint16_t* krow = &kc[lane][0];
 #pragma unroll 4
     for (int d8 = 0; d8 < HD / 8; ++d8) {
         const uint4 raw = reinterpret_cast<const uint4*>(krow)[d8];
         const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
-        float kv[8];
+        const float4 qa = reinterpret_cast<const float4*>(&qs[wv][8 * d8])[0];
+        const float4 qb = reinterpret_cast<const float4*>(&qs[wv][8 * d8])[1];
+        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            kv[2 * e] = __half2float(__ushort_as_half((uint16_t)(r4[e] & 0xFFFFu)));
-            kv[2 * e + 1] = __half2float(__ushort_as_half((uint16_t)(r4[e] >> 16)));
-        }
-#pragma unroll
-        for (int u = 0; u < NQW; ++u) {
-            const int h = wv + 4 * u;
-            if (h < NQ) {
-                const float4 qa = reinterpret_cast<const float4*>(&qs[h][8 * d8])[0];
-                const float4 qb = reinterpret_cast<const float4*>(&qs[h][8 * d8])[1];
-                s[u] = fmaf(qa.x, kv[0], s[u]);
-                s[u] = fmaf(qa.y, kv[1], s[u]);
-                s[u] = fmaf(qa.z, kv[2], s[u]);
-                s[u] = fmaf(qa.w, kv[3], s[u]);
-                s[u] = fmaf(qb.x, kv[4], s[u]);
-                s[u] = fmaf(qb.y, kv[5], s[u]);
-                s[u] = fmaf(qb.z, kv[6], s[u]);
-                s[u] = fmaf(qb.w, kv[7], s[u]);
-            }
+            s = fmaf(qv[2 * e], __half2float(__ushort_as_half((uint16_t)(r4[e] & 0xFFFFu))), s);
+            s = fmaf(qv[2 * e + 1], __half2float(__ushort_as_half((uint16_t)(r4[e] >> 16))), s);
         }
     }
     const bool valid = (uint32_t)lane < cnt;
-    float mx[NQW], sum[NQW];
-#pragma unroll
-    for (int u = 0; u < NQW; ++u) {
-        const int h = wv + 4 * u;
-        const float sv = valid ? s[u] * scale : -INFINITY;
-        mx[u] = wave_max(sv);
-        const float p = valid ? expf(sv - mx[u]) : 0.0f;
-        sum[u] = wave_sum(p);
-        if (h < NQ)
-            ps[h][lane] = p;
-    }
-    // P . V: lane holds dims 2 lane, 2 lane + 1 (ps rows were written by this
-    // wave; LDS operations of a wave complete in order)
-    float o0[NQW], o1[NQW];
-#pragma unroll
-    for (int u = 0; u < NQW; ++u)
-        o0[u] = 0.0f, o1[u] = 0.0f;
+    const float sv = valid ? s * scale : -INFINITY;
+    const float mx = wave_max(sv);
+    const float p = valid ? expf(sv - mx) : 0.0f;
+    const float sum = wave_sum(p);
+    ps[wv][lane] = p; // read back by this wave only (LDS operations of a wave complete in order)
+    // P . V: lane holds dims 2 lane, 2 lane + 1
+    float o0 = 0.0f, o1 = 0.0f;
     for (uint32_t t = 0; t < cnt; ++t) {
         const uint32_t vw = reinterpret_cast<const uint32_t*>(&vc[t][0])[lane];
-        const float v0 = __half2float(__ushort_as_half((uint16_t)(vw & 0xFFFFu)));
-        const float v1 = __half2float(__ushort_as_half((uint16_t)(vw >> 16)));
-#pragma unroll
-        for (int u = 0; u < NQW; ++u) {
-            const int h = wv + 4 * u;
-            if (h < NQ) {
-                const float p = ps[h][t];
-                o0[u] = fmaf(p, v0, o0[u]);
-                o1[u] = fmaf(p, v1, o1[u]);
-            }
-        }
+        const float pt = ps[wv][t];
+        o0 = fmaf(pt, __half2float(__ushort_as_half((uint16_t)(vw & 0xFFFFu))), o0);
+        o1 = fmaf(pt, __half2float(__ushort_as_half((uint16_t)(vw >> 16))), o1);
     }
-#pragma unroll
-    for (int u = 0; u < NQW; ++u) {
-        const int h = wv + 4 * u;
-        if (h < NQ) {
-            float* rec = a.part + ((uint64_t)(j * NQ + h) * chunks + chunk) * (HD + 2);
-            reinterpret_cast<float2*>(rec)[lane] = make_float2(o0[u], o1[u]);
-            if (lane == 0) {
-                rec[HD] = mx[u];
-                rec[HD + 1] = sum[u];
-            }
-        }
+    float* rec = a.part + ((uint64_t)qh * chunks + chunk) * (HD + 2);
+    reinterpret_cast<float2*>(rec)[lane] = make_float2(o0, o1);
+    if (lane == 0) {
+        rec[HD] = mx;
+        rec[HD + 1] = sum;
     }
 }
 
 // merge the chunk partials of one q head: out = sum_c e^(m_c - M) o_c /
 // sum_c e^(m_c - M) l_c, i.e. softmax over every position (softmax_in_place,
-// math.rs:728-744) then the weighted sum of values.
-__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part, uint32_t chunks,
-                                                        float* __restrict__ out)
+// math.rs:728-744) then the weighted sum of values.  The per-chunk weights
+// are formed in parallel; each dim's sum runs over half the chunks per
+// thread with independent loads.
+constexpr uint32_t MERGE_MAX_CHUNKS = 1024; // max_context / ATTN_CHUNK (65536 positions)
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, uint32_t chunks,
+                                                         float* __restrict__ out)
 {
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    __shared__ float ec[MERGE_MAX_CHUNKS];
+    __shared__ float red[8];
+    __shared__ float half_acc[HD];
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* ph = part + (uint64_t)h * chunks * (HD + 2);
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < chunks; ++c)
-        M = fmaxf(M, ph[(uint64_t)c * (HD + 2) + HD]);
-    float L = 0.0f, acc = 0.0f;
-    for (uint32_t c = 0; c < chunks; ++c) {
+    float m = -INFINITY;
+    for (uint32_t c = tid; c < chunks; c += 256)
+        m = fmaxf(m, ph[(uint64_t)c * (HD + 2) + HD]);
+    m = wave_max(m);
+    if (lane == 0)
+        red[wv] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    for (uint32_t c = tid; c < chunks; c += 256) {
         const float* rec = ph + (uint64_t)c * (HD + 2);
         const float e = expf(rec[HD] - M);
-        L = fmaf(e, rec[HD + 1], L);
-        acc = fmaf(e, rec[d], acc);
+        ec[c] = e;
+        l = fmaf(e, rec[HD + 1], l);
     }
-    out[(uint64_t)h * HD + d] = acc / L;
+    l = wave_sum(l);
+    if (lane == 0)
+        red[4 + wv] = l;
+    __syncthreads();
+    const float L = (red[4] + red[5]) + (red[6] + red[7]);
+    const uint32_t d = tid & (HD - 1), part_i = tid / HD; // two threads per dim
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t c = part_i;
+    for (; c + 14 < chunks; c += 16) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            acc[u] = fmaf(ec[c + 2 * u], ph[(uint64_t)(c + 2 * u) * (HD + 2) + d], acc[u]);
+    }
+    for (; c < chunks; c += 2)
+        acc[0] = fmaf(ec[c], ph[(uint64_t)c * (HD + 2) + d], acc[0]);
+    float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    if (part_i == 1)
+        half_acc[d] = sum;
+    __syncthreads();
+    if (part_i == 0)
+        out[(uint64_t)h * HD + d] = (sum + half_acc[d]) / L;
 }
 
 // RMSNorm with weight, one workgroup: rms_norm_with_weight_and_epsilon
@@ -360,18 +358,19 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
         return e;
     // 2. chunk partials
     const uint32_t chunks = (a.position + 1 + CH - 1) / CH;
-    const dim3 g2(chunks, a.kv_heads);
     switch (nq) {
-    case 1: hipLaunchKernelGGL((attn_chunk_kernel<1>), g2, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((attn_chunk_kernel<2>), g2, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((attn_chunk_kernel<4>), g2, dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((attn_chunk_kernel<8>), g2, dim3(256), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((attn_chunk_kernel<1>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_chunk_kernel<2>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 2), dim3(256), 0, st, a); break;
     default: return hipErrorInvalidValue;
     }
     if ((e = hipGetLastError()) != hipSuccess)
         return e;
     // 3. merge
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads), dim3(HD), 0, st, (const float*)a.part, chunks,
+    if (chunks > MERGE_MAX_CHUNKS)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads), dim3(256), 0, st, (const float*)a.part, chunks,
                        a.attn_out);
     if ((e = hipGetLastError()) != hipSuccess)
         return e;
