@@ -324,13 +324,16 @@ def stack_bytes_per_token(acfg, mcfg, layers: int, position: int) -> dict:
 
 def bench_stack(args, ctx, ev) -> dict:
     """one token through the 48-layer decode stack —
-    per layer the GQA attention block (pbmoe_attention_decode: q/k/v, q/k norm
-    + RoPE, f16 KV cache at context 4096, o_proj + residual, post-attention
-    RMSNorm) and the C1 MoE layer (pbmoe_moe_layer, the next layer's input
-    RMSNorm fused).  KV rows 0..4094 hold synthetic f16 values, the timed
-    token is position 4095; expert and attention weights are seeded zero-mean
-    4-bit (the stack's activations stay bounded across 48 layers).  The
-    timed steps replay a hipGraph of one token's launches."""
+    per layer the GQA attention block (pbmoe_attention_decode: input RMSNorm
+    inside the q/k/v projection, q/k norm + RoPE, f16 KV cache at context
+    4096, o_proj + residual) and the C1 MoE layer (pbmoe_moe_layer_norm: the
+    post-attention RMSNorm inside the router stage).  --stack-norms split
+    runs the two norms as separate passes instead (post_normed output of the
+    attention call, next-layer norm fused into the MoE combine), for
+    comparison.  KV rows 0..4094 hold synthetic f16 values, the timed token
+    is position 4095; expert and attention weights are seeded zero-mean 4-bit
+    (the stack's activations stay bounded across 48 layers).  The timed steps
+    replay a hipGraph of one token's launches."""
     from pb_amd import abi, synth
     from pb_amd.configs import C1, C4_ATTN, C4_LAYERS
     from pb_amd.flashmoe import AttentionLayer
@@ -360,10 +363,18 @@ def bench_stack(args, ctx, ev) -> dict:
     print(f"[bench] stack setup {time.perf_counter() - t_setup:.1f} s: {L} layers, context {pos + 1}",
           file=sys.stderr, flush=True)
 
+    fused = args.stack_norms == "fused"
+
     def token(parts=("attn", "moe")):
         bufs = ((x_a, h_a), (x_b, h_b))
         for l in range(L):
             (x, h), (xn, hn) = bufs[l % 2], bufs[(l + 1) % 2]
+            if fused:
+                if "attn" in parts:
+                    atts[l].decode(h, h, pos, mid, input_norm=atts[l].input_norm)
+                if "moe" in parts:
+                    moes[l][0].forward_norm(mid, atts[l].post_norm, hn, ids, wts)
+                continue
             if "attn" in parts:
                 atts[l].decode(x, h, pos, mid, post_norm=atts[l].post_norm, post_normed=post)
             if "moe" in parts:
@@ -406,6 +417,7 @@ def bench_stack(args, ctx, ev) -> dict:
         "dtype": "f32 (f16 KV cache, 4-bit weights)",
         "data": "synthetic",
         "config": {"workload": "c4_stack_decode", "layers": L, "context": pos + 1, "hidden": H,
+                   "norms": args.stack_norms,
                    "q_heads": acfg.q_heads, "kv_heads": acfg.kv_heads, "head_dim": acfg.head_dim,
                    "experts": mcfg.experts, "k": mcfg.k, "intermediate": mcfg.intermediate,
                    "quant": "q4 affine g64 f16 scale/bias (zero-mean)"},
@@ -459,6 +471,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stack-norms", choices=("fused", "split"), default="fused",
+                    help="c4_stack: RMSNorms inside the projection/router kernels, or as separate passes")
     ap.add_argument("--prefill", action="store_true",
                     help="layer-major prefill of --tokens (default: the config's) instead of decode")
     ap.add_argument("--expert-phase", action="store_true",

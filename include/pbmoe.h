@@ -242,6 +242,15 @@ int pbmoe_moe_decode(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float
 int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                     uint32_t tokens, uint32_t* ids_out, float* weights_out,
                     const float* next_norm_weight, float* hidden_out, float* next_normed_out);
+/* pbmoe_moe_layer on the un-normalised hidden state: x = RMSNorm(hidden) *
+ * norm_weight (the post-attention norm, rms_norm_with_weight_and_epsilon,
+ * math.rs:151-167, eps = norm_epsilon) is formed inside the router stage,
+ * as CMD2 fuses it after out_proj + residual (metal/mod.rs:2864-2917), and
+ * hidden is the residual.  hidden_out must not alias hidden; tokens <= 16. */
+int pbmoe_moe_layer_norm(pbmoe_ctx* ctx, uint32_t layer, const float* hidden,
+                         const float* norm_weight, uint32_t tokens, uint32_t* ids_out,
+                         float* weights_out, const float* next_norm_weight, float* hidden_out,
+                         float* next_normed_out);
 /* Layer-major prefill (qwen_layer_major_experts, runtime/mod.rs:1151-1161,
  * metal/mod.rs:3583-4106): 1 <= tokens <= 32768.  Same arguments and result
  * contract as pbmoe_moe_decode.  Up to 16 tokens run the decode kernels, so
@@ -342,12 +351,16 @@ int pbmoe_attention_kv_cache(pbmoe_ctx* ctx, uint32_t layer, void** keys, void**
  * over positions 0..position (this position's k/v written to the cache
  * first) -> o_proj; hidden_out [H] = residual + o; when post_norm_weight is
  * not NULL, post_normed_out [H] = RMSNorm(hidden_out) * post_norm_weight.
- * attn_out [q_heads*head_dim] (optional, may be NULL) receives the attention
- * values before o_proj.  All pointers are device memory. */
+ * When input_norm_weight is not NULL, `normed` is the hidden state before
+ * input_layernorm and the RMSNorm (desc->norm_epsilon) is applied inside the
+ * projection kernel (the deferred next-layer norm handoff; callers then pass
+ * the same hidden state as `residual`).  attn_out [q_heads*head_dim]
+ * (optional, may be NULL) receives the attention values before o_proj.  All
+ * pointers are device memory. */
 int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float* normed,
-                           const float* residual, uint32_t position, float* hidden_out,
-                           const float* post_norm_weight, float* post_normed_out,
-                           float* attn_out);
+                           const float* input_norm_weight, const float* residual,
+                           uint32_t position, float* hidden_out, const float* post_norm_weight,
+                           float* post_normed_out, float* attn_out);
 
 #ifdef __cplusplus
 }

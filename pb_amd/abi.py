@@ -122,6 +122,7 @@ _SIG = {
     "pbmoe_route_logits": ([_P, _U32, _P, _U32, _P, _P], C.c_int),
     "pbmoe_moe_decode": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_moe_layer": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
+    "pbmoe_moe_layer_norm": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_moe_prefill": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_dispatch_plan": ([_P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_q4_dequantize": ([_P, _P, _P, _P, _U32, _U32, _U32, _U32, _P], C.c_int),
@@ -130,7 +131,7 @@ _SIG = {
     "pbmoe_bind_attention": ([_P, _U32, C.POINTER(AttnDesc), C.POINTER(AttnWeights)], C.c_int),
     "pbmoe_unbind_attention": ([_P, _U32], C.c_int),
     "pbmoe_attention_kv_cache": ([_P, _U32, C.POINTER(_P), C.POINTER(_P)], C.c_int),
-    "pbmoe_attention_decode": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P], C.c_int),
+    "pbmoe_attention_decode": ([_P, _U32, _P, _P, _P, _U32, _P, _P, _P, _P], C.c_int),
 }
 
 _lib: C.CDLL | None = None

@@ -103,6 +103,7 @@ struct pbmoe_ctx {
     DeviceBuf prefill; // prefill scratch (operand splits, activations, y)
     DeviceBuf plan_work; // multi-workgroup plan scratch of pbmoe_dispatch_plan
     DeviceBuf attn_scratch; // q/k/v, chunk partials and attention values of one decode step
+    DeviceBuf x_normed;     // [T][H] input RMSNorm rows of pbmoe_moe_layer_norm
     hipEvent_t phase_ev[6] = {};
     bool phase_timing = false;
 };
@@ -440,7 +441,7 @@ PBMOE_API int pbmoe_ctx_destroy(pbmoe_ctx* ctx)
     }
     for (DeviceBuf* b : {&ctx->logits, &ctx->act, &ctx->act_shared, &ctx->shared_weight,
                          &ctx->plan, &ctx->route_ids, &ctx->route_w, &ctx->prefill,
-                         &ctx->plan_work, &ctx->attn_scratch})
+                         &ctx->plan_work, &ctx->attn_scratch, &ctx->x_normed})
         free_buf(*b);
     (void)hipFree(ctx->status);
     (void)hipStreamDestroy(ctx->stream);
@@ -884,7 +885,7 @@ PBMOE_API int pbmoe_route_logits(pbmoe_ctx* ctx, uint32_t layer, const float* lo
 static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                         uint32_t tokens, uint32_t* ids, float* weights,
                         const float* next_norm_weight, float* hidden_out, float* next_normed_out,
-                        uint32_t mode)
+                        uint32_t mode, const float* in_norm_weight = nullptr)
 {
     if (!ctx || !x || !residual || !hidden_out || (mode == pbmoe::DECODE_EXPERTS && (!ids || !weights)))
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
@@ -913,11 +914,14 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
     if (tokens > MAX_DECODE_TOKENS)
         return fail(PBMOE_ERR_UNSUPPORTED, "decode expert phase supports at most %u tokens, got %u",
                     MAX_DECODE_TOKENS, tokens);
-    for (const void* p : {(const void*)x, (const void*)residual, (const void*)hidden_out})
+    for (const void* p : {(const void*)x, (const void*)residual, (const void*)hidden_out,
+                          (const void*)in_norm_weight})
         if (!aligned(p, 16))
-            return fail(PBMOE_ERR_ALIGNMENT, "activation buffers must be 16-byte aligned");
+            return fail(PBMOE_ERR_ALIGNMENT, "activation and norm buffers must be 16-byte aligned");
     rc = set_device(ctx);
     if (rc)
+        return rc;
+    if (in_norm_weight && (rc = ensure(ctx, ctx->x_normed, (size_t)tokens * d.hidden * 4)))
         return rc;
     if (mode == pbmoe::DECODE_FULL_LAYER && (!ids || !weights)) {
         if ((rc = ensure(ctx, ctx->route_ids, (size_t)tokens * d.active_experts * 4)))
@@ -932,6 +936,10 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
     if ((rc = decode_args(ctx, b, x, residual, tokens, ids, weights, next_norm_weight, hidden_out,
                           next_normed_out, &sh, &a)))
         return rc;
+    if (in_norm_weight) {
+        a.in_norm_w = in_norm_weight;
+        a.x_normed = static_cast<float*>(ctx->x_normed.ptr);
+    }
     HIP_TRY(pbmoe::launch_decode_layer(ctx->stream, a, mode));
     return ok();
 }
@@ -958,6 +966,26 @@ PBMOE_API int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x,
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "ids_out and weights_out must be given together");
     return expert_phase(ctx, layer, x, residual, tokens, ids_out, weights_out, next_norm_weight,
                         hidden_out, next_normed_out, pbmoe::DECODE_FULL_LAYER);
+}
+
+// The same layer taking the un-normalised hidden state: the input RMSNorm
+// (the post-attention norm, rms_norm_with_weight_and_epsilon,
+// math.rs:151-167, as CMD2 fuses it after out_proj + residual,
+// metal/mod.rs:2864-2917) runs inside the router stage, and `hidden` is also
+// the residual.  Saves the separate norm launch of a decode step.
+PBMOE_API int pbmoe_moe_layer_norm(pbmoe_ctx* ctx, uint32_t layer, const float* hidden,
+                                   const float* norm_weight, uint32_t tokens, uint32_t* ids_out,
+                                   float* weights_out, const float* next_norm_weight,
+                                   float* hidden_out, float* next_normed_out)
+{
+    if (!norm_weight)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if ((ids_out == nullptr) != (weights_out == nullptr))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ids_out and weights_out must be given together");
+    if (hidden && hidden == hidden_out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "hidden_out must not alias hidden");
+    return expert_phase(ctx, layer, hidden, hidden, tokens, ids_out, weights_out, next_norm_weight,
+                        hidden_out, next_normed_out, pbmoe::DECODE_FULL_LAYER, norm_weight);
 }
 
 static size_t align256(size_t v)
@@ -1316,7 +1344,8 @@ PBMOE_API int pbmoe_attention_kv_cache(pbmoe_ctx* ctx, uint32_t layer, void** ke
 }
 
 PBMOE_API int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float* normed,
-                                     const float* residual, uint32_t position, float* hidden_out,
+                                     const float* input_norm_weight, const float* residual,
+                                     uint32_t position, float* hidden_out,
                                      const float* post_norm_weight, float* post_normed_out,
                                      float* attn_out)
 {
@@ -1331,8 +1360,8 @@ PBMOE_API int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float
     if (position >= b.desc.max_context)
         return fail(PBMOE_ERR_SHAPE, "position %u beyond the KV cache (%u positions)", position,
                     b.desc.max_context);
-    for (const void* p : {(const void*)normed, (const void*)residual, (const void*)hidden_out,
-                          (const void*)post_normed_out, (const void*)attn_out})
+    for (const void* p : {(const void*)normed, (const void*)input_norm_weight, (const void*)residual,
+                          (const void*)hidden_out, (const void*)post_normed_out, (const void*)attn_out})
         if (p && !aligned(p, 16))
             return fail(PBMOE_ERR_ALIGNMENT, "activation buffers must be 16-byte aligned");
     int rc = set_device(ctx);
@@ -1351,6 +1380,7 @@ PBMOE_API int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float
     pbmoe::AttnArgs a = b.base;
     a.position = position;
     a.normed = normed;
+    a.in_norm_w = input_norm_weight;
     a.residual = residual;
     a.hidden_out = hidden_out;
     a.post_norm_w = post_norm_weight;

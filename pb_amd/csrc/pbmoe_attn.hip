@@ -43,6 +43,8 @@ struct RowsArgs {
     uint32_t first[4];
     uint32_t group_shift;
     const float* x;        // [cols]
+    const float* norm_w;   // null, or RMSNorm weight [cols]: x is normalised first
+    float eps;
     const float* residual; // null or [total rows]
     float* y;              // [total rows]
 };
@@ -51,22 +53,30 @@ template <int SBT, int CPL>
 __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
 {
     constexpr int RPW = 2;
+    // x is staged in LDS once per workgroup with coalesced loads (a lane's
+    // own 32-float chunk read straight from memory would touch a different
+    // cache line in every lane); chunks sit XP floats apart so that the
+    // lanes' 16-byte reads of consecutive chunks fall on distinct banks.
+    constexpr int XP = 36;
+    __shared__ __align__(16) float xl[WAVE * CPL * XP];
+    __shared__ float red[4];
     const int lane = threadIdx.x & 63;
     const uint32_t r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
-    if (r0 >= a.first[a.n_mat])
-        return;
+    const bool active = r0 < a.first[a.n_mat];
+    const uint32_t rr = active ? r0 : 0u; // idle waves still reach the barrier
     uint32_t mi = 0;
-    while (mi + 1 < a.n_mat && r0 >= a.first[mi + 1])
+    while (mi + 1 < a.n_mat && rr >= a.first[mi + 1])
         ++mi;
     const Q4Mat m = a.m[mi];
-    const uint32_t row0 = r0 - a.first[mi];
-    const uint32_t chunks = m.cols / 32, gpr = m.cols >> a.group_shift;
+    const uint32_t row0 = rr - a.first[mi];
+    const uint32_t cols = a.m[0].cols; // every matrix of one launch has the same columns
+    const uint32_t chunks = cols / 32, gpr = cols >> a.group_shift;
     uint4 w[RPW][CPL];
     float sc[RPW][CPL], bi[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const uint32_t row = row0 + r;
-        const uint4* wp = reinterpret_cast<const uint4*>(m.codes + (uint64_t)row * (m.cols / 2));
+        const uint4* wp = reinterpret_cast<const uint4*>(m.codes + (uint64_t)row * (cols / 2));
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const uint32_t ch = lane + WAVE * c;
@@ -78,6 +88,33 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
             }
         }
     }
+    // Stage x (times the norm weight when the input RMSNorm is fused).  Every
+    // row product is linear in the norm's scale, so the sums are multiplied
+    // by 1 / sqrt(mean(x^2) + eps) at the end (math.rs:151-167).
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2 * CPL; ++j) {
+        const uint32_t f = threadIdx.x + 256u * j; // float4 index
+        if (f < cols / 4) {
+            float4 v = reinterpret_cast<const float4*>(a.x)[f];
+            if (a.norm_w) {
+                const float4 nw = reinterpret_cast<const float4*>(a.norm_w)[f];
+                ss = fmaf(v.x, v.x, ss), ss = fmaf(v.y, v.y, ss), ss = fmaf(v.z, v.z, ss), ss = fmaf(v.w, v.w, ss);
+                v.x *= nw.x, v.y *= nw.y, v.z *= nw.z, v.w *= nw.w;
+            }
+            *reinterpret_cast<float4*>(&xl[(f >> 3) * XP + (f & 7) * 4]) = v;
+        }
+    }
+    if (a.norm_w) {
+        ss = wave_sum(ss);
+        if (lane == 0)
+            red[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    if (!active)
+        return;
+    const float inv_rms =
+        a.norm_w ? 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)cols + a.eps) : 1.0f;
     float acc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
@@ -86,7 +123,7 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
     for (int c = 0; c < CPL; ++c) {
         const uint32_t ch = lane + WAVE * c;
         if (ch < chunks) {
-            const float4* x4 = reinterpret_cast<const float4*>(a.x + ch * 32);
+            const float4* x4 = reinterpret_cast<const float4*>(&xl[ch * XP]);
             float xv[32];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -104,7 +141,7 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
     }
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-        const float s = wave_sum(acc[r]);
+        const float s = wave_sum(acc[r]) * inv_rms;
         if (lane == r) {
             const uint32_t o = r0 + r;
             a.y[o] = a.residual ? a.residual[o] + s : s;
@@ -351,6 +388,8 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
     r.first[0] = 0, r.first[1] = qw, r.first[2] = qw + kvw, r.first[3] = qw + 2 * kvw;
     r.group_shift = a.group_shift;
     r.x = a.normed;
+    r.norm_w = a.in_norm_w;
+    r.eps = a.post_eps;
     r.residual = nullptr;
     r.y = a.qkv;
     hipError_t e = a.sb_dtype == 2 ? launch_rows<2>(st, r) : launch_rows<1>(st, r);
@@ -381,6 +420,7 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
     o.first[0] = 0, o.first[1] = a.hidden;
     o.group_shift = a.group_shift;
     o.x = a.attn_out;
+    o.norm_w = nullptr;
     o.residual = a.residual;
     o.y = a.hidden_out;
     e = a.sb_dtype == 2 ? launch_rows<2>(st, o) : launch_rows<1>(st, o);

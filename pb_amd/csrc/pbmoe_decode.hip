@@ -44,7 +44,38 @@ struct RouterArgs {
     float* logits;        // [T][E]
     float* act_shared;    // [T][Is]
     float* shared_weight; // [T]
+    const float* norm_w;  // null, or the input RMSNorm weight [H]: x is the hidden state
+    float eps;
+    float* x_out;         // [T][H] normalised rows, written by the last workgroup (norm_w set)
 };
+
+// Fused input RMSNorm (rms_norm_with_weight_and_epsilon, math.rs:151-167).
+// Every product W . (x * inv_rms * w) is linear in the scale, so a wave
+// dots W with x * w and multiplies the wave sum by inv_rms, which it forms
+// from sum(x^2) over the same x registers: no extra loads, no barrier.
+//
+// x [t][col .. col+8) as two float4; with norm_w: the squares go to ss and
+// the values are multiplied by the weight.
+__device__ __forceinline__ void load_x8(const float* __restrict__ x, uint64_t off, const float* norm_w,
+                                        uint32_t col, float4& u, float4& v, float& ss)
+{
+    const float4* xp = reinterpret_cast<const float4*>(x + off);
+    u = xp[0], v = xp[1];
+    if (norm_w) {
+        ss = fmaf(u.x, u.x, ss), ss = fmaf(u.y, u.y, ss), ss = fmaf(u.z, u.z, ss), ss = fmaf(u.w, u.w, ss);
+        ss = fmaf(v.x, v.x, ss), ss = fmaf(v.y, v.y, ss), ss = fmaf(v.z, v.z, ss), ss = fmaf(v.w, v.w, ss);
+        const float4 w0 = *reinterpret_cast<const float4*>(norm_w + col);
+        const float4 w1 = *reinterpret_cast<const float4*>(norm_w + col + 4);
+        u.x *= w0.x, u.y *= w0.y, u.z *= w0.z, u.w *= w0.w;
+        v.x *= w1.x, v.y *= w1.y, v.z *= w1.z, v.w *= w1.w;
+    }
+}
+
+// 1 / sqrt(mean(x^2) + eps) from this lane's partial sum of squares
+__device__ __forceinline__ float inv_rms_of(float ss, uint32_t H, float eps)
+{
+    return 1.0f / sqrtf(wave_sum(ss) / (float)H + eps);
+}
 
 template <int WDT>
 __device__ __forceinline__ void load_dense8(const void* w, uint64_t off, float (&v)[8])
@@ -72,7 +103,8 @@ __device__ __forceinline__ void load_dense8(const void* w, uint64_t off, float (
 // dense row . x for every token (8 columns per lane per chunk of 512)
 template <int WDT, int CR>
 __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, const float* x,
-                                               uint32_t T, uint32_t H, float* out, uint32_t out_stride)
+                                               uint32_t T, uint32_t H, float* out, uint32_t out_stride,
+                                               const float* norm_w, float eps)
 {
     const int lane = threadIdx.x & 63;
     float wv[CR][8];
@@ -88,13 +120,13 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
         }
     }
     for (uint32_t t = 0; t < T; ++t) {
-        float acc0 = 0.0f, acc1 = 0.0f;
+        float acc0 = 0.0f, acc1 = 0.0f, ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < CR; ++c) {
             const uint32_t col = (uint32_t)lane * 8 + c * 512;
             if (col < H) {
-                const float4* xp = reinterpret_cast<const float4*>(x + (uint64_t)t * H + col);
-                const float4 u = xp[0], v = xp[1];
+                float4 u, v;
+                load_x8(x, (uint64_t)t * H + col, norm_w, col, u, v, ss);
                 acc0 = fmaf(wv[c][0], u.x, acc0);
                 acc1 = fmaf(wv[c][1], u.y, acc1);
                 acc0 = fmaf(wv[c][2], u.z, acc0);
@@ -105,7 +137,9 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
                 acc1 = fmaf(wv[c][7], v.w, acc1);
             }
         }
-        const float s = wave_sum(acc0 + acc1);
+        float s = wave_sum(acc0 + acc1);
+        if (norm_w)
+            s *= inv_rms_of(ss, H, eps);
         if (lane == 0)
             out[(uint64_t)t * out_stride] = s;
     }
@@ -123,7 +157,8 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
     const uint32_t n_waves = gridDim.x * 4;
     for (uint32_t task = wave_id; task < n_tasks; task += n_waves) {
         if (task < n_router) {
-            dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, a.x, T, H, a.logits + task, n_router);
+            dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, a.x, T, H, a.logits + task, n_router,
+                                    a.norm_w, a.eps);
         } else if (task < n_router + Is) {
             const uint32_t i = task - n_router;
             const ExpertSet& s = a.sh;
@@ -146,31 +181,64 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
                 }
             }
             for (uint32_t t = 0; t < T; ++t) {
-                float pg = 0.0f, pu = 0.0f;
+                float pg = 0.0f, pu = 0.0f, ss = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CS; ++c) {
                     const uint32_t ch = lane + WAVE * c;
                     if (ch < chunks) {
-                        float xs;
-                        const float* xp = a.x + (uint64_t)t * H + ch * 32;
-                        const float qg = q4_chunk_qx(wg[c], xp, xs);
-                        float xs2;
-                        const float qu = q4_chunk_qx(wu[c], xp, xs2);
+                        float xv[32];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            float4 u, v;
+                            load_x8(a.x, (uint64_t)t * H + ch * 32 + 8 * q, a.norm_w, ch * 32 + 8 * q, u, v, ss);
+                            xv[8 * q] = u.x, xv[8 * q + 1] = u.y, xv[8 * q + 2] = u.z, xv[8 * q + 3] = u.w;
+                            xv[8 * q + 4] = v.x, xv[8 * q + 5] = v.y, xv[8 * q + 6] = v.z, xv[8 * q + 7] = v.w;
+                        }
+                        float xs = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < 32; q += 8)
+                            xs += ((xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3])) +
+                                  ((xv[q + 4] + xv[q + 5]) + (xv[q + 6] + xv[q + 7]));
+                        const float qg = q4_chunk_qx_reg(wg[c], xv);
+                        const float qu = q4_chunk_qx_reg(wu[c], xv);
                         pg = fmaf(sg[c], qg, fmaf(bg[c], xs, pg));
                         pu = fmaf(su[c], qu, fmaf(bu[c], xs, pu));
                     }
                 }
-                const float g = wave_sum(pg);
-                const float u = wave_sum(pu);
+                float g = wave_sum(pg);
+                float u = wave_sum(pu);
+                if (a.norm_w) {
+                    const float inv = inv_rms_of(ss, H, a.eps);
+                    g *= inv, u *= inv;
+                }
                 if (lane == 0)
                     a.act_shared[(uint64_t)t * Is + i] = (g / (1.0f + expf(-g))) * u;
             }
         } else if (a.sgate_w) {
-            dense_row_dots<GDT, CR>(a.sgate_w, 0, a.x, T, H, a.shared_weight, 1);
+            dense_row_dots<GDT, CR>(a.sgate_w, 0, a.x, T, H, a.shared_weight, 1, a.norm_w, a.eps);
             // sigma applied by the consumer: shared_weight holds the gate logit
         } else if (lane == 0) {
             for (uint32_t t = 0; t < T; ++t)
                 a.shared_weight[t] = 80.0f; // sigma(80) = 1 (metal/mod.rs:4666-4669)
+        }
+    }
+    // the extra last workgroup (no tasks) writes the normalised rows for the
+    // gate/up kernel, wave w the tokens w, w + 4, ...
+    if (a.norm_w && blockIdx.x == gridDim.x - 1) {
+        for (uint32_t t = threadIdx.x >> 6; t < T; t += 4) {
+            const float* xr = a.x + (uint64_t)t * H;
+            float ss = 0.0f;
+            for (uint32_t i = (uint32_t)lane * 4; i < H; i += 256) {
+                const float4 v = *reinterpret_cast<const float4*>(xr + i);
+                ss = fmaf(v.x, v.x, ss), ss = fmaf(v.y, v.y, ss), ss = fmaf(v.z, v.z, ss), ss = fmaf(v.w, v.w, ss);
+            }
+            const float inv = inv_rms_of(ss, H, a.eps);
+            for (uint32_t i = (uint32_t)lane * 4; i < H; i += 256) {
+                const float4 v = *reinterpret_cast<const float4*>(xr + i);
+                const float4 w = *reinterpret_cast<const float4*>(a.norm_w + i);
+                *reinterpret_cast<float4*>(a.x_out + (uint64_t)t * H + i) =
+                    make_float4((v.x * inv) * w.x, (v.y * inv) * w.y, (v.z * inv) * w.z, (v.w * inv) * w.w);
+            }
         }
     }
 }
@@ -749,6 +817,9 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     a.sgate_w = do_shared ? d.sgate_w : nullptr;
     a.sgate_dtype = d.sgate_dtype;
     a.x = d.x;
+    a.norm_w = d.in_norm_w;
+    a.eps = d.eps;
+    a.x_out = d.x_normed;
     a.tokens = d.tokens;
     a.hidden = d.hidden;
     a.logits = d.logits;
@@ -764,7 +835,9 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
         }
         return hipSuccess;
     }
-    const uint32_t blocks = (tasks + 3) / 4;
+    // with the fused norm, one more workgroup (past every task) writes the
+    // normalised rows
+    const uint32_t blocks = (tasks + 3) / 4 + (a.norm_w ? 1u : 0u);
     const uint32_t cr = (d.hidden + 511) / 512;
     const uint32_t cs = (d.hidden / 32 + 63) / 64;
     if (cr > 16 || cs > 4)
@@ -822,7 +895,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     ea.ids = d.ids;
     ea.weights = d.weights;
     ea.plan = d.plan;
-    ea.x = d.x;
+    ea.x = d.in_norm_w ? d.x_normed : d.x; // normalised by the router stage
     ea.tokens = T;
     ea.hidden = H;
     ea.act = d.act;
@@ -926,6 +999,8 @@ hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mod
 {
     if (mode != DECODE_ROUTE_ONLY && (!set_ok(d.ex) || (d.shared && !set_ok(*d.shared))))
         return hipErrorInvalidValue; // the kernels index scales with group_shift
+    if (d.in_norm_w && (mode != DECODE_FULL_LAYER || !d.x_normed || d.tokens > (uint32_t)DEC_T))
+        return hipErrorInvalidValue; // the fused norm runs in the router stage of the full layer
     hipError_t err;
     if (mode == DECODE_ROUTE_ONLY) {
         // router rows, then the routing stage of one wave per token

@@ -78,7 +78,9 @@ struct DecodeArgs {
     const ExpertSet* shared;   // host pointer, null without a shared expert
     const void* sgate_w;       // shared gate row [H], null: sigma = 1
     uint32_t sgate_dtype;
-    const float* x;            // [T][H]
+    const float* x;            // [T][H] (the hidden state when in_norm_w is set)
+    const float* in_norm_w;    // null, or input RMSNorm weight [H] (full layer only)
+    float* x_normed;           // [T][H] scratch: RMSNorm(x) * in_norm_w
     const float* residual;     // [T][H]
     uint32_t tokens, hidden;
     float* act;                // [T*K][I]
@@ -164,7 +166,8 @@ struct AttnArgs {
     uint16_t* cache_k;     // [max_context][kv_heads][head_dim] f16
     uint16_t* cache_v;
     uint32_t position;
-    const float* normed;   // [H]
+    const float* normed;   // [H]: the normalised input, or the hidden state when in_norm_w is set
+    const float* in_norm_w; // null, or the input RMSNorm weight [H] (normalised inside)
     const float* residual; // [H]
     float* hidden_out;     // [H]
     const float* post_norm_w; // null: no post-attention norm

@@ -97,6 +97,17 @@ class MoeLayer:
                                     next_norm.ptr if next_norm is not None else None, hidden_out.ptr,
                                     next_normed.ptr if next_normed is not None else None))
 
+    # -- whole block from the un-normalised hidden state (CMD2's fused
+    #    post-attention RMSNorm, metal/mod.rs:2864-2917) --------------------
+    def forward_norm(self, hidden: DeviceArray, norm_weight: DeviceArray, hidden_out: DeviceArray,
+                     ids: DeviceArray | None = None, weights: DeviceArray | None = None,
+                     next_norm: DeviceArray | None = None, next_normed: DeviceArray | None = None):
+        check(lib().pbmoe_moe_layer_norm(self.ctx.handle, self.index, hidden.ptr, norm_weight.ptr,
+                                         hidden.shape[0], ids.ptr if ids is not None else None,
+                                         weights.ptr if weights is not None else None,
+                                         next_norm.ptr if next_norm is not None else None, hidden_out.ptr,
+                                         next_normed.ptr if next_normed is not None else None))
+
     # -- layer-major prefill (qwen_layer_major_experts) -----------------------
     def qwen_layer_major_experts(self, x: DeviceArray, residual: DeviceArray, ids: DeviceArray,
                                  weights: DeviceArray, hidden_out: DeviceArray,
@@ -182,9 +193,12 @@ class AttentionLayer:
 
     def decode(self, normed: DeviceArray, residual: DeviceArray, position: int, hidden_out: DeviceArray,
                post_norm: DeviceArray | None = None, post_normed: DeviceArray | None = None,
-               attn_out: DeviceArray | None = None):
-        check(lib().pbmoe_attention_decode(self.ctx.handle, self.index, normed.ptr, residual.ptr, position,
-                                           hidden_out.ptr, post_norm.ptr if post_norm is not None else None,
+               attn_out: DeviceArray | None = None, input_norm: DeviceArray | None = None):
+        """input_norm given: `normed` is the hidden state before input_layernorm."""
+        check(lib().pbmoe_attention_decode(self.ctx.handle, self.index, normed.ptr,
+                                           input_norm.ptr if input_norm is not None else None, residual.ptr,
+                                           position, hidden_out.ptr,
+                                           post_norm.ptr if post_norm is not None else None,
                                            post_normed.ptr if post_normed is not None else None,
                                            attn_out.ptr if attn_out is not None else None))
 

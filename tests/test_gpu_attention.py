@@ -110,13 +110,40 @@ def test_attention_long_context_matches_oracle(ctx, pos):
     abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
 
 
+@pytest.mark.parametrize("acfg", [SHAPES[1], C4_ATTN], ids=["t_q16_kv4", "c4"])
+def test_attention_fused_input_norm_matches_oracle(ctx, acfg):
+    """The input RMSNorm formed inside the q/k/v projection kernel
+    (input_norm given, the un-normalised hidden state passed): positions
+    0..69 against the oracle on oracle-normalised rows, with the hidden state
+    also the residual."""
+    layer = 54
+    dev = AttentionLayer(ctx, layer, acfg).bind_synth(SEED, layer)
+    orc_l = _oracle(acfg, layer)
+    H = acfg.hidden
+    rng = np.random.default_rng(11)
+    x_d, h_d = ctx.array((H,), F), ctx.array((H,), F)
+    n_d, a_d = ctx.array((H,), F), ctx.array((acfg.q_width,), F)
+    for pos in range(70):
+        x = (rng.standard_normal(H) * 3.0).astype(F)
+        x_d.upload(x)
+        dev.decode(x_d, x_d, pos, h_d, post_norm=dev.post_norm, post_normed=n_d, attn_out=a_d,
+                   input_norm=dev.input_norm)
+        ctx.sync()
+        ref_att, ref_o = orc_l.decode(orc.rms_norm(x, dev.input_norm_h, acfg.eps), pos)
+        _check_attention(a_d.download(), ref_att, f"{acfg.name} pos {pos}")
+        ref_h = x + ref_o
+        assert_layer_tolerance(h_d.download(), ref_h, f"{acfg.name} hidden pos {pos}")
+        assert_layer_tolerance(n_d.download(), orc.rms_norm(ref_h, dev.post_norm_h, acfg.eps), "post_normed")
+    abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
+
+
 def test_attention_rejects_position_beyond_cache(ctx):
     acfg = synth.AttnConfig("t_small", hidden=512, q_heads=8, kv_heads=2, max_context=16)
     layer = 52
     dev = AttentionLayer(ctx, layer, acfg).bind_synth(SEED, layer)
     H = acfg.hidden
     x_d, h_d = ctx.array((H,), F), ctx.array((H,), F)
-    rc = abi.lib().pbmoe_attention_decode(ctx.handle, layer, x_d.ptr, x_d.ptr, 16, h_d.ptr, None, None, None)
+    rc = abi.lib().pbmoe_attention_decode(ctx.handle, layer, x_d.ptr, None, x_d.ptr, 16, h_d.ptr, None, None, None)
     assert rc == abi.ERR_SHAPE
     abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
 

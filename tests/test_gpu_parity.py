@@ -13,7 +13,7 @@ from oracle import oracle as orc
 from pb_amd import abi, synth
 from pb_amd.configs import C1, C2, C3, C5
 from pb_amd.flashmoe import dispatch_plan
-from tests.gpu_common import SEED, DeviceLayer, assert_layer_tolerance
+from tests.gpu_common import SEED, DeviceLayer, assert_layer_tolerance, max_abs_rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -289,6 +289,69 @@ def test_fused_layer_matches_split_and_oracle(ctx, cfg, T, order):
     exact = dl.exact_block(xh, rh, ids_h, w.download()) if np.max(np.abs(ref_h)) > 1e3 else None
     mx, rel = assert_layer_tolerance(out.download(), ref_h, exact=exact)
     _say(f"[result] fused {cfg.name} T={T}: max_abs={mx:.3e} rel_l2={rel:.3e}")
+
+
+@pytest.mark.parametrize("cfg,T", [(C1, 1), (C2, 1), (C2, 8), (C2, 16), (C5, 2)])
+def test_fused_norm_layer_matches_oracle(ctx, cfg, T):
+    """pbmoe_moe_layer_norm: the input RMSNorm (rms_norm_with_weight_and_epsilon,
+    math.rs:151-167) formed inside the router stage, hidden also the residual.
+    Routes equal those of pbmoe_moe_layer on the host-normalised rows (the
+    weights to f32 rounding of the norm), hidden and next-normed rows within
+    the bar of the oracle on oracle-normalised rows."""
+    _say(f"[test] fused-norm layer {cfg.name} T={T}")
+    dl = _layer(ctx, cfg, 0)
+    _, hh = synth.activations(SEED, 90 + T, T, cfg.hidden)
+    rng = np.random.default_rng(T)
+    nw = rng.uniform(0.5, 1.5, cfg.hidden).astype(np.float32)
+    nn = rng.uniform(0.5, 1.5, cfg.hidden).astype(np.float32)
+    # reference rows: the norm in f64, rounded once (a sequential f32 sum of
+    # H squares carries ~1e-5 relative error, a uniform scale on every x)
+    h64 = hh.astype(np.float64)
+    xh = (h64 / np.sqrt(np.mean(h64 * h64, axis=1, keepdims=True) + 1e-6) * nw).astype(np.float32)
+    h, nw_d, nn_d = ctx.to_device(hh), ctx.to_device(nw), ctx.to_device(nn)
+    ids = ctx.array((T, cfg.k), np.uint32)
+    w = ctx.array((T, cfg.k), np.float32)
+    out = ctx.array((T, cfg.hidden), np.float32)
+    nxt = ctx.array((T, cfg.hidden), np.float32)
+    dl.moe.forward_norm(h, nw_d, out, ids, w, nn_d, nxt)
+    x_ref = ctx.to_device(xh)
+    ids_split = ctx.array((T, cfg.k), np.uint32)
+    w_split = ctx.array((T, cfg.k), np.float32)
+    out_split = ctx.array((T, cfg.hidden), np.float32)
+    dl.moe.forward(x_ref, h, out_split, ids_split, w_split)
+    ctx.sync()
+    ids_h = ids.download().astype(np.int32)
+    np.testing.assert_array_equal(ids_h, ids_split.download().astype(np.int32))
+    np.testing.assert_allclose(w.download(), w_split.download(), rtol=1e-5, atol=1e-7)
+    w_h = w.download()
+    ref_h, ref_n = dl.oracle_block(xh, hh, ids_h, w_h, next_norm=nn)
+    if np.max(np.abs(ref_h)) > 1e3:
+        # Large outputs (the uncentred H=7168 layer, |h| ~ 3e4) amplify the
+        # f32 rounding of the normalised rows, which the device and the host
+        # norm round differently: the bar is the oracle's own response to a
+        # one-ulp perturbation of every element of x.
+        pr = np.random.default_rng(1)
+        xp = np.where(pr.random(xh.shape) < 0.5, np.nextafter(xh, np.inf), np.nextafter(xh, -np.inf))
+        ref_p, _ = dl.oracle_block(xp.astype(np.float32), hh, ids_h, w_h)
+        sens = float(np.max(np.abs(ref_p.astype(np.float64) - ref_h)))
+        mx, rel = max_abs_rel_l2(out.download(), ref_h)
+        _say(f"[result] fused-norm {cfg.name} T={T}: one-ulp sensitivity {sens:.3e}")
+        assert rel <= 2e-3 and mx <= max(1e-2, 4.0 * sens), f"max_abs={mx:.3e} rel_l2={rel:.3e} sens={sens:.3e}"
+        assert max_abs_rel_l2(nxt.download(), ref_n)[1] <= 2e-3
+    else:
+        mx, rel = assert_layer_tolerance(out.download(), ref_h)
+        assert_layer_tolerance(nxt.download(), ref_n, "next normed")
+    _say(f"[result] fused-norm {cfg.name} T={T}: max_abs={mx:.3e} rel_l2={rel:.3e}")
+
+
+def test_fused_norm_layer_rejects_aliasing(ctx):
+    dl = _layer(ctx, C1, 0)
+    h = ctx.array((1, C1.hidden), np.float32)
+    nw = ctx.array((C1.hidden,), np.float32)
+    rc = abi.lib().pbmoe_moe_layer_norm(ctx.handle, dl.moe.index, h.ptr, nw.ptr, 1, None, None, None, h.ptr, None)
+    assert rc == abi.ERR_INVALID_ARGUMENT
+    rc = abi.lib().pbmoe_moe_layer_norm(ctx.handle, dl.moe.index, h.ptr, None, 1, None, None, None, h.ptr, None)
+    assert rc == abi.ERR_INVALID_ARGUMENT
 
 
 def test_fused_layer_repeated_calls_are_deterministic(ctx):
