@@ -592,7 +592,10 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 // loads that do not wait for the routes; with more tokens they are read from
 // L2 per unit.
 // ---------------------------------------------------------------------------
-constexpr uint32_t STAGE_FLOATS = 12288; // 48 KB of staged activations
+constexpr uint32_t STAGE_FLOATS = 12288; // activations staged (54 KB of LDS in XP-padded chunks)
+// Staged chunk q (32 floats) sits at q * XP floats, so that the lanes'
+// 16-byte reads of consecutive chunks fall on distinct banks.
+constexpr int XP = 36;
 
 struct DownArgs {
     ExpertSet ex, sh;
@@ -618,7 +621,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     constexpr int SLOTS = 256 / LPR;
     __shared__ float ylds[DEC_ROUTES][R];
     __shared__ float yshl[DEC_T][R];
-    __shared__ float astage[STAGE_FLOATS];
+    __shared__ __align__(16) float astage[STAGE_FLOATS / 32 * XP];
     __shared__ float xsl[STAGE_FLOATS / 32]; // per-chunk sums of the staged activations
     const int gl = threadIdx.x % LPR;
     const int slot_id = threadIdx.x / LPR;
@@ -636,14 +639,15 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     if (a.stage) {
         const uint32_t n4 = (routes * I) / 4;
         const float4* src = reinterpret_cast<const float4*>(a.act);
-        float4* dst = reinterpret_cast<float4*>(astage);
         for (uint32_t i = threadIdx.x; i < n4; i += 256)
-            dst[i] = src[i];
+            *reinterpret_cast<float4*>(&astage[(i >> 3) * XP + (i & 7) * 4]) = src[i];
         if (a.has_shared) {
             const uint32_t m4 = (T * I) / 4;
             const float4* s2 = reinterpret_cast<const float4*>(a.act_shared);
-            for (uint32_t i = threadIdx.x; i < m4; i += 256)
-                dst[n4 + i] = s2[i];
+            for (uint32_t i = threadIdx.x; i < m4; i += 256) {
+                const uint32_t d = n4 + i; // I % 32 == 0: the shared rows start on a chunk
+                *reinterpret_cast<float4*>(&astage[(d >> 3) * XP + (d & 7) * 4]) = s2[i];
+            }
         }
     }
     const uint32_t n_routed = a.use_plan ? a.plan.unique_count[0] : routes;
@@ -691,7 +695,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             __syncthreads(); // staged activations visible
             const uint32_t n_chunks = (routes + (a.has_shared ? T : 0u)) * (I / 32);
             for (uint32_t q = threadIdx.x; q < n_chunks; q += 256) {
-                const float4* c4 = reinterpret_cast<const float4*>(astage + q * 32);
+                const float4* c4 = reinterpret_cast<const float4*>(astage + q * XP);
                 float sum = 0.0f;
 #pragma unroll
                 for (int v = 0; v < 8; ++v) {
@@ -723,12 +727,12 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                 if (live[m]) {
                     if (a.stage) {
                         const uint32_t rt = shared ? routes + j : g0 + j;
-                        const float* av = astage + (uint64_t)rt * I;
+                        const float* av = astage + rt * (I / 32) * XP;
                         const float* xs = xsl + rt * (I / 32);
 #pragma unroll
                         for (int c = 0; c < CPL; ++c) {
                             const uint32_t ch = gl + LPR * c;
-                            const float qx = q4_chunk_q(w[m][c], av + ch * 32);
+                            const float qx = q4_chunk_q(w[m][c], av + ch * XP);
                             part = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs[ch], part));
                         }
                     } else {
