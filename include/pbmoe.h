@@ -58,7 +58,9 @@ typedef enum pbmoe_status {
     PBMOE_ERR_TIMEOUT = 8,          /* device wait exceeded its limit         */
     PBMOE_ERR_NOT_BOUND = 9,        /* layer / router / shared not bound      */
     PBMOE_ERR_OUT_OF_MEMORY = 10,
-    PBMOE_ERR_NONFINITE = 11        /* non-finite router score or weight      */
+    PBMOE_ERR_NONFINITE = 11,       /* non-finite router score or weight      */
+    PBMOE_ERR_IO = 12,              /* expert pack file missing or unreadable */
+    PBMOE_ERR_FORMAT = 13           /* expert pack metadata malformed         */
 } pbmoe_status;
 
 typedef enum pbmoe_dtype {
@@ -195,6 +197,41 @@ int pbmoe_download(pbmoe_ctx* ctx, void* dst_host, const void* src_device, size_
 int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc* desc,
                      const pbmoe_q4_layout* expert_layout, const void* slots,
                      size_t slots_bytes, uint32_t mem_flags);
+
+/* ---- on-disk expert packs (experts/mod.rs:283-454, 2478-2519;
+ *      experts/store.rs:481-565) ---------------------------------------- */
+/* root/layer_NN.json describes root/layer_NN.bin: `experts` fixed slots of
+ * `expert_size` bytes back to back (expert e at e * expert_size). */
+typedef struct pbmoe_pack_info {
+    char format[48];      /* metadata format, e.g. "FIXED_Q4_EXPERT_LAYER_V1" */
+    uint32_t layer;
+    uint32_t experts;
+    uint64_t expert_size; /* slot bytes */
+    uint64_t file_bytes;  /* size of layer_NN.bin, 0 when absent */
+    uint32_t packs;       /* per-expert entries */
+    uint32_t records;     /* per-tensor records over all entries */
+} pbmoe_pack_info;
+/* Read and validate root/layer_NN.json (read_expert_layer_pack_metadata +
+ * ExpertLayerPackMetadata::validate, experts/mod.rs:2501-2519, 372-429):
+ * known format, layer, non-zero sizes, experts in range and unique, no pack
+ * beyond its slot.  PBMOE_ERR_IO: missing or unreadable file;
+ * PBMOE_ERR_FORMAT: malformed or inconsistent metadata. */
+int pbmoe_pack_inspect(const char* root, uint32_t layer, pbmoe_pack_info* info);
+/* Bind layer `layer` from the pack of file layer `file_layer`: the checks of
+ * ExpertSlotStore::resolve_execution_descriptor_from for fixed-Q4 storage
+ * (experts/store.rs:481-565: format FIXED_Q4_EXPERT_LAYER_V1, slot size ==
+ * expert_layout->expert_bytes, experts and entries == desc->experts, every
+ * entry a whole slot, file size == experts * slot size), per-tensor records
+ * (when present) matching the layout, then the file is streamed into HBM
+ * (two pinned staging buffers, parallel positioned reads) and owned by the
+ * binding, as the resident backing of prepare_resident_expert_backing
+ * (metal/mod.rs:1382-1402).  Same descriptor rules as pbmoe_bind_layer. */
+int pbmoe_bind_layer_file(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc* desc,
+                          const pbmoe_q4_layout* expert_layout, const char* root,
+                          uint32_t file_layer);
+/* Device address and size of layer `layer`'s bound slots (the resident
+ * table of ScheduledResidentExpertTable, expert_access.rs:705-798). */
+int pbmoe_layer_slots(pbmoe_ctx* ctx, uint32_t layer, const void** slots, size_t* bytes);
 /* Router projection W [experts][hidden] (dense F16/BF16/F32, the declared
  * resident router of metal/projection.rs:184-281) and, for sigmoid routing,
  * the per-expert selection bias [experts] f32 (e_score_correction_bias). */

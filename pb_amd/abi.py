@@ -27,6 +27,8 @@ ERR_TIMEOUT = 8
 ERR_NOT_BOUND = 9
 ERR_OUT_OF_MEMORY = 10
 ERR_NONFINITE = 11
+ERR_IO = 12
+ERR_FORMAT = 13
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ROUTING_SOFTMAX_TOPK, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED = 0, 1, 2
@@ -79,6 +81,13 @@ class LayerDesc(C.Structure):
 
 _P = C.c_void_p
 _U32 = C.c_uint32
+class PackInfo(C.Structure):
+    """pbmoe_pack_info: metadata of root/layer_NN.json."""
+    _fields_ = [("format", C.c_char * 48), ("layer", C.c_uint32), ("experts", C.c_uint32),
+                ("expert_size", C.c_uint64), ("file_bytes", C.c_uint64), ("packs", C.c_uint32),
+                ("records", C.c_uint32)]
+
+
 class AttnDesc(C.Structure):
     """pbmoe_attn_desc."""
     _fields_ = [("hidden", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32),
@@ -115,6 +124,9 @@ _SIG = {
     "pbmoe_upload": ([_P, _P, _P, C.c_size_t], C.c_int),
     "pbmoe_download": ([_P, _P, _P, C.c_size_t], C.c_int),
     "pbmoe_bind_layer": ([_P, _U32, C.POINTER(LayerDesc), C.POINTER(Q4Layout), _P, C.c_size_t, _U32], C.c_int),
+    "pbmoe_pack_inspect": ([C.c_char_p, _U32, C.POINTER(PackInfo)], C.c_int),
+    "pbmoe_bind_layer_file": ([_P, _U32, C.POINTER(LayerDesc), C.POINTER(Q4Layout), C.c_char_p, _U32], C.c_int),
+    "pbmoe_layer_slots": ([_P, _U32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)], C.c_int),
     "pbmoe_bind_router": ([_P, _U32, _P, _U32, _P, _U32], C.c_int),
     "pbmoe_bind_shared": ([_P, _U32, C.POINTER(Q4Layout), _P, _P, _U32, _U32], C.c_int),
     "pbmoe_unbind_layer": ([_P, _U32], C.c_int),
@@ -171,6 +183,13 @@ def q4_layout_fixed(hidden: int, intermediate: int, group_size: int, sb_dtype: i
     lay = Q4Layout()
     check(lib().pbmoe_q4_layout_fixed(hidden, intermediate, group_size, sb_dtype, C.byref(lay)))
     return lay
+
+
+def pack_inspect(root: str, layer: int) -> PackInfo:
+    """pbmoe_pack_inspect: parsed and validated root/layer_NN.json."""
+    info = PackInfo()
+    check(lib().pbmoe_pack_inspect(str(root).encode(), layer, C.byref(info)))
+    return info
 
 
 def validate_routes(ids, scores, active_experts: int, experts: int) -> int:

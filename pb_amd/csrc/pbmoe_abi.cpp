@@ -6,8 +6,11 @@
 // scratch buffers, and launch the gfx950 kernels on the context stream.
 // Errors are explicit status codes plus a thread-local message; there is no
 // fallback implementation behind any entry point.
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
@@ -19,6 +22,7 @@
 
 #include "../../include/pbmoe.h"
 #include "pbmoe_internal.h"
+#include "pbmoe_pack.h"
 
 #define PBMOE_API extern "C" __attribute__((visibility("default")))
 
@@ -566,12 +570,10 @@ PBMOE_API int pbmoe_download(pbmoe_ctx* ctx, void* dst, const void* src, size_t 
     return ok();
 }
 
-PBMOE_API int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc* d,
-                               const pbmoe_q4_layout* layout, const void* slots,
-                               size_t slots_bytes, uint32_t flags)
+// Layer descriptor + slot layout checks shared by pbmoe_bind_layer and
+// pbmoe_bind_layer_file.
+static int check_layer_desc(const pbmoe_layer_desc* d, const pbmoe_q4_layout* layout)
 {
-    if (!ctx || !d || !layout || !slots)
-        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
     if (d->experts == 0 || d->experts > MAX_EXPERTS)
         return fail(PBMOE_ERR_UNSUPPORTED, "experts=%u outside 1..=%u", d->experts, MAX_EXPERTS);
     if (d->active_experts == 0 || d->active_experts > d->experts)
@@ -614,7 +616,16 @@ PBMOE_API int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer
         return fail(PBMOE_ERR_UNSUPPORTED,
                     "shared intermediate %u must equal routed intermediate %u",
                     d->shared_intermediate, d->intermediate);
-    int rc = check_layout(layout, d->hidden, d->intermediate);
+    return check_layout(layout, d->hidden, d->intermediate);
+}
+
+PBMOE_API int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc* d,
+                               const pbmoe_q4_layout* layout, const void* slots,
+                               size_t slots_bytes, uint32_t flags)
+{
+    if (!ctx || !d || !layout || !slots)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_layer_desc(d, layout);
     if (rc)
         return rc;
     if (slots_bytes < (size_t)layout->expert_bytes * d->experts)
@@ -636,6 +647,245 @@ PBMOE_API int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer
     }
     b.slots = static_cast<const uint8_t*>(dev);
     b.slots_bytes = (size_t)layout->expert_bytes * d->experts;
+    return ok();
+}
+
+// ---- on-disk expert packs (layer_NN.bin + layer_NN.json) -------------------
+
+static void copy_format(char (&dst)[48], const std::string& src)
+{
+    const size_t n = std::min(src.size(), sizeof(dst) - 1);
+    memcpy(dst, src.data(), n);
+    dst[n] = 0;
+}
+
+PBMOE_API int pbmoe_pack_inspect(const char* root, uint32_t layer, pbmoe_pack_info* info)
+{
+    if (!root || !info)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    pbmoe::pack::LayerMeta m;
+    std::string err;
+    int rc = pbmoe::pack::read_layer_meta(root, layer, &m, &err);
+    if (rc)
+        return fail(rc, "%s", err.c_str());
+    *info = pbmoe_pack_info{};
+    copy_format(info->format, m.format);
+    info->layer = (uint32_t)m.layer;
+    info->experts = (uint32_t)std::min<uint64_t>(m.experts, UINT32_MAX);
+    info->expert_size = m.expert_size;
+    const int64_t fb = pbmoe::pack::file_size(pbmoe::pack::layer_bin_path(root, layer));
+    info->file_bytes = fb < 0 ? 0 : (uint64_t)fb;
+    info->packs = (uint32_t)m.packs.size();
+    for (const auto& p : m.packs)
+        info->records += (uint32_t)p.records.size();
+    return ok();
+}
+
+// Per-tensor records of a fixed-Q4 pack, when present, must describe the
+// bound layout: copy_pbq4_record_to_fixed_q4_component (experts/slots.rs:
+// 1056-1113) writes one record per projection with record_offset and
+// packed_bytes of its weight component, the projection's shape, the layout's
+// group size, groups = scale count, scale_bias_dtype "BF16".  F16 is
+// accepted for an F16 layout.
+static int check_pack_records(const pbmoe::pack::LayerMeta& m, const pbmoe_q4_layout* l,
+                              uint32_t hidden, uint32_t inter, const std::string& path)
+{
+    static const char* const suffix[3] = {"gate_proj.weight", "up_proj.weight", "down_proj.weight"};
+    for (const auto& p : m.packs) {
+        for (const auto& r : p.records) {
+            int proj = -1;
+            for (int q = 0; q < 3; ++q) {
+                const size_t n = strlen(suffix[q]);
+                if (r.tensor.size() >= n && r.tensor.compare(r.tensor.size() - n, n, suffix[q]) == 0)
+                    proj = q;
+            }
+            if (proj < 0)
+                return fail(PBMOE_ERR_FORMAT, "%s expert %llu: record %s is not a gate/up/down projection",
+                            path.c_str(), (unsigned long long)p.expert, r.tensor.c_str());
+            const pbmoe_component& w = l->components[3 * proj];
+            const pbmoe_component& sc = l->components[3 * proj + 1];
+            const uint64_t rows = proj == 2 ? hidden : inter, cols = proj == 2 ? inter : hidden;
+            if (r.shape.size() != 2 || r.shape[0] != rows || r.shape[1] != cols)
+                return fail(PBMOE_ERR_FORMAT, "%s expert %llu: record %s shape does not match %llux%llu",
+                            path.c_str(), (unsigned long long)p.expert, r.tensor.c_str(),
+                            (unsigned long long)rows, (unsigned long long)cols);
+            if (r.record_offset != w.offset || r.packed_bytes != w.bytes)
+                return fail(PBMOE_ERR_FORMAT,
+                            "%s expert %llu: record %s at offset %llu (%llu bytes), layout has %llu (%llu)",
+                            path.c_str(), (unsigned long long)p.expert, r.tensor.c_str(),
+                            (unsigned long long)r.record_offset, (unsigned long long)r.packed_bytes,
+                            (unsigned long long)w.offset, (unsigned long long)w.bytes);
+            if (r.group_size != l->group_size || r.groups != sc.bytes / 2)
+                return fail(PBMOE_ERR_FORMAT, "%s expert %llu: record %s has %llu groups of %llu, layout %llu of %u",
+                            path.c_str(), (unsigned long long)p.expert, r.tensor.c_str(),
+                            (unsigned long long)r.groups, (unsigned long long)r.group_size,
+                            (unsigned long long)(sc.bytes / 2), l->group_size);
+            const bool bf16 = strcasecmp(r.scale_bias_dtype.c_str(), "BF16") == 0 ||
+                              strcasecmp(r.scale_bias_dtype.c_str(), "BFLOAT16") == 0;
+            const bool f16 = strcasecmp(r.scale_bias_dtype.c_str(), "F16") == 0 ||
+                             strcasecmp(r.scale_bias_dtype.c_str(), "FLOAT16") == 0;
+            if ((l->scale_bias_dtype == PBMOE_DTYPE_BF16 && !bf16) || (l->scale_bias_dtype == PBMOE_DTYPE_F16 && !f16))
+                return fail(PBMOE_ERR_DTYPE, "%s expert %llu: record %s scale/bias dtype %s does not match the layout",
+                            path.c_str(), (unsigned long long)p.expert, r.tensor.c_str(),
+                            r.scale_bias_dtype.c_str());
+        }
+    }
+    return ok();
+}
+
+// Copy `bytes` of the file at `path` into device memory through two pinned
+// staging buffers: while the copy engine moves chunk i, reader threads fill
+// chunk i + 1 with positioned reads (the reference reads expert bytes with
+// parallel pread, experts/mod.rs:267-281).
+static int stream_file_to_device(pbmoe_ctx* ctx, const std::string& path, uint64_t bytes, uint8_t* dev)
+{
+    constexpr size_t CHUNK = 64u << 20;
+    constexpr int READERS = 4;
+    const int fd = open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0)
+        return fail(PBMOE_ERR_IO, "failed to open %s: %s", path.c_str(), strerror(errno));
+    void* pin[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    int rc = ok();
+    hipError_t he = hipSuccess;
+    for (int i = 0; i < 2 && he == hipSuccess; ++i) {
+        he = hipHostMalloc(&pin[i], CHUNK, hipHostMallocDefault);
+        if (he == hipSuccess)
+            he = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
+    }
+    if (he != hipSuccess)
+        rc = fail(PBMOE_ERR_DEVICE, "staging buffers: %s", hipGetErrorString(he));
+    uint64_t off = 0;
+    for (uint32_t i = 0; rc == 0 && off < bytes; ++i) {
+        const int b = i & 1;
+        if (i >= 2 && (he = hipEventSynchronize(done[b])) != hipSuccess) {
+            rc = fail(PBMOE_ERR_DEVICE, "staging wait: %s", hipGetErrorString(he));
+            break;
+        }
+        const size_t n = (size_t)std::min<uint64_t>(CHUNK, bytes - off);
+        std::atomic<int> read_err{0};
+        std::thread readers[READERS];
+        for (int k = 0; k < READERS; ++k) {
+            readers[k] = std::thread([&, k]() {
+                size_t lo = n * k / READERS, hi = n * (k + 1) / READERS;
+                uint8_t* dst = static_cast<uint8_t*>(pin[b]);
+                while (lo < hi) {
+                    const ssize_t got = pread(fd, dst + lo, hi - lo, (off_t)(off + lo));
+                    if (got < 0 && errno == EINTR)
+                        continue;
+                    if (got <= 0) {
+                        read_err.store(got < 0 ? errno : EIO);
+                        return;
+                    }
+                    lo += (size_t)got;
+                }
+            });
+        }
+        for (auto& t : readers)
+            t.join();
+        if (read_err.load()) {
+            rc = fail(PBMOE_ERR_IO, "failed to read %s at %llu: %s", path.c_str(), (unsigned long long)off,
+                      strerror(read_err.load()));
+            break;
+        }
+        if ((he = hipMemcpyAsync(dev + off, pin[b], n, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+            (he = hipEventRecord(done[b], ctx->stream)) != hipSuccess) {
+            rc = fail(PBMOE_ERR_DEVICE, "upload: %s", hipGetErrorString(he));
+            break;
+        }
+        off += n;
+    }
+    // the staging buffers may still be read by queued copies
+    he = hipStreamSynchronize(ctx->stream);
+    if (he != hipSuccess && rc == 0)
+        rc = fail(PBMOE_ERR_DEVICE, "upload: %s", hipGetErrorString(he));
+    for (int i = 0; i < 2; ++i) {
+        if (done[i])
+            (void)hipEventDestroy(done[i]);
+        if (pin[i])
+            (void)hipHostFree(pin[i]);
+    }
+    close(fd);
+    return rc;
+}
+
+// Bind layer `layer` from root/layer_NN.json + layer_NN.bin (NN = file_layer):
+// the fixed-Q4 checks of ExpertSlotStore::resolve_execution_descriptor_from
+// (experts/store.rs:481-565), then the slots are streamed into HBM, as the
+// resident backing of prepare_resident_expert_backing (metal/mod.rs:1382-1402).
+PBMOE_API int pbmoe_bind_layer_file(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc* d,
+                                    const pbmoe_q4_layout* layout, const char* root, uint32_t file_layer)
+{
+    namespace pk = pbmoe::pack;
+    if (!ctx || !d || !layout || !root)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_layer_desc(d, layout);
+    if (rc)
+        return rc;
+    pk::LayerMeta m;
+    std::string err;
+    if ((rc = pk::read_layer_meta(root, file_layer, &m, &err)))
+        return fail(rc, "%s", err.c_str());
+    const std::string json = pk::layer_json_path(root, file_layer);
+    if (m.format != pk::FORMAT_FIXED_Q4)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "unsupported expert storage at layer %u: format %s; expected %s (PBQ4 formats are "
+                    "import compatibility only)", file_layer, m.format.c_str(), pk::FORMAT_FIXED_Q4);
+    if (m.expert_size != layout->expert_bytes)
+        return fail(PBMOE_ERR_SHAPE, "expert storage layer %u has slot size %llu, expected %llu", file_layer,
+                    (unsigned long long)m.expert_size, (unsigned long long)layout->expert_bytes);
+    if (m.experts != d->experts || m.packs.size() != d->experts)
+        return fail(PBMOE_ERR_SHAPE, "expert storage layer %u declares %llu experts and %zu records, expected %u",
+                    file_layer, (unsigned long long)m.experts, m.packs.size(), d->experts);
+    for (uint32_t e = 0; e < d->experts; ++e) {
+        const pk::Pack* p = m.pack_for(e);
+        if (!p)
+            return fail(PBMOE_ERR_FORMAT, "expert storage layer %u is missing expert %u", file_layer, e);
+        if (p->packed_bytes != m.expert_size)
+            return fail(PBMOE_ERR_FORMAT,
+                        "expert storage layer %u expert %u has %llu bytes, expected whole-slot payload %llu",
+                        file_layer, e, (unsigned long long)p->packed_bytes, (unsigned long long)m.expert_size);
+    }
+    if ((rc = check_pack_records(m, layout, d->hidden, d->intermediate, json)))
+        return rc;
+    const std::string bin = pk::layer_bin_path(root, file_layer);
+    const int64_t fsize = pk::file_size(bin);
+    const uint64_t want = (uint64_t)d->experts * layout->expert_bytes;
+    if (fsize < 0)
+        return fail(PBMOE_ERR_IO, "failed to stat expert layer %s: %s", bin.c_str(), strerror(errno));
+    if ((uint64_t)fsize != want)
+        return fail(PBMOE_ERR_SHAPE, "expert storage layer %u has file size %lld, expected %llu", file_layer,
+                    (long long)fsize, (unsigned long long)want);
+    if ((rc = set_device(ctx)))
+        return rc;
+    DeviceBuf buf;
+    if (hipMalloc(&buf.ptr, want) != hipSuccess)
+        return fail(PBMOE_ERR_OUT_OF_MEMORY, "no device memory for %llu slot bytes", (unsigned long long)want);
+    buf.bytes = want;
+    if ((rc = stream_file_to_device(ctx, bin, want, static_cast<uint8_t*>(buf.ptr)))) {
+        free_buf(buf);
+        return rc;
+    }
+    LayerBinding& b = ctx->layers[layer];
+    free_buf(b.slots_owned);
+    b.desc = *d;
+    b.layout = *layout;
+    b.slots_owned = buf;
+    b.slots = static_cast<const uint8_t*>(buf.ptr);
+    b.slots_bytes = want;
+    return ok();
+}
+
+PBMOE_API int pbmoe_layer_slots(pbmoe_ctx* ctx, uint32_t layer, const void** slots, size_t* bytes)
+{
+    if (!ctx || !slots || !bytes)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    *slots = b->slots;
+    *bytes = b->slots_bytes;
     return ok();
 }
 

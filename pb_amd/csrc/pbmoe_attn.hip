@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
     const float scale = 1.0f / sqrtf((float)HD);
     float s = 0.0f;
     const uint16_t* krow = &kc[lane][0];
-#pragma unroll 4
+#pragma unroll
     for (int d8 = 0; d8 < HD / 8; ++d8) {
         const uint4 raw = reinterpret_cast<const uint4*>(krow)[d8];
         const uint32_t r4[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -270,14 +270,20 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
     const float p = valid ? expf(sv - mx) : 0.0f;
     const float sum = wave_sum(p);
     ps[wv][lane] = p; // read back by this wave only (LDS operations of a wave complete in order)
-    // P . V: lane holds dims 2 lane, 2 lane + 1
-    float o0 = 0.0f, o1 = 0.0f;
-    for (uint32_t t = 0; t < cnt; ++t) {
-        const uint32_t vw = reinterpret_cast<const uint32_t*>(&vc[t][0])[lane];
-        const float pt = ps[wv][t];
-        o0 = fmaf(pt, __half2float(__ushort_as_half((uint16_t)(vw & 0xFFFFu))), o0);
-        o1 = fmaf(pt, __half2float(__ushort_as_half((uint16_t)(vw >> 16))), o1);
+    // P . V: lane holds dims 2 lane, 2 lane + 1.  All CH rows, unrolled so
+    // that the LDS reads overlap: rows past cnt hold zeros and have p = 0.
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < CH; t += 2) {
+        const uint32_t va = reinterpret_cast<const uint32_t*>(&vc[t][0])[lane];
+        const uint32_t vb = reinterpret_cast<const uint32_t*>(&vc[t + 1][0])[lane];
+        const float pa = ps[wv][t], pb = ps[wv][t + 1];
+        o0 = fmaf(pa, __half2float(__ushort_as_half((uint16_t)(va & 0xFFFFu))), o0);
+        o1 = fmaf(pa, __half2float(__ushort_as_half((uint16_t)(va >> 16))), o1);
+        o2 = fmaf(pb, __half2float(__ushort_as_half((uint16_t)(vb & 0xFFFFu))), o2);
+        o3 = fmaf(pb, __half2float(__ushort_as_half((uint16_t)(vb >> 16))), o3);
     }
+    o0 += o2, o1 += o3;
     float* rec = a.part + ((uint64_t)qh * chunks + chunk) * (HD + 2);
     reinterpret_cast<float2*>(rec)[lane] = make_float2(o0, o1);
     if (lane == 0) {
@@ -288,10 +294,12 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
 
 // merge the chunk partials of one q head: out = sum_c e^(m_c - M) o_c /
 // sum_c e^(m_c - M) l_c, i.e. softmax over every position (softmax_in_place,
-// math.rs:728-744) then the weighted sum of values.  The per-chunk weights
-// are formed in parallel; each dim's sum runs over half the chunks per
-// thread with independent loads.
+// math.rs:728-744) then the weighted sum of values.  Two threads per dim,
+// each over every other chunk.  The partials were just written by other
+// XCDs, so every round trip is slow: the values of the first MERGE_BLOCK
+// chunks are loaded together with the (m, l) pairs, before any reduction.
 constexpr uint32_t MERGE_MAX_CHUNKS = 1024; // max_context / ATTN_CHUNK (65536 positions)
+constexpr int MERGE_BLOCK = 64;             // chunks whose values are loaded up front
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, uint32_t chunks,
                                                          float* __restrict__ out)
 {
@@ -300,37 +308,56 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     __shared__ float half_acc[HD];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* ph = part + (uint64_t)h * chunks * (HD + 2);
+    const uint32_t d = tid & (HD - 1), part_i = tid / HD; // two threads per dim
+    constexpr int PV = MERGE_BLOCK / 2;
+    float val[PV];
+#pragma unroll
+    for (int u = 0; u < PV; ++u) {
+        const uint32_t c = part_i + 2 * u;
+        val[u] = c < chunks ? ph[(uint64_t)c * (HD + 2) + d] : 0.0f;
+    }
     float m = -INFINITY;
-    for (uint32_t c = tid; c < chunks; c += 256)
-        m = fmaxf(m, ph[(uint64_t)c * (HD + 2) + HD]);
+    float ml[MERGE_MAX_CHUNKS / 256][2];
+#pragma unroll
+    for (int u = 0; u < (int)(MERGE_MAX_CHUNKS / 256); ++u) {
+        const uint32_t c = tid + 256 * u;
+        ml[u][0] = -INFINITY, ml[u][1] = 0.0f;
+        if (c < chunks) {
+            const float2 v = *reinterpret_cast<const float2*>(ph + (uint64_t)c * (HD + 2) + HD);
+            ml[u][0] = v.x, ml[u][1] = v.y;
+            m = fmaxf(m, v.x);
+        }
+    }
     m = wave_max(m);
     if (lane == 0)
         red[wv] = m;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float l = 0.0f;
-    for (uint32_t c = tid; c < chunks; c += 256) {
-        const float* rec = ph + (uint64_t)c * (HD + 2);
-        const float e = expf(rec[HD] - M);
-        ec[c] = e;
-        l = fmaf(e, rec[HD + 1], l);
+#pragma unroll
+    for (int u = 0; u < (int)(MERGE_MAX_CHUNKS / 256); ++u) {
+        const uint32_t c = tid + 256 * u;
+        if (c < chunks) {
+            const float e = expf(ml[u][0] - M);
+            ec[c] = e;
+            l = fmaf(e, ml[u][1], l);
+        }
     }
     l = wave_sum(l);
     if (lane == 0)
         red[4 + wv] = l;
     __syncthreads();
     const float L = (red[4] + red[5]) + (red[6] + red[7]);
-    const uint32_t d = tid & (HD - 1), part_i = tid / HD; // two threads per dim
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t c = part_i;
-    for (; c + 14 < chunks; c += 16) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            acc[u] = fmaf(ec[c + 2 * u], ph[(uint64_t)(c + 2 * u) * (HD + 2) + d], acc[u]);
+    for (int u = 0; u < PV; ++u) {
+        const uint32_t c = part_i + 2 * u;
+        if (c < chunks)
+            acc[u & 3] = fmaf(ec[c], val[u], acc[u & 3]);
     }
-    for (; c < chunks; c += 2)
+    for (uint32_t c = part_i + MERGE_BLOCK; c < chunks; c += 2) // long contexts
         acc[0] = fmaf(ec[c], ph[(uint64_t)c * (HD + 2) + d], acc[0]);
-    float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     if (part_i == 1)
         half_acc[d] = sum;
     __syncthreads();

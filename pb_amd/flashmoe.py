@@ -68,6 +68,28 @@ class MoeLayer:
                                           abi.MEM_DEVICE))
         return self
 
+    def bind_file(self, root: str, file_layer: int, router: DeviceArray, selection_bias: DeviceArray | None = None,
+                  shared_layout=None, shared_slot: DeviceArray | None = None,
+                  shared_gate: DeviceArray | None = None) -> "MoeLayer":
+        """Experts from root/layer_NN.bin + .json (pbmoe_bind_layer_file), the
+        dense router and shared expert from device arrays."""
+        self._keep = [router, selection_bias, shared_slot, shared_gate]
+        check(lib().pbmoe_bind_layer_file(self.ctx.handle, self.index, C.byref(self.desc), C.byref(self.layout),
+                                          str(root).encode(), file_layer))
+        check(lib().pbmoe_bind_router(self.ctx.handle, self.index, router.ptr, abi.DTYPE_F16,
+                                      selection_bias.ptr if selection_bias is not None else None, abi.MEM_DEVICE))
+        if shared_slot is not None:
+            check(lib().pbmoe_bind_shared(self.ctx.handle, self.index, C.byref(shared_layout), shared_slot.ptr,
+                                          shared_gate.ptr if shared_gate is not None else None, abi.DTYPE_F16,
+                                          abi.MEM_DEVICE))
+        return self
+
+    def slots(self):
+        """(device address, bytes) of the bound expert slots."""
+        p, n = C.c_void_p(), C.c_size_t()
+        check(lib().pbmoe_layer_slots(self.ctx.handle, self.index, C.byref(p), C.byref(n)))
+        return p.value, n.value
+
     # -- router prep + routing stage (metal/mod.rs:2943-3013) ----------------
     def route(self, x: DeviceArray, ids: DeviceArray, weights: DeviceArray, logits: DeviceArray | None = None):
         tokens = x.shape[0]
