@@ -102,3 +102,34 @@ class DeviceLayer:
 
     def oracle_logits(self, x):
         return np.stack([orc.router_logits(self.host.router_f16, x[t], orc.DT_F16) for t in range(x.shape[0])])
+
+
+class HipGraph:
+    """Stream capture into an instantiated hipGraph (the replay path the
+    benchmark times), through the HIP runtime's C API."""
+
+    def __init__(self, stream: int, fn):
+        hip = C.CDLL("libamdhip64.so")
+        hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        hip.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p,
+                                            C.c_size_t]
+        hip.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        hip.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        hip.hipGraphDestroy.argtypes = [C.c_void_p]
+        self.hip, self.stream = hip, stream
+        assert hip.hipStreamBeginCapture(C.c_void_p(stream), 0) == 0
+        try:
+            fn()
+        finally:
+            self.graph = C.c_void_p()
+            assert hip.hipStreamEndCapture(C.c_void_p(stream), C.byref(self.graph)) == 0
+        self.exec = C.c_void_p()
+        assert hip.hipGraphInstantiate(C.byref(self.exec), self.graph, None, None, 0) == 0
+
+    def launch(self):
+        assert self.hip.hipGraphLaunch(self.exec, C.c_void_p(self.stream)) == 0
+
+    def close(self):
+        self.hip.hipGraphExecDestroy(self.exec)
+        self.hip.hipGraphDestroy(self.graph)
