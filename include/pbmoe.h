@@ -106,8 +106,13 @@ typedef struct pbmoe_q4_layout {
 typedef enum pbmoe_routing {
     PBMOE_ROUTING_SOFTMAX_TOPK = 0,     /* routing_softmax_top_k, math.rs:771-783      */
     PBMOE_ROUTING_SIGMOID_NOAUX = 1,    /* routing_sigmoid_noaux_top_k, math.rs:788-819 */
-    PBMOE_ROUTING_SIGMOID_GROUPED = 2   /* DeepSeek-V3 group-limited noaux (no reference
+    PBMOE_ROUTING_SIGMOID_GROUPED = 2,  /* DeepSeek-V3 group-limited noaux (no reference
                                            counterpart; equals SIGMOID_NOAUX at n_group=1) */
+    PBMOE_ROUTING_SQRT_SOFTPLUS = 3     /* DeepSeek-V4: p = sqrt(softplus(l)), select on
+                                           p + bias (bias optional; ties -> lower index),
+                                           weights p (deepseek_v4_router_probabilities /
+                                           deepseek_v4_select_routes, deepseek.rs:1300-1394);
+                                           canonical route order only */
 } pbmoe_routing;
 
 typedef enum pbmoe_normalization {      /* QwenMoeRoutingWeightNormalization,
@@ -234,7 +239,8 @@ int pbmoe_bind_layer_file(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer_desc
 int pbmoe_layer_slots(pbmoe_ctx* ctx, uint32_t layer, const void** slots, size_t* bytes);
 /* Router projection W [experts][hidden] (dense F16/BF16/F32, the declared
  * resident router of metal/projection.rs:184-281) and, for sigmoid routing,
- * the per-expert selection bias [experts] f32 (e_score_correction_bias). */
+ * the per-expert selection bias [experts] f32 (e_score_correction_bias);
+ * optional (NULL) for the DeepSeek-V4 router. */
 int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weight, uint32_t dtype,
                       const float* selection_bias, uint32_t mem_flags);
 /* Shared expert: one Q4 slot with its own layout (intermediate =

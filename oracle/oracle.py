@@ -22,7 +22,7 @@ LIB_PATH = os.path.join(HERE, "liboracle_pbmoe.so")
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ORDER_CANONICAL, ORDER_REFERENCE_SLOT = 0, 1
 NORM_RENORMALIZE, NORM_DEEPSEEK_FLOOR, NORM_PRESERVE_FULL = 0, 1, 2
-ROUTING_SOFTMAX, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED = 0, 1, 2
+ROUTING_SOFTMAX, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED, ROUTING_SQRT_SOFTPLUS = 0, 1, 2, 3
 
 _lib = None
 
@@ -100,6 +100,29 @@ def routing_sigmoid_noaux_top_k(logits, bias, k: int, order: int = ORDER_REFEREN
     ids = np.empty(max(k, 1), np.int32)
     w = np.empty(max(k, 1), np.float32)
     n = lib().or_routing_sigmoid_noaux_top_k(_p(s), _p(b), C.c_int(s.size), C.c_int(k), C.c_int(order), _p(ids), _p(w))
+    return ids[:n].tolist(), w[:n].copy()
+
+
+def sqrt_softplus(logits) -> np.ndarray:
+    """deepseek_v4_router_probabilities (deepseek.rs:1300-1324), element-wise."""
+    s = _f32(logits).ravel()
+    out = np.empty_like(s)
+    for i, v in enumerate(s):
+        out[i] = lib().or_sqrt_softplus(C.c_float(float(v)))
+    return out
+
+
+def routing_sqrt_softplus_top_k(logits, bias, k: int):
+    """deepseek_v4_router_probabilities + deepseek_v4_select_routes
+    (deepseek.rs:1300-1394); bias None = no correction bias."""
+    s = _f32(logits)
+    b = _f32(bias) if bias is not None else None
+    ids = np.empty(max(k, 1), np.int32)
+    w = np.empty(max(k, 1), np.float32)
+    n = lib().or_routing_sqrt_softplus_top_k(_p(s), _p(b) if b is not None else None, C.c_int(s.size), C.c_int(k),
+                                             _p(ids), _p(w))
+    if n < 0:
+        raise ValueError("non-finite DeepSeek-V4 router input")
     return ids[:n].tolist(), w[:n].copy()
 
 
@@ -389,6 +412,9 @@ def _declare():
     L.or_routing_softmax_top_k.restype = C.c_int
     L.or_routing_sigmoid_noaux_top_k.restype = C.c_int
     L.or_routing_sigmoid_grouped_top_k.restype = C.c_int
+    L.or_routing_sqrt_softplus_top_k.restype = C.c_int
+    L.or_sqrt_softplus.restype = C.c_float
+    L.or_sqrt_softplus.argtypes = [C.c_float]
     L.or_renormalize.restype = C.c_int
 
 

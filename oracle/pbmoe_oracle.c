@@ -22,6 +22,9 @@
  *     vector (tests/scheduler.rs:826-860), f64 brute force, RoPE closed forms
  *     (identity at position 0, norm preservation per pair, the i = 0
  *     frequency equals the position) and the softmax/GQA invariants.
+ *   or_routing_sqrt_softplus_top_k (DeepSeek-V4 router): no golden vector in
+ *     the reference's tests; pinned by f64 closed forms of the three softplus
+ *     branches, a brute-force stable sort and exact ties.
  *   or_routing_sigmoid_grouped_top_k (DeepSeek-V3 group-limited routing):
  *     no reference implementation exists; pinned only by its n_group=1
  *     reduction to routing_sigmoid_noaux_top_k and by brute-force invariants
@@ -272,6 +275,47 @@ int or_routing_sigmoid_grouped_top_k(const float* logits, const float* bias, int
     for (int s = 0; s < kk; ++s)
         w[s] = or_sigmoid(logits[ids[s]]);
     free(biased), free(gscore), free(masked);
+    return kk;
+}
+
+/* ------------------------------------------------------------------------
+ * a20 DeepSeek-V4 router (deepseek.rs:1300-1394):
+ *   deepseek_v4_router_probabilities: p_e = sqrt(softplus(l_e)) in f32 with
+ *     softplus = l (l > 20), exp(l) (l < -20), ln_1p(exp(l)) otherwise;
+ *   deepseek_v4_select_routes: experts ordered by p + bias with total_cmp,
+ *     descending, ties to the lower index (a stable sort), the first k, each
+ *     with its unbiased p.  bias may be NULL (no correction bias: p + 0).
+ * The reference fixes n = 256 and k = 6; the arithmetic is the same for
+ * any n, k.  Returns -1 on a non-finite logit or bias.
+ * ---------------------------------------------------------------------- */
+float or_sqrt_softplus(float l)
+{
+    float sp = l > 20.0f ? l : (l < -20.0f ? expf(l) : log1pf(expf(l)));
+    return sqrtf(sp);
+}
+
+int or_routing_sqrt_softplus_top_k(const float* logits, const float* bias, int n, int k, int32_t* ids,
+                                   float* w)
+{
+    float* biased = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    float vals[1024];
+    if (!biased || k > 1024) {
+        free(biased);
+        return -1;
+    }
+    for (int e = 0; e < n; ++e) {
+        const float pe = or_sqrt_softplus(logits[e]);
+        const float be = bias ? bias[e] : 0.0f;
+        if (!isfinite(logits[e]) || !isfinite(pe) || pe < 0.0f || !isfinite(be)) {
+            free(biased);
+            return -1;
+        }
+        biased[e] = pe + be;
+    }
+    int kk = or_top_k_sorted(biased, n, k, ids, vals);
+    for (int s = 0; s < kk; ++s)
+        w[s] = or_sqrt_softplus(logits[ids[s]]);
+    free(biased);
     return kk;
 }
 
@@ -644,7 +688,9 @@ int or_moe_block(const or_q4_layout* lay, const uint8_t* slots, int experts,
  * Route T rows from router logits: softmax/sigmoid selection, then the
  * scheduler's renormalisation (the CPU routing stage of metal/mod.rs:
  * 3005-3013 followed by expert_access.rs:80-135).
- * kind: 0 softmax top-k, 1 sigmoid noaux, 2 sigmoid grouped.
+ * kind: 0 softmax top-k, 1 sigmoid noaux, 2 sigmoid grouped, 3 DeepSeek-V4
+ * sqrt-softplus (then batch_route_rows' floor renormalisation and scale,
+ * metal/deepseek_execution.rs:3547-3583, with policy DEEPSEEK_FLOOR).
  * ---------------------------------------------------------------------- */
 int or_route_rows(const float* logits, const float* bias, int rows, int experts, int k, int kind,
                   int order, int n_group, int topk_group, int policy, float routed_scale,
@@ -663,9 +709,11 @@ int or_route_rows(const float* logits, const float* bias, int rows, int experts,
             kk = or_routing_softmax_top_k(l, experts, k, order, ids + (size_t)t * k, p);
         else if (kind == 1)
             kk = or_routing_sigmoid_noaux_top_k(l, bias, experts, k, order, ids + (size_t)t * k, p);
-        else
+        else if (kind == 2)
             kk = or_routing_sigmoid_grouped_top_k(l, bias, experts, k, n_group, topk_group,
                                                   ids + (size_t)t * k, p);
+        else
+            kk = or_routing_sqrt_softplus_top_k(l, bias, experts, k, ids + (size_t)t * k, p);
         if (kk != k)
             return OR_ERR_ROUTE;
         int rc = or_renormalize(p, k, policy, routed_scale, weights + (size_t)t * k);

@@ -31,7 +31,7 @@ ERR_IO = 12
 ERR_FORMAT = 13
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-ROUTING_SOFTMAX_TOPK, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED = 0, 1, 2
+ROUTING_SOFTMAX_TOPK, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED, ROUTING_SQRT_SOFTPLUS = 0, 1, 2, 3
 NORM_RENORMALIZE_SELECTED, NORM_DEEPSEEK_FLOOR, NORM_PRESERVE_FULL_SOFTMAX = 0, 1, 2
 ORDER_CANONICAL, ORDER_REFERENCE_SLOT = 0, 1
 MEM_HOST, MEM_DEVICE = 0, 1

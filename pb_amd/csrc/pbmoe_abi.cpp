@@ -570,6 +570,13 @@ PBMOE_API int pbmoe_download(pbmoe_ctx* ctx, void* dst, const void* src, size_t 
     return ok();
 }
 
+// Sigmoid routing selects on sigmoid(l) + bias and needs the bias; the
+// DeepSeek-V4 router's correction bias is optional (deepseek.rs:1361-1374).
+static bool needs_selection_bias(uint32_t routing)
+{
+    return routing == PBMOE_ROUTING_SIGMOID_NOAUX || routing == PBMOE_ROUTING_SIGMOID_GROUPED;
+}
+
 // Layer descriptor + slot layout checks shared by pbmoe_bind_layer and
 // pbmoe_bind_layer_file.
 static int check_layer_desc(const pbmoe_layer_desc* d, const pbmoe_q4_layout* layout)
@@ -587,7 +594,7 @@ static int check_layer_desc(const pbmoe_layer_desc* d, const pbmoe_q4_layout* la
     if (d->intermediate == 0 || d->intermediate % 256 || d->intermediate > MAX_INTERMEDIATE)
         return fail(PBMOE_ERR_UNSUPPORTED, "intermediate=%u must be a multiple of 256 and <= %u",
                     d->intermediate, MAX_INTERMEDIATE);
-    if (d->routing > PBMOE_ROUTING_SIGMOID_GROUPED)
+    if (d->routing > PBMOE_ROUTING_SQRT_SOFTPLUS)
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown routing %u", d->routing);
     if (d->normalization == PBMOE_NORM_PRESERVE_FULL_SOFTMAX)
         return fail(PBMOE_ERR_UNSUPPORTED,
@@ -599,6 +606,9 @@ static int check_layer_desc(const pbmoe_layer_desc* d, const pbmoe_q4_layout* la
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown route order %u", d->route_order);
     if (!(std::isfinite(d->routed_scale) && d->routed_scale > 0.0f))
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "routed expert scale must be positive and finite");
+    if (d->routing == PBMOE_ROUTING_SQRT_SOFTPLUS && d->route_order == PBMOE_ORDER_REFERENCE_SLOT)
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "the DeepSeek-V4 router orders routes by a stable sort; use the canonical order");
     if (d->routing == PBMOE_ROUTING_SIGMOID_GROUPED) {
         if (d->n_group == 0 || d->n_group > 64 || d->experts % d->n_group ||
             d->topk_group == 0 || d->topk_group > d->n_group ||
@@ -900,7 +910,7 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
         return rc;
     if (dtype > PBMOE_DTYPE_BF16)
         return fail(PBMOE_ERR_DTYPE, "router dtype %u not one of F32/F16/BF16", dtype);
-    if (b->desc.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !selection_bias)
+    if (needs_selection_bias(b->desc.routing) && !selection_bias)
         return fail(PBMOE_ERR_INVALID_ARGUMENT,
                     "sigmoid routing requires the per-expert selection bias");
     if (flags == PBMOE_MEM_DEVICE && !aligned(weight, 16))
@@ -1009,7 +1019,7 @@ static pbmoe::RouteParams route_params(const pbmoe_layer_desc& d)
 static int route_many(pbmoe_ctx* ctx, LayerBinding* b, const float* logits, uint32_t tokens,
                       uint32_t* ids, float* weights)
 {
-    if (b->desc.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+    if (needs_selection_bias(b->desc.routing) && !b->sel_bias)
         return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
     HIP_TRY(pbmoe::launch_route_topk(ctx->stream, logits, b->sel_bias, tokens, route_params(b->desc),
                                      ids, weights, ctx->status));
@@ -1086,7 +1096,7 @@ PBMOE_API int pbmoe_route(pbmoe_ctx* ctx, uint32_t layer, const float* x, uint32
         return rc;
     if (!b->router)
         return fail(PBMOE_ERR_NOT_BOUND, "layer %u has no bound router projection", layer);
-    if (b->desc.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+    if (needs_selection_bias(b->desc.routing) && !b->sel_bias)
         return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
     if (!aligned(x, 16))
         return fail(PBMOE_ERR_ALIGNMENT, "x must be 16-byte aligned");
@@ -1158,7 +1168,7 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
         if (b->shared_gate && b->shared_gate_dtype != b->router_dtype)
             return fail(PBMOE_ERR_UNSUPPORTED,
                         "the fused layer needs the shared gate and router in one dtype");
-        if (d.routing != PBMOE_ROUTING_SOFTMAX_TOPK && !b->sel_bias)
+        if (needs_selection_bias(d.routing) && !b->sel_bias)
             return fail(PBMOE_ERR_NOT_BOUND, "sigmoid routing needs the selection bias (bind_router)");
     }
     if (tokens > MAX_DECODE_TOKENS)

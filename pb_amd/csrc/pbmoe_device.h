@@ -103,6 +103,22 @@ __device__ __forceinline__ uint32_t total_key(float f)
 }
 
 __device__ __forceinline__ float sigmoidf_(float l) { return 1.0f / (1.0f + expf(-l)); }
+
+// DeepSeek-V4 router probability sqrt(softplus(l)) in f32, softplus = l above
+// 20, exp(l) below -20, log1p(exp(l)) between
+// (deepseek_v4_router_probabilities, deepseek.rs:1300-1324)
+__device__ __forceinline__ float sqrt_softplusf_(float l)
+{
+    const float sp = l > 20.0f ? l : (l < -20.0f ? expf(l) : log1pf(expf(l)));
+    return sqrtf(sp);
+}
+
+// probability of the sigmoid-family routing kinds (1, 2: sigmoid; 3:
+// sqrt-softplus); the selection score adds the per-expert bias when given
+__device__ __forceinline__ float route_prob(uint32_t kind, float l)
+{
+    return kind == 3 ? sqrt_softplusf_(l) : sigmoidf_(l);
+}
 __device__ __forceinline__ float fast_sigmoid(float l) { return 1.0f / (1.0f + __expf(-l)); }
 
 template <int SBT>
@@ -364,7 +380,7 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             uint32_t e = lane + WAVE * j;
-            sel[j] = e < E ? sigmoidf_(raw[j]) + bias[e] : 0.0f;
+            sel[j] = e < E ? route_prob(p.kind, raw[j]) + (bias ? bias[e] : 0.0f) : 0.0f;
         }
     }
 
@@ -472,7 +488,7 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
         float ev = expf(v - mx);
         prob = have_inv ? ev * inv_sum : ev;
     } else {
-        prob = sigmoidf_(v);
+        prob = route_prob(p.kind, v);
     }
     // renormalisation over the K selected probabilities (lanes < K)
     const float sum = wave_sum((uint32_t)lane < K ? prob : 0.0f);
@@ -554,7 +570,7 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             const uint32_t e = tid + 256 * j;
-            sel[j] = e < E ? sigmoidf_(raw[j]) + bias[e] : 0.0f;
+            sel[j] = e < E ? route_prob(p.kind, raw[j]) + (bias ? bias[e] : 0.0f) : 0.0f;
         }
     }
     // per-thread keys sorted descending (ascending index on equal keys)
@@ -630,7 +646,7 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
         const float ev = expf(v - mx);
         prob = have_inv ? ev * (1.0f / sum) : ev;
     } else {
-        prob = sigmoidf_(v);
+        prob = route_prob(p.kind, v);
     }
     const float sum = wave_sum((uint32_t)lane < K ? prob : 0.0f);
     float inv;
