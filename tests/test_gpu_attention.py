@@ -137,6 +137,37 @@ def test_attention_fused_input_norm_matches_oracle(ctx, acfg):
     abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
 
 
+@pytest.mark.parametrize("pos", [4096, 6000, 20479])
+def test_attention_beyond_the_merge_block_matches_oracle(ctx, pos):
+    """Contexts past 64 chunks (4096 positions): the merge kernel loads the
+    first 64 chunks' values up front and folds the rest in a second loop;
+    65, 94 and 320 chunks, C4 head shape with a 20480-position cache."""
+    acfg = synth.AttnConfig("c4_long", hidden=2048, q_heads=32, kv_heads=4, max_context=20480)
+    layer = 55
+    dev = AttentionLayer(ctx, layer, acfg).bind_synth(SEED, layer)
+    orc_l = _oracle(acfg, layer)
+    rng = np.random.default_rng(pos)
+    kw = acfg.kv_width
+    keys = (rng.standard_normal((pos, kw)) * 1.5).astype(np.float16)
+    vals = rng.standard_normal((pos, kw)).astype(np.float16)
+    kp, vp = dev.kv_cache()
+    abi.check(abi.lib().pbmoe_upload(ctx.handle, kp, keys.ctypes.data, keys.nbytes))
+    abi.check(abi.lib().pbmoe_upload(ctx.handle, vp, vals.ctypes.data, vals.nbytes))
+    orc_l.cache_k[:pos] = keys.astype(F)
+    orc_l.cache_v[:pos] = vals.astype(F)
+    H = acfg.hidden
+    x = rng.standard_normal(H).astype(F)
+    r = rng.standard_normal(H).astype(F)
+    x_d, r_d = ctx.to_device(x), ctx.to_device(r)
+    h_d, a_d = ctx.array((H,), F), ctx.array((acfg.q_width,), F)
+    dev.decode(x_d, r_d, pos, h_d, attn_out=a_d)
+    ctx.sync()
+    ref_att, ref_o = orc_l.decode(x, pos)
+    _check_attention(a_d.download(), ref_att, f"pos {pos}")
+    assert_layer_tolerance(h_d.download(), r + ref_o, "hidden")
+    abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
+
+
 def test_attention_rejects_position_beyond_cache(ctx):
     acfg = synth.AttnConfig("t_small", hidden=512, q_heads=8, kv_heads=2, max_context=16)
     layer = 52
