@@ -1,6 +1,6 @@
 """Benchmark of the MoE block hot path on one MI355X.
 
-Workload: Qwen3-Next-style MoE layer, batch-1 decode —
+Workload C2: Qwen3-Next-style MoE layer, batch-1 decode —
 H=2048, 512 routed experts, top-10 softmax routing renormalised, expert
 intermediate 512, one sigmoid-gated shared expert (intermediate 512), 4-bit
 affine weights with group 64 and f16 scale/bias, seeded synthetic data.
@@ -323,7 +323,7 @@ def stack_bytes_per_token(acfg, mcfg, layers: int, position: int) -> dict:
 
 
 def bench_stack(args, ctx, ev) -> dict:
-    """one token through the 48-layer decode stack —
+    """Workload C4: one token through the 48-layer decode stack —
     per layer the GQA attention block (pbmoe_attention_decode: input RMSNorm
     inside the q/k/v projection, q/k norm + RoPE, f16 KV cache at context
     4096, o_proj + residual) and the C1 MoE layer (pbmoe_moe_layer_norm: the

@@ -91,7 +91,7 @@ typedef struct pbmoe_component {
 
 /* Fixed-slot 4-bit affine expert layout: QwenMoeQ4ExpertLayout
  * (model_family.rs:954-1068) plus the 2-byte scale/bias dtype tag
- * (BF16 in the reference artifacts, F16 for the BASELINE configs).
+ * (BF16 in the reference artifacts, F16 for the benchmark shapes).
  * Packed weights: rows x cols/2 bytes, low nibble first, i.e. column 8w+i at
  * bits 4i of little-endian uint32 word w (shaders.metal:37-65).  Gate/up are
  * [intermediate][hidden], down is [hidden][intermediate]; scale and bias are

@@ -230,7 +230,7 @@ int or_routing_sigmoid_noaux_top_k(const float* logits, const float* bias, int n
 }
 
 /* ------------------------------------------------------------------------
- * DeepSeek-V3 group-limited noaux_tc routing.
+ * DeepSeek-V3 group-limited noaux_tc routing (workload C5).
  * No reference implementation (GLM rejects n_group != 1,
  * model_family.rs:613-614).  Textbook definition:
  *   biased_e = sigmoid(l_e) + bias_e

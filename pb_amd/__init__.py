@@ -4,7 +4,7 @@ The product is the C-ABI library ``libpbmoe.so`` (include/pbmoe.h) holding
 hand-written HIP kernels; this package carries its sources (``csrc/``), the
 build script, a ctypes binding (``abi``), the host-side mirror of the
 reference operator seam (``flashmoe``), the seeded input generator
-(``synth``) and the BASELINE workload shapes (``configs``).
+(``synth``) and the benchmark workload shapes C1-C5 (``configs``).
 """
 from . import abi, configs, synth  # noqa: F401
 

@@ -1,4 +1,4 @@
-"""The BASELINE workload shapes of the MoE block.
+"""The benchmark workload shapes of the MoE block.
 
 C1  CPU-runnable single layer: H2048, E128, K8 softmax renormalised, I768.
 C2  Qwen3-Next decode: H2048, E512, K10, I512 + sigmoid-gated shared I512.
@@ -6,7 +6,7 @@ C3  prefill of 2048 tokens through the C1 layer with drawn Zipf(1.1) logits.
 C4  48 decode layers: GQA attention (C4_ATTN) + the C1 MoE layer, context 4096.
 C5  DeepSeek-V3 shape: H7168, E256, K8 sigmoid, 8 groups / topk_group 4,
     per-expert selection bias, I2048 + shared I2048 (ungated), routed
-    scale 2.5 (the DeepSeek-V3 routed_scaling_factor; BASELINE leaves it open).
+    scale 2.5 (the DeepSeek-V3 routed_scaling_factor; the workload leaves it open).
 All: 4-bit affine, group 64, f16 scale/bias.
 """
 from __future__ import annotations

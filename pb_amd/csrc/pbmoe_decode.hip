@@ -846,7 +846,7 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     const uint32_t cs = (d.hidden / 32 + 63) / 64;
     if (cr > 16 || cs > 4)
         return hipErrorInvalidValue;
-    // router/gate dtypes: the BASELINE layers use f16 for both; other
+    // router/gate dtypes: the benchmark layers use f16 for both; other
     // combinations share the f16 gate path only when the gate is f16
     const uint32_t gdt = a.sgate_w ? d.sgate_dtype : d.router_dtype;
     const uint32_t wdt = a.experts ? d.router_dtype : gdt;

@@ -127,7 +127,7 @@ PBM_EXPORT void pbm_fill_uniform_f32(uint64_t seed, uint32_t tensor, uint32_t la
         out[i] = pbm_uniform(pbm_draw(key, i), lo, width);
 }
 
-/* Drawn router logits with a Zipf(s) expert load (BASELINE prefill config):
+/* Drawn router logits with a Zipf(s) expert load (the C3 prefill workload):
  * logits[t][e] = 0.1*N(0,1) + 4*[e in S_t], where S_t holds k distinct
  * experts drawn with P(rank r) ~ r^-s over a seeded permutation of ids.
  * The continuous noise keeps exact ties away.  hist (optional) receives the

@@ -105,7 +105,7 @@ def drawn_logits_zipf(seed: int, layer: int, tokens: int, experts: int, k: int, 
 
 @dataclass
 class MoeConfig:
-    """One BASELINE workload shape (see configs in pb_amd.configs)."""
+    """One benchmark workload shape (see configs in pb_amd.configs)."""
     name: str
     hidden: int
     intermediate: int
@@ -119,7 +119,7 @@ class MoeConfig:
     shared_intermediate: int = 0
     shared_gated: bool = False
     group: int = 64
-    sb_dtype: int = 1           # f16 scale/bias (BASELINE); 2 = bf16 (reference)
+    sb_dtype: int = 1           # f16 scale/bias (benchmark shapes); 2 = bf16 (reference artifacts)
     tokens: int = 1
 
 
@@ -170,7 +170,7 @@ def activations(seed: int, layer: int, tokens: int, hidden: int):
 @dataclass
 class AttnConfig:
     """The GQA attention layer before each MoE block of the decode stack
-    (32 q heads, 4 kv heads, head_dim 128, f16 KV
+    (workload C4: 32 q heads, 4 kv heads, head_dim 128, f16 KV
     cache, RMSNorm eps 1e-6, RoPE theta 1e6, Q4 projections)."""
     name: str
     hidden: int

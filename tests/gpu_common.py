@@ -20,7 +20,7 @@ def max_abs_rel_l2(got: np.ndarray, ref: np.ndarray):
 
 
 def assert_layer_tolerance(got: np.ndarray, ref: np.ndarray, what: str = "hidden", exact=None):
-    """BASELINE bar: max-abs <= 1e-2 and relative L2 <= 2e-3 against the fp32
+    """Parity bar: max-abs <= 1e-2 and relative L2 <= 2e-3 against the fp32
     oracle.  Where outputs are so large that 1e-2 is below the oracle's own
     f32 rounding error (|h| ~ 3e4 in the H=7168 shape: one f32 ulp is 4e-3),
     `exact` (the fp64 evaluation) decides instead: the result must be no

@@ -1,5 +1,5 @@
 """Seeded generator: conversions are exact RNE, streams are deterministic and
-have the BASELINE distributions.  CPU only."""
+have the benchmark input distributions.  CPU only."""
 import numpy as np
 import torch
 
