@@ -305,7 +305,8 @@ __global__ __launch_bounds__(PLAN_WAVES * 64) void dispatch_plan_kernel(
 //          (unique ids, group starts/counts, slots) over experts;
 //   place: per block the single-workgroup placement with absolute bases.
 // ---------------------------------------------------------------------------
-constexpr uint32_t PLAN_CHUNK = PLAN_WAVES * 256;
+constexpr uint32_t PLAN_CHUNK = PLAN_WAVES * 64; // one route per lane
+constexpr uint32_t PLAN_SINGLE_MAX = 2048;        // routes the one-workgroup kernel takes
 
 __global__ __launch_bounds__(PLAN_WAVES * 64) void plan_count_kernel(
     const uint32_t* __restrict__ ids, uint32_t routes, uint32_t experts, uint32_t* __restrict__ cnt,
@@ -341,12 +342,17 @@ __global__ __launch_bounds__(PLAN_MAX_E) void plan_scan_kernel(const uint32_t* _
 {
     __shared__ uint32_t sa[PLAN_MAX_E], sb[PLAN_MAX_E];
     const uint32_t e = threadIdx.x;
+    constexpr uint32_t NB = 16; // block counts loaded together
     uint32_t run = 0;
     if (e < experts) {
-        for (uint32_t b = 0; b < nblk; ++b) {
-            const uint32_t v = cnt[(uint64_t)b * experts + e];
-            base[(uint64_t)b * experts + e] = run;
-            run += v;
+        for (uint32_t b0 = 0; b0 < nblk; b0 += NB) {
+            uint32_t v[NB];
+#pragma unroll
+            for (uint32_t j = 0; j < NB; ++j)
+                v[j] = b0 + j < nblk ? cnt[(uint64_t)(b0 + j) * experts + e] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < NB; ++j)
+                run += v[j];
         }
     }
     sa[e] = run;
@@ -370,8 +376,20 @@ __global__ __launch_bounds__(PLAN_MAX_E) void plan_scan_kernel(const uint32_t* _
             plan.groups[2 * sl + 1] = run;
         }
         slot_of[e] = sl;
-        for (uint32_t b = 0; b < nblk; ++b)
-            base[(uint64_t)b * experts + e] += start;
+        // absolute base of every block: start + the counts of the blocks before
+        uint32_t acc = start;
+        for (uint32_t b0 = 0; b0 < nblk; b0 += NB) {
+            uint32_t v[NB];
+#pragma unroll
+            for (uint32_t j = 0; j < NB; ++j)
+                v[j] = b0 + j < nblk ? cnt[(uint64_t)(b0 + j) * experts + e] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < NB; ++j)
+                if (b0 + j < nblk) {
+                    base[(uint64_t)(b0 + j) * experts + e] = acc;
+                    acc += v[j];
+                }
+        }
     }
     if (e == 0)
         plan.unique_count[0] = sb[PLAN_MAX_E - 1];
@@ -381,64 +399,53 @@ __global__ __launch_bounds__(PLAN_WAVES * 64) void plan_place_kernel(
     const uint32_t* __restrict__ ids, uint32_t routes, uint32_t experts, uint32_t k, Plan plan,
     const uint32_t* __restrict__ base, const uint32_t* __restrict__ slot_of)
 {
+    static_assert(PLAN_CHUNK == PLAN_WAVES * 64, "one route per lane");
     __shared__ uint32_t wcnt[PLAN_WAVES][PLAN_MAX_E];
     __shared__ uint32_t slt[PLAN_MAX_E];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nthr = PLAN_WAVES * 64;
+    const uint32_t r = blockIdx.x * PLAN_CHUNK + tid; // wave wv owns routes 64 wv .. 64 wv + 63 of the block
+    const bool valid = r < routes;
+    const uint32_t e = valid ? ids[r] : 0xFFFFFFFFu;
+    const bool in_range = valid && e < experts;
     for (int i = tid; i < PLAN_WAVES * PLAN_MAX_E; i += nthr)
         (&wcnt[0][0])[i] = 0;
-    for (uint32_t e = tid; e < experts; e += nthr)
-        slt[e] = slot_of[e];
+    for (uint32_t x = tid; x < experts; x += nthr)
+        slt[x] = slot_of[x];
     __syncthreads();
-    const uint32_t r_begin = blockIdx.x * PLAN_CHUNK + wv * (PLAN_CHUNK / PLAN_WAVES);
-    const uint32_t r_end = min(routes, r_begin + PLAN_CHUNK / PLAN_WAVES);
-    for (uint32_t r = r_begin + lane; r < r_end; r += 64) {
-        const uint32_t e = ids[r];
-        if (e < experts)
-            atomicAdd(&wcnt[wv][e], 1u);
-    }
+    if (in_range)
+        atomicAdd(&wcnt[wv][e], 1u);
     __syncthreads();
-    for (uint32_t e = tid; e < experts; e += nthr) {
-        uint32_t run = base[(uint64_t)blockIdx.x * experts + e];
+    // per expert: the block's absolute base, then the exclusive prefix over waves
+    for (uint32_t x = tid; x < experts; x += nthr) {
+        uint32_t run = base[(uint64_t)blockIdx.x * experts + x];
         for (int w = 0; w < PLAN_WAVES; ++w) {
-            const uint32_t c = wcnt[w][e];
-            wcnt[w][e] = run;
+            const uint32_t c = wcnt[w][x];
+            wcnt[w][x] = run;
             run += c;
         }
     }
     __syncthreads();
-    for (uint32_t r0 = r_begin; r0 < r_end; r0 += 64) {
-        const uint32_t r = r0 + lane;
-        const bool valid = r < r_end;
-        const uint32_t e = valid ? ids[r] : 0xFFFFFFFFu;
-        const bool in_range = valid && e < experts;
-        uint64_t remaining = __ballot(in_range);
-        uint64_t peers = 0;
-        while (remaining) {
-            const int leader = __ffsll((unsigned long long)remaining) - 1;
-            const uint32_t le = __shfl(e, leader);
-            const uint64_t m = __ballot(in_range && e == le);
-            if (in_range && e == le)
-                peers = m;
-            remaining &= ~m;
-        }
-        if (in_range) {
-            const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-            const uint32_t pos = wcnt[wv][e] + __popcll(peers & below);
-            plan.src_rows[pos] = r / k;
-            plan.out_idx[r] = pos;
-            plan.route_slots[r] = slt[e];
-        } else if (valid) {
-            plan.out_idx[r] = 0xFFFFFFFFu;
-            plan.route_slots[r] = 0xFFFFFFFFu;
-        }
-        if (in_range) {
-            const int top = 63 - __clzll((long long)peers);
-            if (top == lane)
-                wcnt[wv][e] += __popcll(peers);
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    // rank among this wave's earlier lanes with the same expert (stable order)
+    uint64_t remaining = __ballot(in_range);
+    uint64_t peers = 0;
+    while (remaining) {
+        const int leader = __ffsll((unsigned long long)remaining) - 1;
+        const uint32_t le = __shfl(e, leader);
+        const uint64_t m = __ballot(in_range && e == le);
+        if (in_range && e == le)
+            peers = m;
+        remaining &= ~m;
+    }
+    if (in_range) {
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        const uint32_t pos = wcnt[wv][e] + __popcll(peers & below);
+        plan.src_rows[pos] = r / k;
+        plan.out_idx[r] = pos;
+        plan.route_slots[r] = slt[e];
+    } else if (valid) {
+        plan.out_idx[r] = 0xFFFFFFFFu;
+        plan.route_slots[r] = 0xFFFFFFFFu;
     }
 }
 
@@ -451,7 +458,7 @@ uint32_t plan_work_words(uint32_t routes, uint32_t experts)
 hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t routes,
                                 uint32_t experts, uint32_t k, const Plan& plan, uint32_t* status)
 {
-    if (routes <= PLAN_CHUNK || plan.work == nullptr) {
+    if (routes <= PLAN_SINGLE_MAX || plan.work == nullptr) {
         dispatch_plan_kernel<<<1, PLAN_WAVES * 64, 0, s>>>(ids, routes, experts, k, plan, status);
         return hipGetLastError();
     }

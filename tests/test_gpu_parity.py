@@ -238,7 +238,7 @@ def _plan_ref(ids, E):
 
 
 @pytest.mark.parametrize("T,K,E,seed", [(1, 8, 128, 0), (7, 10, 512, 1), (16, 10, 512, 2), (300, 6, 64, 3),
-                                        (1000, 16, 1024, 4)])
+                                        (1000, 16, 1024, 4), (5000, 8, 300, 5)])
 def test_dispatch_plan_bit_exact_random(ctx, T, K, E, seed):
     _say(f"[test] plan random T={T} K={K} E={E}")
     rng = np.random.default_rng(seed)
