@@ -177,7 +177,14 @@ int pbmoe_renormalize_routes(const float* scores, uint32_t count, uint32_t norma
 /* MetalExecutionContext::compile_resolved counterpart (runtime/mod.rs:648-687). */
 int pbmoe_ctx_create(int device, pbmoe_ctx** out);
 int pbmoe_ctx_destroy(pbmoe_ctx* ctx);
-/* The context's HIP stream (hipStream_t) for event timing by the caller. */
+/* The context's HIP stream (hipStream_t) for event timing by the caller.
+ * Work recorded from this stream into a hipGraph references the context's
+ * scratch buffers (routes, plans, activations, attention partials) as they
+ * are at capture time.  These grow on demand, and growing frees the old
+ * allocation after a stream synchronisation, which is an error while the
+ * stream is capturing.  Graph users therefore make one call of every shape
+ * they will replay before capturing, and make no larger call on the context
+ * while the graph may still be replayed. */
 int pbmoe_ctx_stream(pbmoe_ctx* ctx, void** stream);
 /* Wait for all work on the context stream (commit_and_wait, ffi.rs:613-634,
  * with the 120 s limit of metal/mod.rs:539-540) and report deferred device

@@ -137,11 +137,13 @@ __global__ __launch_bounds__(64) void tile_table_kernel(const uint32_t* __restri
 }
 
 // ---------------------------------------------------------------------------
-// split: one workgroup per token row.  hi/lo f16 of x * 2^-e in K order,
-// sums of x * 2^-e per 32 columns, rowscale = 2^e (e > 0 only for rows
-// whose magnitude would leave the f16 range), and whether any lo is nonzero
-// (rows of f16-valued inputs have lo == 0 throughout; the gate/up GEMM then
-// skips the lo products, which would add exact zeros).
+// split: one workgroup per token row, one 8-column block per thread and
+// step (two 16-byte loads, one 16-byte store each for hi and lo).  hi/lo f16
+// of x * 2^-e in K order, sums of x * 2^-e per 32 columns (four lanes),
+// rowscale = 2^e (e > 0 only for rows whose magnitude would leave the f16
+// range), and whether any lo is nonzero (rows of f16-valued inputs have
+// lo == 0 throughout; the gate/up GEMM then skips the lo products, which
+// would add exact zeros).  cols is a multiple of 64.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, uint32_t cols,
                                                          uint16_t* __restrict__ hi,
@@ -153,10 +155,14 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const float* xr = x + (uint64_t)t * cols;
+    const float4* xr = reinterpret_cast<const float4*>(x + (uint64_t)t * cols);
+    const uint32_t nb = cols / 8;
     float amax = 0.0f;
-    for (uint32_t c = threadIdx.x; c < cols; c += 256)
-        amax = fmaxf(amax, fabsf(xr[c]));
+    for (uint32_t b = threadIdx.x; b < nb; b += 256) {
+        const float4 p = xr[2 * b], q = xr[2 * b + 1];
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w))));
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
+    }
     amax = wave_max(amax);
     if (lane == 0)
         red[wv] = amax;
@@ -168,25 +174,30 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     const float f = ldexpf(1.0f, -e);
     if (threadIdx.x == 0)
         rowscale[t] = ldexpf(1.0f, e);
-    // each wave handles 64-column groups; lane = column within the group
     int any_lo = 0;
-    for (uint32_t g = wv; g < cols / 64; g += 4) {
-        const uint32_t c = g * 64 + lane;
-        const float v = xr[c] * f;
-        const _Float16 h = (_Float16)v;
-        const _Float16 l = (_Float16)(v - (float)h);
-        const uint64_t o = (uint64_t)t * cols + (c & ~7u) + kpos(c & 7u);
-        hi[o] = __builtin_bit_cast(uint16_t, h);
-        lo[o] = __builtin_bit_cast(uint16_t, l);
-        any_lo |= l != (_Float16)0.0f;
-        float s = v; // sums per 32 columns: lanes 0..31 and 32..63
+    // nb is a multiple of 4: the four blocks of 32 columns are on four
+    // consecutive lanes, all present or all absent
+    for (uint32_t b = threadIdx.x; b < nb; b += 256) {
+        const float4 p = xr[2 * b], q = xr[2 * b + 1]; // L2 hits: read above
+        const float v[8] = {p.x * f, p.y * f, p.z * f, p.w * f, q.x * f, q.y * f, q.z * f, q.w * f};
+        uint32_t hw[4], lw[4];
+        // K order inside the block: c0 c4 c1 c5 c2 c6 c3 c7 (word j = columns j, j + 4)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const _Float16 ha = (_Float16)v[j], hb = (_Float16)v[j + 4];
+            const _Float16 la = (_Float16)(v[j] - (float)ha), lb = (_Float16)(v[j + 4] - (float)hb);
+            hw[j] = __builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+            lw[j] = __builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+            any_lo |= la != (_Float16)0.0f || lb != (_Float16)0.0f;
+        }
+        const uint64_t o = (uint64_t)t * cols + 8 * b;
+        *reinterpret_cast<uint4*>(hi + o) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *reinterpret_cast<uint4*>(lo + o) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
         s += __shfl_xor(s, 1);
         s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        s += __shfl_xor(s, 8);
-        s += __shfl_xor(s, 16);
-        if ((lane & 31) == 0)
-            sum32[(uint64_t)t * (cols / 32) + g * 2 + (lane >> 5)] = s;
+        if ((lane & 3) == 0)
+            sum32[(uint64_t)t * (cols / 32) + b / 4] = s;
     }
     any_lo = __syncthreads_or(any_lo);
     if (threadIdx.x == 0)
