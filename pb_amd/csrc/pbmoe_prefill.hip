@@ -99,15 +99,25 @@ __device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 // tile table: for every used expert ceil(count / 64) tiles (item, start);
 // the shared expert, when present, is item U with all T tokens.  One wave:
 // a scan of per-item tile counts, then each lane writes its item's tiles.
+// Runs in the last workgroup of the split launch (both follow the plan and
+// precede the GEMMs).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void tile_table_kernel(const uint32_t* __restrict__ unique_count,
-                                                       const uint32_t* __restrict__ groups,
-                                                       uint32_t has_shared, uint32_t tokens,
-                                                       uint32_t* __restrict__ tiles,
-                                                       uint32_t* __restrict__ tile_count)
+struct TileArgs {
+    const uint32_t* unique_count;
+    const uint32_t* groups;
+    uint32_t has_shared;
+    uint32_t tokens;
+    uint32_t* tiles;
+    uint32_t* tile_count;
+};
+
+__device__ void tile_table_wave(const TileArgs& a)
 {
-    const uint32_t lane = threadIdx.x;
-    const uint32_t U = unique_count[0];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t* groups = a.groups;
+    const uint32_t has_shared = a.has_shared, tokens = a.tokens;
+    uint32_t* tiles = a.tiles;
+    const uint32_t U = a.unique_count[0];
     const uint32_t items = U + has_shared;
     uint32_t base = 0;
     for (uint32_t u0 = 0; u0 < items; u0 += 64) {
@@ -133,7 +143,7 @@ __global__ __launch_bounds__(64) void tile_table_kernel(const uint32_t* __restri
         base += __shfl(inc, 63);
     }
     if (lane == 0)
-        tile_count[0] = base;
+        a.tile_count[0] = base;
 }
 
 // ---------------------------------------------------------------------------
@@ -150,8 +160,13 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
                                                          uint16_t* __restrict__ lo,
                                                          float* __restrict__ sum32,
                                                          float* __restrict__ rowscale,
-                                                         uint32_t* __restrict__ lo_any)
+                                                         uint32_t* __restrict__ lo_any, TileArgs ta)
 {
+    if (blockIdx.x == gridDim.x - 1) { // the tile table
+        if (threadIdx.x < 64)
+            tile_table_wave(ta);
+        return;
+    }
     __shared__ float red[4];
     const uint32_t t = blockIdx.x;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -830,11 +845,8 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     hipError_t err = launch_dispatch_plan(st, p.ids, routes, ex.count, K, p.plan, p.status);
     if (err != hipSuccess)
         return err;
-    tile_table_kernel<<<1, 64, 0, st>>>(p.plan.unique_count, p.plan.groups, has_shared, T, p.tiles,
-                                        p.tile_count);
-    if ((err = hipGetLastError()) != hipSuccess)
-        return err;
-    split_rows_kernel<<<T, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any);
+    const TileArgs ta{p.plan.unique_count, p.plan.groups, has_shared, T, p.tiles, p.tile_count};
+    split_rows_kernel<<<T + 1, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any, ta);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     if (has_shared && p.sgate_w) {
