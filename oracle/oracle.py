@@ -127,8 +127,12 @@ def routing_sqrt_softplus_top_k(logits, bias, k: int):
 
 
 def routing_sigmoid_grouped_top_k(logits, bias, k: int, n_group: int, topk_group: int):
-    """DeepSeek-V3 group-limited noaux routing (no reference implementation;
-    parity unpinned beyond the n_group=1 reduction to math.rs:788-819)."""
+    """DeepSeek-V3 group-limited noaux routing.  No reference implementation
+    exists: pinned by the n_group=1 reduction to math.rs:788-819 and by a
+    brute-force restatement of the published definition.  The selection
+    bias is required (e_score_correction_bias)."""
+    if bias is None:
+        raise ValueError("grouped sigmoid routing needs the selection bias")
     s = _f32(logits)
     b = _f32(bias)
     ids = np.empty(max(k, 1), np.int32)

@@ -26,9 +26,11 @@
  *     the reference's tests; pinned by f64 closed forms of the three softplus
  *     branches, a brute-force stable sort and exact ties.
  *   or_routing_sigmoid_grouped_top_k (DeepSeek-V3 group-limited routing):
- *     no reference implementation exists; pinned only by its n_group=1
- *     reduction to routing_sigmoid_noaux_top_k and by brute-force invariants
- *     -> parity unpinned beyond that reduction.
+ *     no reference implementation exists; pinned by its n_group=1 reduction
+ *     to routing_sigmoid_noaux_top_k and by an independent brute-force
+ *     restatement of DeepSeek-V3's published definition (group score = sum
+ *     of the two largest biased scores, keep topk_group groups, top-k among
+ *     their experts; ties to the lower index), exact ties included.
  */
 #include <math.h>
 #include <stdint.h>

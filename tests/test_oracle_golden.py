@@ -141,6 +141,23 @@ def test_grouped_routing_brute_force(seed):
     np.testing.assert_allclose(w, sig[ids], rtol=1e-6, atol=0)  # numpy exp vs libm expf: 1 ulp
 
 
+def test_grouped_routing_exact_ties_brute_force():
+    """Every group has the same top-2 sum and experts repeat across groups:
+    the lower group index and then the lower expert index win."""
+    n, k, ng, tg = 32, 5, 4, 2
+    base = np.array([0.3, -1.2, 2.0, 0.7, 2.0, -0.4, 0.3, 1.1], F)
+    logits = np.tile(base, ng)
+    ids, w = orc.routing_sigmoid_grouped_top_k(logits, np.zeros(n, F), k, ng, tg)
+    sig = (F(1) / (F(1) + np.exp(-logits))).astype(F)
+    per = n // ng
+    gs = [float(np.sort(sig[g * per:(g + 1) * per])[-2:].sum(dtype=F)) for g in range(ng)]
+    keep = sorted(range(ng), key=lambda g: (-gs[g], g))[:tg]
+    assert keep == [0, 1]
+    cand = [e for e in range(n) if e // per in keep]
+    brute = sorted(cand, key=lambda e: (-float(sig[e]), e))[:k]
+    assert ids == brute == [2, 4, 10, 12, 7]
+
+
 # ---------------------------------------------------------- renormalise ----
 def test_renormalize_scale_golden():
     # tests/scheduler.rs:4100-4128
