@@ -12,7 +12,7 @@ import pytest
 from oracle import oracle as orc
 from pb_amd import abi, synth
 from pb_amd.configs import C1, C2, C3, C5
-from pb_amd.flashmoe import dispatch_plan
+from pb_amd.flashmoe import MoeLayer, dispatch_plan
 from tests.gpu_common import SEED, DeviceLayer, assert_layer_tolerance, max_abs_rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -174,6 +174,34 @@ def test_grouped_sigmoid_routing_c5(ctx):
                                     routed_scale=C5.routed_scale)
     np.testing.assert_array_equal(ids.download().astype(np.int32), ref_ids)
     np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6)
+
+
+@pytest.mark.parametrize("T", [1, 40])
+def test_grouped_sigmoid_routing_exact_ties(ctx, T):
+    """Every group of the C5 router ties (same logits in each group, zero
+    bias): the lower group and then the lower expert index win, on the
+    few-token and the many-token routing kernels."""
+    _say(f"[test] grouped sigmoid routing ties T={T}")
+    dl = _layer(ctx, C5, 0)
+    zero_bias = ctx.to_device(np.zeros(C5.experts, np.float32))
+    m = MoeLayer(ctx, 90, C5, dl.layout).bind_device(dl.slots, dl.router, zero_bias, dl.host.shared_layout,
+                                                     dl.shared, dl.gate)
+    per = C5.experts // C5.n_group
+    base = (np.random.default_rng(7).standard_normal(per) * 2).astype(np.float32)
+    base[[3, 17]] = base.max() + 1.0  # an exact tie inside the group as well
+    l = np.tile(np.tile(base, C5.n_group), (T, 1))
+    ids = ctx.array((T, C5.k), np.uint32)
+    w = ctx.array((T, C5.k), np.float32)
+    m.route_logits(ctx.to_device(l), ids, w)
+    ctx.sync()
+    ref_ids, ref_w = orc.route_rows(l, C5.k, orc.ROUTING_SIGMOID_GROUPED, orc.ORDER_CANONICAL,
+                                    bias=np.zeros(C5.experts, np.float32), n_group=C5.n_group,
+                                    topk_group=C5.topk_group, routed_scale=C5.routed_scale)
+    got = ids.download().astype(np.int32)
+    np.testing.assert_array_equal(got, ref_ids)
+    assert got[0][0] == 3 and got[0][1] == 17 and got[0][2] == per + 3  # group 0, then group 1
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6)
+    m.unbind()
 
 
 # ------------------------------------------------------------ expert phase ---
