@@ -1,0 +1,111 @@
+"""GPU: one token through the full C4 decode stack at its benchmark size
+(48 decoder layers, GQA attention at position 4095 over a synthetic f16 KV
+cache, C1 MoE layers with zero-mean experts, both RMSNorms fused into their
+consumers).  Every layer is checked against the oracle given the device's
+own input for that layer (teacher forcing: errors do not compound across
+the 48 layers), and the whole token replayed from a hipGraph equals the
+eager token bit for bit."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from pb_amd import abi, synth
+from pb_amd.configs import C1, C4_ATTN, C4_LAYERS
+from pb_amd.flashmoe import AttentionLayer
+from tests.gpu_common import SEED, DeviceLayer, HipGraph, assert_layer_tolerance
+
+pytestmark = pytest.mark.gpu
+F = np.float32
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = abi.Context(0)
+    yield c
+    c.close()
+
+
+def _attn_oracle(acfg, layer):
+    mats = synth.attn_host_mats(acfg, SEED, layer, abi.q4_layout_fixed)
+    qn, kn, _, _ = synth.attn_norms(acfg, SEED, layer)
+    return orc.AttnOracle(mats, qn, kn, acfg.hidden, acfg.q_heads, acfg.kv_heads, acfg.head_dim,
+                          acfg.rope_theta, acfg.group, acfg.sb_dtype, acfg.max_context)
+
+
+def test_full_c4_stack_token_matches_oracle_per_layer(ctx):
+    acfg, mcfg, L = C4_ATTN, C1, C4_LAYERS
+    H, pos = acfg.hidden, acfg.max_context - 1
+    _say(f"[test] full C4 stack: {L} layers, position {pos}")
+    rng = np.random.default_rng(SEED)
+    keys = rng.standard_normal((pos, acfg.kv_width)).astype(np.float16)
+    vals = rng.standard_normal((pos, acfg.kv_width)).astype(np.float16)
+    layers = []
+    for l in range(L):
+        att = AttentionLayer(ctx, 200 + l, acfg).bind_synth(SEED, l)
+        kp, vp = att.kv_cache()
+        abi.check(abi.lib().pbmoe_upload(ctx.handle, kp, keys.ctypes.data, keys.nbytes))
+        abi.check(abi.lib().pbmoe_upload(ctx.handle, vp, vals.ctypes.data, vals.nbytes))
+        moe = DeviceLayer(ctx, mcfg, l, index=200 + l, centred=True)
+        layers.append((att, moe))
+    ctx.sync()
+    _say("[info] layers bound")
+    h0 = synth.activations(SEED, 4000, 1, H)[1]
+    h_a, h_b, mid = ctx.to_device(h0), ctx.array((1, H), F), ctx.array((1, H), F)
+    ids = ctx.array((1, mcfg.k), np.uint32)
+    w = ctx.array((1, mcfg.k), F)
+    bufs = (h_a, h_b)
+
+    def layer_step(l):
+        att, moe = layers[l]
+        h, hn = bufs[l % 2], bufs[(l + 1) % 2]
+        att.decode(h, h, pos, mid, input_norm=att.input_norm)
+        moe.moe.forward_norm(mid, att.post_norm, hn, ids, w)
+
+    # eager token, one layer at a time, each layer against the oracle
+    worst = 0.0
+    for l in range(L):
+        att, moe = layers[l]
+        h_in = bufs[l % 2].download().ravel()
+        layer_step(l)
+        ctx.sync()
+        mid_d = mid.download().ravel()
+        out_d = bufs[(l + 1) % 2].download().ravel()
+        got_ids, got_w = ids.download().astype(np.int32), w.download()
+        ref_att = _attn_oracle(acfg, l)
+        ref_att.cache_k[:pos] = keys.astype(F)
+        ref_att.cache_v[:pos] = vals.astype(F)
+        _, o = ref_att.decode(orc.rms_norm(h_in, att.input_norm_h, acfg.eps), pos)
+        assert_layer_tolerance(mid_d, h_in + o, f"layer {l} attention hidden")
+        assert len(set(got_ids[0].tolist())) == mcfg.k and got_ids.max() < mcfg.experts
+        post = orc.rms_norm(mid_d, att.post_norm_h, acfg.eps)
+        ref_out, _ = moe.oracle_block(post.reshape(1, H), mid_d.reshape(1, H), got_ids, got_w)
+        mx, _ = assert_layer_tolerance(out_d, ref_out.ravel(), f"layer {l} hidden")
+        worst = max(worst, mx)
+        if l % 8 == 7:
+            _say(f"[info] layers 0..{l} within the bar (worst max-abs {worst:.2e})")
+    final = bufs[L % 2].download()
+
+    # the same token captured as one hipGraph and replayed: bitwise equal
+    graph = HipGraph(ctx.stream(), lambda: [layer_step(l) for l in range(L)])
+    for rep in range(2):
+        h_a.upload(h0)
+        h_b.upload(np.full((1, H), np.nan, F))
+        ctx.sync()
+        graph.launch()
+        ctx.sync()
+        np.testing.assert_array_equal(bufs[L % 2].download().view(np.uint32), final.view(np.uint32),
+                                      err_msg=f"replay {rep}")
+    graph.close()
+    _say(f"[result] full C4 stack: {L} layers within the bar, graph replays bitwise equal")
+    for att, moe in layers:
+        abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, att.index))
+        moe.moe.unbind()
