@@ -169,6 +169,28 @@ def test_prefill_c5_shape(ctx):
     _check_rows(dl, xh, rh, ids.download().astype(np.int32), w.download(), got, np.arange(T), tag="C5")
 
 
+def test_prefill_c5_full_chunk(ctx):
+    """C5 at its benchmark size: 1024 tokens through the DeepSeek-V3-shaped
+    layer (group-limited sigmoid routing on the device); sampled rows (every
+    64th plus rows of the most and least loaded experts) against the oracle,
+    and a second call bitwise identical."""
+    _say("[test] prefill C5 1024 tokens")
+    dl = _layer(ctx, C5)
+    T = 1024
+    xh, rh = synth.activations(SEED, 306, T, C5.hidden)
+    x, ids, w = _routes(ctx, dl, xh)
+    got, _ = _prefill(ctx, dl, x, rh, ids, w)
+    again, _ = _prefill(ctx, dl, x, rh, ids, w)
+    np.testing.assert_array_equal(got.view(np.uint32), again.view(np.uint32))
+    ids_h, w_h = ids.download().astype(np.int32), w.download()
+    counts = np.bincount(ids_h.ravel(), minlength=C5.experts)
+    heavy, light = int(np.argmax(counts)), int(np.argmin(np.where(counts > 0, counts, 1 << 30)))
+    rows = set(range(0, T, 64))
+    rows |= set(np.nonzero((ids_h == light).any(1))[0][:4].tolist())
+    rows |= set(np.nonzero((ids_h == heavy).any(1))[0][-4:].tolist())
+    _check_rows(dl, xh, rh, ids_h, w_h, got, np.array(sorted(rows)), tag="C5 1024")
+
+
 def test_prefill_out_of_range_route_is_reported(ctx):
     _say("[test] prefill bad route")
     dl = _layer(ctx, C1)
