@@ -107,34 +107,66 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
                                                const float* norm_w, float eps)
 {
     const int lane = threadIdx.x & 63;
-    float wv[CR][8];
+    // 16-bit weights stay packed in registers until use (half the VGPRs of
+    // converted floats: CR = 16 for H = 7168)
+    constexpr int WW = WDT == 0 ? 8 : 4; // 32-bit words per 8 weights
+    uint32_t wr[CR][WW];
 #pragma unroll
     for (int c = 0; c < CR; ++c) {
         const uint32_t col = (uint32_t)lane * 8 + c * 512;
-        if (col < H) {
-            load_dense8<WDT>(w, row_off + col, wv[c]);
-        } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                wv[c][i] = 0.0f;
+        for (int i = 0; i < WW; ++i)
+            wr[c][i] = 0u;
+        if (col < H) {
+            if constexpr (WDT == 0) {
+                const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + row_off + col);
+                const uint4 a = p[0], b = p[1];
+                wr[c][0] = a.x, wr[c][1] = a.y, wr[c][2] = a.z, wr[c][3] = a.w;
+                wr[c][4] = b.x, wr[c][5] = b.y, wr[c][6] = b.z, wr[c][7] = b.w;
+            } else {
+                const uint4 raw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + row_off + col);
+                wr[c][0] = raw.x, wr[c][1] = raw.y, wr[c][2] = raw.z, wr[c][3] = raw.w;
+            }
         }
     }
     for (uint32_t t = 0; t < T; ++t) {
+        // conversions stay inside the token loop (hoisted, they would hold
+        // 8 floats per chunk)
+#pragma unroll
+        for (int c = 0; c < CR; ++c)
+#pragma unroll
+            for (int i = 0; i < WW; ++i)
+                asm volatile("" : "+v"(wr[c][i]));
         float acc0 = 0.0f, acc1 = 0.0f, ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < CR; ++c) {
             const uint32_t col = (uint32_t)lane * 8 + c * 512;
             if (col < H) {
+                float wv8[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (WDT == 0) {
+                        wv8[2 * i] = __uint_as_float(wr[c][2 * i]);
+                        wv8[2 * i + 1] = __uint_as_float(wr[c][2 * i + 1]);
+                    } else if constexpr (WDT == 2) {
+                        wv8[2 * i] = __uint_as_float(wr[c][i] << 16);
+                        wv8[2 * i + 1] = __uint_as_float(wr[c][i] & 0xFFFF0000u);
+                    } else {
+                        wv8[2 * i] = __half2float(__ushort_as_half((uint16_t)(wr[c][i] & 0xFFFFu)));
+                        wv8[2 * i + 1] = __half2float(__ushort_as_half((uint16_t)(wr[c][i] >> 16)));
+                    }
+                }
+                const float (&wvc)[8] = wv8;
                 float4 u, v;
                 load_x8(x, (uint64_t)t * H + col, norm_w, col, u, v, ss);
-                acc0 = fmaf(wv[c][0], u.x, acc0);
-                acc1 = fmaf(wv[c][1], u.y, acc1);
-                acc0 = fmaf(wv[c][2], u.z, acc0);
-                acc1 = fmaf(wv[c][3], u.w, acc1);
-                acc0 = fmaf(wv[c][4], v.x, acc0);
-                acc1 = fmaf(wv[c][5], v.y, acc1);
-                acc0 = fmaf(wv[c][6], v.z, acc0);
-                acc1 = fmaf(wv[c][7], v.w, acc1);
+                acc0 = fmaf(wvc[0], u.x, acc0);
+                acc1 = fmaf(wvc[1], u.y, acc1);
+                acc0 = fmaf(wvc[2], u.z, acc0);
+                acc1 = fmaf(wvc[3], u.w, acc1);
+                acc0 = fmaf(wvc[4], v.x, acc0);
+                acc1 = fmaf(wvc[5], v.y, acc1);
+                acc0 = fmaf(wvc[6], v.z, acc0);
+                acc1 = fmaf(wvc[7], v.w, acc1);
             }
         }
         float s = wave_sum(acc0 + acc1);
@@ -181,6 +213,14 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
                 }
             }
             for (uint32_t t = 0; t < T; ++t) {
+                // the nibble conversions do not depend on the token: without
+                // this opaque step the compiler hoists them out of the loop
+                // (32 floats per chunk and matrix: one wave per SIMD at CS = 4)
+#pragma unroll
+                for (int c = 0; c < CS; ++c) {
+                    asm volatile("" : "+v"(wg[c].x), "+v"(wg[c].y), "+v"(wg[c].z), "+v"(wg[c].w));
+                    asm volatile("" : "+v"(wu[c].x), "+v"(wu[c].y), "+v"(wu[c].z), "+v"(wu[c].w));
+                }
                 float pg = 0.0f, pu = 0.0f, ss = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CS; ++c) {
@@ -614,15 +654,19 @@ struct DownArgs {
     uint32_t* status;
 };
 
-template <int SBT, int LPR, int CPL, int MAXR>
+// STG: the variant with the LDS staging (direct mode); without it the
+// workgroup holds no staging buffer, so more workgroups fit a CU (layers
+// whose activations never fit STAGE_FLOATS, such as I = 2048 with K = 8).
+template <int SBT, int LPR, int CPL, int MAXR, bool STG>
 __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 {
     constexpr int R = DOWN_R;
     constexpr int SLOTS = 256 / LPR;
     __shared__ float ylds[DEC_ROUTES][R];
     __shared__ float yshl[DEC_T][R];
-    __shared__ __align__(16) float astage[STAGE_FLOATS / 32 * XP];
-    __shared__ float xsl[STAGE_FLOATS / 32]; // per-chunk sums of the staged activations
+    __shared__ __align__(16) float astage[STG ? STAGE_FLOATS / 32 * XP : 4];
+    __shared__ float xsl[STG ? STAGE_FLOATS / 32 : 4]; // per-chunk sums of the staged activations
+    const bool stage = STG && a.stage;
     const int gl = threadIdx.x % LPR;
     const int slot_id = threadIdx.x / LPR;
     const uint32_t row_base = blockIdx.x * R;
@@ -636,7 +680,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     float res_v = 0.0f;
     if (threadIdx.x < T * R)
         res_v = a.residual[(uint64_t)(threadIdx.x / R) * a.hidden + row_base + threadIdx.x % R];
-    if (a.stage) {
+    if (stage) {
         const uint32_t n4 = (routes * I) / 4;
         const float4* src = reinterpret_cast<const float4*>(a.act);
         for (uint32_t i = threadIdx.x; i < n4; i += 256)
@@ -691,7 +735,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                 bi[m][c] = sb_at<SBT>(slot + set.down.b_off, gi);
             }
         }
-        if (a.stage && u0 == 0) {
+        if (stage && u0 == 0) {
             __syncthreads(); // staged activations visible
             const uint32_t n_chunks = (routes + (a.has_shared ? T : 0u)) * (I / 32);
             for (uint32_t q = threadIdx.x; q < n_chunks; q += 256) {
@@ -725,7 +769,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             for (uint32_t j = 0; j < n; ++j) {
                 float part = 0.0f;
                 if (live[m]) {
-                    if (a.stage) {
+                    if (stage) {
                         const uint32_t rt = shared ? routes + j : g0 + j;
                         const float* av = astage + rt * (I / 32) * XP;
                         const float* xs = xsl + rt * (I / 32);
@@ -756,7 +800,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
         }
     }
-    if (a.stage && n_units == 0) {
+    if (stage && n_units == 0) {
         __syncthreads();
         __syncthreads();
     }
@@ -971,16 +1015,21 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     da.hidden_out = d.hidden_out;
     da.status = d.status;
     dim3 g2(H / DOWN_R);
-#define PBM_DN(L, C, M)                                                                        \
-    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M>), g2, dim3(256), 0, st, phase_event(d, 4), \
+#define PBM_DN(L, C, M, S)                                                                     \
+    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M, S>), g2, dim3(256), 0, st, phase_event(d, 4), \
                           phase_event(d, 5), 0, da)
     switch (I) {
-    case 256: PBM_DN(8, 1, 4); break;
-    case 512: PBM_DN(8, 2, 4); break;
-    case 768: PBM_DN(8, 3, 4); break;
-    case 1024: PBM_DN(16, 2, 4); break;
-    case 1536: PBM_DN(16, 3, 4); break;
-    case 2048: PBM_DN(16, 4, 4); break;
+    case 256: PBM_DN(8, 1, 4, true); break;
+    case 512: PBM_DN(8, 2, 4, true); break;
+    case 768: PBM_DN(8, 3, 4, true); break;
+    case 1024: PBM_DN(16, 2, 4, true); break;
+    case 1536: PBM_DN(16, 3, 4, true); break;
+    case 2048: // never staged with K >= 6: 32 lanes x 2 chunks per row, no staging buffer
+        if (da.stage)
+            PBM_DN(16, 4, 4, true);
+        else
+            PBM_DN(32, 2, 4, false);
+        break;
     default: return hipErrorInvalidValue;
     }
 #undef PBM_DN

@@ -41,7 +41,7 @@ __device__ __forceinline__ float readlane_f(float v, int lane)
 template <int W>
 __device__ __forceinline__ float group_sum(float v)
 {
-    static_assert(W == 2 || W == 4 || W == 8 || W == 16, "group width");
+    static_assert(W == 2 || W == 4 || W == 8 || W == 16 || W == 32, "group width");
     v += dpp_f<DPP_QUAD_1032>(v);
     if constexpr (W >= 4)
         v += dpp_f<DPP_QUAD_2301>(v);
@@ -49,6 +49,8 @@ __device__ __forceinline__ float group_sum(float v)
         v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
     if constexpr (W >= 16)
         v += dpp_f<DPP_ROW_MIRROR>(v);
+    if constexpr (W >= 32)
+        v += __shfl_xor(v, 16);
     return v;
 }
 
