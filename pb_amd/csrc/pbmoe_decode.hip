@@ -750,6 +750,42 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
             __syncthreads();
         }
+        if (!STG && !a.use_plan) {
+            // one token, activations read from L2: every unit's loads in one
+            // straight-line block (no token loop between them), so that they
+            // are in flight together instead of one round trip per unit
+            float part[MAXR];
+#pragma unroll
+            for (int m = 0; m < MAXR; ++m) {
+                part[m] = 0.0f;
+                const uint32_t unit = u0 + slot_id + SLOTS * m;
+                if (unit < n_units && live[m]) {
+                    const bool shared = a.has_shared && it[m] == n_routed;
+                    const float* av = shared ? a.act_shared : a.act + (uint64_t)it[m] * I;
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) {
+                        const uint32_t ch = gl + LPR * c;
+                        float xs;
+                        const float qx = q4_chunk_qx(w[m][c], av + ch * 32, xs);
+                        part[m] = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs, part[m]));
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MAXR; ++m) {
+                const uint32_t unit = u0 + slot_id + SLOTS * m;
+                if (unit >= n_units)
+                    continue;
+                const float y = group_sum<LPR>(part[m]);
+                if (gl == 0) {
+                    if (a.has_shared && it[m] == n_routed)
+                        yshl[0][rw[m]] = y;
+                    else
+                        ylds[it[m]][rw[m]] = y;
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int m = 0; m < MAXR; ++m) {
             const uint32_t unit = u0 + slot_id + SLOTS * m;
