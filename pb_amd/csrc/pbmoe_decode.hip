@@ -1064,7 +1064,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
         if (da.stage)
             PBM_DN(16, 4, 4, true);
         else
-            PBM_DN(32, 2, 4, false);
+            PBM_DN(16, 4, 3, false); // 48 units per pass: the 36 of K = 8 + shared in one
         break;
     default: return hipErrorInvalidValue;
     }
