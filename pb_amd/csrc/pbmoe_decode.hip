@@ -987,7 +987,10 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     ea.has_shared = d.shared != nullptr;
     if (ea.has_shared)
         ea.sh = *d.shared;
-    constexpr int RPW = 2;
+    // two rows per wave; four where two would need several rounds of
+    // resident workgroups (large I and H: fewer workgroups, so the routing
+    // each of them repeats is done fewer times)
+    const int RPW = (max_items * (I / 2) + 3) / 4 > 2 * GATEUP_RESIDENT_WGS && I % 4 == 0 ? 4 : 2;
     const uint32_t waves = max_items * (I / RPW);
     const uint32_t cpl = (H / 32 + 63) / 64;
     const uint32_t epl = (d.rp.experts + 63) / 64;
@@ -1012,8 +1015,14 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     }
     dim3 g1(ea.pf_base + ea.pf_wgs);
 #define PBM_GU(C, EP)                                                                          \
-    hipExtLaunchKernelGGL((route_gateup_kernel<SBT, C, RPW, EP>), g1, dim3(256), 0, st, phase_event(d, 2), \
-                          phase_event(d, 3), 0, ea)
+    do {                                                                                       \
+        if (RPW == 4)                                                                          \
+            hipExtLaunchKernelGGL((route_gateup_kernel<SBT, C, 4, EP>), g1, dim3(256), 0, st,  \
+                                  phase_event(d, 2), phase_event(d, 3), 0, ea);                \
+        else                                                                                   \
+            hipExtLaunchKernelGGL((route_gateup_kernel<SBT, C, 2, EP>), g1, dim3(256), 0, st,  \
+                                  phase_event(d, 2), phase_event(d, 3), 0, ea);                \
+    } while (0)
 #define PBM_GU_E(C)                                                                            \
     do {                                                                                       \
         if (epl <= 2) PBM_GU(C, 2);                                                            \
