@@ -100,63 +100,64 @@ __device__ __forceinline__ void load_dense8(const void* w, uint64_t off, float (
     }
 }
 
-// dense row . x for every token (8 columns per lane per chunk of 512)
+// dense row . x for every token (8 columns per lane per chunk of 512).
+// Rows longer than CR chunks (H > 512 CR) are taken in passes of CR chunks
+// per token, the weights reloaded per pass (L2 hits after the first token).
+template <int WDT>
+__device__ __forceinline__ void dense8_to_float(const uint32_t (&wr)[WDT == 0 ? 8 : 4], float (&wv8)[8])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (WDT == 0) {
+            wv8[2 * i] = __uint_as_float(wr[2 * i]);
+            wv8[2 * i + 1] = __uint_as_float(wr[2 * i + 1]);
+        } else if constexpr (WDT == 2) {
+            wv8[2 * i] = __uint_as_float(wr[i] << 16);
+            wv8[2 * i + 1] = __uint_as_float(wr[i] & 0xFFFF0000u);
+        } else {
+            wv8[2 * i] = __half2float(__ushort_as_half((uint16_t)(wr[i] & 0xFFFFu)));
+            wv8[2 * i + 1] = __half2float(__ushort_as_half((uint16_t)(wr[i] >> 16)));
+        }
+    }
+}
+
 template <int WDT, int CR>
 __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, const float* x,
                                                uint32_t T, uint32_t H, float* out, uint32_t out_stride,
                                                const float* norm_w, float eps)
 {
     const int lane = threadIdx.x & 63;
-    // 16-bit weights stay packed in registers until use (half the VGPRs of
-    // converted floats: CR = 16 for H = 7168)
+    // 16-bit weights stay packed in registers until use
     constexpr int WW = WDT == 0 ? 8 : 4; // 32-bit words per 8 weights
     uint32_t wr[CR][WW];
-#pragma unroll
-    for (int c = 0; c < CR; ++c) {
-        const uint32_t col = (uint32_t)lane * 8 + c * 512;
-#pragma unroll
-        for (int i = 0; i < WW; ++i)
-            wr[c][i] = 0u;
-        if (col < H) {
-            if constexpr (WDT == 0) {
-                const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + row_off + col);
-                const uint4 a = p[0], b = p[1];
-                wr[c][0] = a.x, wr[c][1] = a.y, wr[c][2] = a.z, wr[c][3] = a.w;
-                wr[c][4] = b.x, wr[c][5] = b.y, wr[c][6] = b.z, wr[c][7] = b.w;
-            } else {
-                const uint4 raw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + row_off + col);
-                wr[c][0] = raw.x, wr[c][1] = raw.y, wr[c][2] = raw.z, wr[c][3] = raw.w;
-            }
-        }
-    }
-    for (uint32_t t = 0; t < T; ++t) {
-        // conversions stay inside the token loop (hoisted, they would hold
-        // 8 floats per chunk)
-#pragma unroll
-        for (int c = 0; c < CR; ++c)
-#pragma unroll
-            for (int i = 0; i < WW; ++i)
-                asm volatile("" : "+v"(wr[c][i]));
-        float acc0 = 0.0f, acc1 = 0.0f, ss = 0.0f;
+    auto load_pass = [&](uint32_t base) {
 #pragma unroll
         for (int c = 0; c < CR; ++c) {
-            const uint32_t col = (uint32_t)lane * 8 + c * 512;
-            if (col < H) {
-                float wv8[8];
+            const uint32_t col = base + (uint32_t)lane * 8 + c * 512;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if constexpr (WDT == 0) {
-                        wv8[2 * i] = __uint_as_float(wr[c][2 * i]);
-                        wv8[2 * i + 1] = __uint_as_float(wr[c][2 * i + 1]);
-                    } else if constexpr (WDT == 2) {
-                        wv8[2 * i] = __uint_as_float(wr[c][i] << 16);
-                        wv8[2 * i + 1] = __uint_as_float(wr[c][i] & 0xFFFF0000u);
-                    } else {
-                        wv8[2 * i] = __half2float(__ushort_as_half((uint16_t)(wr[c][i] & 0xFFFFu)));
-                        wv8[2 * i + 1] = __half2float(__ushort_as_half((uint16_t)(wr[c][i] >> 16)));
-                    }
+            for (int i = 0; i < WW; ++i)
+                wr[c][i] = 0u;
+            if (col < H) {
+                if constexpr (WDT == 0) {
+                    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + row_off + col);
+                    const uint4 a = p[0], b = p[1];
+                    wr[c][0] = a.x, wr[c][1] = a.y, wr[c][2] = a.z, wr[c][3] = a.w;
+                    wr[c][4] = b.x, wr[c][5] = b.y, wr[c][6] = b.z, wr[c][7] = b.w;
+                } else {
+                    const uint4 raw =
+                        *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w) + row_off + col);
+                    wr[c][0] = raw.x, wr[c][1] = raw.y, wr[c][2] = raw.z, wr[c][3] = raw.w;
                 }
-                const float (&wvc)[8] = wv8;
+            }
+        }
+    };
+    auto dot_pass = [&](uint32_t base, uint32_t t, float& acc0, float& acc1, float& ss) {
+#pragma unroll
+        for (int c = 0; c < CR; ++c) {
+            const uint32_t col = base + (uint32_t)lane * 8 + c * 512;
+            if (col < H) {
+                float wvc[8];
+                dense8_to_float<WDT>(wr[c], wvc);
                 float4 u, v;
                 load_x8(x, (uint64_t)t * H + col, norm_w, col, u, v, ss);
                 acc0 = fmaf(wvc[0], u.x, acc0);
@@ -168,6 +169,24 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
                 acc0 = fmaf(wvc[6], v.z, acc0);
                 acc1 = fmaf(wvc[7], v.w, acc1);
             }
+        }
+    };
+    const bool one_pass = H <= (uint32_t)CR * 512;
+    if (one_pass)
+        load_pass(0);
+    for (uint32_t t = 0; t < T; ++t) {
+        float acc0 = 0.0f, acc1 = 0.0f, ss = 0.0f;
+        for (uint32_t base = 0; base < H; base += CR * 512) {
+            if (!one_pass)
+                load_pass(base);
+            // conversions stay inside the token loop (hoisted, they would
+            // hold 8 floats per chunk)
+#pragma unroll
+            for (int c = 0; c < CR; ++c)
+#pragma unroll
+                for (int i = 0; i < WW; ++i)
+                    asm volatile("" : "+v"(wr[c][i]));
+            dot_pass(base, t, acc0, acc1, ss);
         }
         float s = wave_sum(acc0 + acc1);
         if (norm_w)
@@ -943,8 +962,7 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
 #define PBM_RS_CR(W, G, S)                                                                     \
     do {                                                                                       \
         if (cr <= 4) PBM_RS_CS(W, G, S, 4);                                                    \
-        else if (cr <= 8) PBM_RS_CS(W, G, S, 8);                                               \
-        else PBM_RS_CS(W, G, S, 16);                                                           \
+        else PBM_RS_CS(W, G, S, 8); /* longer rows in passes of 8 chunks */                    \
     } while (0)
     if (wdt != gdt)
         return hipErrorInvalidValue; // bind validates matching dtypes
