@@ -676,7 +676,9 @@ struct DownArgs {
 // STG: the variant with the LDS staging (direct mode); without it the
 // workgroup holds no staging buffer, so more workgroups fit a CU (layers
 // whose activations never fit STAGE_FLOATS, such as I = 2048 with K = 8).
-template <int SBT, int LPR, int CPL, int MAXR, bool STG>
+// ONE: one token without the dispatch plan only (the token-loop path is not
+// compiled, which keeps the registers of the straight-line path low).
+template <int SBT, int LPR, int CPL, int MAXR, bool STG, bool ONE = false>
 __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 {
     constexpr int R = DOWN_R;
@@ -769,7 +771,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
             __syncthreads();
         }
-        if (!STG && !a.use_plan) {
+        if (ONE || (!STG && !a.use_plan)) {
             // one token, activations read from L2: every unit's loads in one
             // straight-line block (no token loop between them), so that they
             // are in flight together instead of one round trip per unit
@@ -805,6 +807,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
             continue;
         }
+        if constexpr (!ONE) {
 #pragma unroll
         for (int m = 0; m < MAXR; ++m) {
             const uint32_t unit = u0 + slot_id + SLOTS * m;
@@ -853,6 +856,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                         ylds[g0 + j][rw[m]] = y;
                 }
             }
+        }
         }
     }
     if (stage && n_units == 0) {
@@ -1090,8 +1094,11 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     case 2048: // never staged with K >= 6: 32 lanes x 2 chunks per row, no staging buffer
         if (da.stage)
             PBM_DN(16, 4, 4, true);
+        else if (!da.use_plan) // one token: 48 units per pass, the 36 of K = 8 + shared in one
+            hipExtLaunchKernelGGL((down_combine_kernel<SBT, 16, 4, 3, false, true>), g2, dim3(256), 0, st,
+                                  phase_event(d, 4), phase_event(d, 5), 0, da);
         else
-            PBM_DN(16, 4, 3, false); // 48 units per pass: the 36 of K = 8 + shared in one
+            PBM_DN(32, 2, 4, false);
         break;
     default: return hipErrorInvalidValue;
     }
