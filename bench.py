@@ -120,9 +120,12 @@ def cpu_baseline(cfg, host_layers, tokens: int, budget_s: float, threads: int):
     # pre-generate inputs and the host slots each sampled token needs (untimed)
     for i in range(64):
         host = host_layers[i % len(host_layers)]
+        route_kw = dict(kind=cfg.routing, order=orc.ORDER_CANONICAL if cfg.routing >= 2 else orc.ORDER_REFERENCE_SLOT,
+                        bias=host.selection_bias, n_group=cfg.n_group, topk_group=cfg.topk_group,
+                        policy=cfg.normalization, routed_scale=cfg.routed_scale)
         xh, rh = synth.activations(SEED + 17, i, tokens, cfg.hidden)
         logits = np.stack([orc.router_logits(host.router_f16, xh[t]) for t in range(tokens)])
-        ids, w = orc.route_rows(logits, cfg.k, orc.ROUTING_SOFTMAX, orc.ORDER_REFERENCE_SLOT)
+        ids, w = orc.route_rows(logits, cfg.k, **route_kw)
         uniq = sorted(set(int(e) for e in ids.ravel()))
         slots = np.concatenate([synth.q4_experts(SEED, synth.T_EXPERT, host.layer, e, 1, cfg.hidden, cfg.intermediate,
                                                  cfg.group, cfg.sb_dtype, lay.offsets, int(lay.expert_bytes))
@@ -132,21 +135,45 @@ def cpu_baseline(cfg, host_layers, tokens: int, budget_s: float, threads: int):
         if host.shared_layout is not None:
             sl = orc.make_layout(cfg.hidden, cfg.shared_intermediate, cfg.group, cfg.sb_dtype,
                                  host.shared_layout.offsets, int(host.shared_layout.expert_bytes))
-        samples.append((host, xh, rh, np.vectorize(remap.get)(ids).astype(np.int32), len(uniq), slots, sl))
+        samples.append((host, xh, rh, np.vectorize(remap.get)(ids).astype(np.int32), len(uniq), slots, sl, route_kw))
     done, t_total = 0, 0.0
     while t_total < budget_s and done < 4096:
-        host, xh, rh, rid, nu, slots, sl = samples[done % len(samples)]
+        host, xh, rh, rid, nu, slots, sl, route_kw = samples[done % len(samples)]
         t0 = time.perf_counter()
-        logits = np.stack([orc.router_logits(host.router_f16, xh[t]) for t in range(tokens)])
-        _, w = orc.route_rows(logits, cfg.k, orc.ROUTING_SOFTMAX, orc.ORDER_REFERENCE_SLOT)
+        logits = np.stack([orc.router_logits_mt(host.router_f16, xh[t], orc.DT_F16, threads) for t in range(tokens)])
+        _, w = orc.route_rows(logits, cfg.k, **route_kw)
         orc.moe_block(olay, slots, nu, xh, rh, rid, w, shared_layout=sl, shared_slot=host.shared_slot,
                       shared_gate_w=host.shared_gate_f16, threads=threads)
         t_total += time.perf_counter() - t0
         done += 1
     us = t_total / done / tokens * 1e6
+    how = "one thread (the reference's sequential loop)" if threads == 1 else \
+        f"{threads} OpenMP threads over router rows and (token, expert) jobs"
     return {"value": round(us, 3), "unit": "us/token/layer", "cores": threads, "kind": "port",
             "sample": f"{done} single-call layers x {tokens} token(s) of the same config "
-                      f"({t_total:.1f} s, oracle router+routing+experts+combine)"}
+                      f"({t_total:.1f} s, oracle router+routing+experts+combine, {how})"}
+
+
+def host_cores() -> int:
+    """Cores the all-cores baseline uses: OMP_NUM_THREADS where set (the GPU
+    box sets it to its CPU share), else the visible CPUs; at most 16."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, min(n, 16))
+
+
+def cpu_baselines(cfg, host_layers, tokens: int, budget_s: float) -> dict:
+    """The oracle on all cores (the reported baseline) and on one core (the
+    reference's own sequential path), each on about `budget_s` of work."""
+    cores = host_cores()
+    one = cpu_baseline(cfg, host_layers, tokens, budget_s, 1)
+    if cores == 1:
+        return one
+    rec = cpu_baseline(cfg, host_layers, tokens, budget_s, cores)
+    rec["single_core"] = one
+    return rec
 
 
 KERNEL_NAMES = {"stage": "router_stage_kernel", "gateup": "route_gateup_kernel", "down": "down_combine_kernel"}
@@ -221,14 +248,18 @@ def bench_prefill(args, cfg, ctx, ev) -> dict:
     for i in range(args.warmup):
         step(i)
     ctx.sync()
-    a, b = ev.create(), ev.create()
-    ev.record(a, stream)
-    for i in range(args.steps):
+    K = max(20, args.steps)
+    marks = [ev.create() for _ in range(K + 1)]
+    ev.record(marks[0], stream)
+    for i in range(K):
         step(i)
-    ev.record(b, stream)
-    us_step = ev.elapsed_ms(a, b) * 1e3 / args.steps
+        ev.record(marks[i + 1], stream)
     ctx.sync()
-    n_ph = min(args.steps, 64)
+    per_step = np.asarray([ev.elapsed_ms(marks[i], marks[i + 1]) * 1e3 for i in range(K)])
+    us_step = float(np.median(per_step))
+    spread = {"median_us": round(us_step, 3), "min_us": round(float(per_step.min()), 3),
+              "max_us": round(float(per_step.max()), 3), "steps": K}
+    n_ph = min(K, 64)
     evs = [[ev.create() for _ in range(6)] for _ in range(n_ph)]
     for i in range(n_ph):
         arr = (C.c_void_p * 6)(*[e.value for e in evs[i]])
@@ -261,9 +292,11 @@ def bench_prefill(args, cfg, ctx, ev) -> dict:
         "value": round(us_step / T, 4),
         "unit": "us/token/layer",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": K,
         "warmup": args.warmup,
         "ms_per_step": round(us_step / 1e3, 6),
+        "spread": spread,
+        "timing": "median over the steps, each bracketed by hipEvents (back to back on the library stream)",
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -383,18 +416,23 @@ def bench_stack(args, ctx, ev) -> dict:
     for _ in range(args.warmup):
         token()
     ctx.sync()
-    a, b = ev.create(), ev.create()
     res = {}
+    K = max(20, args.steps)
+    spread = {}
     for name, parts in (("token", ("attn", "moe")), ("attention", ("attn",)), ("moe", ("moe",))):
         graph = ev.capture(stream, lambda: token(parts))
         ev.launch_graph(graph, stream)
         ctx.sync()
-        ev.record(a, stream)
-        for _ in range(args.steps):
+        marks = [ev.create() for _ in range(K + 1)]
+        ev.record(marks[0], stream)
+        for i in range(K):
             ev.launch_graph(graph, stream)
-        ev.record(b, stream)
-        res[name] = ev.elapsed_ms(a, b) / args.steps
+            ev.record(marks[i + 1], stream)
         ctx.sync()
+        per = np.asarray([ev.elapsed_ms(marks[i], marks[i + 1]) for i in range(K)])
+        res[name] = float(np.median(per))
+        spread[name] = {"median_ms": round(res[name], 4), "min_ms": round(float(per.min()), 4),
+                        "max_ms": round(float(per.max()), 4)}
     ms = res["token"]
     nbytes = stack_bytes_per_token(acfg, mcfg, L, pos)
     gbps = nbytes["total"] / (ms * 1e-3) / 1e9
@@ -408,9 +446,11 @@ def bench_stack(args, ctx, ev) -> dict:
         "value": round(1e3 / ms, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": K,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
+        "spread": spread,
+        "timing": f"median over {K} back-to-back replays of one token's hipGraph, each bracketed by hipEvents",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -464,7 +504,9 @@ def cpu_stack_baseline(acfg, mcfg, host_layers, pos: int, keys, vals, budget_s: 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--steps", type=int, default=480,
+                    help="steps timed per replay (decode: MoE layers; c4_stack: tokens; prefill: layer calls)")
+    ap.add_argument("--replays", type=int, default=20, help="timed replays of the --steps steps (at least 20)")
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="c2_qwen3next_decode")
     ap.add_argument("--tokens", type=int, default=1)
@@ -517,6 +559,7 @@ def main() -> int:
           flush=True)
 
     L = len(layers)
+    K, R = args.steps, max(20, args.replays)
 
     def step(i):
         # one MoE layer for the batch: router + routing + experts + combine
@@ -528,24 +571,29 @@ def main() -> int:
     a, b = ev.create(), ev.create()
     # plain stream: one ABI call per step
     ev.record(a, stream)
-    for i in range(args.steps):
+    for i in range(K):
         step(i)
     ev.record(b, stream)
-    us_stream = ev.elapsed_ms(a, b) * 1e3 / args.steps
+    us_stream = ev.elapsed_ms(a, b) * 1e3 / K
     ctx.sync()
-    # production decode loop: the steps of one pass over the layer copies
-    # captured once as a hipGraph and replayed (same kernels, same inputs)
-    graph = ev.capture(stream, lambda: [step(i) for i in range(L)])
-    reps = max(1, args.steps // L)
-    ev.launch_graph(graph, stream)
+    # production decode loop: K steps captured as a hipGraph (step i on layer
+    # copy i % L, the next replay continuing where the last one stopped) and
+    # replayed R times back to back; the median replay is the headline
+    starts = [(r * K) % L for r in range(R)]
+    graphs = {s0: ev.capture(stream, lambda s0=s0: [step(s0 + i) for i in range(K)]) for s0 in sorted(set(starts))}
+    for s0 in graphs:
+        ev.launch_graph(graphs[s0], stream)
     ctx.sync()
-    ev.record(a, stream)
-    for _ in range(reps):
-        ev.launch_graph(graph, stream)
-    ev.record(b, stream)
-    us_step = ev.elapsed_ms(a, b) * 1e3 / (reps * L)
+    marks = [ev.create() for _ in range(R + 1)]
+    ev.record(marks[0], stream)
+    for r in range(R):
+        ev.launch_graph(graphs[starts[r]], stream)
+        ev.record(marks[r + 1], stream)
     ctx.sync()
-    steps_timed = reps * L
+    per_step = np.asarray([ev.elapsed_ms(marks[r], marks[r + 1]) * 1e3 / K for r in range(R)])
+    us_step = float(np.median(per_step))
+    spread = {"median_us": round(us_step, 3), "min_us": round(float(per_step.min()), 3),
+              "max_us": round(float(per_step.max()), 3), "replays": R, "steps_per_replay": K}
 
     us_expert = None
     if args.expert_phase:
@@ -559,13 +607,14 @@ def main() -> int:
         ev.record(b, stream)
         us_expert = round(ev.elapsed_ms(a, b) * 1e3 / args.steps, 3)
         ctx.sync()
-    print(f"[bench] {us_step:.2f} us/layer (graph), {us_stream:.2f} us/layer (stream), "
-          f"expert phase {us_expert} us", file=sys.stderr, flush=True)
+    print(f"[bench] {us_step:.2f} us/layer (graph, median of {R} replays of {K} steps; min {per_step.min():.2f}, "
+          f"max {per_step.max():.2f}), {us_stream:.2f} us/layer (stream), expert phase {us_expert} us",
+          file=sys.stderr, flush=True)
 
     # per-kernel durations of the same steps (stream mode): the library
     # records hipEvents between its three kernels (pbmoe_set_phase_events)
     # (start/stop events attached to each kernel's dispatch packet)
-    n_ph = min(args.steps, 512)
+    n_ph = max(min(K, 512), 48)
     evs = [[ev.create() for _ in range(6)] for _ in range(n_ph)]
     for i in range(n_ph):
         arr = (C.c_void_p * 6)(*[e.value for e in evs[i]])
@@ -599,15 +648,14 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        threads = 1
-        cpu = cpu_baseline(cfg, [h for _, h in layers[:4]], T, args.cpu_seconds, threads)
+        cpu = cpu_baselines(cfg, [h for _, h in layers[:4]], T, args.cpu_seconds)
 
     rec = {
         "metric": METRIC,
         "value": round(us_step / T, 3),
         "unit": "us/token/layer",
         "n_gpus": 1,
-        "steps": steps_timed,
+        "steps": K,
         "warmup": args.warmup,
         "ms_per_step": round(us_step / 1e3, 6),
         "higher_is_better": False,
@@ -623,7 +671,9 @@ def main() -> int:
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "expert_phase_us": us_expert,
         "stream_us_per_layer": round(us_stream, 3),
-        "timing": "hipGraph replay of the per-layer launches (stream_us_per_layer: one ABI call per step)",
+        "timing": f"median over {R} back-to-back hipGraph replays of {K} layer steps each (step i on layer copy "
+                  f"i mod {L}); stream_us_per_layer: the same {K} steps as one ABI call each",
+        "spread": spread,
         "roofline": {"bound": "hbm", "achieved": dom_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": KERNEL_NAMES[dominant], "bytes_per_launch": ph_bytes[dominant],

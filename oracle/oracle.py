@@ -58,6 +58,17 @@ def router_logits(w: np.ndarray, x: np.ndarray, dtype: int = DT_F16) -> np.ndarr
     return out
 
 
+def router_logits_mt(w: np.ndarray, x: np.ndarray, dtype: int = DT_F16, threads: int = 1) -> np.ndarray:
+    """router_logits with the rows split over OpenMP threads (bitwise equal)."""
+    w = np.ascontiguousarray(w)
+    x = _f32(x)
+    experts, hidden = w.shape
+    out = np.empty(experts, np.float32)
+    lib().or_router_logits_mt(_p(w), C.c_int(dtype), _p(x), C.c_int(experts), C.c_int(hidden), _p(out),
+                              C.c_int(threads))
+    return out
+
+
 def routing_top_k(scores, k: int):
     """math.rs:746-769 — replacement-slot scan, slot order."""
     s = _f32(scores)

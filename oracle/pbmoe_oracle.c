@@ -87,6 +87,21 @@ void or_router_logits(const void* w, int w_dtype, const float* x, int experts, i
     }
 }
 
+/* The same rows split over `threads` OpenMP threads (the all-cores CPU
+ * baseline): each row is still one sequential sum, so the result is
+ * bitwise that of or_router_logits. */
+void or_router_logits_mt(const void* w, int w_dtype, const float* x, int experts, int hidden,
+                         float* out, int threads)
+{
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+#endif
+    for (int e = 0; e < experts; ++e) {
+        const char* row = (const char*)w + (size_t)e * hidden * (w_dtype == OR_DT_F32 ? 4 : 2);
+        or_router_logits(row, w_dtype, x, 1, hidden, out + e);
+    }
+}
+
 /* ------------------------------------------------------------------------
  * a2  routing_top_k_iter — K-slot replacement scan, slot order
  *     math.rs:746-769

@@ -11,6 +11,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -46,9 +47,21 @@ def build_synth() -> str:
 
 
 def build_hip() -> str:
+    """Each source compiles to its own object (host code + gfx950 code
+    object) in parallel; one link makes the shared library."""
     out = os.path.join(HERE, "libpbmoe.so")
     tmp = out + ".tmp"
-    _run([HIPCC, *HIP_FLAGS, "-o", tmp, *[os.path.join(CSRC, s) for s in HIP_SOURCES]])
+    objdir = os.path.join(ROOT, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+    jobs = []
+    for s in HIP_SOURCES:
+        obj = os.path.join(objdir, s.rsplit(".", 1)[0] + ".o")
+        jobs.append(([HIPCC, *compile_flags, "-c", "-o", obj, os.path.join(CSRC, s)], obj))
+    workers = max(1, min(len(jobs), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(lambda j: _run(j[0]), jobs))
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for _, o in jobs]])
     os.replace(tmp, out)
     return out
 

@@ -60,7 +60,6 @@ constexpr uint32_t MAX_K = 16;
 constexpr uint32_t MAX_DECODE_TOKENS = 16;
 constexpr uint32_t MAX_PREFILL_TOKENS = 32768;
 constexpr uint32_t MAX_HIDDEN = 8192;
-constexpr uint32_t MAX_INTERMEDIATE = 2048;
 
 struct DeviceBuf {
     void* ptr = nullptr;
@@ -144,13 +143,16 @@ int set_device(pbmoe_ctx* ctx)
 int adopt(pbmoe_ctx* ctx, const void* src, size_t bytes, uint32_t flags, DeviceBuf& owned,
           const void** out)
 {
+    if (flags != PBMOE_MEM_HOST && flags != PBMOE_MEM_DEVICE)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown memory flags %u", flags);
+    if (owned.ptr) { // a copy made by an earlier bind: no launch may still read it
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        free_buf(owned);
+    }
     if (flags == PBMOE_MEM_DEVICE) {
         *out = src;
         return ok();
     }
-    if (flags != PBMOE_MEM_HOST)
-        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown memory flags %u", flags);
-    free_buf(owned);
     HIP_TRY(hipMalloc(&owned.ptr, bytes));
     owned.bytes = bytes;
     HIP_TRY(hipMemcpyAsync(owned.ptr, src, bytes, hipMemcpyHostToDevice, ctx->stream));
@@ -577,6 +579,26 @@ static bool needs_selection_bias(uint32_t routing)
     return routing == PBMOE_ROUTING_SIGMOID_NOAUX || routing == PBMOE_ROUTING_SIGMOID_GROUPED;
 }
 
+// Drop whatever is bound at `layer` (slots, router, selection bias, shared
+// expert), after the stream has finished every launch that may read it.  A
+// rebind therefore starts from an empty binding: the router and the shared
+// expert sized for the old descriptor are never used with the new one.
+static int release_layer(pbmoe_ctx* ctx, uint32_t layer)
+{
+    auto it = ctx->layers.find(layer);
+    if (it == ctx->layers.end())
+        return PBMOE_OK;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    LayerBinding& b = it->second;
+    free_buf(b.slots_owned);
+    free_buf(b.router_owned);
+    free_buf(b.bias_owned);
+    free_buf(b.shared_owned);
+    free_buf(b.gate_owned);
+    ctx->layers.erase(it);
+    return PBMOE_OK;
+}
+
 // Layer descriptor + slot layout checks shared by pbmoe_bind_layer and
 // pbmoe_bind_layer_file.
 static int check_layer_desc(const pbmoe_layer_desc* d, const pbmoe_q4_layout* layout)
@@ -591,9 +613,13 @@ static int check_layer_desc(const pbmoe_layer_desc* d, const pbmoe_q4_layout* la
     if (d->hidden == 0 || d->hidden % 256 || d->hidden > MAX_HIDDEN)
         return fail(PBMOE_ERR_UNSUPPORTED, "hidden=%u must be a multiple of 256 and <= %u",
                     d->hidden, MAX_HIDDEN);
-    if (d->intermediate == 0 || d->intermediate % 256 || d->intermediate > MAX_INTERMEDIATE)
-        return fail(PBMOE_ERR_UNSUPPORTED, "intermediate=%u must be a multiple of 256 and <= %u",
-                    d->intermediate, MAX_INTERMEDIATE);
+    // the decode down kernel is instantiated for these row lengths only
+    switch (d->intermediate) {
+    case 256: case 512: case 768: case 1024: case 1536: case 2048: break;
+    default:
+        return fail(PBMOE_ERR_UNSUPPORTED,
+                    "intermediate=%u is not one of 256, 512, 768, 1024, 1536, 2048", d->intermediate);
+    }
     if (d->routing > PBMOE_ROUTING_SQRT_SOFTPLUS)
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown routing %u", d->routing);
     if (d->normalization == PBMOE_NORM_PRESERVE_FULL_SOFTMAX)
@@ -646,12 +672,15 @@ PBMOE_API int pbmoe_bind_layer(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_layer
     rc = set_device(ctx);
     if (rc)
         return rc;
+    if ((rc = release_layer(ctx, layer)))
+        return rc;
     LayerBinding& b = ctx->layers[layer];
     b.desc = *d;
     b.layout = *layout;
     const void* dev = nullptr;
     rc = adopt(ctx, slots, (size_t)layout->expert_bytes * d->experts, flags, b.slots_owned, &dev);
     if (rc) {
+        free_buf(b.slots_owned);
         ctx->layers.erase(layer);
         return rc;
     }
@@ -876,8 +905,11 @@ PBMOE_API int pbmoe_bind_layer_file(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_
         free_buf(buf);
         return rc;
     }
+    if ((rc = release_layer(ctx, layer))) {
+        free_buf(buf);
+        return rc;
+    }
     LayerBinding& b = ctx->layers[layer];
-    free_buf(b.slots_owned);
     b.desc = *d;
     b.layout = *layout;
     b.slots_owned = buf;
@@ -985,20 +1017,13 @@ PBMOE_API int pbmoe_unbind_layer(pbmoe_ctx* ctx, uint32_t layer)
 {
     if (!ctx)
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
-    auto it = ctx->layers.find(layer);
-    if (it == ctx->layers.end())
+    if (ctx->layers.find(layer) == ctx->layers.end())
         return fail(PBMOE_ERR_NOT_BOUND, "layer %u is not bound", layer);
     int rc = set_device(ctx);
     if (rc)
         return rc;
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
-    LayerBinding& b = it->second;
-    free_buf(b.slots_owned);
-    free_buf(b.router_owned);
-    free_buf(b.bias_owned);
-    free_buf(b.shared_owned);
-    free_buf(b.gate_owned);
-    ctx->layers.erase(it);
+    if ((rc = release_layer(ctx, layer)))
+        return rc;
     return ok();
 }
 

@@ -56,8 +56,9 @@ def test_fixed_layout_rejections():
     L = abi.lib()
     assert L.pbmoe_q4_layout_fixed(0, 512, 64, abi.DTYPE_F16, C.byref(out)) == abi.ERR_SHAPE
     assert L.pbmoe_q4_layout_fixed(2048, 500, 64, abi.DTYPE_F16, C.byref(out)) == abi.ERR_SHAPE
+    assert b"must be divisible by group_size" in L.pbmoe_last_error()
     assert L.pbmoe_q4_layout_fixed(2048, 512, 64, abi.DTYPE_F32, C.byref(out)) == abi.ERR_DTYPE
-    assert b"divisible" in L.pbmoe_last_error() or True
+    assert b"must be F16 or BF16" in L.pbmoe_last_error()
 
 
 def test_layout_validate_rejects_gaps_and_totals():

@@ -4,7 +4,9 @@ meet max-abs <= 1e-2 and relative L2 <= 2e-3 against the fp32 oracle."""
 from __future__ import annotations
 
 import ctypes as C
+import math
 import sys
+from dataclasses import replace
 
 import numpy as np
 import pytest
@@ -13,6 +15,7 @@ from oracle import oracle as orc
 from pb_amd import abi, synth
 from pb_amd.configs import C1, C2, C3, C5
 from pb_amd.flashmoe import MoeLayer, dispatch_plan
+from pb_amd.synth import MoeConfig
 from tests.gpu_common import SEED, DeviceLayer, assert_layer_tolerance, max_abs_rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -201,6 +204,72 @@ def test_grouped_sigmoid_routing_exact_ties(ctx, T):
     np.testing.assert_array_equal(got, ref_ids)
     assert got[0][0] == 3 and got[0][1] == 17 and got[0][2] == per + 3  # group 0, then group 1
     np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6)
+    m.unbind()
+
+
+# GLM-style plain sigmoid routing (routing_sigmoid_noaux_top_k, math.rs:788-819):
+# select on sigmoid(l) + bias, weight by the unbiased sigmoid(l), renormalise,
+# scale by routed_scaling_factor.  Shapes of C1 and C2 with a selection bias.
+C1_SIG = replace(C1, name="c1_sigmoid_noaux", routing=abi.ROUTING_SIGMOID_NOAUX, routed_scale=2.5)
+C2_SIG = replace(C2, name="c2_sigmoid_noaux", routing=abi.ROUTING_SIGMOID_NOAUX)
+
+
+@pytest.mark.parametrize("cfg,T,order", [(C1_SIG, 1, abi.ORDER_REFERENCE_SLOT), (C1_SIG, 8, abi.ORDER_CANONICAL),
+                                         (C2_SIG, 4, abi.ORDER_REFERENCE_SLOT), (C2_SIG, 8, abi.ORDER_CANONICAL),
+                                         (C2_SIG, 40, abi.ORDER_REFERENCE_SLOT), (C1_SIG, 40, abi.ORDER_CANONICAL)])
+def test_sigmoid_noaux_routing_bit_exact_on_device_logits(ctx, cfg, T, order):
+    """Plain sigmoid routing with a per-expert bias, in the reference's
+    replacement-slot order and in canonical order, on the decode path
+    (T <= 16: routing inside the router/gate-up kernels) and the many-token
+    routing kernel (T = 40): ids bit-exact against the oracle on the
+    device's own logits, weights within 4e-6 relative."""
+    _say(f"[test] sigmoid noaux {cfg.name} T={T} order={order}")
+    dl = _layer(ctx, cfg, 0, order)
+    xh, _ = synth.activations(SEED, 5, T, cfg.hidden)
+    _, ids, w, logits = _route(ctx, dl, xh)
+    l = logits.download()
+    ref_ids, ref_w = orc.route_rows(l, cfg.k, orc.ROUTING_SIGMOID_NOAUX, order, bias=dl.host.selection_bias,
+                                    routed_scale=cfg.routed_scale)
+    got = ids.download().astype(np.int32)
+    np.testing.assert_array_equal(got, ref_ids)
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6, atol=0)
+    if T >= 4:  # the bias changes the selection: without it some token picks other experts
+        plain_ids, _ = orc.route_rows(l, cfg.k, orc.ROUTING_SIGMOID_NOAUX, order,
+                                      bias=np.zeros(cfg.experts, np.float32), routed_scale=cfg.routed_scale)
+        assert not np.array_equal(np.sort(plain_ids, 1), np.sort(got, 1))
+
+
+@pytest.mark.parametrize("order", [abi.ORDER_REFERENCE_SLOT, abi.ORDER_CANONICAL])
+def test_sigmoid_noaux_reference_golden_on_device(ctx, order):
+    """math.rs:1521-1532 on the device: logits [0, 2, -2], bias [1, -1, 0],
+    K = 2 selects experts 0 and 2 (the bias outranks expert 1's larger
+    logit) with unbiased weights sigmoid(0) = 0.5 and sigmoid(-2),
+    renormalised."""
+    _say(f"[test] sigmoid noaux golden order={order}")
+    cfg = MoeConfig("glm_noaux_golden", hidden=256, intermediate=256, experts=3, k=2,
+                    routing=abi.ROUTING_SIGMOID_NOAUX, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    sb_dtype=abi.DTYPE_F16)
+    lay = abi.q4_layout_fixed(cfg.hidden, cfg.intermediate, cfg.group, cfg.sb_dtype)
+    slots = ctx.array(cfg.experts * lay.expert_bytes, np.uint8)
+    abi.check(abi.lib().pbmoe_synth_fill_q4(ctx.handle, slots.ptr, C.byref(lay), cfg.hidden, cfg.intermediate,
+                                            SEED, synth.T_EXPERT, 0, 0, cfg.experts))
+    router = ctx.to_device(np.zeros((cfg.experts, cfg.hidden), np.uint16))
+    bias = ctx.to_device(np.asarray([1.0, -1.0, 0.0], np.float32))
+    m = MoeLayer(ctx, 91, cfg, lay, order).bind_device(slots, router, bias)
+    ids = ctx.array((1, 2), np.uint32)
+    w = ctx.array((1, 2), np.float32)
+    m.route_logits(ctx.to_device(np.asarray([[0.0, 2.0, -2.0]], np.float32)), ids, w)
+    ctx.sync()
+    got_ids, got_w = ids.download()[0].astype(np.int32), w.download()[0]
+    assert sorted(got_ids.tolist()) == [0, 2]
+    p = {0: 0.5, 2: 1.0 / (1.0 + math.exp(2.0))}
+    total = p[0] + p[2]
+    for e, wt in zip(got_ids.tolist(), got_w.tolist()):
+        assert abs(wt - p[e] / total) < 1e-6
+    ref_ids, ref_w = orc.route_rows(np.asarray([[0.0, 2.0, -2.0]], np.float32), 2, orc.ROUTING_SIGMOID_NOAUX, order,
+                                    bias=np.asarray([1.0, -1.0, 0.0], np.float32))
+    np.testing.assert_array_equal(got_ids[None, :], ref_ids)
+    np.testing.assert_allclose(got_w[None, :], ref_w, rtol=4e-6)
     m.unbind()
 
 

@@ -72,6 +72,7 @@ def test_full_c4_stack_token_matches_oracle_per_layer(ctx):
 
     # eager token, one layer at a time, each layer against the oracle
     worst = 0.0
+    close_calls = 0
     for l in range(L):
         att, moe = layers[l]
         h_in = bufs[l % 2].download().ravel()
@@ -87,11 +88,27 @@ def test_full_c4_stack_token_matches_oracle_per_layer(ctx):
         assert_layer_tolerance(mid_d, h_in + o, f"layer {l} attention hidden")
         assert len(set(got_ids[0].tolist())) == mcfg.k and got_ids.max() < mcfg.experts
         post = orc.rms_norm(mid_d, att.post_norm_h, acfg.eps)
+        # routes: the oracle's router + softmax top-k on the oracle-normalised
+        # row.  The device sums in another order and applies the norm as a
+        # scale after the row sums, so ids may differ only for a token whose
+        # K/K+1 logit gap lies inside the error bound of the two paths.
+        ref_l = moe.oracle_logits(post.reshape(1, H))
+        ref_ids, ref_w = orc.route_rows(ref_l, mcfg.k, orc.ROUTING_SOFTMAX, orc.ORDER_CANONICAL)
+        wr = synth.f16_to_f32(moe.host.router_f16)
+        bound = (2 * (H + 64) * 2.0**-24 * (np.abs(post) @ np.abs(wr).T) + 8 * 2.0**-24 * np.abs(ref_l[0])).max()
+        srt = np.sort(ref_l[0])[::-1]
+        if srt[mcfg.k - 1] - srt[mcfg.k] > bound:
+            np.testing.assert_array_equal(got_ids, ref_ids, err_msg=f"layer {l} routes")
+            np.testing.assert_allclose(got_w, ref_w, rtol=1e-4, err_msg=f"layer {l} route weights")
+        else:
+            close_calls += 1
         ref_out, _ = moe.oracle_block(post.reshape(1, H), mid_d.reshape(1, H), got_ids, got_w)
         mx, _ = assert_layer_tolerance(out_d, ref_out.ravel(), f"layer {l} hidden")
         worst = max(worst, mx)
         if l % 8 == 7:
             _say(f"[info] layers 0..{l} within the bar (worst max-abs {worst:.2e})")
+    _say(f"[info] routes equal the oracle's in {L - close_calls} layers; {close_calls} inside the margin")
+    assert close_calls <= L // 8
     final = bufs[L % 2].download()
 
     # the same token captured as one hipGraph and replayed: bitwise equal
