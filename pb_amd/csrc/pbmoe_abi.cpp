@@ -14,6 +14,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -107,6 +108,9 @@ struct pbmoe_ctx {
     DeviceBuf plan_work; // multi-workgroup plan scratch of pbmoe_dispatch_plan
     DeviceBuf attn_scratch; // q/k/v, chunk partials and attention values of one decode step
     DeviceBuf x_normed;     // [T][H] input RMSNorm rows of pbmoe_moe_layer_norm
+    DeviceBuf persist;      // tagged-word scratch of the one-launch batch-1 decode (zeroed on allocation)
+    bool persist_enabled = false; // PBMOE_DECODE_KERNELS=1 selects the one-launch decode for one token
+    uint32_t cus = 0;            // compute units of the device
     hipEvent_t phase_ev[6] = {};
     bool phase_timing = false;
 };
@@ -130,6 +134,20 @@ int ensure(pbmoe_ctx* ctx, DeviceBuf& b, size_t bytes)
     size_t want = bytes < 256 ? 256 : bytes;
     HIP_TRY(hipMalloc(&b.ptr, want));
     b.bytes = want;
+    return ok();
+}
+
+// ensure() for buffers whose contents must start at zero: a new allocation
+// is cleared by a fill kernel before first use.
+int ensure_zeroed(pbmoe_ctx* ctx, DeviceBuf& b, size_t bytes)
+{
+    if (b.bytes >= bytes && b.ptr)
+        return ok();
+    int rc = ensure(ctx, b, bytes);
+    if (rc)
+        return rc;
+    HIP_TRY(pbmoe::launch_fill_u32(ctx->stream, static_cast<uint32_t*>(b.ptr), 0u, b.bytes / 4));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
     return ok();
 }
 
@@ -407,7 +425,10 @@ PBMOE_API int pbmoe_ctx_create(int device, pbmoe_ctx** out)
                     device, prop.gcnArchName);
     pbmoe_ctx* ctx = new pbmoe_ctx();
     ctx->device = device;
+    ctx->cus = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : 0u;
     hipError_t e = hipSetDevice(device);
+    if (const char* k = std::getenv("PBMOE_DECODE_KERNELS"))
+        ctx->persist_enabled = std::strcmp(k, "1") == 0;
     if (e == hipSuccess)
         e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess)
@@ -493,6 +514,10 @@ PBMOE_API int pbmoe_sync(pbmoe_ctx* ctx)
         if (st & (pbmoe::ST_BAD_SUM | pbmoe::ST_NEGATIVE))
             return fail(PBMOE_ERR_ROUTE,
                         "selected expert probabilities must have a positive finite sum");
+        if (st & pbmoe::ST_TIMEOUT)
+            return fail(PBMOE_ERR_TIMEOUT,
+                        "a workgroup of the one-launch decode waited too long for another (the grid was "
+                        "not resident at once); the call's results are invalid");
         if (st & pbmoe::ST_F16_RANGE)
             return fail(PBMOE_ERR_NONFINITE,
                         "a prefill SwiGLU activation exceeded the f16 operand range (|a| > 65504)");
@@ -1061,6 +1086,8 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     const uint32_t K = d.active_experts, H = d.hidden, I = d.intermediate;
     const uint32_t routes = tokens * K;
     int rc;
+    pbmoe::Plan plan{};
+    float *logits, *act, *act_shared, *shared_weight;
     if ((rc = ensure(ctx, ctx->logits, (size_t)tokens * d.experts * 4)))
         return rc;
     if ((rc = ensure(ctx, ctx->act, (size_t)routes * I * 4)))
@@ -1069,15 +1096,18 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
         return rc;
     if ((rc = ensure(ctx, ctx->shared_weight, (size_t)tokens * 4)))
         return rc;
-    pbmoe::Plan plan{};
     if ((rc = plan_buffers(ctx, d.experts, routes, &plan)))
         return rc;
+    logits = static_cast<float*>(ctx->logits.ptr);
+    act = static_cast<float*>(ctx->act.ptr);
+    act_shared = static_cast<float*>(ctx->act_shared.ptr);
+    shared_weight = static_cast<float*>(ctx->shared_weight.ptr);
     *a = pbmoe::DecodeArgs{};
     a->router_w = b->router;
     a->router_dtype = b->router_dtype;
     a->sel_bias = b->sel_bias;
     a->rp = route_params(d);
-    a->logits = static_cast<float*>(ctx->logits.ptr);
+    a->logits = logits;
     a->ids = ids;
     a->weights = weights;
     a->ex = make_set(b->slots, b->layout, d.experts, H, I);
@@ -1092,9 +1122,9 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     a->residual = residual;
     a->tokens = tokens;
     a->hidden = H;
-    a->act = static_cast<float*>(ctx->act.ptr);
-    a->act_shared = static_cast<float*>(ctx->act_shared.ptr);
-    a->shared_weight = static_cast<float*>(ctx->shared_weight.ptr);
+    a->act = act;
+    a->act_shared = act_shared;
+    a->shared_weight = shared_weight;
     a->hidden_out = hidden_out;
     a->next_norm_w = next_norm_weight;
     a->eps = d.norm_epsilon > 0.0f ? d.norm_epsilon : 1e-6f;
@@ -1105,6 +1135,16 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     a->phase_timing = ctx->phase_timing;
     for (int i = 0; i < 6; ++i)
         a->phase_ev[i] = ctx->phase_ev[i];
+    // one token: the whole layer in one persistent launch where the shape allows
+    a->persist = nullptr;
+    pbmoe::PersistPlan pp{};
+    if (ctx->persist_enabled && pbmoe::persist_plan(*a, ctx->cus, &pp)) {
+        const size_t bytes = pp.words * 8;
+        if ((rc = ensure_zeroed(ctx, ctx->persist, bytes)))
+            return rc;
+        a->persist = static_cast<uint64_t*>(ctx->persist.ptr);
+        a->pplan = pp;
+    }
     return ok();
 }
 

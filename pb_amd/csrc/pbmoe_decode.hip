@@ -1133,6 +1133,8 @@ hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mod
         return launch_route_topk(st, d.logits, d.sel_bias, d.tokens, d.rp, d.ids, d.weights, d.status);
     }
     const bool full = mode == DECODE_FULL_LAYER;
+    if (d.persist) // one token: the whole layer in one persistent launch
+        return launch_persist_decode(st, d, full, d.pplan, d.persist);
     err = launch_router_stage(st, d, full, d.shared != nullptr);
     if (err != hipSuccess)
         return err;

@@ -85,7 +85,7 @@ def test_unsupported_intermediate_rejected_at_bind(ctx, inter):
     """Intermediate sizes without a decode down-kernel instance are refused
     by pbmoe_bind_layer with UNSUPPORTED, before anything is launched."""
     _say(f"[test] intermediate {inter} rejected")
-    cfg = replace(C1, name=f"c1_i{inter}", intermediate=inter, experts=2)
+    cfg = replace(C1, name=f"c1_i{inter}", intermediate=inter, experts=2, k=2)
     desc = layer_desc(cfg)
     lay = abi.q4_layout_fixed(cfg.hidden, inter, cfg.group, cfg.sb_dtype)
     slots = ctx.array(2 * lay.expert_bytes, np.uint8)
