@@ -292,6 +292,20 @@ int pbmoe_moe_decode(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float
 int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                     uint32_t tokens, uint32_t* ids_out, float* weights_out,
                     const float* next_norm_weight, float* hidden_out, float* next_normed_out);
+/* pbmoe_moe_layer without any allocation.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, results and errors as pbmoe_moe_layer; every scratch buffer
+ * (logits, activations, plan, and the routes when ids_out/weights_out are
+ * NULL) comes from one static device array of PBMOE_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends.  A call whose scratch would exceed
+ * it returns PBMOE_ERR_UNSUPPORTED.  All calls on one GPU share that array:
+ * calls that overlap on one GPU (two streams, two contexts) race and must
+ * be serialised by the caller. */
+#define PBMOE_NOALLOC_SCRATCH_BYTES (8u << 20)
+int pbmoe_moe_layer_noalloc(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
+                            uint32_t tokens, uint32_t* ids_out, float* weights_out,
+                            const float* next_norm_weight, float* hidden_out, float* next_normed_out);
 /* pbmoe_moe_layer on the un-normalised hidden state: x = RMSNorm(hidden) *
  * norm_weight (the post-attention norm, rms_norm_with_weight_and_epsilon,
  * math.rs:151-167, eps = norm_epsilon) is formed inside the router stage,

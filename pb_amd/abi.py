@@ -134,6 +134,7 @@ _SIG = {
     "pbmoe_route_logits": ([_P, _U32, _P, _U32, _P, _P], C.c_int),
     "pbmoe_moe_decode": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_moe_layer": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
+    "pbmoe_moe_layer_noalloc": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_moe_layer_norm": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_moe_prefill": ([_P, _U32, _P, _P, _U32, _P, _P, _P, _P, _P], C.c_int),
     "pbmoe_dispatch_plan": ([_P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _P, _P], C.c_int),

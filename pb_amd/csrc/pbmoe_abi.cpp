@@ -427,6 +427,8 @@ PBMOE_API int pbmoe_ctx_create(int device, pbmoe_ctx** out)
     ctx->device = device;
     ctx->cus = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : 0u;
     hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess)
+        e = pbmoe::static_scratch_init(device); // device address of the static scratch, once per device
     if (const char* k = std::getenv("PBMOE_DECODE_KERNELS"))
         ctx->persist_enabled = std::strcmp(k, "1") == 0;
     if (e == hipSuccess)
@@ -1076,11 +1078,41 @@ static int route_many(pbmoe_ctx* ctx, LayerBinding* b, const float* logits, uint
     return ok();
 }
 
-// Fill the decode launch description for a bound layer; sizes the scratch.
+// Byte offsets of the decode scratch of `tokens` rows inside one region
+// (each piece 256-byte aligned): the layout of the static scratch used by
+// pbmoe_moe_layer_noalloc.
+struct DecodeScratchLayout {
+    size_t logits, act, act_shared, shared_weight, plan, route_ids, route_w, total;
+};
+
+static DecodeScratchLayout decode_scratch_layout(const pbmoe_layer_desc& d, uint32_t tokens)
+{
+    const size_t routes = (size_t)tokens * d.active_experts;
+    DecodeScratchLayout l{};
+    size_t at = 0;
+    auto take = [&at](size_t bytes) {
+        const size_t off = at;
+        at += (bytes + 255) / 256 * 256;
+        return off;
+    };
+    l.logits = take((size_t)tokens * d.experts * 4);
+    l.act = take(routes * d.intermediate * 4);
+    l.act_shared = take((size_t)tokens * (d.shared_intermediate + 1) * 4);
+    l.shared_weight = take((size_t)tokens * 4);
+    l.plan = take(((size_t)d.experts * 3 + 1 + routes * 3 + pbmoe::plan_work_words((uint32_t)routes, d.experts)) * 4);
+    l.route_ids = take(routes * 4);
+    l.route_w = take(routes * 4);
+    l.total = at;
+    return l;
+}
+
+// Fill the decode launch description for a bound layer.  Scratch: grown in
+// the context's own buffers, or carved from `fixed` (the static scratch of
+// the allocation-free entry point; its size was checked by the caller).
 static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const float* residual,
                        uint32_t tokens, uint32_t* ids, float* weights, const float* next_norm_weight,
                        float* hidden_out, float* next_normed_out, pbmoe::ExpertSet* sh,
-                       pbmoe::DecodeArgs* a)
+                       pbmoe::DecodeArgs* a, uint8_t* fixed = nullptr)
 {
     const pbmoe_layer_desc& d = b->desc;
     const uint32_t K = d.active_experts, H = d.hidden, I = d.intermediate;
@@ -1088,20 +1120,36 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     int rc;
     pbmoe::Plan plan{};
     float *logits, *act, *act_shared, *shared_weight;
-    if ((rc = ensure(ctx, ctx->logits, (size_t)tokens * d.experts * 4)))
-        return rc;
-    if ((rc = ensure(ctx, ctx->act, (size_t)routes * I * 4)))
-        return rc;
-    if ((rc = ensure(ctx, ctx->act_shared, (size_t)tokens * (d.shared_intermediate + 1) * 4)))
-        return rc;
-    if ((rc = ensure(ctx, ctx->shared_weight, (size_t)tokens * 4)))
-        return rc;
-    if ((rc = plan_buffers(ctx, d.experts, routes, &plan)))
-        return rc;
-    logits = static_cast<float*>(ctx->logits.ptr);
-    act = static_cast<float*>(ctx->act.ptr);
-    act_shared = static_cast<float*>(ctx->act_shared.ptr);
-    shared_weight = static_cast<float*>(ctx->shared_weight.ptr);
+    if (fixed) {
+        const DecodeScratchLayout l = decode_scratch_layout(d, tokens);
+        logits = reinterpret_cast<float*>(fixed + l.logits);
+        act = reinterpret_cast<float*>(fixed + l.act);
+        act_shared = reinterpret_cast<float*>(fixed + l.act_shared);
+        shared_weight = reinterpret_cast<float*>(fixed + l.shared_weight);
+        uint32_t* p = reinterpret_cast<uint32_t*>(fixed + l.plan);
+        plan.unique_ids = p;
+        plan.unique_count = p + d.experts;
+        plan.groups = p + d.experts + 1;
+        plan.route_slots = p + d.experts * 3 + 1;
+        plan.src_rows = plan.route_slots + routes;
+        plan.out_idx = plan.src_rows + routes;
+        plan.work = plan.out_idx + routes;
+    } else {
+        if ((rc = ensure(ctx, ctx->logits, (size_t)tokens * d.experts * 4)))
+            return rc;
+        if ((rc = ensure(ctx, ctx->act, (size_t)routes * I * 4)))
+            return rc;
+        if ((rc = ensure(ctx, ctx->act_shared, (size_t)tokens * (d.shared_intermediate + 1) * 4)))
+            return rc;
+        if ((rc = ensure(ctx, ctx->shared_weight, (size_t)tokens * 4)))
+            return rc;
+        if ((rc = plan_buffers(ctx, d.experts, routes, &plan)))
+            return rc;
+        logits = static_cast<float*>(ctx->logits.ptr);
+        act = static_cast<float*>(ctx->act.ptr);
+        act_shared = static_cast<float*>(ctx->act_shared.ptr);
+        shared_weight = static_cast<float*>(ctx->shared_weight.ptr);
+    }
     *a = pbmoe::DecodeArgs{};
     a->router_w = b->router;
     a->router_dtype = b->router_dtype;
@@ -1140,9 +1188,15 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     pbmoe::PersistPlan pp{};
     if (ctx->persist_enabled && pbmoe::persist_plan(*a, ctx->cus, &pp)) {
         const size_t bytes = pp.words * 8;
-        if ((rc = ensure_zeroed(ctx, ctx->persist, bytes)))
-            return rc;
-        a->persist = static_cast<uint64_t*>(ctx->persist.ptr);
+        if (fixed) {
+            uint8_t* region = fixed - pbmoe::STATIC_PERSIST_BYTES;
+            if (bytes <= pbmoe::STATIC_PERSIST_BYTES)
+                a->persist = reinterpret_cast<uint64_t*>(region);
+        } else {
+            if ((rc = ensure_zeroed(ctx, ctx->persist, bytes)))
+                return rc;
+            a->persist = static_cast<uint64_t*>(ctx->persist.ptr);
+        }
         a->pplan = pp;
     }
     return ok();
@@ -1210,7 +1264,7 @@ PBMOE_API int pbmoe_route_logits(pbmoe_ctx* ctx, uint32_t layer, const float* lo
 static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                         uint32_t tokens, uint32_t* ids, float* weights,
                         const float* next_norm_weight, float* hidden_out, float* next_normed_out,
-                        uint32_t mode, const float* in_norm_weight = nullptr)
+                        uint32_t mode, const float* in_norm_weight = nullptr, bool noalloc = false)
 {
     if (!ctx || !x || !residual || !hidden_out || (mode == pbmoe::DECODE_EXPERTS && (!ids || !weights)))
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
@@ -1246,6 +1300,27 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
     rc = set_device(ctx);
     if (rc)
         return rc;
+    uint8_t* fixed = nullptr;
+    if (noalloc) {
+        // every scratch byte from the device's static scratch: no allocation
+        size_t cap = 0;
+        fixed = static_cast<uint8_t*>(pbmoe::static_scratch(ctx->device, &cap));
+        if (!fixed)
+            return fail(PBMOE_ERR_DEVICE, "static scratch of device %d was not set up", ctx->device);
+        // the first STATIC_PERSIST_BYTES hold the one-launch path's tagged
+        // words; the rest the three-kernel path's buffers
+        fixed += pbmoe::STATIC_PERSIST_BYTES;
+        cap -= pbmoe::STATIC_PERSIST_BYTES;
+        const DecodeScratchLayout l = decode_scratch_layout(d, tokens);
+        if (l.total > cap)
+            return fail(PBMOE_ERR_UNSUPPORTED,
+                        "allocation-free layer: %u tokens of this layer need %zu scratch bytes, the static "
+                        "scratch holds %zu", tokens, l.total, cap);
+        if (mode == pbmoe::DECODE_FULL_LAYER && (!ids || !weights)) {
+            ids = reinterpret_cast<uint32_t*>(fixed + l.route_ids);
+            weights = reinterpret_cast<float*>(fixed + l.route_w);
+        }
+    }
     if (in_norm_weight && (rc = ensure(ctx, ctx->x_normed, (size_t)tokens * d.hidden * 4)))
         return rc;
     if (mode == pbmoe::DECODE_FULL_LAYER && (!ids || !weights)) {
@@ -1259,7 +1334,7 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
     pbmoe::DecodeArgs a;
     pbmoe::ExpertSet sh;
     if ((rc = decode_args(ctx, b, x, residual, tokens, ids, weights, next_norm_weight, hidden_out,
-                          next_normed_out, &sh, &a)))
+                          next_normed_out, &sh, &a, fixed)))
         return rc;
     if (in_norm_weight) {
         a.in_norm_w = in_norm_weight;
@@ -1291,6 +1366,19 @@ PBMOE_API int pbmoe_moe_layer(pbmoe_ctx* ctx, uint32_t layer, const float* x,
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "ids_out and weights_out must be given together");
     return expert_phase(ctx, layer, x, residual, tokens, ids_out, weights_out, next_norm_weight,
                         hidden_out, next_normed_out, pbmoe::DECODE_FULL_LAYER);
+}
+
+// pbmoe_moe_layer with every scratch buffer in the device's static scratch
+// (no allocation; see include/pbmoe.h).
+PBMOE_API int pbmoe_moe_layer_noalloc(pbmoe_ctx* ctx, uint32_t layer, const float* x,
+                                      const float* residual, uint32_t tokens, uint32_t* ids_out,
+                                      float* weights_out, const float* next_norm_weight,
+                                      float* hidden_out, float* next_normed_out)
+{
+    if ((ids_out == nullptr) != (weights_out == nullptr))
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "ids_out and weights_out must be given together");
+    return expert_phase(ctx, layer, x, residual, tokens, ids_out, weights_out, next_norm_weight,
+                        hidden_out, next_normed_out, pbmoe::DECODE_FULL_LAYER, nullptr, true);
 }
 
 // The same layer taking the un-normalised hidden state: the input RMSNorm

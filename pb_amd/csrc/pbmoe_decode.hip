@@ -17,7 +17,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 
+#include "pbmoe.h"
 #include "pbmoe_device.h"
 #include "pbmoe_internal.h"
 
@@ -1116,6 +1118,52 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
 static bool set_ok(const ExpertSet& s)
 {
     return (1u << s.group_shift) == s.group && s.group >= 32 && s.group <= 128;
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch of pbmoe_moe_layer_noalloc.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): static_scratch_init looks up the device address once per device
+// and every launch uses that pointer.
+// ---------------------------------------------------------------------------
+constexpr size_t STATIC_SCRATCH_BYTES = PBMOE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+} // namespace
+
+hipError_t static_scratch_init(int device)
+{
+    if (device < 0 || device >= MAX_DEVICES)
+        return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device])
+        return hipSuccess;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+        return e;
+    if (!p)
+        return hipErrorInvalidSymbol;
+    // the tagged words of the one-launch decode start from zero (epoch 0)
+    e = hipMemset(p, 0, STATIC_PERSIST_BYTES);
+    if (e != hipSuccess)
+        return e;
+    g_scratch_ptr[device] = p;
+    return hipSuccess;
+}
+
+void* static_scratch(int device, size_t* bytes)
+{
+    if (bytes)
+        *bytes = STATIC_SCRATCH_BYTES;
+    if (device < 0 || device >= MAX_DEVICES)
+        return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_ptr[device];
 }
 
 hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mode)

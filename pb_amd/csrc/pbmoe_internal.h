@@ -147,6 +147,15 @@ struct PersistArgs {
 bool persist_plan(const DecodeArgs& d, uint32_t max_wgs, PersistPlan* p);
 hipError_t launch_persist_decode(hipStream_t s, const DecodeArgs& d, bool full, const PersistPlan& p,
                                  uint64_t* scratch);
+// Static scratch of the allocation-free decode entry point: a file-scope
+// device array in pbmoe_decode.hip.  static_scratch_init looks up its address
+// on `device` (which must be current) once; static_scratch returns it (null
+// before init) and its size.
+hipError_t static_scratch_init(int device);
+void* static_scratch(int device, size_t* bytes);
+// the first bytes of the static scratch: the one-launch decode's tagged words
+// (cleared once at set-up); the rest holds the three-kernel decode buffers
+constexpr size_t STATIC_PERSIST_BYTES = 4u << 20;
 // Prefill path (grouped GEMM on the matrix cores, any token count).
 struct PrefillArgs {
     ExpertSet ex;              // routed experts
