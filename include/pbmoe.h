@@ -103,6 +103,15 @@ typedef struct pbmoe_q4_layout {
     pbmoe_component components[9];
 } pbmoe_q4_layout;
 
+/* One resident Q4 projection [rows][cols]: codes rows*cols/2 bytes (low
+ * nibble = even column), scale and bias [rows][cols/group] 2-byte each
+ * (the q4_mmap_fma_matvec_bf16_scale_bias operand, shaders.metal:488-660). */
+typedef struct pbmoe_q4_matrix {
+    const void* codes;
+    const void* scales;
+    const void* biases;
+} pbmoe_q4_matrix;
+
 typedef enum pbmoe_routing {
     PBMOE_ROUTING_SOFTMAX_TOPK = 0,     /* routing_softmax_top_k, math.rs:771-783      */
     PBMOE_ROUTING_SIGMOID_NOAUX = 1,    /* routing_sigmoid_noaux_top_k, math.rs:788-819 */
@@ -257,6 +266,24 @@ int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weight, uint32
 int pbmoe_bind_shared(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_layout* shared_layout,
                       const void* shared_slot, const void* gate_weight, uint32_t gate_dtype,
                       uint32_t mem_flags);
+/* Q4 router projection (the ResidentMmapMatvecProjection::Q4 router of
+ * metal/projection.rs:232-259, computed as q4_mmap_fma_matvec /
+ * q4_mmap_fma_matvec_bf16_scale_bias, shaders.metal:488-660): codes
+ * [experts][hidden/2] (low nibble first), scales and biases
+ * [experts][hidden/group_size] in scale_bias_dtype, which must be the
+ * experts' scale/bias dtype; group_size 32, 64 or 128.  Replaces a router
+ * bound before; selection_bias as for pbmoe_bind_router.  Device codes
+ * 16-byte aligned. */
+int pbmoe_bind_router_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_matrix* weight,
+                         uint32_t group_size, uint32_t scale_bias_dtype,
+                         const float* selection_bias, uint32_t mem_flags);
+/* Q4 shared-expert gate row W_sg [1][hidden] (a Q4 mlp.shared_expert_gate,
+ * resident like the router above): replaces the gate given to
+ * pbmoe_bind_shared, which must come first (a later pbmoe_bind_shared
+ * replaces this gate again).  The fused decode layer needs the router and
+ * the shared gate in one dtype, so a Q4 gate goes with a Q4 router there. */
+int pbmoe_bind_shared_gate_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_matrix* gate,
+                              uint32_t group_size, uint32_t scale_bias_dtype, uint32_t mem_flags);
 int pbmoe_unbind_layer(pbmoe_ctx* ctx, uint32_t layer);
 
 /* ---- router (CMD2 router projection + routing stage) -------------------- */
@@ -385,15 +412,6 @@ typedef struct pbmoe_attn_desc {
     uint32_t group_size;   /* Q4 group of the four projections */
     uint32_t scale_bias_dtype; /* PBMOE_DTYPE_F16 or PBMOE_DTYPE_BF16 */
 } pbmoe_attn_desc;
-
-/* One resident Q4 projection [rows][cols]: codes rows*cols/2 bytes (low
- * nibble = even column), scale and bias [rows][cols/group] 2-byte each
- * (the q4_mmap_fma_matvec_bf16_scale_bias operand, shaders.metal:488-660). */
-typedef struct pbmoe_q4_matrix {
-    const void* codes;
-    const void* scales;
-    const void* biases;
-} pbmoe_q4_matrix;
 
 /* q [q_heads*head_dim][H], k and v [kv_heads*head_dim][H], o [H][q_heads*
  * head_dim]; q_norm / k_norm [head_dim] f32 (self_attn.q_norm / k_norm, both

@@ -20,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle_pbmoe.so")
 
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+DT_Q4 = 3  # a Q4 shared gate row in moe_block (shared_gate_w = (codes, scales, biases, group, sb_dtype))
 ORDER_CANONICAL, ORDER_REFERENCE_SLOT = 0, 1
 NORM_RENORMALIZE, NORM_DEEPSEEK_FLOOR, NORM_PRESERVE_FULL = 0, 1, 2
 ROUTING_SOFTMAX, ROUTING_SIGMOID_NOAUX, ROUTING_SIGMOID_GROUPED, ROUTING_SQRT_SOFTPLUS = 0, 1, 2, 3
@@ -199,6 +200,22 @@ def q4_fma_matvec(packed, x, scales, biases, rows: int, cols: int, group: int, s
     return out
 
 
+def router_logits_q4(packed, scales, biases, x, experts: int, hidden: int, group: int,
+                     sb_dtype: int = DT_F16) -> np.ndarray:
+    """Logits [T][experts] of a Q4 router: the resident Q4 projection
+    (ResidentMmapMatvecProjection::Q4, metal/projection.rs:232-259, kernel
+    q4_mmap_fma_matvec[_bf16_scale_bias], shaders.metal:488-660) in the
+    arithmetic of math.rs:861-911 (q4_fma_matvec) for every token row."""
+    xx = np.atleast_2d(_f32(x))
+    return np.stack([q4_fma_matvec(packed, xx[t], scales, biases, experts, hidden, group, sb_dtype)
+                     for t in range(xx.shape[0])])
+
+
+class _Q4Rows(C.Structure):
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p), ("group", C.c_int),
+                ("sb_dtype", C.c_int)]
+
+
 def q4_explicit_matvec(packed, x, scales, biases, rows: int, cols: int, group: int, sb_dtype: int = DT_F32):
     """tests/scheduler.rs:308-325 — sum of (q*s+b)*x."""
     pk = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
@@ -310,12 +327,23 @@ def moe_block(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarray, 
     out = np.empty((rows, hidden), np.float32)
     nn = np.empty((rows, hidden), np.float32) if next_norm_w is not None else None
     nw = _f32(next_norm_w) if next_norm_w is not None else None
-    sg = np.ascontiguousarray(shared_gate_w) if shared_gate_w is not None else None
+    keep = []
+    if shared_gate_w is None:
+        gate_arg = None
+    elif shared_gate_dtype == DT_Q4:  # (codes, scales, biases, group, sb_dtype)
+        codes, scales, biases, group, sbt = shared_gate_w
+        keep = [np.ascontiguousarray(codes, dtype=np.uint8), _sb(scales, sbt), _sb(biases, sbt)]
+        q = _Q4Rows(keep[0].ctypes.data, keep[1].ctypes.data, keep[2].ctypes.data, group, sbt)
+        keep.append(q)
+        gate_arg = C.byref(q)
+    else:
+        keep = [np.ascontiguousarray(shared_gate_w)]
+        gate_arg = _p(keep[0])
     rc = lib().or_moe_block(
         C.byref(layout), _p(slots), C.c_int(experts),
         C.byref(shared_layout) if shared_layout is not None else None,
         _p(shared_slot) if shared_slot is not None else None,
-        _p(sg) if sg is not None else None, C.c_int(shared_gate_dtype),
+        gate_arg, C.c_int(shared_gate_dtype),
         _p(xx), _p(rr), C.c_int(rows), C.c_int(k), _p(ii), _p(ww),
         _p(nw) if nw is not None else None, C.c_float(eps), _p(out),
         _p(nn) if nn is not None else None, C.c_int(threads))

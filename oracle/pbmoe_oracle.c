@@ -635,6 +635,17 @@ void or_combine(const float* residual, const float* y, const float* w, int k, co
     }
 }
 
+/* A resident Q4 row set (a Q4 router or shared-expert gate projection,
+ * ResidentMmapMatvecProjection::Q4, metal/projection.rs:232-259), given to
+ * or_moe_block as its shared gate when shared_gate_dtype == OR_DT_Q4. */
+typedef struct {
+    const uint8_t* codes;
+    const void* scales;
+    const void* biases;
+    int group, sb_dtype;
+} or_q4_rows;
+#define OR_DT_Q4 3
+
 int or_moe_block(const or_q4_layout* lay, const uint8_t* slots, int experts,
                  const or_q4_layout* shared_lay, const uint8_t* shared_slot,
                  const void* shared_gate_w, int shared_gate_dtype, const float* x,
@@ -680,7 +691,10 @@ int or_moe_block(const or_q4_layout* lay, const uint8_t* slots, int experts,
             } else if (shared_lay) {
                 or_expert_swiglu(shared_lay, shared_slot, xt, S + (size_t)t * H, scratch);
                 float g = 80.0f;
-                if (shared_gate_w)
+                if (shared_gate_w && shared_gate_dtype == OR_DT_Q4) {
+                    const or_q4_rows* q = (const or_q4_rows*)shared_gate_w;
+                    or_q4_fma_matvec(q->codes, xt, q->scales, q->biases, q->sb_dtype, 1, H, q->group, &g);
+                } else if (shared_gate_w)
                     or_router_logits(shared_gate_w, shared_gate_dtype, xt, 1, H, &g);
                 sw[t] = or_sigmoid(g);
             } else {

@@ -73,18 +73,20 @@ struct LayerBinding {
     const uint8_t* slots = nullptr;
     size_t slots_bytes = 0;
     DeviceBuf slots_owned;
-    const void* router = nullptr;
-    uint32_t router_dtype = 0;
-    DeviceBuf router_owned;
+    const void* router = nullptr; // dense weight, or the codes of router_q4
+    uint32_t router_dtype = 0;    // PBMOE_DTYPE_*, or pbmoe::DT_Q4
+    pbmoe::Q4Rows router_q4{};
+    DeviceBuf router_owned, router_s_owned, router_b_owned;
     const float* sel_bias = nullptr;
     DeviceBuf bias_owned;
     bool has_shared = false;
     pbmoe_q4_layout shared_layout{};
     const uint8_t* shared_slot = nullptr;
     DeviceBuf shared_owned;
-    const void* shared_gate = nullptr;
+    const void* shared_gate = nullptr; // dense row, or the codes of gate_q4
     uint32_t shared_gate_dtype = 0;
-    DeviceBuf gate_owned;
+    pbmoe::Q4Rows gate_q4{};
+    DeviceBuf gate_owned, gate_s_owned, gate_b_owned;
 };
 
 // Attention layer: weights referenced, KV cache and rotary table owned.
@@ -618,10 +620,9 @@ static int release_layer(pbmoe_ctx* ctx, uint32_t layer)
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     LayerBinding& b = it->second;
     free_buf(b.slots_owned);
-    free_buf(b.router_owned);
-    free_buf(b.bias_owned);
-    free_buf(b.shared_owned);
-    free_buf(b.gate_owned);
+    for (DeviceBuf* o : {&b.router_owned, &b.router_s_owned, &b.router_b_owned, &b.bias_owned,
+                         &b.shared_owned, &b.gate_owned, &b.gate_s_owned, &b.gate_b_owned})
+        free_buf(*o);
     ctx->layers.erase(it);
     return PBMOE_OK;
 }
@@ -985,6 +986,9 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
         return rc;
     b->router = dev;
     b->router_dtype = dtype;
+    b->router_q4 = pbmoe::Q4Rows{};
+    free_buf(b->router_s_owned); // a Q4 router bound before (the stream was synchronised by adopt)
+    free_buf(b->router_b_owned);
     b->sel_bias = nullptr;
     if (selection_bias) {
         rc = adopt(ctx, selection_bias, (size_t)b->desc.experts * 4, flags, b->bias_owned, &dev);
@@ -992,6 +996,99 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
             return rc;
         b->sel_bias = static_cast<const float*>(dev);
     }
+    return ok();
+}
+
+// Adopt a Q4 matrix [rows][cols] (codes, then 2-byte scales and biases
+// [rows][cols / group]) into `out`, copying host memory into the owned buffers.
+static int adopt_q4(pbmoe_ctx* ctx, const pbmoe_q4_matrix* m, uint32_t rows, uint32_t cols, uint32_t group,
+                    uint32_t flags, DeviceBuf& oc, DeviceBuf& os, DeviceBuf& ob, pbmoe::Q4Rows* out)
+{
+    if (!m->codes || !m->scales || !m->biases)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "Q4 matrix needs codes, scales and biases");
+    if (group != 32 && group != 64 && group != 128)
+        return fail(PBMOE_ERR_UNSUPPORTED, "Q4 group size %u not one of 32/64/128", group);
+    if (cols % group)
+        return fail(PBMOE_ERR_SHAPE, "Q4 columns %u not divisible by group size %u", cols, group);
+    if (flags == PBMOE_MEM_DEVICE && (!aligned(m->codes, 16) || !aligned(m->scales, 2) || !aligned(m->biases, 2)))
+        return fail(PBMOE_ERR_ALIGNMENT, "device Q4 codes must be 16-byte and scales/biases 2-byte aligned");
+    const size_t sb = (size_t)rows * (cols / group) * 2;
+    const void *c = nullptr, *sc = nullptr, *bi = nullptr;
+    int rc = adopt(ctx, m->codes, (size_t)rows * cols / 2, flags, oc, &c);
+    if (!rc)
+        rc = adopt(ctx, m->scales, sb, flags, os, &sc);
+    if (!rc)
+        rc = adopt(ctx, m->biases, sb, flags, ob, &bi);
+    if (rc)
+        return rc;
+    out->codes = static_cast<const uint8_t*>(c);
+    out->scales = static_cast<const uint8_t*>(sc);
+    out->biases = static_cast<const uint8_t*>(bi);
+    out->gshift = group == 32 ? 5u : (group == 64 ? 6u : 7u);
+    return PBMOE_OK;
+}
+
+PBMOE_API int pbmoe_bind_router_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_matrix* weight,
+                                   uint32_t group_size, uint32_t scale_bias_dtype,
+                                   const float* selection_bias, uint32_t flags)
+{
+    if (!ctx || !weight)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    if (scale_bias_dtype != b->layout.scale_bias_dtype)
+        return fail(PBMOE_ERR_UNSUPPORTED, "Q4 router scale/bias dtype %u must match the experts' (%u)",
+                    scale_bias_dtype, b->layout.scale_bias_dtype);
+    if (needs_selection_bias(b->desc.routing) && !selection_bias)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT,
+                    "sigmoid routing requires the per-expert selection bias");
+    if ((rc = set_device(ctx)))
+        return rc;
+    pbmoe::Q4Rows q{};
+    if ((rc = adopt_q4(ctx, weight, b->desc.experts, b->desc.hidden, group_size, flags, b->router_owned,
+                       b->router_s_owned, b->router_b_owned, &q)))
+        return rc;
+    b->router_q4 = q;
+    b->router = q.codes;
+    b->router_dtype = pbmoe::DT_Q4;
+    b->sel_bias = nullptr;
+    if (selection_bias) {
+        const void* dev = nullptr;
+        rc = adopt(ctx, selection_bias, (size_t)b->desc.experts * 4, flags, b->bias_owned, &dev);
+        if (rc)
+            return rc;
+        b->sel_bias = static_cast<const float*>(dev);
+    }
+    return ok();
+}
+
+PBMOE_API int pbmoe_bind_shared_gate_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_matrix* gate,
+                                        uint32_t group_size, uint32_t scale_bias_dtype, uint32_t flags)
+{
+    if (!ctx || !gate)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    LayerBinding* b;
+    int rc = get_layer(ctx, layer, &b);
+    if (rc)
+        return rc;
+    if (!b->has_shared)
+        return fail(PBMOE_ERR_NOT_BOUND, "layer %u: bind the shared expert before its Q4 gate", layer);
+    if (!b->desc.shared_gated)
+        return fail(PBMOE_ERR_SHAPE, "layer %u declares an ungated shared expert", layer);
+    if (scale_bias_dtype != b->layout.scale_bias_dtype)
+        return fail(PBMOE_ERR_UNSUPPORTED, "Q4 gate scale/bias dtype %u must match the experts' (%u)",
+                    scale_bias_dtype, b->layout.scale_bias_dtype);
+    if ((rc = set_device(ctx)))
+        return rc;
+    pbmoe::Q4Rows q{};
+    if ((rc = adopt_q4(ctx, gate, 1, b->desc.hidden, group_size, flags, b->gate_owned, b->gate_s_owned,
+                       b->gate_b_owned, &q)))
+        return rc;
+    b->gate_q4 = q;
+    b->shared_gate = q.codes;
+    b->shared_gate_dtype = pbmoe::DT_Q4;
     return ok();
 }
 
@@ -1036,6 +1133,9 @@ PBMOE_API int pbmoe_bind_shared(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_l
         b->shared_gate = dev;
         b->shared_gate_dtype = gate_dtype;
     }
+    b->gate_q4 = pbmoe::Q4Rows{};
+    free_buf(b->gate_s_owned); // a Q4 gate bound before (the stream was synchronised by adopt)
+    free_buf(b->gate_b_owned);
     b->has_shared = true;
     return ok();
 }
@@ -1166,6 +1266,8 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     }
     a->sgate_w = b->shared_gate;
     a->sgate_dtype = b->shared_gate_dtype;
+    a->router_q4 = b->router_q4;
+    a->sgate_q4 = b->gate_q4;
     a->x = x;
     a->residual = residual;
     a->tokens = tokens;
@@ -1240,7 +1342,8 @@ PBMOE_API int pbmoe_route(pbmoe_ctx* ctx, uint32_t layer, const float* x, uint32
         logits = static_cast<float*>(ctx->logits.ptr);
     }
     HIP_TRY(pbmoe::launch_router_logits(ctx->stream, b->router, b->router_dtype, x, tokens,
-                                        b->desc.experts, b->desc.hidden, logits));
+                                        b->desc.experts, b->desc.hidden, logits, &b->router_q4,
+                                        b->layout.scale_bias_dtype));
     return route_many(ctx, b, logits, tokens, ids, weights);
 }
 
@@ -1475,6 +1578,7 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     }
     a.sgate_w = b->has_shared ? b->shared_gate : nullptr;
     a.sgate_dtype = b->shared_gate_dtype;
+    a.sgate_q4 = b->gate_q4;
     a.ids = ids;
     a.weights = weights;
     a.x = x;

@@ -36,6 +36,8 @@ constexpr int DOWN_R = 4;                 // output rows per down workgroup
 // ---------------------------------------------------------------------------
 struct RouterArgs {
     const void* router_w;
+    Q4Rows router_q4;     // WDT == DT_Q4
+    Q4Rows sgate_q4;      // GDT == DT_Q4
     uint32_t experts;     // 0: no router rows
     ExpertSet sh;
     uint32_t shared_rows; // 0: no shared expert
@@ -198,6 +200,63 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
     }
 }
 
+// Q4 row . x for every token (a Q4 router row or shared gate row): lane l
+// takes the 32-column chunks l + 64 c; the row is s . sum(q x) + b . sum(x)
+// per group, the factored form of the dequantised row.
+template <int SBT, int CS>
+__device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const float* x, uint32_t T, uint32_t H,
+                                            float* out, uint32_t out_stride, const float* norm_w, float eps)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t chunks = H / 32, gpr = H >> m.gshift;
+    const uint4* wp = reinterpret_cast<const uint4*>(m.codes + row * (H / 2));
+    uint4 w[CS];
+    float sc[CS], bi[CS];
+#pragma unroll
+    for (int c = 0; c < CS; ++c) {
+        const uint32_t ch = lane + WAVE * c;
+        w[c] = make_uint4(0, 0, 0, 0);
+        sc[c] = 0.0f, bi[c] = 0.0f;
+        if (ch < chunks) {
+            w[c] = wp[ch];
+            const uint64_t gi = row * gpr + ((ch * 32u) >> m.gshift);
+            sc[c] = sb_at<SBT>(m.scales, gi);
+            bi[c] = sb_at<SBT>(m.biases, gi);
+        }
+    }
+    for (uint32_t t = 0; t < T; ++t) {
+#pragma unroll
+        for (int c = 0; c < CS; ++c) // keep the nibble conversions inside the token loop
+            asm volatile("" : "+v"(w[c].x), "+v"(w[c].y), "+v"(w[c].z), "+v"(w[c].w));
+        float p = 0.0f, ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CS; ++c) {
+            const uint32_t ch = lane + WAVE * c;
+            if (ch < chunks) {
+                float xv[32];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float4 u, v;
+                    load_x8(x, (uint64_t)t * H + ch * 32 + 8 * q, norm_w, ch * 32 + 8 * q, u, v, ss);
+                    xv[8 * q] = u.x, xv[8 * q + 1] = u.y, xv[8 * q + 2] = u.z, xv[8 * q + 3] = u.w;
+                    xv[8 * q + 4] = v.x, xv[8 * q + 5] = v.y, xv[8 * q + 6] = v.z, xv[8 * q + 7] = v.w;
+                }
+                float xs = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 32; q += 8)
+                    xs += ((xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3])) +
+                          ((xv[q + 4] + xv[q + 5]) + (xv[q + 6] + xv[q + 7]));
+                p = fmaf(sc[c], q4_chunk_qx_reg(w[c], xv), fmaf(bi[c], xs, p));
+            }
+        }
+        float r = wave_sum(p);
+        if (norm_w)
+            r *= inv_rms_of(ss, H, eps);
+        if (lane == 0)
+            out[(uint64_t)t * out_stride] = r;
+    }
+}
+
 template <int WDT, int GDT, int SBT, int CR, int CS>
 __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
 {
@@ -210,8 +269,11 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
     const uint32_t n_waves = gridDim.x * 4;
     for (uint32_t task = wave_id; task < n_tasks; task += n_waves) {
         if (task < n_router) {
-            dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, a.x, T, H, a.logits + task, n_router,
-                                    a.norm_w, a.eps);
+            if constexpr (WDT == (int)DT_Q4)
+                q4_row_dots<SBT, CS>(a.router_q4, task, a.x, T, H, a.logits + task, n_router, a.norm_w, a.eps);
+            else
+                dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, a.x, T, H, a.logits + task, n_router,
+                                        a.norm_w, a.eps);
         } else if (task < n_router + Is) {
             const uint32_t i = task - n_router;
             const ExpertSet& s = a.sh;
@@ -276,7 +338,10 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
                     a.act_shared[(uint64_t)t * Is + i] = (g / (1.0f + expf(-g))) * u;
             }
         } else if (a.sgate_w) {
-            dense_row_dots<GDT, CR>(a.sgate_w, 0, a.x, T, H, a.shared_weight, 1, a.norm_w, a.eps);
+            if constexpr (GDT == (int)DT_Q4)
+                q4_row_dots<SBT, CS>(a.sgate_q4, 0, a.x, T, H, a.shared_weight, 1, a.norm_w, a.eps);
+            else
+                dense_row_dots<GDT, CR>(a.sgate_w, 0, a.x, T, H, a.shared_weight, 1, a.norm_w, a.eps);
             // sigma applied by the consumer: shared_weight holds the gate logit
         } else if (lane == 0) {
             for (uint32_t t = 0; t < T; ++t)
@@ -925,6 +990,8 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     a.shared_rows = do_shared && d.shared ? d.shared->gate.rows : 0u;
     a.sgate_w = do_shared ? d.sgate_w : nullptr;
     a.sgate_dtype = d.sgate_dtype;
+    a.router_q4 = d.router_q4;
+    a.sgate_q4 = d.sgate_q4;
     a.x = d.x;
     a.norm_w = d.in_norm_w;
     a.eps = d.eps;
@@ -972,7 +1039,14 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     } while (0)
     if (wdt != gdt)
         return hipErrorInvalidValue; // bind validates matching dtypes
-    if (sbt == 2) {
+    // a Q4 router or gate row carries the layer's scale/bias dtype
+    const uint32_t qsb = wdt == DT_Q4 ? d.ex.sb_dtype : sbt;
+    if (wdt == DT_Q4 && a.shared_rows && sbt != qsb)
+        return hipErrorInvalidValue;
+    if (wdt == DT_Q4) {
+        if (qsb == 2) PBM_RS_CS(DT_Q4, DT_Q4, 2, 4);
+        else PBM_RS_CS(DT_Q4, DT_Q4, 1, 4);
+    } else if (sbt == 2) {
         if (wdt == 0) PBM_RS_CR(0, 0, 2);
         else if (wdt == 2) PBM_RS_CR(2, 2, 2);
         else PBM_RS_CR(1, 1, 2);

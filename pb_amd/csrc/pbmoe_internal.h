@@ -36,6 +36,18 @@ struct ExpertSet {
     Q4Proj gate, up, down;
 };
 
+// A resident Q4 projection [rows][cols] given as separate arrays: codes
+// rows*cols/2 bytes, 2-byte scale and bias [rows][cols >> gshift] (their
+// dtype is the layer's scale/bias dtype).  Used for a Q4 router and a Q4
+// shared-expert gate row (dtype code DT_Q4).
+struct Q4Rows {
+    const uint8_t* codes;
+    const uint8_t* scales;
+    const uint8_t* biases;
+    uint32_t gshift;
+};
+constexpr uint32_t DT_Q4 = 3; // weight dtype code beside 0 f32, 1 f16, 2 bf16
+
 // Routing parameters for the routing kernel.
 struct RouteParams {
     uint32_t experts, k, kind, order, norm, n_group, topk_group;
@@ -53,8 +65,10 @@ struct Plan {
     uint32_t* work;        // multi-workgroup scratch (plan_work_words), or null
 };
 
+// w_dtype DT_Q4: the router is `q4` (scale/bias dtype sb_dtype), w unused
 hipError_t launch_router_logits(hipStream_t s, const void* w, uint32_t w_dtype, const float* x,
-                                uint32_t tokens, uint32_t experts, uint32_t hidden, float* logits);
+                                uint32_t tokens, uint32_t experts, uint32_t hidden, float* logits,
+                                const Q4Rows* q4 = nullptr, uint32_t sb_dtype = 1);
 hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bias, uint32_t tokens,
                              const RouteParams& p, uint32_t* ids, float* weights,
                              uint32_t* status);
@@ -79,7 +93,8 @@ enum : uint32_t { DECODE_FULL_LAYER = 0, DECODE_EXPERTS = 1, DECODE_ROUTE_ONLY =
 
 struct DecodeArgs {
     const void* router_w;      // null: route from the given logits
-    uint32_t router_dtype;
+    uint32_t router_dtype;     // 0 f32, 1 f16, 2 bf16, DT_Q4 (router_q4)
+    Q4Rows router_q4;
     const float* sel_bias;     // [E] for sigmoid routing
     RouteParams rp;
     float* logits;             // [T][E]
@@ -88,7 +103,8 @@ struct DecodeArgs {
     ExpertSet ex;              // routed experts
     const ExpertSet* shared;   // host pointer, null without a shared expert
     const void* sgate_w;       // shared gate row [H], null: sigma = 1
-    uint32_t sgate_dtype;
+    uint32_t sgate_dtype;      // as router_dtype (DT_Q4: sgate_q4)
+    Q4Rows sgate_q4;
     const float* x;            // [T][H] (the hidden state when in_norm_w is set)
     const float* in_norm_w;    // null, or input RMSNorm weight [H] (full layer only)
     float* x_normed;           // [T][H] scratch: RMSNorm(x) * in_norm_w
@@ -161,7 +177,8 @@ struct PrefillArgs {
     ExpertSet ex;              // routed experts
     const ExpertSet* shared;   // host pointer, null without a shared expert
     const void* sgate_w;       // shared gate row [H], null: sigma(80) = 1
-    uint32_t sgate_dtype;
+    uint32_t sgate_dtype;      // 0 f32, 1 f16, 2 bf16, DT_Q4 (sgate_q4)
+    Q4Rows sgate_q4;
     const uint32_t* ids;       // [T][K]
     const float* weights;      // [T][K]
     const float* x;            // [T][H]

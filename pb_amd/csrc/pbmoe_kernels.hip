@@ -89,10 +89,61 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
     }
 }
 
+// Q4 router rows: one wave per expert row, lane l takes the 32-column
+// chunks l + 64 c; per chunk s . sum(q x) + b . sum(x) (the factored form of
+// the dequantised row, q4_mmap_fma_matvec of the reference's shaders).
+template <int SBT, int TT>
+__global__ __launch_bounds__(256) void router_logits_q4_kernel(Q4Rows m, const float* __restrict__ x,
+                                                               uint32_t tokens, uint32_t experts,
+                                                               uint32_t hidden, float* __restrict__ logits)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (e >= experts)
+        return;
+    const uint32_t chunks = hidden / 32, gpr = hidden >> m.gshift;
+    const uint4* wp = reinterpret_cast<const uint4*>(m.codes + (uint64_t)e * (hidden / 2));
+    for (uint32_t t0 = 0; t0 < tokens; t0 += TT) {
+        float acc[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            acc[t] = 0.0f;
+        for (uint32_t ch = lane; ch < chunks; ch += WAVE) {
+            const uint4 w = wp[ch];
+            const uint64_t gi = (uint64_t)e * gpr + ((ch * 32u) >> m.gshift);
+            const float sc = sb_at<SBT>(m.scales, gi), bi = sb_at<SBT>(m.biases, gi);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                if (t0 + t < tokens) {
+                    float xs;
+                    const float qx = q4_chunk_qx(w, x + (uint64_t)(t0 + t) * hidden + ch * 32u, xs);
+                    acc[t] = fmaf(sc, qx, fmaf(bi, xs, acc[t]));
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            float v = wave_sum(acc[t]);
+            if (lane == 0 && t0 + t < tokens)
+                logits[(uint64_t)(t0 + t) * experts + e] = v;
+        }
+    }
+}
+
 hipError_t launch_router_logits(hipStream_t s, const void* w, uint32_t w_dtype, const float* x,
-                                uint32_t tokens, uint32_t experts, uint32_t hidden, float* logits)
+                                uint32_t tokens, uint32_t experts, uint32_t hidden, float* logits,
+                                const Q4Rows* q4, uint32_t sb_dtype)
 {
     dim3 grid((experts + 3) / 4), block(256);
+    if (w_dtype == DT_Q4) {
+        if (!q4)
+            return hipErrorInvalidValue;
+        if (sb_dtype == 2)
+            router_logits_q4_kernel<2, 4><<<grid, block, 0, s>>>(*q4, x, tokens, experts, hidden, logits);
+        else
+            router_logits_q4_kernel<1, 4><<<grid, block, 0, s>>>(*q4, x, tokens, experts, hidden, logits);
+        return hipGetLastError();
+    }
     switch (w_dtype) {
     case 0:
         router_logits_kernel<0, 4><<<grid, block, 0, s>>>(w, x, tokens, experts, hidden, logits);

@@ -813,7 +813,10 @@ bool persist_plan(const DecodeArgs& d, uint32_t max_wgs, PersistPlan* p)
     if (d.tokens != 1 || d.hidden != 2048 || d.rp.experts > 1024 || d.rp.experts == 0 || d.rp.experts % 4 ||
         d.rp.k > (uint32_t)MAX_K || d.rp.k == 0)
         return false;
-    if ((d.router_w && d.router_dtype == 0) || (d.sgate_w && d.sgate_dtype == 0))
+    // 16-bit dense router and gate rows only (f32 and Q4 rows take the
+    // three-kernel decode)
+    if ((d.router_w && (d.router_dtype == 0 || d.router_dtype == DT_Q4)) ||
+        (d.sgate_w && (d.sgate_dtype == 0 || d.sgate_dtype == DT_Q4)))
         return false;
     if (d.router_w && d.sgate_w && d.router_dtype != d.sgate_dtype)
         return false;

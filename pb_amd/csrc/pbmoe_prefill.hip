@@ -755,6 +755,30 @@ __global__ __launch_bounds__(256) void gate_row_kernel(const void* __restrict__ 
         out[t] = acc;
 }
 
+// the same for a Q4 gate row [1][hidden]: lane l takes the 32-column chunks
+// l + 64 c, s . sum(q x) + b . sum(x) per chunk
+template <int SBT>
+__global__ __launch_bounds__(256) void gate_row_q4_kernel(Q4Rows m, const float* __restrict__ x, uint32_t tokens,
+                                                         uint32_t hidden, float* __restrict__ out)
+{
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= tokens)
+        return;
+    const float* xr = x + (uint64_t)t * hidden;
+    const uint4* wp = reinterpret_cast<const uint4*>(m.codes);
+    float acc = 0.0f;
+    for (uint32_t ch = lane; ch < hidden / 32; ch += 64) {
+        const uint32_t gi = (ch * 32u) >> m.gshift;
+        float xs;
+        const float qx = q4_chunk_qx(wp[ch], xr + ch * 32u, xs);
+        acc = fmaf(sb_at<SBT>(m.scales, gi), qx, fmaf(sb_at<SBT>(m.biases, gi), xs, acc));
+    }
+    acc = wave_sum(acc);
+    if (lane == 0)
+        out[t] = acc;
+}
+
 // h[t][c] = (r + sum_k w[t,k] y[out_idx[t,k]][c]) + sw_t * S[t][c], then
 // the optional next-layer RMSNorm.  One workgroup per token.
 __global__ __launch_bounds__(256) void prefill_combine_kernel(
@@ -851,7 +875,11 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
         return err;
     if (has_shared && p.sgate_w) {
         const dim3 gg((T + 3) / 4);
-        if (p.sgate_dtype == 0)
+        if (p.sgate_dtype == DT_Q4 && ex.sb_dtype == 2)
+            gate_row_q4_kernel<2><<<gg, 256, 0, st>>>(p.sgate_q4, p.x, T, H, p.shared_logit);
+        else if (p.sgate_dtype == DT_Q4)
+            gate_row_q4_kernel<1><<<gg, 256, 0, st>>>(p.sgate_q4, p.x, T, H, p.shared_logit);
+        else if (p.sgate_dtype == 0)
             gate_row_kernel<0><<<gg, 256, 0, st>>>(p.sgate_w, p.x, T, H, p.shared_logit);
         else if (p.sgate_dtype == 2)
             gate_row_kernel<2><<<gg, 256, 0, st>>>(p.sgate_w, p.x, T, H, p.shared_logit);

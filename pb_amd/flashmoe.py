@@ -84,6 +84,30 @@ class MoeLayer:
                                           abi.MEM_DEVICE))
         return self
 
+    def bind_router_q4(self, codes: DeviceArray, scales: DeviceArray, biases: DeviceArray, group: int,
+                       selection_bias: DeviceArray | None = None) -> "MoeLayer":
+        """A resident Q4 router [experts][hidden] in place of the dense one
+        (pbmoe_bind_router_q4; the Q4 arm of encode_resident_projection_rows,
+        metal/projection.rs:232-259).  Scale/bias dtype = the experts'."""
+        self._keep += [codes, scales, biases, selection_bias]
+        m = abi.Q4Matrix()
+        m.codes, m.scales, m.biases = codes.ptr, scales.ptr, biases.ptr
+        check(lib().pbmoe_bind_router_q4(self.ctx.handle, self.index, C.byref(m), group, self.cfg.sb_dtype,
+                                         selection_bias.ptr if selection_bias is not None else None,
+                                         abi.MEM_DEVICE))
+        return self
+
+    def bind_shared_gate_q4(self, codes: DeviceArray, scales: DeviceArray, biases: DeviceArray,
+                            group: int) -> "MoeLayer":
+        """A resident Q4 shared-expert gate row [1][hidden] in place of the
+        dense one given to the shared binding (pbmoe_bind_shared_gate_q4)."""
+        self._keep += [codes, scales, biases]
+        m = abi.Q4Matrix()
+        m.codes, m.scales, m.biases = codes.ptr, scales.ptr, biases.ptr
+        check(lib().pbmoe_bind_shared_gate_q4(self.ctx.handle, self.index, C.byref(m), group, self.cfg.sb_dtype,
+                                              abi.MEM_DEVICE))
+        return self
+
     def slots(self):
         """(device address, bytes) of the bound expert slots."""
         p, n = C.c_void_p(), C.c_size_t()

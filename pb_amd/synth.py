@@ -19,6 +19,7 @@ T_EXPERT, T_ROUTER, T_SHARED, T_SHARED_GATE, T_INPUT, T_RESIDUAL, T_ROUTER_BIAS,
 # attention layer of the decode stack: q and o share one pseudo slot (gate =
 # W_q, down = W_o), k and v another (gate = W_k, up = W_v); norm weights
 T_ATTN_QO, T_ATTN_KV, T_ATTN_NORM, T_LAYER_NORM, T_KV_FILL = range(9, 14)
+T_ROUTER_Q4, T_SHARED_GATE_Q4 = 14, 15
 
 _lib = None
 
@@ -233,6 +234,25 @@ def attn_host_mats(acfg: AttnConfig, seed: int, layer: int, layout_fn) -> dict:
         return part(slot, lay, first).copy(), scales, centred_bias(biases, scales, acfg.sb_dtype)
 
     return {"q": mat(qo, lqo, 0), "o": mat(qo, lqo, 6), "k": mat(kv, lkv, 0), "v": mat(kv, lkv, 3)}
+
+
+def q4_matrix(seed: int, tensor: int, layer: int, rows: int, cols: int, group: int, sb_dtype: int, layout_fn):
+    """A Q4 matrix [rows][cols] as (codes u8 [rows*cols/2], scales u16,
+    biases u16 [rows][cols/group]): the gate projection of one seeded pseudo
+    slot (rows rounded up to the group), biases centred as for the attention
+    matrices.  Used for a Q4 router and a Q4 shared-expert gate row."""
+    pad = -(-rows // group) * group
+    lay = layout_fn(cols, pad, group, sb_dtype)
+    slot = q4_experts(seed, tensor, layer, 0, 1, cols, pad, group, sb_dtype, lay.offsets, int(lay.expert_bytes))
+
+    def part(comp):
+        c = lay.components[comp]
+        return slot[int(c.offset):int(c.offset) + int(c.bytes)]
+
+    codes = part(0)[:rows * cols // 2].copy()
+    scales = part(1).view(np.uint16)[:rows * (cols // group)].copy()
+    biases = part(2).view(np.uint16)[:rows * (cols // group)]
+    return codes, scales, centred_bias(biases, scales, sb_dtype)
 
 
 def _sb_to_f32(a: np.ndarray, sb_dtype: int) -> np.ndarray:

@@ -41,7 +41,7 @@ class DeviceLayer:
     oracle needs (expert slots are regenerated on the host on demand)."""
 
     def __init__(self, ctx: abi.Context, cfg, layer: int, route_order: int = abi.ORDER_CANONICAL,
-                 index: int | None = None, centred: bool = False):
+                 index: int | None = None, centred: bool = False, q4_router: bool = False):
         self.ctx, self.cfg, self.layer, self.centred = ctx, cfg, layer, centred
         H, I, E = cfg.hidden, cfg.intermediate, cfg.experts
         self.layout = abi.q4_layout_fixed(H, I, cfg.group, cfg.sb_dtype)
@@ -60,6 +60,17 @@ class DeviceLayer:
         self.gate = ctx.to_device(h.shared_gate_f16) if h.shared_gate_f16 is not None else None
         self.moe = MoeLayer(ctx, layer if index is None else index, cfg, self.layout, route_order)
         self.moe.bind_device(self.slots, self.router, self.bias, h.shared_layout, self.shared, self.gate)
+        # Q4 router and shared gate row (in place of the dense ones): host
+        # (codes, scales, biases) triples, or None
+        self.q4_router = self.q4_gate = None
+        if q4_router:
+            self.q4_router = synth.q4_matrix(SEED, synth.T_ROUTER_Q4, layer, E, H, cfg.group, cfg.sb_dtype,
+                                             abi.q4_layout_fixed)
+            self.moe.bind_router_q4(*[ctx.to_device(a) for a in self.q4_router], cfg.group, self.bias)
+            if cfg.shared_gated:
+                self.q4_gate = synth.q4_matrix(SEED, synth.T_SHARED_GATE_Q4, layer, 1, H, cfg.group,
+                                               cfg.sb_dtype, abi.q4_layout_fixed)
+                self.moe.bind_shared_gate_q4(*[ctx.to_device(a) for a in self.q4_gate], cfg.group)
 
     # oracle views ----------------------------------------------------------
     def oracle_layout(self):
@@ -85,15 +96,21 @@ class DeviceLayer:
         remap = {e: i for i, e in enumerate(uniq)}
         return np.concatenate(parts), np.vectorize(remap.get)(ids).astype(np.int32), len(uniq)
 
+    def _oracle_gate(self):
+        if self.q4_gate is not None:
+            return self.q4_gate + (self.cfg.group, self.cfg.sb_dtype), orc.DT_Q4
+        return self.host.shared_gate_f16, orc.DT_F16
+
     def oracle_block(self, x, residual, ids, weights, next_norm=None, threads=8):
         slots, rid, n = self.compact_slots(ids)
         h = self.host
+        gw, gdt = self._oracle_gate()
         return orc.moe_block(self.oracle_layout(), slots, n, x, residual, rid, weights,
                              shared_layout=self.oracle_shared_layout(), shared_slot=h.shared_slot,
-                             shared_gate_w=h.shared_gate_f16, shared_gate_dtype=orc.DT_F16,
-                             next_norm_w=next_norm, threads=threads)
+                             shared_gate_w=gw, shared_gate_dtype=gdt, next_norm_w=next_norm, threads=threads)
 
     def exact_block(self, x, residual, ids, weights, threads=8):
+        assert self.q4_gate is None, "the fp64 block takes a dense shared gate row"
         slots, rid, n = self.compact_slots(ids)
         h = self.host
         return orc.moe_block_f64(self.oracle_layout(), slots, n, x, residual, rid, weights,
@@ -101,6 +118,9 @@ class DeviceLayer:
                                  shared_gate_w=h.shared_gate_f16, shared_gate_dtype=orc.DT_F16, threads=threads)
 
     def oracle_logits(self, x):
+        if self.q4_router is not None:
+            cfg = self.cfg
+            return orc.router_logits_q4(*self.q4_router, x, cfg.experts, cfg.hidden, cfg.group, cfg.sb_dtype)
         return np.stack([orc.router_logits(self.host.router_f16, x[t], orc.DT_F16) for t in range(x.shape[0])])
 
 

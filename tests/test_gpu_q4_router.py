@@ -1,0 +1,202 @@
+"""GPU: a resident Q4 router projection and a Q4 shared-expert gate row (the
+Q4 arm of encode_resident_projection_rows, metal/projection.rs:232-259,
+kernel q4_mmap_fma_matvec[_bf16_scale_bias], shaders.metal:488-660), bound
+through pbmoe_bind_router_q4 / pbmoe_bind_shared_gate_q4 and checked
+against the oracle (router_logits_q4 and moe_block with a Q4 gate, both over
+q4_fma_matvec, math.rs:861-911).
+
+Logits: within the summation bound of the device's factored form
+s*sum(q x) + b*sum(x) against the oracle's fma form.  Routes: ids bit-exact
+against the oracle's routing of the device's own logits.  Layer: the parity
+bar against the oracle block on the device's routes."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import sys
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from pb_amd import abi, synth
+from pb_amd.configs import C1, C2
+from tests.gpu_common import SEED, DeviceLayer, assert_layer_tolerance
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+C1_BF = replace(C1, name="c1_bf16_scale_bias", sb_dtype=abi.DTYPE_BF16)
+C2_SIG = replace(C2, name="c2_sigmoid_noaux", routing=abi.ROUTING_SIGMOID_NOAUX)
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = abi.Context(0)
+    yield c
+    c.close()
+
+
+def _kind(cfg):
+    return orc.ROUTING_SIGMOID_NOAUX if cfg.routing == abi.ROUTING_SIGMOID_NOAUX else orc.ROUTING_SOFTMAX
+
+
+def _bound(dl, xh):
+    """2 (H + 64) u sum_c |w_ec| |x_tc| with |w| <= 15|s| + |b| per group."""
+    cfg = dl.cfg
+    codes, sc, bi = dl.q4_router
+    s = synth._sb_to_f32(sc, cfg.sb_dtype).astype(np.float64).reshape(cfg.experts, -1)
+    b = synth._sb_to_f32(bi, cfg.sb_dtype).astype(np.float64).reshape(cfg.experts, -1)
+    wabs = np.repeat(15.0 * np.abs(s) + np.abs(b), cfg.group, axis=1)
+    return 2 * (cfg.hidden + 64) * U * (np.abs(xh.astype(np.float64)) @ wabs.T)
+
+
+@pytest.mark.parametrize("cfg,T,order", [(C2, 1, abi.ORDER_REFERENCE_SLOT), (C2, 8, abi.ORDER_CANONICAL),
+                                         (C1, 4, abi.ORDER_CANONICAL), (C1_BF, 1, abi.ORDER_REFERENCE_SLOT),
+                                         (C1_BF, 40, abi.ORDER_CANONICAL), (C2, 40, abi.ORDER_REFERENCE_SLOT),
+                                         (C2_SIG, 1, abi.ORDER_REFERENCE_SLOT), (C2_SIG, 40, abi.ORDER_CANONICAL)])
+def test_q4_router_logits_and_routes(ctx, cfg, T, order):
+    """pbmoe_route with a Q4 router: T <= 16 through the decode router stage,
+    T = 40 through the many-token router kernel; f16 and bf16 scale/bias;
+    softmax and sigmoid (with selection bias) routing."""
+    _say(f"[test] q4 router {cfg.name} T={T} order={order}")
+    dl = DeviceLayer(ctx, cfg, 40 + T, order, index=600, q4_router=True)
+    xh, _ = synth.activations(SEED, 800 + T, T, cfg.hidden)
+    x = ctx.to_device(xh)
+    ids = ctx.array((T, cfg.k), np.uint32)
+    w = ctx.array((T, cfg.k), np.float32)
+    logits = ctx.array((T, cfg.experts), np.float32)
+    dl.moe.route(x, ids, w, logits)
+    ctx.sync()
+    got = logits.download()
+    ref = dl.oracle_logits(xh)
+    bound = _bound(dl, xh)
+    assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) / bound))
+    assert float(np.std(ref)) > 0.1  # the seeded router spreads the logits
+    ref_ids, ref_w = orc.route_rows(got, cfg.k, _kind(cfg), order, bias=dl.host.selection_bias,
+                                    routed_scale=cfg.routed_scale)
+    np.testing.assert_array_equal(ids.download().astype(np.int32), ref_ids)
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6, atol=0)
+    dl.moe.unbind()
+
+
+def _kernels_context(kernels):
+    old = os.environ.get("PBMOE_DECODE_KERNELS")
+    os.environ["PBMOE_DECODE_KERNELS"] = kernels
+    try:
+        return abi.Context(0)
+    finally:
+        if old is None:
+            os.environ.pop("PBMOE_DECODE_KERNELS", None)
+        else:
+            os.environ["PBMOE_DECODE_KERNELS"] = old
+
+
+@pytest.mark.parametrize("T,kernels", [(1, None), (4, None), (1, "1")])
+def test_q4_router_and_gate_fused_layer(ctx, T, kernels):
+    """pbmoe_moe_layer on C2 (gated shared expert) with a Q4 router and a Q4
+    shared gate row: routes bit-exact against the oracle's routing of the
+    oracle's logits wherever the K/K+1 gap exceeds the logit bound, the
+    hidden state and next-layer norm within the bar of the oracle block with
+    the Q4 gate.  kernels="1" asks for the one-launch decode, which takes
+    16-bit dense router rows only, so the call runs the three-kernel path."""
+    _say(f"[test] q4 router+gate layer T={T} kernels={kernels}")
+    c = _kernels_context(kernels) if kernels else ctx
+    try:
+        cfg = C2
+        dl = DeviceLayer(c, cfg, 50 + T, abi.ORDER_REFERENCE_SLOT, index=601, q4_router=True)
+        assert dl.q4_gate is not None
+        xh, rh = synth.activations(SEED, 820 + T, T, cfg.hidden)
+        nw = synth.uniform_f32(SEED, 96, 0, 0, 0, cfg.hidden, 0.5, 1.0)
+        x, r = c.to_device(xh), c.to_device(rh)
+        out = c.array((T, cfg.hidden), np.float32)
+        nn = c.array((T, cfg.hidden), np.float32)
+        ids = c.array((T, cfg.k), np.uint32)
+        w = c.array((T, cfg.k), np.float32)
+        dl.moe.forward(x, r, out, ids, w, c.to_device(nw), nn)
+        c.sync()
+        gi, gw = ids.download().astype(np.int32), w.download()
+        ref_l = dl.oracle_logits(xh)
+        ref_ids, ref_w = orc.route_rows(ref_l, cfg.k, orc.ROUTING_SOFTMAX, orc.ORDER_REFERENCE_SLOT)
+        bound = _bound(dl, xh)
+        for t in range(T):
+            srt = np.sort(ref_l[t])[::-1]
+            if srt[cfg.k - 1] - srt[cfg.k] > bound[t].max():
+                np.testing.assert_array_equal(gi[t], ref_ids[t])
+                np.testing.assert_allclose(gw[t], ref_w[t], rtol=1e-4)
+        ref_h, ref_n = dl.oracle_block(xh, rh, gi, gw, next_norm=nw)
+        mx, rel = assert_layer_tolerance(out.download(), ref_h)
+        assert_layer_tolerance(nn.download(), ref_n, "next_normed")
+        _say(f"[result] q4 router+gate T={T}: max_abs={mx:.3e} rel_l2={rel:.3e}")
+        # the Q4 gate replaced the dense gate bound with the shared expert:
+        # the output is nearer the Q4-gate block than the dense-gate block
+        slots, rid, n = dl.compact_slots(gi)
+        ref_dense, _ = orc.moe_block(dl.oracle_layout(), slots, n, xh, rh, rid, gw,
+                                     shared_layout=dl.oracle_shared_layout(), shared_slot=dl.host.shared_slot,
+                                     shared_gate_w=dl.host.shared_gate_f16, shared_gate_dtype=orc.DT_F16)
+        assert mx < float(np.max(np.abs(out.download() - ref_dense)))
+        dl.moe.unbind()
+    finally:
+        if kernels:
+            c.close()
+
+
+def test_q4_gate_prefill_matches_oracle(ctx):
+    """Layer-major prefill (pbmoe_moe_prefill) of 64 tokens with the Q4
+    shared gate row, on routes from the Q4 many-token router."""
+    _say("[test] q4 gate prefill T=64")
+    cfg, T = C2, 64
+    dl = DeviceLayer(ctx, cfg, 60, abi.ORDER_CANONICAL, index=602, q4_router=True)
+    xh, rh = synth.activations(SEED, 840, T, cfg.hidden)
+    x, r = ctx.to_device(xh), ctx.to_device(rh)
+    ids = ctx.array((T, cfg.k), np.uint32)
+    w = ctx.array((T, cfg.k), np.float32)
+    out = ctx.array((T, cfg.hidden), np.float32)
+    dl.moe.route(x, ids, w)
+    dl.moe.qwen_layer_major_experts(x, r, ids, w, out)
+    ctx.sync()
+    gi, gw = ids.download().astype(np.int32), w.download()
+    ref_h, _ = dl.oracle_block(xh, rh, gi, gw)
+    mx, rel = assert_layer_tolerance(out.download(), ref_h)
+    _say(f"[result] q4 gate prefill: max_abs={mx:.3e} rel_l2={rel:.3e}")
+    dl.moe.unbind()
+
+
+def test_q4_router_bind_errors(ctx):
+    """Refusals at bind time: a scale/bias dtype other than the experts', a
+    group size the kernels do not take, missing arrays, a gate before the
+    shared expert is bound."""
+    _say("[test] q4 router bind errors")
+    cfg = C2
+    L = abi.lib()
+    lay = abi.q4_layout_fixed(cfg.hidden, cfg.intermediate, cfg.group, cfg.sb_dtype)
+    slots = ctx.array(cfg.experts * lay.expert_bytes, np.uint8)
+    from pb_amd.flashmoe import layer_desc
+    desc = layer_desc(cfg)
+    abi.check(L.pbmoe_bind_layer(ctx.handle, 603, C.byref(desc), C.byref(lay), slots.ptr, slots.nbytes,
+                                 abi.MEM_DEVICE))
+    codes = ctx.array(cfg.experts * cfg.hidden // 2, np.uint8)
+    sb = ctx.array(cfg.experts * cfg.hidden // 32, np.uint16)
+    m = abi.Q4Matrix()
+    m.codes, m.scales, m.biases = codes.ptr, sb.ptr, sb.ptr
+    assert L.pbmoe_bind_router_q4(ctx.handle, 603, C.byref(m), cfg.group, abi.DTYPE_BF16, None,
+                                  abi.MEM_DEVICE) == abi.ERR_UNSUPPORTED
+    assert b"scale/bias" in L.pbmoe_last_error()
+    assert L.pbmoe_bind_router_q4(ctx.handle, 603, C.byref(m), 16, cfg.sb_dtype, None,
+                                  abi.MEM_DEVICE) == abi.ERR_UNSUPPORTED
+    assert b"group" in L.pbmoe_last_error()
+    bad = abi.Q4Matrix()
+    bad.codes, bad.scales, bad.biases = codes.ptr, sb.ptr, None
+    assert L.pbmoe_bind_router_q4(ctx.handle, 603, C.byref(bad), cfg.group, cfg.sb_dtype, None,
+                                  abi.MEM_DEVICE) == abi.ERR_INVALID_ARGUMENT
+    assert L.pbmoe_bind_shared_gate_q4(ctx.handle, 603, C.byref(m), cfg.group, cfg.sb_dtype,
+                                       abi.MEM_DEVICE) == abi.ERR_NOT_BOUND
+    abi.check(L.pbmoe_bind_router_q4(ctx.handle, 603, C.byref(m), cfg.group, cfg.sb_dtype, None,
+                                     abi.MEM_DEVICE))
+    abi.check(L.pbmoe_unbind_layer(ctx.handle, 603))

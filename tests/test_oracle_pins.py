@@ -1,5 +1,6 @@
 """Pins for the oracle functions that the layer goldens leave open: the
-router projection (a1), the sigmoid-gated shared expert of the combine, and
+router projection (a1, dense and Q4), the sigmoid-gated shared expert of the
+combine (dense and Q4 gate row), and
 the reference's two-layer deferred-handoff golden.  Reference paths are
 relative to src/inference/flashmoe/ of Jc2k/pb.  CPU only.
 
@@ -182,6 +183,97 @@ def test_shared_gate_sigmoid_closed_form(gate):
     hf, _ = orc.moe_block(lay, np.tile(slot, 9), 9, NORMED[None, :], RESIDUAL[None, :], ids, w,
                           shared_layout=lay, shared_slot=shared)
     assert np.max(np.abs(hf[0] - (r + 3.0 * y))) <= 4e-6  # no gate row: sigmoid(80) = 1
+
+
+# ------------------------------------------- Q4 router and Q4 shared gate ---
+def _bf16(v):
+    return (np.asarray(v, F).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def _q4_case(E, H, group, sbt, seed):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 256, E * H // 2, dtype=np.uint8)
+    s = rng.uniform(0.004, 0.02, E * (H // group)).astype(F)
+    b = (-7.5 * s * rng.uniform(0.8, 1.2, s.size)).astype(F)
+    if sbt == orc.DT_F16:
+        sc, bi = s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+        s64, b64 = sc.view(np.float16).astype(np.float64), bi.view(np.float16).astype(np.float64)
+    else:
+        sc, bi = _bf16(s), _bf16(b)
+        s64 = (sc.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        b64 = (bi.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    q = np.empty(E * H, np.float64)
+    q[0::2], q[1::2] = codes & 15, codes >> 4  # low nibble = even column
+    rep = lambda a: np.repeat(a.reshape(E, H // group), group, axis=1)
+    w = q.reshape(E, H) * rep(s64) + rep(b64)
+    return codes, sc, bi, w, 15.0 * np.abs(rep(s64)) + np.abs(rep(b64))
+
+
+@pytest.mark.parametrize("E,H,group,sbt", [(512, 2048, 64, orc.DT_F16), (128, 2048, 32, orc.DT_BF16),
+                                            (40, 768, 128, orc.DT_F16)])
+def test_router_logits_q4_match_fp64_dequantised_product(E, H, group, sbt):
+    """The Q4 router (projection.rs:232-259 over q4_fma_matvec, math.rs:
+    861-911): logits[t][e] = sum_c (q[e][c] s[e][g(c)] + b[e][g(c)]) x[t][c]
+    with the low nibble of byte j at column 2j and g(c) = c / group.  The
+    f32 result lies within 2(H+2)u sum|w||x| of the fp64 value of the
+    dequantised product; reading the nibbles swapped or the groups per
+    column of the transposed matrix fails that bound."""
+    codes, sc, bi, w, wabs = _q4_case(E, H, group, sbt, 3 + E)
+    x = np.random.default_rng(7).standard_normal((3, H)).astype(F)
+    got = orc.router_logits_q4(codes, sc, bi, x, E, H, group, sbt)
+    assert got.shape == (3, E)
+    x64 = x.astype(np.float64)
+    exact = x64 @ w.T
+    bound = 2 * (H + 2) * U * (np.abs(x64) @ wabs.T)
+    assert np.all(np.abs(got - exact) <= bound)
+    swapped = np.empty_like(codes)
+    swapped[:] = (codes >> 4) | ((codes & 15) << 4)
+    wrong = orc.router_logits_q4(swapped, sc, bi, x, E, H, group, sbt)
+    assert np.mean(np.abs(wrong - exact) > bound) > 0.9
+
+
+def test_shared_gate_q4_zero_row_is_the_reference_q4_router_case():
+    """tests/scheduler.rs:1316-1577 binds the shared router as a Q4 row whose
+    codes and bias are zero (scale 1): gate logit 0, sigma = 0.5, so the
+    combine is r + y + 0.5 y exactly as with a zero dense row."""
+    lay, slot = _identity_slot_layout()
+    ids, w = _routes()
+    zero = (np.zeros(1, np.uint8), _bf16([1.0]), _bf16([0.0]), 2, orc.DT_BF16)
+    h, _ = orc.moe_block(lay, np.tile(slot, 9), 9, NORMED[None, :], RESIDUAL[None, :], ids, w,
+                         shared_layout=lay, shared_slot=slot, shared_gate_w=zero, shared_gate_dtype=orc.DT_Q4)
+    expected = RESIDUAL.astype(np.float64) + 1.5 * _silu_sq(NORMED)
+    assert np.max(np.abs(h[0] - expected)) <= 2e-6
+
+
+@pytest.mark.parametrize("byte,scale,bias", [(0x3A, 0.25, -1.0), (0x0F, -0.5, 0.75), (0xF1, 0.125, 0.5)])
+def test_shared_gate_q4_closed_form(byte, scale, bias):
+    """A Q4 gate row over H = 2: codes (byte & 15, byte >> 4), one group of
+    2 columns; logit = (q0 s + b) n0 + (q1 s + b) n1, h = r + y +
+    sigmoid(logit) * 2y (shared down scale 2).  Fails for swapped nibbles
+    (all three bytes have distinct nibbles), for a missing bias term or a
+    gate on the residual."""
+    lay, slot = _identity_slot_layout()
+    shared = slot.copy()
+    shared[40:44] = [0x00, 0x40, 0x00, 0x40]  # down scales bf16 2.0
+    ids, w = _routes()
+    gate = (np.asarray([byte], np.uint8), _bf16([scale]), _bf16([bias]), 2, orc.DT_BF16)
+    h, _ = orc.moe_block(lay, np.tile(slot, 9), 9, NORMED[None, :], RESIDUAL[None, :], ids, w,
+                         shared_layout=lay, shared_slot=shared, shared_gate_w=gate, shared_gate_dtype=orc.DT_Q4)
+    n = NORMED.astype(np.float64)
+    r = RESIDUAL.astype(np.float64)
+    y = _silu_sq(NORMED)
+    q0, q1 = byte & 15, byte >> 4
+
+    def expect(l):
+        return r + y + 2.0 * y / (1.0 + math.exp(-l))
+
+    logit = (q0 * scale + bias) * n[0] + (q1 * scale + bias) * n[1]
+    assert np.max(np.abs(h[0] - expect(logit))) <= 4e-6
+    wrong = [(q1 * scale + bias) * n[0] + (q0 * scale + bias) * n[1],    # nibbles swapped
+             q0 * scale * n[0] + q1 * scale * n[1],                       # bias dropped
+             (q0 * scale + bias) * r[0] + (q1 * scale + bias) * r[1]]     # residual input
+    for l in wrong:
+        assert np.max(np.abs(h[0] - expect(l))) > 1e-4
 
 
 # ------------------------------------------- two-layer deferred handoff ---
