@@ -181,8 +181,8 @@ KERNEL_NAMES = {"stage": "router_stage_kernel", "gateup": "route_gateup_kernel",
 
 def load_traffic(phase: str, workload: str):
     """HBM bytes per launch of a kernel from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the plain-copy
-    calibration), or None when no summary covers this kernel/workload."""
+    summary (written by --pmc-summary ... --traffic-out), or None when no
+    summary covers this kernel/workload."""
     path = os.path.join(ROOT, "profiles", "decode_traffic.json")
     try:
         with open(path) as f:
@@ -205,6 +205,158 @@ def copy_calibration(ctx, mb: int, reps: int) -> None:
         assert hip.hipMemcpyAsync(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), n, 3, C.c_void_p(ctx.stream())) == 0
     ctx.sync()
     print(f"[bench] copy calibration: {reps} x {n} bytes device-to-device", file=sys.stderr, flush=True)
+
+
+def read_calibration(ctx, mb: int, reps: int) -> None:
+    """pbmoe_stream_read over a device buffer of known size (16-byte lane
+    loads, the access shape of the decode weight reads): the reference
+    point for the read-traffic counters of a PMC run."""
+    from pb_amd import abi
+    n = mb << 20
+    src, out = ctx.array(n, np.uint8), ctx.array(1, np.uint32)
+    for _ in range(reps):
+        abi.check(abi.lib().pbmoe_stream_read(ctx.handle, src.ptr, n, out.ptr))
+    ctx.sync()
+    print(f"[bench] read calibration: {reps} x {n} bytes", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 PMC summaries (--pmc-summary): per-kernel means of the counters
+# of one or more rocprofv3 output directories (rocpd SQLite databases)
+# ---------------------------------------------------------------------------
+SIMD_NUM = 1024  # MI355X: 256 CUs x 4 SIMDs
+XCD_NUM = 8      # rocpd stores GRBM_GUI_ACTIVE summed over the 8 XCDs of a dispatch
+CALIB_READ_KERNEL, CALIB_COPY_KERNEL = "stream_read_kernel", "__amd_rocclr_copyBuffer"
+
+
+def _short_kernel(name: str) -> str:
+    base = name.split("(")[0].replace("void ", "").strip()
+    return base.split("::")[-1] if "::" in base else base
+
+
+def pmc_collect(dirs) -> dict:
+    """{kernel (template arguments kept): {"dispatches": n, "duration_us": mean,
+    counter: mean value per dispatch, ...}} over every *_results.db under dirs."""
+    import glob
+    import sqlite3
+    vals: dict = {}
+    for d in dirs:
+        for db in sorted(glob.glob(os.path.join(d, "**", "*_results.db"), recursive=True)):
+            con = sqlite3.connect(db)
+            for kname, cname, v, dur, did in con.execute(
+                    "select kernel_name, counter_name, value, duration, dispatch_id from counters_collection"):
+                k = vals.setdefault(_short_kernel(kname), {"_disp": {}, "_ctr": {}})
+                k["_disp"][(db, did)] = dur
+                k["_ctr"].setdefault(cname, {}).setdefault((db, did), 0.0)
+                k["_ctr"][cname][(db, did)] += v  # instances of one dispatch are summed
+            con.close()
+    out = {}
+    for kname, k in vals.items():
+        rec = {"dispatches": len(k["_disp"]), "duration_us": float(np.mean(list(k["_disp"].values()))) / 1e3,
+               "max": {}}
+        for cname, per in k["_ctr"].items():
+            rec[cname] = float(np.mean(list(per.values())))
+            rec["max"][cname] = float(np.max(list(per.values())))
+        out[kname] = rec
+    return out
+
+
+def _read_bytes(r: dict):
+    """FETCH_SIZE's request terms: 128-byte (TCC_BUBBLE), 32-byte and the
+    remaining 64-byte requests of TCC_EA0_RDREQ."""
+    b, r32, rall = r.get("TCC_BUBBLE_sum"), r.get("TCC_EA0_RDREQ_32B_sum"), r.get("TCC_EA0_RDREQ_sum")
+    if b is None or r32 is None or rall is None:
+        return None
+    return 128.0 * b + 64.0 * (rall - b - r32) + 32.0 * r32
+
+
+def _write_bytes(r: dict):
+    w, w64 = r.get("TCC_EA0_WRREQ_sum"), r.get("TCC_EA0_WRREQ_64B_sum")
+    if w is None or w64 is None:
+        return None
+    return 64.0 * w64 + 32.0 * (w - w64)
+
+
+def _find(summary: dict, needle: str):
+    return next((v for k, v in summary.items() if needle in k), None)
+
+
+def pmc_derive(summary: dict, read_cal_bytes: int = 0, copy_cal_bytes: int = 0) -> dict:
+    """Derived per-kernel figures: MFMA busy (% of SIMD cycles), shader clock,
+    VALU instructions per MFMA, and read/write bytes from the raw TCC request
+    terms, scaled by the read-stream and copy calibration launches when
+    present (known bytes over the bytes the same terms report for them)."""
+    # the calibration launches are the largest dispatches of their kernels
+    # (the runtime's copy kernel also serves the small uploads)
+    cal = {}
+    rk = _find(summary, CALIB_READ_KERNEL)
+    if rk and read_cal_bytes and _read_bytes(rk["max"]):
+        cal["read_scale"] = read_cal_bytes / _read_bytes(rk["max"])
+    ck = _find(summary, CALIB_COPY_KERNEL)
+    if ck and copy_cal_bytes and _write_bytes(ck["max"]):
+        cal["write_scale"] = copy_cal_bytes / _write_bytes(ck["max"])
+        if _read_bytes(ck["max"]):
+            cal["copy_read_scale"] = copy_cal_bytes / _read_bytes(ck["max"])
+    out = {"calibration": cal, "kernels": {}}
+    for k, r in summary.items():
+        d = {"dispatches": r["dispatches"], "duration_us": round(r["duration_us"], 3)}
+        gui = r.get("GRBM_GUI_ACTIVE")
+        if gui:
+            gui /= XCD_NUM  # cycles of one XCD
+            d["clock_ghz"] = round(gui / (r["duration_us"] * 1e3), 3)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in r:
+                d["mfma_busy_pct"] = round(100.0 * r["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * SIMD_NUM), 2)
+        if r.get("SQ_INSTS_MFMA"):
+            if "SQ_INSTS_VALU" in r:
+                d["valu_per_mfma"] = round((r["SQ_INSTS_VALU"] - r["SQ_INSTS_MFMA"]) / r["SQ_INSTS_MFMA"], 2)
+            if "SQ_INSTS_LDS" in r:
+                d["lds_per_mfma"] = round(r["SQ_INSTS_LDS"] / r["SQ_INSTS_MFMA"], 3)
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in r:
+            d["mfma_f16_tflops"] = round(r["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512 / (r["duration_us"] * 1e-6) / 1e12, 1)
+        rb, wb = _read_bytes(r), _write_bytes(r)
+        if rb is not None:
+            d["read_bytes_counted"] = int(rb)
+            if "read_scale" in cal:
+                d["read_bytes"] = int(rb * cal["read_scale"])
+        if wb is not None:
+            d["write_bytes_counted"] = int(wb)
+            if "write_scale" in cal:
+                d["write_bytes"] = int(wb * cal["write_scale"])
+        for c in r:
+            if c not in ("dispatches", "duration_us", "max"):
+                d[c] = round(r[c], 1)
+        out["kernels"][k] = d
+    return out
+
+
+def write_traffic(rec: dict, config: str, tokens: int, path: str) -> None:
+    """Per decode kernel of `config`: calibrated read + write bytes per launch
+    beside the algorithmic bytes (configs.decode_phase_bytes)."""
+    from pb_amd.configs import CONFIGS, decode_phase_bytes
+    cfg = CONFIGS[config]
+    alg = decode_phase_bytes(cfg, cfg.k, tokens)
+    cal = rec["calibration"]
+    if "read_scale" not in cal or "write_scale" not in cal:
+        raise SystemExit("traffic needs both calibration launches (--read-calibration-mb, --copy-calibration-mb)")
+    ent = {}
+    for phase, kname in KERNEL_NAMES.items():
+        k = next((v for n, v in rec["kernels"].items() if n.startswith(kname)), None)
+        if k is None or "read_bytes" not in k or "write_bytes" not in k:
+            continue
+        t = k["read_bytes"] + k["write_bytes"]
+        ent[kname] = {"read_bytes": k["read_bytes"], "write_bytes": k["write_bytes"], "traffic_bytes": t,
+                      "algorithmic_bytes": alg[phase], "traffic_over_algorithmic": round(t / alg[phase], 3),
+                      "dispatches": k["dispatches"]}
+    out = {config: ent, "calibration": {
+        "method": "TCC_EA0_RDREQ / RDREQ_32B / TCC_BUBBLE and TCC_EA0_WRREQ / WRREQ_64B per dispatch, as bytes "
+                  "by FETCH_SIZE's and WRITE_SIZE's request sizes, each scaled by known-size reference launches "
+                  "(pbmoe_stream_read: reads; runtime copy: writes)",
+        "read_scale": round(cal["read_scale"], 4), "write_scale": round(cal["write_scale"], 4),
+        "copy_read_scale": round(cal.get("copy_read_scale", float("nan")), 4)}, "sources": rec["sources"]}
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+        f.write("\n")
+    print(f"[bench] traffic written to {path}", file=sys.stderr)
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16
@@ -521,7 +673,27 @@ def main() -> int:
                     help="also time pbmoe_moe_decode alone (routes fixed)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run a plain device copy of this size (PMC calibration runs)")
+    ap.add_argument("--read-calibration-mb", type=int, default=0,
+                    help="also run pbmoe_stream_read over a buffer of this size (PMC calibration runs)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 PMC output directories instead of benchmarking (no GPU)")
+    ap.add_argument("--pmc-out", help="with --pmc-summary: also write the JSON summary to this file")
+    ap.add_argument("--traffic-out", help="with --pmc-summary over a decode run of --config: write the per-kernel "
+                                          "HBM traffic file that the roofline's traffic field reads")
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        rec = pmc_derive(pmc_collect(args.pmc_summary), args.read_calibration_mb << 20,
+                         args.copy_calibration_mb << 20)
+        rec["sources"] = args.pmc_summary
+        txt = json.dumps(rec, indent=1, sort_keys=True)
+        if args.pmc_out:
+            with open(args.pmc_out, "w") as f:
+                f.write(txt + "\n")
+        print(txt)
+        if args.traffic_out:
+            write_traffic(rec, args.config, args.tokens, args.traffic_out)
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X only: the MoE block is single-GPU in this build "
@@ -684,6 +856,8 @@ def main() -> int:
     }
     if args.copy_calibration_mb:
         copy_calibration(ctx, args.copy_calibration_mb, 3)
+    if args.read_calibration_mb:
+        read_calibration(ctx, args.read_calibration_mb, 3)
     print(json.dumps(rec))
     ctx.close()
     return 0

@@ -206,6 +206,12 @@ int pbmoe_sync(pbmoe_ctx* ctx);
  * 0 router stage, 1 gate/up, 2 down + combine.  Grouped prefill (more than
  * 16 tokens): 0 gate/up GEMM, 1 down GEMM, 2 combine.  count == 0 disables. */
 int pbmoe_set_phase_events(pbmoe_ctx* ctx, void* const* events, uint32_t count);
+/* Measurement reference (no counterpart in the reference): read the device
+ * buffer src[0, bytes) once with one 16-byte load per lane, the access shape
+ * of the decode weight loads, and store the XOR of all its 32-bit words in
+ * the device word *xor_out.  Hardware traffic counters of this launch
+ * calibrate those of the MoE kernels.  bytes: a multiple of 16. */
+int pbmoe_stream_read(pbmoe_ctx* ctx, const void* src, size_t bytes, uint32_t* xor_out);
 int pbmoe_device_alloc(pbmoe_ctx* ctx, size_t bytes, void** dptr);
 int pbmoe_device_free(pbmoe_ctx* ctx, void* dptr);
 int pbmoe_upload(pbmoe_ctx* ctx, void* dst_device, const void* src_host, size_t bytes);

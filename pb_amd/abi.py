@@ -129,6 +129,7 @@ _SIG = {
     "pbmoe_layer_slots": ([_P, _U32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)], C.c_int),
     "pbmoe_bind_router": ([_P, _U32, _P, _U32, _P, _U32], C.c_int),
     "pbmoe_bind_shared": ([_P, _U32, C.POINTER(Q4Layout), _P, _P, _U32, _U32], C.c_int),
+    "pbmoe_stream_read": ([_P, _P, C.c_size_t, _P], C.c_int),
     "pbmoe_bind_router_q4": ([_P, _U32, C.POINTER(Q4Matrix), _U32, _U32, _P, _U32], C.c_int),
     "pbmoe_bind_shared_gate_q4": ([_P, _U32, C.POINTER(Q4Matrix), _U32, _U32, _U32], C.c_int),
     "pbmoe_unbind_layer": ([_P, _U32], C.c_int),

@@ -554,6 +554,20 @@ PBMOE_API int pbmoe_set_phase_events(pbmoe_ctx* ctx, void* const* events, uint32
     return ok();
 }
 
+// Measurement reference: a read stream of known size (see the header).
+PBMOE_API int pbmoe_stream_read(pbmoe_ctx* ctx, const void* src, size_t bytes, uint32_t* xor_out)
+{
+    if (!ctx || !src || !xor_out)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "null argument");
+    if (bytes == 0 || bytes % 16 || !aligned(src, 16) || !aligned(xor_out, 4))
+        return fail(PBMOE_ERR_ALIGNMENT, "stream read needs a 16-byte aligned source of a multiple of 16 bytes");
+    int rc = set_device(ctx);
+    if (rc)
+        return rc;
+    HIP_TRY(pbmoe::launch_stream_read(ctx->stream, src, bytes, xor_out));
+    return ok();
+}
+
 PBMOE_API int pbmoe_device_alloc(pbmoe_ctx* ctx, size_t bytes, void** dptr)
 {
     if (!ctx || !dptr)

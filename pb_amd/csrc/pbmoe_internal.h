@@ -221,6 +221,8 @@ hipError_t launch_synth_center(hipStream_t s, uint8_t* slots, uint64_t stride, c
                                uint32_t hidden, uint32_t intermediate, uint32_t group, uint32_t sb_dtype,
                                uint32_t count);
 hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t value, uint64_t n);
+// XOR of every 32-bit word of src[0, bytes) into *out (bytes a multiple of 16)
+hipError_t launch_stream_read(hipStream_t s, const void* src, uint64_t bytes, uint32_t* out);
 
 // One resident Q4 matrix [rows][cols] (codes, 2-byte scale and bias rows).
 struct Q4Mat {

@@ -675,6 +675,41 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n)
         p[i] = v;
 }
 
+// A plain read stream with the access shape of the decode weight loads: one
+// 16-byte load per lane and step, grid-stride over n16 chunks; the words are
+// XOR-folded (so the loads cannot be dropped) into *out with one atomic per
+// workgroup.  The reference point for the PMC traffic counters.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ src, uint64_t n16,
+                                                          uint32_t* __restrict__ out)
+{
+    __shared__ uint32_t red[4];
+    uint32_t acc = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256) {
+        const uint4 v = src[i];
+        acc ^= (v.x ^ v.y) ^ (v.z ^ v.w);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        atomicXor(out, (red[0] ^ red[1]) ^ (red[2] ^ red[3]));
+}
+
+hipError_t launch_stream_read(hipStream_t s, const void* src, uint64_t bytes, uint32_t* out)
+{
+    fill_u32_kernel<<<1, 64, 0, s>>>(out, 0u, 1);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    const uint64_t n16 = bytes / 16;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>(std::max<uint64_t>((n16 + 255) / 256, 1), 2048);
+    stream_read_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint4*>(src), n16, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t value, uint64_t n)
 {
     uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 1024);

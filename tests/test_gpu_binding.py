@@ -94,3 +94,19 @@ def test_unsupported_intermediate_rejected_at_bind(ctx, inter):
     assert rc == abi.ERR_UNSUPPORTED
     assert b"intermediate" in abi.lib().pbmoe_last_error()
     assert abi.lib().pbmoe_unbind_layer(ctx.handle, 60) == abi.ERR_NOT_BOUND
+
+
+def test_stream_read_xor_of_buffer(ctx):
+    """pbmoe_stream_read (the traffic-counter calibration launch) reads every
+    16-byte chunk: its XOR of all 32-bit words equals the host's; a size that
+    is not a multiple of 16 is refused."""
+    _say("[test] stream read")
+    rng = np.random.default_rng(3)
+    h = rng.integers(0, 2**32, (1 << 20) + 4 * 37, dtype=np.uint32)
+    d = ctx.to_device(h)
+    out = ctx.array(1, np.uint32)
+    L = abi.lib()
+    abi.check(L.pbmoe_stream_read(ctx.handle, d.ptr, h.nbytes, out.ptr))
+    ctx.sync()
+    assert int(out.download()[0]) == int(np.bitwise_xor.reduce(h))
+    assert L.pbmoe_stream_read(ctx.handle, d.ptr, h.nbytes - 4, out.ptr) == abi.ERR_ALIGNMENT
