@@ -477,8 +477,9 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     // the instructions of steps g - 1 and g were all issued after the
     // staging of group g + 1 (the order inside one step is the compiler's).
     constexpr int VMW = (PF - 1) * (DW + NMAT * WL) + (PF >= 2 ? NMAT : 0);
-    auto step = [&](auto lo_tag, uint32_t g, auto b_tag, auto tail_tag, Words& w) {
+    auto step = [&](auto lo_tag, auto tf_tag, uint32_t g, auto b_tag, auto tail_tag, Words& w) {
         constexpr bool LO = decltype(lo_tag)::value; // lo products of the activations
+        constexpr int NTF = decltype(tf_tag)::value; // 32-token fragments holding tokens of the item
         constexpr int NHL = LO ? 2 : 1;
         constexpr int B = decltype(b_tag)::value;    // g % NBUF
         constexpr bool TAIL = decltype(tail_tag)::value;
@@ -514,7 +515,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
             w_load(g + 2, w);
         const uint8_t* xb = lds + B * L::TILE_BYTES;
 #pragma unroll
-        for (int tf = 0; tf < 2; ++tf) {
+        for (int tf = 0; tf < NTF; ++tf) {
             half8_t ah[NSTEP], al[NSTEP];
 #pragma unroll
             for (int k = 0; k < NSTEP; ++k) {
@@ -567,24 +568,35 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    auto iter = [&](auto lo_tag, uint32_t g, auto tail_tag) {
-        step(lo_tag, g, I0{}, tail_tag, w0);
-        step(lo_tag, g + 1, I1{}, tail_tag, w1);
+    auto iter = [&](auto lo_tag, auto tf_tag, uint32_t g, auto tail_tag) {
+        step(lo_tag, tf_tag, g, I0{}, tail_tag, w0);
+        step(lo_tag, tf_tag, g + 1, I1{}, tail_tag, w1);
         if constexpr (NBUF == 4) {
-            step(lo_tag, g + 2, I2{}, tail_tag, w0);
-            step(lo_tag, g + 3, I3{}, tail_tag, w1);
+            step(lo_tag, tf_tag, g + 2, I2{}, tail_tag, w0);
+            step(lo_tag, tf_tag, g + 3, I3{}, tail_tag, w1);
         }
     };
-    auto run = [&](auto lo_tag) {
+    auto run = [&](auto lo_tag, auto tf_tag) {
         uint32_t g = 0;
         for (; g + NBUF < G; g += NBUF) // G is a multiple of NBUF
-            iter(lo_tag, g, std::false_type{});
-        iter(lo_tag, g, std::true_type{});
+            iter(lo_tag, tf_tag, g, std::false_type{});
+        iter(lo_tag, tf_tag, g, std::true_type{});
     };
-    if (tile_lo)
-        run(std::true_type{});
-    else
-        run(std::false_type{});
+    // the last tile of an item often holds at most 32 tokens: the second
+    // fragment's MFMAs, LDS reads and scale FMAs would only produce rows
+    // that are never written
+    const bool two_frag = cnt - n0 > 32;
+    if (tile_lo) {
+        if (two_frag)
+            run(std::true_type{}, I2{});
+        else
+            run(std::true_type{}, I1{});
+    } else {
+        if (two_frag)
+            run(std::false_type{}, I2{});
+        else
+            run(std::false_type{}, I1{});
+    }
     // the last step waited for every load and met the other waves: the
     // staging buffers are free for the epilogue
 
@@ -593,63 +605,76 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     //      the group sums split into f16 hi + lo.  Vector loads through buffer
     //      resources (reads past a row are masked, past the buffer return 0) ----
     const rsrc_t sum_r = make_rsrc(a.b_sum32, a.b_rows * C32 * 4);
-    for (uint32_t k0 = 0; k0 < G; k0 += 16) {
-        const uint32_t gb = k0 + 8 * h; // first group of this lane half
-        half8_t bw[NMAT];
+    // the loads of MAXS slices of 16 groups are issued together (one memory
+    // round trip instead of MAXS); loads of a slice past G read in-bounds
+    // neighbouring data or zeros and are masked below
+    constexpr int MAXS = KS >= 4 ? 1 : 2;
+    for (uint32_t k00 = 0; k00 < G; k00 += 16 * MAXS) {
+        uint32_t b2[MAXS][NMAT][4]; // 8 consecutive 16-bit biases per slice (4-byte aligned: G is even)
+        u32x4 v4[MAXS][2][2 * KS];  // sums per 32 columns of groups gb .. gb + 7
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            uint32_t b2[4]; // 8 consecutive 16-bit biases (4-byte aligned: G is even)
+        for (int sl = 0; sl < MAXS; ++sl) {
+            const uint32_t gb = k00 + 16 * sl + 8 * h; // first group of this lane half
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                b2[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff, b_soff[m] + gb * 2 + 4 * q, 0);
+            for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint16_t raw = (uint16_t)(b2[j / 2] >> (16 * (j & 1)));
-                float bv;
-                if constexpr (SBT == 2)
-                    bv = __uint_as_float((uint32_t)raw << 16);
-                else
-                    bv = __half2float(__ushort_as_half(raw));
-                bw[m][j] = gb + j < G ? (_Float16)bv : (_Float16)0.0f;
+                for (int q = 0; q < 4; ++q)
+                    b2[sl][m][q] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff, b_soff[m] + gb * 2 + 4 * q, 0);
+#pragma unroll
+            for (int tf = 0; tf < 2; ++tf) {
+                const uint32_t brow = row_lds[32 * tf + n32];
+                const uint32_t rrow = brow != 0xFFFFFFFFu ? brow : 0u;
+#pragma unroll
+                for (int q = 0; q < 2 * KS; ++q)
+                    v4[sl][tf][q] = __builtin_amdgcn_raw_buffer_load_b128(sum_r, rrow * C32 * 4, (gb * KS + 4 * q) * 4, 0);
             }
         }
 #pragma unroll
-        for (int tf = 0; tf < 2; ++tf) {
-            const uint32_t brow = row_lds[32 * tf + n32];
-            const bool bvalid = brow != 0xFFFFFFFFu;
-            float sv[8 * KS]; // sums per 32 columns of groups gb .. gb + 7
+        for (int sl = 0; sl < MAXS; ++sl) {
+            const uint32_t gb = k00 + 16 * sl + 8 * h;
+            if (k00 + 16 * sl >= G)
+                break;
+            half8_t bw[NMAT];
 #pragma unroll
-            for (int q = 0; q < 2 * KS; ++q) {
-                const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(sum_r, (bvalid ? brow : 0u) * C32 * 4,
-                                                                       (gb * KS + 4 * q) * 4, 0);
+            for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    sv[4 * q + e] = __uint_as_float(v4[e]);
-            }
-            half8_t xh, xl;
+                for (int j = 0; j < 8; ++j) {
+                    const uint16_t raw = (uint16_t)(b2[sl][m][j / 2] >> (16 * (j & 1)));
+                    float bv;
+                    if constexpr (SBT == 2)
+                        bv = __uint_as_float((uint32_t)raw << 16);
+                    else
+                        bv = __half2float(__ushort_as_half(raw));
+                    bw[m][j] = gb + j < G ? (_Float16)bv : (_Float16)0.0f;
+                }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float v = 0.0f;
+            for (int tf = 0; tf < 2; ++tf) {
+                const bool bvalid = row_lds[32 * tf + n32] != 0xFFFFFFFFu;
+                half8_t xh, xl;
 #pragma unroll
-                for (int c = 0; c < KS; ++c)
-                    v += sv[j * KS + c];
-                if (!bvalid || gb + j >= G)
-                    v = 0.0f;
-                const _Float16 hv = (_Float16)v;
-                xh[j] = hv;
-                xl[j] = (_Float16)(v - (float)hv);
-            }
+                for (int j = 0; j < 8; ++j) {
+                    float v = 0.0f;
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-                float16_t c;
+                    for (int c = 0; c < KS; ++c)
+                        v += __uint_as_float(v4[sl][tf][(j * KS + c) / 4][(j * KS + c) % 4]);
+                    if (!bvalid || gb + j >= G)
+                        v = 0.0f;
+                    const _Float16 hv = (_Float16)v;
+                    xh[j] = hv;
+                    xl[j] = (_Float16)(v - (float)hv);
+                }
 #pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    c[j] = 0.0f;
-                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, bw[m], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, bw[m], c, 0, 0, 0);
+                for (int m = 0; m < NMAT; ++m) {
+                    float16_t c;
 #pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    acc[tf][m][j] += c[j];
+                    for (int j = 0; j < 16; ++j)
+                        c[j] = 0.0f;
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, bw[m], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, bw[m], c, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        acc[tf][m][j] += c[j];
+                }
             }
         }
     }
