@@ -5,6 +5,7 @@ the fp32 oracle (fp64 evaluation deciding where outputs are too large for
 1e-2 to be above f32 rounding)."""
 from __future__ import annotations
 
+import os
 import sys
 
 import numpy as np
@@ -69,11 +70,15 @@ def _prefill(ctx, dl, x, rh, ids, w, norm=None):
     return out.download(), (nn.download() if nn is not None else None)
 
 
+THREADS = max(1, min(16, os.cpu_count() or 1))  # the oracle's OpenMP threads
+
+
 def _check_rows(dl, xh, rh, ids_h, w_h, got, rows, norm_h=None, got_n=None, tag=""):
-    ref_h, ref_n = dl.oracle_block(xh[rows], rh[rows], ids_h[rows], w_h[rows], next_norm=norm_h)
+    ref_h, ref_n = dl.oracle_block(xh[rows], rh[rows], ids_h[rows], w_h[rows], next_norm=norm_h,
+                                   threads=THREADS)
     exact = None
     if np.max(np.abs(ref_h)) > 1e3:
-        exact = dl.exact_block(xh[rows], rh[rows], ids_h[rows], w_h[rows])
+        exact = dl.exact_block(xh[rows], rh[rows], ids_h[rows], w_h[rows], threads=THREADS)
     mx, rel = assert_layer_tolerance(got[rows], ref_h, exact=exact)
     _say(f"[result] prefill {tag}: rows={len(rows)} max_abs={mx:.3e} rel_l2={rel:.3e}")
     if norm_h is not None:
@@ -132,8 +137,7 @@ def test_prefill_tile_boundaries(ctx):
 
 def test_prefill_c3_zipf(ctx):
     """C3: 2048 tokens, Zipf(1.1)-drawn router logits, routed on the device;
-    sampled rows against the oracle (every 16th row plus rows of the most
-    and least loaded experts); a second call is bitwise identical."""
+    every row against the oracle; a second call is bitwise identical."""
     _say("[test] prefill C3 zipf")
     dl = _layer(ctx, C1)
     T = C3.tokens
@@ -150,12 +154,7 @@ def test_prefill_c3_zipf(ctx):
     ids_h, w_h = ids.download().astype(np.int32), w.download()
     counts = np.bincount(ids_h.ravel(), minlength=C3.experts)
     _say(f"[info] C3 expert load max={counts.max()} min={counts.min()} used={np.count_nonzero(counts)}")
-    heavy, light = int(np.argmax(counts)), int(np.argmin(np.where(counts > 0, counts, 1 << 30)))
-    rows = set(range(0, T, 16))
-    rows |= set(np.nonzero((ids_h == light).any(1))[0][:8].tolist())
-    rows |= set(np.nonzero((ids_h == heavy).any(1))[0][-8:].tolist())
-    rows = np.array(sorted(rows))
-    _check_rows(dl, xh, rh, ids_h, w_h, got, rows, tag="C3 zipf")
+    _check_rows(dl, xh, rh, ids_h, w_h, got, np.arange(T), tag="C3 zipf")
 
 
 def test_prefill_c5_shape(ctx):
@@ -172,8 +171,8 @@ def test_prefill_c5_shape(ctx):
 def test_prefill_c5_full_chunk(ctx):
     """C5 at its benchmark size: 1024 tokens through the DeepSeek-V3-shaped
     layer (group-limited sigmoid routing on the device); sampled rows (every
-    64th plus rows of the most and least loaded experts) against the oracle,
-    and a second call bitwise identical."""
+    16th plus rows of the most and least loaded experts) against the oracle
+    and its fp64 evaluation, and a second call bitwise identical."""
     _say("[test] prefill C5 1024 tokens")
     dl = _layer(ctx, C5)
     T = 1024
@@ -185,7 +184,7 @@ def test_prefill_c5_full_chunk(ctx):
     ids_h, w_h = ids.download().astype(np.int32), w.download()
     counts = np.bincount(ids_h.ravel(), minlength=C5.experts)
     heavy, light = int(np.argmax(counts)), int(np.argmin(np.where(counts > 0, counts, 1 << 30)))
-    rows = set(range(0, T, 64))
+    rows = set(range(0, T, 16))
     rows |= set(np.nonzero((ids_h == light).any(1))[0][:4].tolist())
     rows |= set(np.nonzero((ids_h == heavy).any(1))[0][-4:].tolist())
     _check_rows(dl, xh, rh, ids_h, w_h, got, np.array(sorted(rows)), tag="C5 1024")
