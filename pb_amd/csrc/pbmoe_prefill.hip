@@ -469,15 +469,134 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
 
     // Pipeline (the loop is unrolled by NBUF, so buffers and registers have
     // fixed roles).  Step g, buffer g % NBUF: stage group g + PF into buffer
-    // (g + PF) % NBUF, which held group g - 1 (read before the last barrier);
-    // unpack group g's codes from w[g & 1], then load group g + 2's codes into
-    // those registers; the MFMAs; wait until this wave's loads of group
-    // g + 1's tile have landed and meet the other waves at the barrier.  The
-    // last NBUF steps (TAIL) issue no loads past group G - 1.  Wait counts:
-    // the instructions of steps g - 1 and g were all issued after the
-    // staging of group g + 1 (the order inside one step is the compiler's).
+    // (g + PF) % NBUF, which held group g - 1 (read before the last barrier).
+    // The MFMAs of group g use codes unpacked during step g - 1 (wf_cur);
+    // beside them the step unpacks group g + 1's codes (w, into wf_next; then
+    // group g + 3's codes are loaded into w) and applies the group scales to
+    // finished fragments: fragment 0 of group g while fragment 1's MFMAs run,
+    // fragment 1 of group g - 1 while fragment 0's run.  None of that VALU
+    // work depends on the MFMAs beside it, so the wave issues it while the
+    // matrix core works.  Then wait until this wave's loads of group g + 1's
+    // tile have landed and meet the other waves at the barrier.  The last
+    // NBUF steps (TAIL) issue no loads past group G - 1.  Wait counts: the
+    // instructions of steps g - 1 and g were all issued after the staging of
+    // group g + 1 (the order inside one step is the compiler's).
     constexpr int VMW = (PF - 1) * (DW + NMAT * WL) + (PF >= 2 ? NMAT : 0);
-    auto step = [&](auto lo_tag, auto tf_tag, uint32_t g, auto b_tag, auto tail_tag, Words& w) {
+    constexpr bool PIPE = !GATEUP && KS <= 2; // larger groups: the pipeline spills
+    typedef half8_t Unpacked[NMAT][NSTEP];
+    Unpacked wfA, wfB;              // unpacked codes of even / odd groups
+    float16_t pf1[NMAT];             // fragment 1's partial products, scaled one step later
+    float sa_prev[NMAT];            // their group scales
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+        sa_prev[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            pf1[m][j] = 0.0f;
+    }
+    auto unpack_m = [&](Words& w, Unpacked& wf, int m) {
+#pragma unroll
+        for (int k = 0; k < NSTEP; ++k) {
+            // keeps each unpack in its step: without it the compiler hoists
+            // the unpacks of load-free tail steps and spills
+            asm volatile("" : "+v"(w[m][k]));
+            wf[m][k] = unpack8(w[m][k], magic);
+        }
+    };
+    auto step = [&](auto lo_tag, auto tf_tag, uint32_t g, auto b_tag, auto tail_tag, Words& w, Unpacked& wf_cur,
+                    Unpacked& wf_next) {
+        constexpr bool LO = decltype(lo_tag)::value; // lo products of the activations
+        constexpr int NTF = decltype(tf_tag)::value; // 32-token fragments holding tokens of the item
+        constexpr int NHL = LO ? 2 : 1;
+        constexpr int B = decltype(b_tag)::value;    // g % NBUF
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        constexpr bool ST = !TAIL || B + PF < NBUF;  // stage group g + PF
+        constexpr bool UNP = !TAIL || B + 1 < NBUF;  // unpack group g + 1
+        constexpr bool WLD = !TAIL || B + 3 < NBUF;  // codes of group g + 3
+        constexpr bool SLD = B % 2 == 0 && (!TAIL || B + 2 < NBUF); // scales of groups g + 2, g + 3
+        // VMEM instructions of tail step b (b = -1: the steady step before)
+        constexpr auto cnt = [](int b) {
+            if (b < 0)
+                return DW + NMAT * WL;
+            return (b + PF < NBUF ? DW : 0) + (b % 2 == 0 && b + 2 < NBUF ? NMAT : 0) +
+                   (b + 3 < NBUF ? NMAT * WL : 0);
+        };
+        constexpr int WAIT = PF < 2 ? 0 : (TAIL ? cnt(B - 1) + cnt(B) : VMW);
+        if constexpr (ST)
+            stage(g + PF, (B + PF) % NBUF);
+        if constexpr (SLD)
+            s_load(g + 2, spb);
+        float sa[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            sa[m] = s_of(spa[m], g);
+        const uint8_t* xb = lds + B * L::TILE_BYTES;
+        auto mfmas = [&](int tf, float16_t (&p)[NMAT]) {
+            half8_t ah[NSTEP], al[NSTEP];
+#pragma unroll
+            for (int k = 0; k < NSTEP; ++k) {
+                ah[k] = *reinterpret_cast<const half8_t*>(xb + tf * 32 * CH * 16 + rd_off[k][0]);
+                if constexpr (LO)
+                    al[k] = *reinterpret_cast<const half8_t*>(xb + tf * 32 * CH * 16 + rd_off[k][1]);
+            }
+#pragma unroll
+            for (int k = 0; k < NSTEP; ++k)
+#pragma unroll
+                for (int hl = 0; hl < NHL; ++hl)
+#pragma unroll
+                    for (int m = 0; m < NMAT; ++m) {
+                        float16_t c;
+                        if (k == 0 && hl == 0) {
+#pragma unroll
+                            for (int j = 0; j < 16; ++j)
+                                c[j] = 0.0f;
+                        } else {
+                            c = p[m];
+                        }
+                        p[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(hl ? al[k] : ah[k], wf_cur[m][k], c, 0, 0, 0);
+                    }
+        };
+        auto scale = [&](int tf, const float16_t (&p)[NMAT], const float (&s)[NMAT]) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    acc[tf][m][j] = fmaf(s[m], p[m][j], acc[tf][m][j]);
+        };
+        // fragment 0 of group g; beside it: group g + 1's unpack (then the
+        // codes of group g + 3 are loaded into the freed registers) and
+        // fragment 1 of group g - 1
+        float16_t p0[NMAT];
+        mfmas(0, p0);
+        if constexpr (UNP) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+                unpack_m(w, wf_next, m);
+        }
+        if constexpr (WLD)
+            w_load(g + 3, w);
+        if constexpr (NTF == 2) {
+            scale(1, pf1, sa_prev);
+            // fragment 1 of group g; beside it: fragment 0 of group g
+            mfmas(1, pf1);
+        }
+        scale(0, p0, sa);
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            sa_prev[m] = sa[m];
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
+        __syncthreads();
+        if constexpr (B % 2 == 1) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+                spa[m] = spb[m];
+        }
+    };
+    // The same step without the software pipeline (codes of group g unpacked
+    // and scaled within step g), for the gate/up GEMM: the pipeline's extra
+    // live registers (next group's codes, a fragment's partial products
+    // across steps) do not fit beside its two weight matrices.
+    auto step_serial = [&](auto lo_tag, auto tf_tag, uint32_t g, auto b_tag, auto tail_tag, Words& w) {
         constexpr bool LO = decltype(lo_tag)::value; // lo products of the activations
         constexpr int NTF = decltype(tf_tag)::value; // 32-token fragments holding tokens of the item
         constexpr int NHL = LO ? 2 : 1;
@@ -554,13 +673,21 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
                 spa[m] = spb[m];
         }
     };
-    // prologue: the first PF tiles and two groups of codes (G >= NBUF > PF)
+    // prologue: the first PF tiles, group 0's codes unpacked, groups 1 and 2's
+    // codes loaded (G >= NBUF > PF)
 #pragma unroll
     for (int d = 0; d < PF; ++d)
         stage(d, d);
     w_load(0, w0);
     s_load(0, spa);
     w_load(1, w1);
+    if constexpr (PIPE) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            unpack_m(w0, wfA, m);
+        if (G > 2)
+            w_load(2, w0);
+    }
 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -569,11 +696,20 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     auto iter = [&](auto lo_tag, auto tf_tag, uint32_t g, auto tail_tag) {
-        step(lo_tag, tf_tag, g, I0{}, tail_tag, w0);
-        step(lo_tag, tf_tag, g + 1, I1{}, tail_tag, w1);
-        if constexpr (NBUF == 4) {
-            step(lo_tag, tf_tag, g + 2, I2{}, tail_tag, w0);
-            step(lo_tag, tf_tag, g + 3, I3{}, tail_tag, w1);
+        if constexpr (PIPE) {
+            step(lo_tag, tf_tag, g, I0{}, tail_tag, w1, wfA, wfB);
+            step(lo_tag, tf_tag, g + 1, I1{}, tail_tag, w0, wfB, wfA);
+            if constexpr (NBUF == 4) {
+                step(lo_tag, tf_tag, g + 2, I2{}, tail_tag, w1, wfA, wfB);
+                step(lo_tag, tf_tag, g + 3, I3{}, tail_tag, w0, wfB, wfA);
+            }
+        } else {
+            step_serial(lo_tag, tf_tag, g, I0{}, tail_tag, w0);
+            step_serial(lo_tag, tf_tag, g + 1, I1{}, tail_tag, w1);
+            if constexpr (NBUF == 4) {
+                step_serial(lo_tag, tf_tag, g + 2, I2{}, tail_tag, w0);
+                step_serial(lo_tag, tf_tag, g + 3, I3{}, tail_tag, w1);
+            }
         }
     };
     auto run = [&](auto lo_tag, auto tf_tag) {
@@ -581,6 +717,13 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
         for (; g + NBUF < G; g += NBUF) // G is a multiple of NBUF
             iter(lo_tag, tf_tag, g, std::false_type{});
         iter(lo_tag, tf_tag, g, std::true_type{});
+        if constexpr (PIPE && decltype(tf_tag)::value == 2) { // fragment 1 of the last group
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    acc[1][m][j] = fmaf(sa_prev[m], pf1[m][j], acc[1][m][j]);
+        }
     };
     // the last tile of an item often holds at most 32 tokens: the second
     // fragment's MFMAs, LDS reads and scale FMAs would only produce rows
