@@ -973,6 +973,28 @@ PBMOE_API int pbmoe_layer_slots(pbmoe_ctx* ctx, uint32_t layer, const void** slo
     return ok();
 }
 
+// After a failed router / gate bind the old pointers may name freed copies:
+// leave the layer without a router (gate) rather than with a dangling one.
+static void drop_router(pbmoe_ctx* ctx, LayerBinding* b)
+{
+    (void)hipStreamSynchronize(ctx->stream);
+    for (DeviceBuf* o : {&b->router_owned, &b->router_s_owned, &b->router_b_owned})
+        free_buf(*o);
+    b->router = nullptr;
+    b->router_dtype = 0;
+    b->router_q4 = pbmoe::Q4Rows{};
+}
+
+static void drop_gate(pbmoe_ctx* ctx, LayerBinding* b)
+{
+    (void)hipStreamSynchronize(ctx->stream);
+    for (DeviceBuf* o : {&b->gate_owned, &b->gate_s_owned, &b->gate_b_owned})
+        free_buf(*o);
+    b->shared_gate = nullptr;
+    b->shared_gate_dtype = 0;
+    b->gate_q4 = pbmoe::Q4Rows{};
+}
+
 PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weight, uint32_t dtype,
                                 const float* selection_bias, uint32_t flags)
 {
@@ -996,8 +1018,10 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
     const void* dev = nullptr;
     rc = adopt(ctx, weight, (size_t)b->desc.experts * b->desc.hidden * esz, flags, b->router_owned,
                &dev);
-    if (rc)
+    if (rc) {
+        drop_router(ctx, b);
         return rc;
+    }
     b->router = dev;
     b->router_dtype = dtype;
     b->router_q4 = pbmoe::Q4Rows{};
@@ -1015,8 +1039,7 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
 
 // Adopt a Q4 matrix [rows][cols] (codes, then 2-byte scales and biases
 // [rows][cols / group]) into `out`, copying host memory into the owned buffers.
-static int adopt_q4(pbmoe_ctx* ctx, const pbmoe_q4_matrix* m, uint32_t rows, uint32_t cols, uint32_t group,
-                    uint32_t flags, DeviceBuf& oc, DeviceBuf& os, DeviceBuf& ob, pbmoe::Q4Rows* out)
+static int check_q4(const pbmoe_q4_matrix* m, uint32_t cols, uint32_t group, uint32_t flags)
 {
     if (!m->codes || !m->scales || !m->biases)
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "Q4 matrix needs codes, scales and biases");
@@ -1024,8 +1047,17 @@ static int adopt_q4(pbmoe_ctx* ctx, const pbmoe_q4_matrix* m, uint32_t rows, uin
         return fail(PBMOE_ERR_UNSUPPORTED, "Q4 group size %u not one of 32/64/128", group);
     if (cols % group)
         return fail(PBMOE_ERR_SHAPE, "Q4 columns %u not divisible by group size %u", cols, group);
+    if (flags != PBMOE_MEM_HOST && flags != PBMOE_MEM_DEVICE)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "unknown memory flags %u", flags);
     if (flags == PBMOE_MEM_DEVICE && (!aligned(m->codes, 16) || !aligned(m->scales, 2) || !aligned(m->biases, 2)))
         return fail(PBMOE_ERR_ALIGNMENT, "device Q4 codes must be 16-byte and scales/biases 2-byte aligned");
+    return PBMOE_OK;
+}
+
+// (arguments checked by check_q4 first)
+static int adopt_q4(pbmoe_ctx* ctx, const pbmoe_q4_matrix* m, uint32_t rows, uint32_t cols, uint32_t group,
+                    uint32_t flags, DeviceBuf& oc, DeviceBuf& os, DeviceBuf& ob, pbmoe::Q4Rows* out)
+{
     const size_t sb = (size_t)rows * (cols / group) * 2;
     const void *c = nullptr, *sc = nullptr, *bi = nullptr;
     int rc = adopt(ctx, m->codes, (size_t)rows * cols / 2, flags, oc, &c);
@@ -1058,12 +1090,14 @@ PBMOE_API int pbmoe_bind_router_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q
     if (needs_selection_bias(b->desc.routing) && !selection_bias)
         return fail(PBMOE_ERR_INVALID_ARGUMENT,
                     "sigmoid routing requires the per-expert selection bias");
-    if ((rc = set_device(ctx)))
+    if ((rc = check_q4(weight, b->desc.hidden, group_size, flags)) || (rc = set_device(ctx)))
         return rc;
     pbmoe::Q4Rows q{};
     if ((rc = adopt_q4(ctx, weight, b->desc.experts, b->desc.hidden, group_size, flags, b->router_owned,
-                       b->router_s_owned, b->router_b_owned, &q)))
+                       b->router_s_owned, b->router_b_owned, &q))) {
+        drop_router(ctx, b);
         return rc;
+    }
     b->router_q4 = q;
     b->router = q.codes;
     b->router_dtype = pbmoe::DT_Q4;
@@ -1094,12 +1128,14 @@ PBMOE_API int pbmoe_bind_shared_gate_q4(pbmoe_ctx* ctx, uint32_t layer, const pb
     if (scale_bias_dtype != b->layout.scale_bias_dtype)
         return fail(PBMOE_ERR_UNSUPPORTED, "Q4 gate scale/bias dtype %u must match the experts' (%u)",
                     scale_bias_dtype, b->layout.scale_bias_dtype);
-    if ((rc = set_device(ctx)))
+    if ((rc = check_q4(gate, b->desc.hidden, group_size, flags)) || (rc = set_device(ctx)))
         return rc;
     pbmoe::Q4Rows q{};
     if ((rc = adopt_q4(ctx, gate, 1, b->desc.hidden, group_size, flags, b->gate_owned, b->gate_s_owned,
-                       b->gate_b_owned, &q)))
+                       b->gate_b_owned, &q))) {
+        drop_gate(ctx, b);
         return rc;
+    }
     b->gate_q4 = q;
     b->shared_gate = q.codes;
     b->shared_gate_dtype = pbmoe::DT_Q4;

@@ -171,7 +171,7 @@ def test_q4_gate_prefill_matches_oracle(ctx):
 def test_q4_router_bind_errors(ctx):
     """Refusals at bind time: a scale/bias dtype other than the experts', a
     group size the kernels do not take, missing arrays, a gate before the
-    shared expert is bound."""
+    shared expert is bound; a refused bind leaves the router bound before it."""
     _say("[test] q4 router bind errors")
     cfg = C2
     L = abi.lib()
@@ -181,6 +181,8 @@ def test_q4_router_bind_errors(ctx):
     desc = layer_desc(cfg)
     abi.check(L.pbmoe_bind_layer(ctx.handle, 603, C.byref(desc), C.byref(lay), slots.ptr, slots.nbytes,
                                  abi.MEM_DEVICE))
+    dense = ctx.to_device(np.zeros((cfg.experts, cfg.hidden), np.uint16))
+    abi.check(L.pbmoe_bind_router(ctx.handle, 603, dense.ptr, abi.DTYPE_F16, None, abi.MEM_DEVICE))
     codes = ctx.array(cfg.experts * cfg.hidden // 2, np.uint8)
     sb = ctx.array(cfg.experts * cfg.hidden // 32, np.uint16)
     m = abi.Q4Matrix()
@@ -197,6 +199,13 @@ def test_q4_router_bind_errors(ctx):
                                   abi.MEM_DEVICE) == abi.ERR_INVALID_ARGUMENT
     assert L.pbmoe_bind_shared_gate_q4(ctx.handle, 603, C.byref(m), cfg.group, cfg.sb_dtype,
                                        abi.MEM_DEVICE) == abi.ERR_NOT_BOUND
+    # the refusals left the dense router bound: routing still runs
+    x = ctx.to_device(np.ones((1, cfg.hidden), np.float32))
+    ids = ctx.array((1, cfg.k), np.uint32)
+    w = ctx.array((1, cfg.k), np.float32)
+    abi.check(L.pbmoe_route(ctx.handle, 603, x.ptr, 1, ids.ptr, w.ptr, None))
+    ctx.sync()
+    np.testing.assert_array_equal(ids.download()[0], np.arange(cfg.k))  # all-zero logits: the lowest ids
     abi.check(L.pbmoe_bind_router_q4(ctx.handle, 603, C.byref(m), cfg.group, cfg.sb_dtype, None,
                                      abi.MEM_DEVICE))
     abi.check(L.pbmoe_unbind_layer(ctx.handle, 603))
