@@ -1168,13 +1168,19 @@ PBMOE_API int pbmoe_bind_shared(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_l
     rc = set_device(ctx);
     if (rc)
         return rc;
+    // from here on the old shared expert may be freed: until the bind
+    // completes the layer has none (a failure leaves it that way)
+    b->has_shared = false;
     const void* dev = nullptr;
     rc = adopt(ctx, shared_slot, sl->expert_bytes, flags, b->shared_owned, &dev);
-    if (rc)
+    if (rc) {
+        b->shared_slot = nullptr;
+        drop_gate(ctx, b);
         return rc;
+    }
     b->shared_layout = *sl;
     b->shared_slot = static_cast<const uint8_t*>(dev);
-    b->shared_gate = nullptr;
+    drop_gate(ctx, b); // a gate bound before, dense or Q4
     if (b->desc.shared_gated && gate_weight) {
         size_t esz = gate_dtype == PBMOE_DTYPE_F32 ? 4 : 2;
         rc = adopt(ctx, gate_weight, (size_t)b->desc.hidden * esz, flags, b->gate_owned, &dev);
@@ -1183,9 +1189,6 @@ PBMOE_API int pbmoe_bind_shared(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q4_l
         b->shared_gate = dev;
         b->shared_gate_dtype = gate_dtype;
     }
-    b->gate_q4 = pbmoe::Q4Rows{};
-    free_buf(b->gate_s_owned); // a Q4 gate bound before (the stream was synchronised by adopt)
-    free_buf(b->gate_b_owned);
     b->has_shared = true;
     return ok();
 }
