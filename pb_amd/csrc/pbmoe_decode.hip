@@ -638,25 +638,43 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
     const ExpertSet& ex = a.ex;
     const uint8_t* slot = ex.base + (uint64_t)e * ex.stride;
     const uint32_t chunks = H / 32, gpr = H >> ex.group_shift;
+    // Every weight load is issued before anything waits on them: no load
+    // sits in a branch (a load inside a divergent branch is waited on at the
+    // branch's end); lanes past the row's last chunk load that chunk again
+    // and do not use it.
     uint4 wg[RPW][CPL], wu[RPW][CPL];
-    float sg[RPW][CPL], bg[RPW][CPL], su[RPW][CPL], bu[RPW][CPL];
+    uint32_t sgr[RPW][CPL], bgr[RPW][CPL], sur[RPW][CPL], bur[RPW][CPL]; // raw 16-bit scale / bias
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const uint32_t row = row0 + r;
         const uint4* gw = reinterpret_cast<const uint4*>(slot + ex.gate.w_off + (uint64_t)row * (H / 2));
         const uint4* uw = reinterpret_cast<const uint4*>(slot + ex.up.w_off + (uint64_t)row * (H / 2));
+        const uint16_t* gs = reinterpret_cast<const uint16_t*>(slot + ex.gate.s_off) + (uint64_t)row * gpr;
+        const uint16_t* gb = reinterpret_cast<const uint16_t*>(slot + ex.gate.b_off) + (uint64_t)row * gpr;
+        const uint16_t* us = reinterpret_cast<const uint16_t*>(slot + ex.up.s_off) + (uint64_t)row * gpr;
+        const uint16_t* ub = reinterpret_cast<const uint16_t*>(slot + ex.up.b_off) + (uint64_t)row * gpr;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const uint32_t ch = lane + WAVE * c;
-            if (ch < chunks) {
-                wg[r][c] = gw[ch];
-                wu[r][c] = uw[ch];
-                const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> ex.group_shift);
-                sg[r][c] = sb_at<SBT>(slot + ex.gate.s_off, gi);
-                bg[r][c] = sb_at<SBT>(slot + ex.gate.b_off, gi);
-                su[r][c] = sb_at<SBT>(slot + ex.up.s_off, gi);
-                bu[r][c] = sb_at<SBT>(slot + ex.up.b_off, gi);
-            }
+            const uint32_t ch = min(lane + WAVE * c, chunks - 1);
+            const uint32_t g = (ch * 32u) >> ex.group_shift;
+            wg[r][c] = gw[ch];
+            wu[r][c] = uw[ch];
+            sgr[r][c] = gs[g];
+            bgr[r][c] = gb[g];
+            sur[r][c] = us[g];
+            bur[r][c] = ub[g];
+        }
+    }
+    // one chunk per lane (CPL 1): the first token's activations are loaded
+    // with the weights (more chunks would not fit the registers)
+    float x0[CPL == 1 ? 32 : 1];
+    if constexpr (CPL == 1) {
+        const uint32_t tok = use_plan ? s.src_rows[g0] : g0 / K;
+        const float4* x4 = reinterpret_cast<const float4*>(a.x + (uint64_t)tok * H + min((uint32_t)lane, chunks - 1) * 32);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 v = x4[q];
+            x0[4 * q] = v.x, x0[4 * q + 1] = v.y, x0[4 * q + 2] = v.z, x0[4 * q + 3] = v.w;
         }
     }
     for (uint32_t j = 0; j < n; ++j) {
@@ -680,14 +698,20 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const uint32_t ch = lane + WAVE * c;
-            if (ch < chunks) {
+            float xv[32];
+            if (CPL == 1 && j == 0) {
+#pragma unroll
+                for (int q = 0; q < 32; ++q)
+                    xv[q] = x0[CPL == 1 ? q : 0];
+            } else if (ch < chunks) {
                 const float4* x4 = reinterpret_cast<const float4*>(xt + ch * 32);
-                float xv[32];
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     const float4 v = x4[q];
                     xv[4 * q] = v.x, xv[4 * q + 1] = v.y, xv[4 * q + 2] = v.z, xv[4 * q + 3] = v.w;
                 }
+            }
+            if (ch < chunks) {
                 float xs = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 32; q += 4)
@@ -696,8 +720,8 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
                 for (int r = 0; r < RPW; ++r) {
                     const float qg = q4_chunk_qx_reg(wg[r][c], xv);
                     const float qu = q4_chunk_qx_reg(wu[r][c], xv);
-                    pg[r] = fmaf(sg[r][c], qg, fmaf(bg[r][c], xs, pg[r]));
-                    pu[r] = fmaf(su[r][c], qu, fmaf(bu[r][c], xs, pu[r]));
+                    pg[r] = fmaf(sb_bits<SBT>(sgr[r][c]), qg, fmaf(sb_bits<SBT>(bgr[r][c]), xs, pg[r]));
+                    pu[r] = fmaf(sb_bits<SBT>(sur[r][c]), qu, fmaf(sb_bits<SBT>(bur[r][c]), xs, pu[r]));
                 }
             }
         }
@@ -760,36 +784,27 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     const uint32_t row_base = blockIdx.x * R;
     const uint32_t T = a.tokens, K = a.k;
     const uint32_t I = a.ex.down.cols;
-    const uint32_t gpr = I >> a.ex.group_shift;
     const uint32_t routes = T * K;
 
-    // loads that do not depend on the routes: residual for the combine and
-    // (direct mode) every route's activations
-    float res_v = 0.0f;
-    if (threadIdx.x < T * R)
-        res_v = a.residual[(uint64_t)(threadIdx.x / R) * a.hidden + row_base + threadIdx.x % R];
-    if (stage) {
-        const uint32_t n4 = (routes * I) / 4;
-        const float4* src = reinterpret_cast<const float4*>(a.act);
-        for (uint32_t i = threadIdx.x; i < n4; i += 256)
-            *reinterpret_cast<float4*>(&astage[(i >> 3) * XP + (i & 7) * 4]) = src[i];
-        if (a.has_shared) {
-            const uint32_t m4 = (T * I) / 4;
-            const float4* s2 = reinterpret_cast<const float4*>(a.act_shared);
-            for (uint32_t i = threadIdx.x; i < m4; i += 256) {
-                const uint32_t d = n4 + i; // I % 32 == 0: the shared rows start on a chunk
-                *reinterpret_cast<float4*>(&astage[(d >> 3) * XP + (d & 7) * 4]) = s2[i];
-            }
-        }
-    }
+    // Load order.  Every load below is issued before anything waits on it,
+    // and none sits in a branch (a load inside a divergent branch is waited
+    // on at the branch's end): the residual, the expert id of each unit (the
+    // previous kernel's routes), the activations to stage (direct mode),
+    // then the weights, whose addresses need the ids; the staged
+    // activations are stored to LDS while the weights are in flight.  Loads
+    // of units and chunks that do not exist read a fixed valid address.
+    const uint32_t ri = min((uint32_t)threadIdx.x, T * R - 1); // lanes >= T * R do not use it
+    const float res_v = a.residual[(uint64_t)(ri / R) * a.hidden + row_base + ri % R];
     const uint32_t n_routed = a.use_plan ? a.plan.unique_count[0] : routes;
     const uint32_t n_items = n_routed + (a.has_shared ? 1u : 0u);
     const uint32_t n_units = n_items * R;
+    const uint32_t* id_src = a.use_plan ? a.plan.unique_ids : a.ids;
+    const uint32_t gsh_e = a.ex.group_shift, gsh_s = a.has_shared ? a.sh.group_shift : gsh_e;
 
     for (uint32_t u0 = 0; u0 < n_units; u0 += SLOTS * MAXR) {
         uint4 w[MAXR][CPL];
-        float sc[MAXR][CPL], bi[MAXR][CPL];
-        uint32_t it[MAXR], rw[MAXR];
+        uint32_t scr[MAXR][CPL], bir[MAXR][CPL]; // raw 16-bit scale / bias, converted where used
+        uint32_t it[MAXR], rw[MAXR], eid[MAXR];
         bool live[MAXR];
 #pragma unroll
         for (int m = 0; m < MAXR; ++m) {
@@ -797,33 +812,62 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             live[m] = unit < n_units;
             it[m] = unit / R;
             rw[m] = unit % R;
-            if (!live[m])
-                continue;
-            const bool shared = a.has_shared && it[m] == n_routed;
-            const ExpertSet& set = shared ? a.sh : a.ex;
-            const uint8_t* slot;
-            if (shared) {
-                slot = a.sh.base;
-            } else {
-                const uint32_t e = a.use_plan ? a.plan.unique_ids[it[m]] : a.ids[it[m]];
-                if (e >= a.ex.count) {
-                    live[m] = false;
-                    continue;
-                }
-                slot = a.ex.base + (uint64_t)e * a.ex.stride;
+            eid[m] = id_src[min(it[m], n_routed > 0 ? n_routed - 1 : 0u)];
+        }
+        constexpr int NST = STG ? STAGE_FLOATS / 4 / 256 : 1;
+        float4 stv[NST];
+        uint32_t n4 = 0, n_st = 0;
+        if (stage && u0 == 0) {
+            n4 = (routes * I) / 4;
+            n_st = n4 + (a.has_shared ? (T * I) / 4 : 0u);
+        }
+        if constexpr (STG) {
+#pragma unroll
+            for (int q = 0; q < NST; ++q) {
+                // (passes that stage nothing read a.act[0])
+                const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
+                // I % 32 == 0: the shared rows start on a chunk
+                const float4* src = i < n4 || n_st == 0 ? reinterpret_cast<const float4*>(a.act) + i
+                                                        : reinterpret_cast<const float4*>(a.act_shared) + (i - n4);
+                stv[q] = *src;
             }
+        }
+#pragma unroll
+        for (int m = 0; m < MAXR; ++m) {
+            const bool shared = a.has_shared && it[m] == n_routed;
+            if (!shared && eid[m] >= a.ex.count)
+                live[m] = false;
+            const bool ok = live[m];
+            // per-field selects between the two sets (kernel arguments)
+            const uint8_t* slot = shared ? a.sh.base : a.ex.base + (uint64_t)(ok ? eid[m] : 0u) * a.ex.stride;
+            const uint64_t w_off = shared ? a.sh.down.w_off : a.ex.down.w_off;
+            const uint64_t s_off = shared ? a.sh.down.s_off : a.ex.down.s_off;
+            const uint64_t b_off = shared ? a.sh.down.b_off : a.ex.down.b_off;
+            const uint32_t gsh = shared ? gsh_s : gsh_e;
             const uint32_t row = row_base + rw[m];
-            const uint4* dw = reinterpret_cast<const uint4*>(slot + set.down.w_off + (uint64_t)row * (I / 2));
+            const uint8_t* dw = slot + w_off + (uint64_t)row * (I / 2);
+            const uint16_t* sp = reinterpret_cast<const uint16_t*>(slot + s_off) + (uint64_t)row * (I >> gsh);
+            const uint16_t* bp = reinterpret_cast<const uint16_t*>(slot + b_off) + (uint64_t)row * (I >> gsh);
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 const uint32_t ch = gl + LPR * c;
-                w[m][c] = dw[ch];
-                const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> set.group_shift);
-                sc[m][c] = sb_at<SBT>(slot + set.down.s_off, gi);
-                bi[m][c] = sb_at<SBT>(slot + set.down.b_off, gi);
+                const uint32_t g = (ch * 32u) >> gsh;
+                w[m][c] = *reinterpret_cast<const uint4*>(ok ? dw + ch * 16u : a.ex.base);
+                scr[m][c] = *(ok ? sp + g : reinterpret_cast<const uint16_t*>(a.ex.base));
+                bir[m][c] = *(ok ? bp + g : reinterpret_cast<const uint16_t*>(a.ex.base));
             }
         }
         if (stage && u0 == 0) {
+            if constexpr (STG) {
+#pragma unroll
+                for (int q = 0; q < NST; ++q) {
+                    // no branch: elements past n_st go to the never-read
+                    // padding of the last chunk
+                    const uint32_t i = threadIdx.x + 256u * q;
+                    const uint32_t d = i < n_st ? (i >> 3) * XP + (i & 7) * 4 : (STAGE_FLOATS / 32 - 1) * XP + 32;
+                    *reinterpret_cast<float4*>(&astage[d]) = stv[q];
+                }
+            }
             __syncthreads(); // staged activations visible
             const uint32_t n_chunks = (routes + (a.has_shared ? T : 0u)) * (I / 32);
             for (uint32_t q = threadIdx.x; q < n_chunks; q += 256) {
@@ -838,6 +882,14 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
             __syncthreads();
         }
+        float sc[MAXR][CPL], bi[MAXR][CPL];
+#pragma unroll
+        for (int m = 0; m < MAXR; ++m)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                sc[m][c] = sb_bits<SBT>(scr[m][c]);
+                bi[m][c] = sb_bits<SBT>(bir[m][c]);
+            }
         if (ONE || (!STG && !a.use_plan)) {
             // one token, activations read from L2: every unit's loads in one
             // straight-line block (no token loop between them), so that they

@@ -123,14 +123,20 @@ __device__ __forceinline__ float route_prob(uint32_t kind, float l)
 }
 __device__ __forceinline__ float fast_sigmoid(float l) { return 1.0f / (1.0f + __expf(-l)); }
 
+// a 16-bit scale/bias value (SBT 2: bf16, else f16) as f32
+template <int SBT>
+__device__ __forceinline__ float sb_bits(uint32_t v)
+{
+    if constexpr (SBT == 2)
+        return __uint_as_float(v << 16);
+    else
+        return __half2float(__ushort_as_half((uint16_t)v));
+}
+
 template <int SBT>
 __device__ __forceinline__ float sb_at(const uint8_t* base, uint64_t i)
 {
-    uint16_t v = reinterpret_cast<const uint16_t*>(base)[i];
-    if constexpr (SBT == 2)
-        return __uint_as_float((uint32_t)v << 16);
-    else
-        return __half2float(__ushort_as_half(v));
+    return sb_bits<SBT>(reinterpret_cast<const uint16_t*>(base)[i]);
 }
 
 // One 16-byte chunk = 32 nibbles (columns 32c .. 32c+31, all in one quant
