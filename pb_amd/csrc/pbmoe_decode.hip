@@ -665,10 +665,12 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
             bur[r][c] = ub[g];
         }
     }
-    // one chunk per lane (CPL 1): the first token's activations are loaded
-    // with the weights (more chunks would not fit the registers)
-    float x0[CPL == 1 ? 32 : 1];
-    if constexpr (CPL == 1) {
+    // one chunk per lane and two rows (X0): the first token's activations
+    // are loaded with the weights (with more chunks or rows the registers
+    // would cost waves per SIMD)
+    constexpr bool X0 = CPL == 1 && RPW == 2;
+    float x0[X0 ? 32 : 1];
+    if constexpr (X0) {
         const uint32_t tok = use_plan ? s.src_rows[g0] : g0 / K;
         const float4* x4 = reinterpret_cast<const float4*>(a.x + (uint64_t)tok * H + min((uint32_t)lane, chunks - 1) * 32);
 #pragma unroll
@@ -699,10 +701,10 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
         for (int c = 0; c < CPL; ++c) {
             const uint32_t ch = lane + WAVE * c;
             float xv[32];
-            if (CPL == 1 && j == 0) {
+            if (X0 && j == 0) {
 #pragma unroll
                 for (int q = 0; q < 32; ++q)
-                    xv[q] = x0[CPL == 1 ? q : 0];
+                    xv[q] = x0[X0 ? q : 0];
             } else if (ch < chunks) {
                 const float4* x4 = reinterpret_cast<const float4*>(xt + ch * 32);
 #pragma unroll
@@ -718,8 +720,8 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
                     xs += (xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3]);
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
-                    const float qg = q4_chunk_qx_reg(wg[r][c], xv);
-                    const float qu = q4_chunk_qx_reg(wu[r][c], xv);
+                    const float qg = q4_chunk_qx_reg<RPW * CPL <= 2>(wg[r][c], xv);
+                    const float qu = q4_chunk_qx_reg<RPW * CPL <= 2>(wu[r][c], xv);
                     pg[r] = fmaf(sb_bits<SBT>(sgr[r][c]), qg, fmaf(sb_bits<SBT>(bgr[r][c]), xs, pg[r]));
                     pu[r] = fmaf(sb_bits<SBT>(sur[r][c]), qu, fmaf(sb_bits<SBT>(bur[r][c]), xs, pu[r]));
                 }

@@ -139,6 +139,21 @@ __device__ __forceinline__ float sb_at(const uint8_t* base, uint64_t i)
     return sb_bits<SBT>(reinterpret_cast<const uint16_t*>(base)[i]);
 }
 
+// The 8 nibbles of a code word as floats, nibble j (columns j) in f[j]: the
+// even and odd nibbles are masked into bytes, and each byte converts with
+// one v_cvt_f32_ubyte{0..3} (2 + 8 instructions per word instead of a
+// bit-field extract and a conversion per nibble).
+__device__ __forceinline__ void q4_word_to_float(uint32_t q, float (&f)[8])
+{
+    uint32_t e = q & 0x0F0F0F0Fu, o = (q >> 4) & 0x0F0F0F0Fu;
+    // opaque: otherwise the two masks fold into a 4-bit extract per nibble
+    asm("" : "+v"(e), "+v"(o));
+    f[0] = (float)(e & 0xFFu), f[2] = (float)((e >> 8) & 0xFFu);
+    f[4] = (float)((e >> 16) & 0xFFu), f[6] = (float)(e >> 24);
+    f[1] = (float)(o & 0xFFu), f[3] = (float)((o >> 8) & 0xFFu);
+    f[5] = (float)((o >> 16) & 0xFFu), f[7] = (float)(o >> 24);
+}
+
 // One 16-byte chunk = 32 nibbles (columns 32c .. 32c+31, all in one quant
 // group since the group size is a multiple of 32).  Returns sum(q * x) and
 // sum(x): row = sum over chunks of s * sum(q*x) + b * sum(x).
@@ -151,15 +166,16 @@ __device__ __forceinline__ float q4_chunk_qx(uint4 w, const float* __restrict__ 
     for (int i = 0; i < 4; ++i) {
         const float4 a = x4[2 * i];
         const float4 b = x4[2 * i + 1];
-        const uint32_t q = words[i];
-        qx0 = fmaf((float)(q & 15u), a.x, qx0);
-        qx1 = fmaf((float)((q >> 4) & 15u), a.y, qx1);
-        qx0 = fmaf((float)((q >> 8) & 15u), a.z, qx0);
-        qx1 = fmaf((float)((q >> 12) & 15u), a.w, qx1);
-        qx0 = fmaf((float)((q >> 16) & 15u), b.x, qx0);
-        qx1 = fmaf((float)((q >> 20) & 15u), b.y, qx1);
-        qx0 = fmaf((float)((q >> 24) & 15u), b.z, qx0);
-        qx1 = fmaf((float)(q >> 28), b.w, qx1);
+        float f[8];
+        q4_word_to_float(words[i], f);
+        qx0 = fmaf(f[0], a.x, qx0);
+        qx1 = fmaf(f[1], a.y, qx1);
+        qx0 = fmaf(f[2], a.z, qx0);
+        qx1 = fmaf(f[3], a.w, qx1);
+        qx0 = fmaf(f[4], b.x, qx0);
+        qx1 = fmaf(f[5], b.y, qx1);
+        qx0 = fmaf(f[6], b.z, qx0);
+        qx1 = fmaf(f[7], b.w, qx1);
         sx += ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
     }
     xs = sx;
@@ -176,35 +192,50 @@ __device__ __forceinline__ float q4_chunk_q(uint4 w, const float* __restrict__ x
     for (int i = 0; i < 4; ++i) {
         const float4 a = x4[2 * i];
         const float4 b = x4[2 * i + 1];
-        const uint32_t q = words[i];
-        qx0 = fmaf((float)(q & 15u), a.x, qx0);
-        qx1 = fmaf((float)((q >> 4) & 15u), a.y, qx1);
-        qx0 = fmaf((float)((q >> 8) & 15u), a.z, qx0);
-        qx1 = fmaf((float)((q >> 12) & 15u), a.w, qx1);
-        qx0 = fmaf((float)((q >> 16) & 15u), b.x, qx0);
-        qx1 = fmaf((float)((q >> 20) & 15u), b.y, qx1);
-        qx0 = fmaf((float)((q >> 24) & 15u), b.z, qx0);
-        qx1 = fmaf((float)(q >> 28), b.w, qx1);
+        float f[8];
+        q4_word_to_float(words[i], f);
+        qx0 = fmaf(f[0], a.x, qx0);
+        qx1 = fmaf(f[1], a.y, qx1);
+        qx0 = fmaf(f[2], a.z, qx0);
+        qx1 = fmaf(f[3], a.w, qx1);
+        qx0 = fmaf(f[4], b.x, qx0);
+        qx1 = fmaf(f[5], b.y, qx1);
+        qx0 = fmaf(f[6], b.z, qx0);
+        qx1 = fmaf(f[7], b.w, qx1);
     }
     return qx0 + qx1;
 }
 
-// Same with the 32 x values already in registers.
+// Same with the 32 x values already in registers.  BYTES = false converts
+// each nibble with its own bit-field extract: more instructions, fewer live
+// registers (kernels holding many chunks of codes per lane keep their
+// waves per SIMD).
+template <bool BYTES = true>
 __device__ __forceinline__ float q4_chunk_qx_reg(uint4 w, const float (&xv)[32])
 {
     float qx0 = 0.0f, qx1 = 0.0f;
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t q = words[i];
-        qx0 = fmaf((float)(q & 15u), xv[8 * i + 0], qx0);
-        qx1 = fmaf((float)((q >> 4) & 15u), xv[8 * i + 1], qx1);
-        qx0 = fmaf((float)((q >> 8) & 15u), xv[8 * i + 2], qx0);
-        qx1 = fmaf((float)((q >> 12) & 15u), xv[8 * i + 3], qx1);
-        qx0 = fmaf((float)((q >> 16) & 15u), xv[8 * i + 4], qx0);
-        qx1 = fmaf((float)((q >> 20) & 15u), xv[8 * i + 5], qx1);
-        qx0 = fmaf((float)((q >> 24) & 15u), xv[8 * i + 6], qx0);
-        qx1 = fmaf((float)(q >> 28), xv[8 * i + 7], qx1);
+        if constexpr (BYTES) {
+            float f[8];
+            q4_word_to_float(words[i], f);
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                qx0 = fmaf(f[j], xv[8 * i + j], qx0);
+                qx1 = fmaf(f[j + 1], xv[8 * i + j + 1], qx1);
+            }
+        } else {
+            const uint32_t q = words[i];
+            qx0 = fmaf((float)(q & 15u), xv[8 * i + 0], qx0);
+            qx1 = fmaf((float)((q >> 4) & 15u), xv[8 * i + 1], qx1);
+            qx0 = fmaf((float)((q >> 8) & 15u), xv[8 * i + 2], qx0);
+            qx1 = fmaf((float)((q >> 12) & 15u), xv[8 * i + 3], qx1);
+            qx0 = fmaf((float)((q >> 16) & 15u), xv[8 * i + 4], qx0);
+            qx1 = fmaf((float)((q >> 20) & 15u), xv[8 * i + 5], qx1);
+            qx0 = fmaf((float)((q >> 24) & 15u), xv[8 * i + 6], qx0);
+            qx1 = fmaf((float)(q >> 28), xv[8 * i + 7], qx1);
+        }
     }
     return qx0 + qx1;
 }
