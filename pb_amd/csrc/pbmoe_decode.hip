@@ -778,6 +778,9 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     constexpr int SLOTS = 256 / LPR;
     __shared__ float ylds[DEC_ROUTES][R];
     __shared__ float yshl[DEC_T][R];
+    __shared__ float c_w[DEC_ROUTES];    // combine inputs, loaded at the start
+    __shared__ uint32_t c_oi[DEC_ROUTES];
+    __shared__ float c_sw[DEC_T];
     __shared__ __align__(16) float astage[STG ? STAGE_FLOATS / 32 * XP : 4];
     __shared__ float xsl[STG ? STAGE_FLOATS / 32 : 4]; // per-chunk sums of the staged activations
     const bool stage = STG && a.stage;
@@ -796,13 +799,28 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     // activations are stored to LDS while the weights are in flight.  Loads
     // of units and chunks that do not exist read a fixed valid address.
     const uint32_t ri = min((uint32_t)threadIdx.x, T * R - 1); // lanes >= T * R do not use it
-    const float res_v = a.residual[(uint64_t)(ri / R) * a.hidden + row_base + ri % R];
+    const uint32_t rq = min((uint32_t)threadIdx.x, routes - 1), tq = min((uint32_t)threadIdx.x, T - 1);
+    // residual, and the combine's route weights, output slots and shared gate
+    // logits (each thread one route, routes <= 256, and one token): loaded
+    // in every pass right after the expert ids, not at the end where they
+    // would cost a round trip, and not before the pass loop, whose header
+    // would wait for them
+    float res_v = 0.0f, cw_v = 0.0f, csl_v = 0.0f;
+    uint32_t coi_v = 0;
     const uint32_t n_routed = a.use_plan ? a.plan.unique_count[0] : routes;
     const uint32_t n_items = n_routed + (a.has_shared ? 1u : 0u);
     const uint32_t n_units = n_items * R;
     const uint32_t* id_src = a.use_plan ? a.plan.unique_ids : a.ids;
     const uint32_t gsh_e = a.ex.group_shift, gsh_s = a.has_shared ? a.sh.group_shift : gsh_e;
 
+    // the fields of both sets as plain values (selected per unit below;
+    // selecting through the argument struct would load them per lane)
+    const uint8_t* const ex_base = a.ex.base;
+    const uint64_t ex_stride = a.ex.stride;
+    const uint32_t ex_count = a.ex.count;
+    const uint64_t ex_w = a.ex.down.w_off, ex_s = a.ex.down.s_off, ex_b = a.ex.down.b_off;
+    const uint8_t* const sh_base = a.has_shared ? a.sh.base : ex_base;
+    const uint64_t sh_w = a.sh.down.w_off, sh_s = a.sh.down.s_off, sh_b = a.sh.down.b_off;
     for (uint32_t u0 = 0; u0 < n_units; u0 += SLOTS * MAXR) {
         uint4 w[MAXR][CPL];
         uint32_t scr[MAXR][CPL], bir[MAXR][CPL]; // raw 16-bit scale / bias, converted where used
@@ -814,8 +832,12 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             live[m] = unit < n_units;
             it[m] = unit / R;
             rw[m] = unit % R;
-            eid[m] = id_src[min(it[m], n_routed > 0 ? n_routed - 1 : 0u)];
+            eid[m] = id_src[min(it[m], routes - 1)]; // n_routed <= routes
         }
+        res_v = a.residual[(uint64_t)(ri / R) * a.hidden + row_base + ri % R];
+        cw_v = a.weights[rq];
+        coi_v = (a.use_plan ? a.plan.out_idx : a.ids)[rq];
+        csl_v = (a.has_shared ? a.shared_logit : a.weights)[tq];
         constexpr int NST = STG ? STAGE_FLOATS / 4 / 256 : 1;
         float4 stv[NST];
         uint32_t n4 = 0, n_st = 0;
@@ -837,14 +859,13 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 #pragma unroll
         for (int m = 0; m < MAXR; ++m) {
             const bool shared = a.has_shared && it[m] == n_routed;
-            if (!shared && eid[m] >= a.ex.count)
+            if (!shared && eid[m] >= ex_count)
                 live[m] = false;
             const bool ok = live[m];
-            // per-field selects between the two sets (kernel arguments)
-            const uint8_t* slot = shared ? a.sh.base : a.ex.base + (uint64_t)(ok ? eid[m] : 0u) * a.ex.stride;
-            const uint64_t w_off = shared ? a.sh.down.w_off : a.ex.down.w_off;
-            const uint64_t s_off = shared ? a.sh.down.s_off : a.ex.down.s_off;
-            const uint64_t b_off = shared ? a.sh.down.b_off : a.ex.down.b_off;
+            const uint8_t* slot = shared ? sh_base : ex_base + (uint64_t)(ok ? eid[m] : 0u) * ex_stride;
+            const uint64_t w_off = shared ? sh_w : ex_w;
+            const uint64_t s_off = shared ? sh_s : ex_s;
+            const uint64_t b_off = shared ? sh_b : ex_b;
             const uint32_t gsh = shared ? gsh_s : gsh_e;
             const uint32_t row = row_base + rw[m];
             const uint8_t* dw = slot + w_off + (uint64_t)row * (I / 2);
@@ -854,9 +875,9 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             for (int c = 0; c < CPL; ++c) {
                 const uint32_t ch = gl + LPR * c;
                 const uint32_t g = (ch * 32u) >> gsh;
-                w[m][c] = *reinterpret_cast<const uint4*>(ok ? dw + ch * 16u : a.ex.base);
-                scr[m][c] = *(ok ? sp + g : reinterpret_cast<const uint16_t*>(a.ex.base));
-                bir[m][c] = *(ok ? bp + g : reinterpret_cast<const uint16_t*>(a.ex.base));
+                w[m][c] = *reinterpret_cast<const uint4*>(ok ? dw + ch * 16u : ex_base);
+                scr[m][c] = *(ok ? sp + g : reinterpret_cast<const uint16_t*>(ex_base));
+                bir[m][c] = *(ok ? bp + g : reinterpret_cast<const uint16_t*>(ex_base));
             }
         }
         if (stage && u0 == 0) {
@@ -979,23 +1000,29 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             }
         }
         }
-    }
+        }
     if (stage && n_units == 0) {
         __syncthreads();
         __syncthreads();
     }
+    if (threadIdx.x < routes) {
+        c_w[threadIdx.x] = cw_v;
+        c_oi[threadIdx.x] = a.use_plan ? coi_v : threadIdx.x;
+    }
+    if (threadIdx.x < T)
+        c_sw[threadIdx.x] = a.has_shared ? sigmoidf_(csl_v) : 0.0f;
     __syncthreads();
     if (threadIdx.x < T * R) {
         const uint32_t t = threadIdx.x / R, r = threadIdx.x % R;
         float moe = 0.0f;
         for (uint32_t kk = 0; kk < K; ++kk) {
             const uint32_t route = t * K + kk;
-            const uint32_t gi = a.use_plan ? a.plan.out_idx[route] : route;
+            const uint32_t gi = c_oi[route];
             const float y = gi < DEC_ROUTES ? ylds[gi][r] : 0.0f;
-            moe = moe + a.weights[route] * y;
+            moe = moe + c_w[route] * y;
         }
         const float rm = res_v + moe;
-        const float sw = a.has_shared ? sigmoidf_(a.shared_logit[t]) : 0.0f;
+        const float sw = c_sw[t];
         const float sv = a.has_shared ? yshl[t][r] : 0.0f;
         a.hidden_out[(uint64_t)t * a.hidden + row_base + r] = rm + sw * sv;
     }
