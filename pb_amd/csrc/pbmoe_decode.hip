@@ -1028,6 +1028,162 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     }
 }
 
+// ---------------------------------------------------------------------------
+// kernel 3, wide variant: one token whose routed + shared activations are
+// too large for the staging buffer of down_combine_kernel (C5: 9 items x
+// 2048 columns).  WIDE_R = 16 output rows per workgroup, so that one staged
+// copy of the activations (72 KB, two workgroups per CU) serves 16 rows of
+// every item and the grid (H / 16 workgroups) is one round of residency.
+// Slot s (16 lanes) owns output row s; pass p takes items 3p .. 3p + 2 for
+// every row at once, so the four slots of a wave read the same activation
+// chunks (LDS broadcast).  Lane gl takes chunks gl + 16c, c < CPL (I = 512
+// CPL).  The activations are stored with float4 j of chunk q at
+// q * 32 + 4 (j ^ (q & 7)), so the 16 lanes of a slot hit distinct banks.
+// ---------------------------------------------------------------------------
+constexpr int WIDE_R = 16;
+constexpr uint32_t WIDE_FLOATS = 18432;
+__device__ __forceinline__ uint32_t wide_f4(uint32_t q, uint32_t j) { return q * 32u + 4u * (j ^ (q & 7u)); }
+
+template <int SBT, int CPL>
+__global__ __launch_bounds__(256, 2) void down_wide_kernel(DownArgs a)
+{
+    constexpr int LPR = 16, MAXR = 3;
+    constexpr int NST = WIDE_FLOATS / 4 / 256; // staged float4 per thread
+    __shared__ __align__(16) float xst[WIDE_FLOATS];
+    __shared__ float xsum[WIDE_FLOATS / 32];
+    __shared__ float yl[MAX_K + 1][WIDE_R];
+    __shared__ float c_w[MAX_K];
+    __shared__ float c_res[WIDE_R];
+    __shared__ float c_sw;
+    const uint32_t tid = threadIdx.x, gl = tid % LPR, slot = tid / LPR;
+    const uint32_t K = a.k, I = a.ex.down.cols, chunks = I / 32;
+    const uint32_t n_items = K + (a.has_shared ? 1u : 0u);
+    const uint32_t row = blockIdx.x * WIDE_R + slot;
+    // loads that need nothing: the routes' expert ids (uniform), the
+    // combine inputs, the residual, then every staged activation
+    uint32_t eid[MAX_K];
+#pragma unroll
+    for (int m = 0; m < MAX_K; ++m)
+        eid[m] = a.ids[min((uint32_t)m, K - 1)];
+    const float cw_v = a.weights[min(tid, K - 1)];
+    const float csl_v = (a.has_shared ? a.shared_logit : a.weights)[0];
+    const float res_v = a.residual[row];
+    const uint32_t n4 = K * I / 4, n_st = n_items * I / 4;
+    float4 stv[NST];
+#pragma unroll
+    for (int q = 0; q < NST; ++q) {
+        const uint32_t i = min(tid + 256u * q, n_st - 1);
+        stv[q] = i < n4 ? reinterpret_cast<const float4*>(a.act)[i]
+                        : reinterpret_cast<const float4*>(a.act_shared)[i - n4];
+    }
+    const uint8_t* const ex_base = a.ex.base;
+    const uint64_t ex_stride = a.ex.stride;
+    const uint64_t ex_w = a.ex.down.w_off, ex_s = a.ex.down.s_off, ex_b = a.ex.down.b_off;
+    const uint8_t* const sh_base = a.has_shared ? a.sh.base : ex_base;
+    const uint64_t sh_w = a.sh.down.w_off, sh_s = a.sh.down.s_off, sh_b = a.sh.down.b_off;
+    const uint32_t gsh_e = a.ex.group_shift, gsh_s = a.has_shared ? a.sh.group_shift : gsh_e;
+    // weights of the units of pass p (items 3p + j): no branch, units past
+    // the last item and experts out of range read slot 0 and are not used
+    uint4 w[MAXR][CPL];
+    uint32_t scr[MAXR][CPL], bir[MAXR][CPL];
+    bool live[MAXR];
+    auto load_pass = [&](uint32_t p) {
+#pragma unroll
+        for (int j = 0; j < MAXR; ++j) {
+            const uint32_t m = 3u * p + j;
+            const bool shared = a.has_shared && m == K;
+            uint32_t e = 0;
+#pragma unroll
+            for (int q = 0; q < MAX_K; ++q)
+                e = (uint32_t)q == m ? eid[q] : e;
+            live[j] = m < n_items && (shared || e < a.ex.count);
+            const bool ok = live[j];
+            const uint8_t* slot_p = shared ? sh_base : ex_base + (uint64_t)(ok ? e : 0u) * ex_stride;
+            const uint64_t w_off = shared ? sh_w : ex_w, s_off = shared ? sh_s : ex_s, b_off = shared ? sh_b : ex_b;
+            const uint32_t gsh = shared ? gsh_s : gsh_e;
+            const uint8_t* dw = slot_p + w_off + (uint64_t)row * (I / 2);
+            const uint16_t* sp = reinterpret_cast<const uint16_t*>(slot_p + s_off) + (uint64_t)row * (I >> gsh);
+            const uint16_t* bp = reinterpret_cast<const uint16_t*>(slot_p + b_off) + (uint64_t)row * (I >> gsh);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t ch = gl + LPR * c;
+                const uint32_t g = (ch * 32u) >> gsh;
+                w[j][c] = *reinterpret_cast<const uint4*>(ok ? dw + ch * 16u : ex_base);
+                scr[j][c] = *(ok ? sp + g : reinterpret_cast<const uint16_t*>(ex_base));
+                bir[j][c] = *(ok ? bp + g : reinterpret_cast<const uint16_t*>(ex_base));
+            }
+        }
+    };
+    load_pass(0);
+    // stage: every element past n_st goes to padding no read touches (the
+    // last float4 of the buffer is beyond n_st * 4 only when the buffer is
+    // not full; then it is never read)
+#pragma unroll
+    for (int q = 0; q < NST; ++q) {
+        const uint32_t i = tid + 256u * q;
+        const uint32_t d = i < n_st ? wide_f4(i >> 3, i & 7u) : WIDE_FLOATS - 4;
+        *reinterpret_cast<float4*>(&xst[d]) = stv[q];
+        // chunk sums: the 8 float4 of chunk i >> 3 sit on 8 consecutive lanes
+        float s4 = (stv[q].x + stv[q].y) + (stv[q].z + stv[q].w);
+        s4 += __shfl_xor(s4, 1);
+        s4 += __shfl_xor(s4, 2);
+        s4 += __shfl_xor(s4, 4);
+        if ((i & 7u) == 0 && i < n_st)
+            xsum[i >> 3] = s4;
+    }
+    if (tid < K)
+        c_w[tid] = cw_v;
+    if (gl == 0)
+        c_res[slot] = res_v;
+    if (tid == 0)
+        c_sw = a.has_shared ? sigmoidf_(csl_v) : 0.0f;
+    __syncthreads();
+    const uint32_t npass = (n_items + MAXR - 1) / MAXR;
+    for (uint32_t p = 0; p < npass; ++p) {
+        if (p > 0)
+            load_pass(p);
+#pragma unroll
+        for (int j = 0; j < MAXR; ++j) {
+            const uint32_t m = 3u * p + j;
+            float part = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t q = m * chunks + gl + LPR * c; // staged chunk (item m)
+                const uint32_t words[4] = {w[j][c].x, w[j][c].y, w[j][c].z, w[j][c].w};
+                float qx0 = 0.0f, qx1 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 xa = *reinterpret_cast<const float4*>(&xst[wide_f4(q, 2 * i)]);
+                    const float4 xb = *reinterpret_cast<const float4*>(&xst[wide_f4(q, 2 * i + 1)]);
+                    float f[8];
+                    q4_word_to_float(words[i], f);
+                    qx0 = fmaf(f[0], xa.x, qx0);
+                    qx1 = fmaf(f[1], xa.y, qx1);
+                    qx0 = fmaf(f[2], xa.z, qx0);
+                    qx1 = fmaf(f[3], xa.w, qx1);
+                    qx0 = fmaf(f[4], xb.x, qx0);
+                    qx1 = fmaf(f[5], xb.y, qx1);
+                    qx0 = fmaf(f[6], xb.z, qx0);
+                    qx1 = fmaf(f[7], xb.w, qx1);
+                }
+                part = fmaf(sb_bits<SBT>(scr[j][c]), qx0 + qx1, fmaf(sb_bits<SBT>(bir[j][c]), xsum[q], part));
+            }
+            const float y = group_sum<LPR>(live[j] ? part : 0.0f);
+            if (gl == 0 && m < n_items)
+                yl[m][slot] = y;
+        }
+    }
+    __syncthreads();
+    if (tid < WIDE_R) {
+        float moe = 0.0f;
+        for (uint32_t k = 0; k < K; ++k)
+            moe = moe + c_w[k] * yl[k][tid];
+        const float rm = c_res[tid] + moe;
+        const float sv = a.has_shared ? yl[K][tid] : 0.0f;
+        a.hidden_out[(uint64_t)blockIdx.x * WIDE_R + tid] = rm + c_sw * sv;
+    }
+}
+
 // next-layer RMSNorm: one block per token (rms_norm_reduced)
 __global__ __launch_bounds__(256) void next_norm_kernel(const float* __restrict__ h,
                                                         const float* __restrict__ w,
@@ -1166,6 +1322,11 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     ea.has_shared = d.shared != nullptr;
     if (ea.has_shared)
         ea.sh = *d.shared;
+    // one token whose activations do not fit the down kernel's staging
+    // buffer: the wide down kernel (16 rows per workgroup, 72 KB staged)
+    const uint32_t d_items = K + (d.shared ? 1u : 0u);
+    const bool wide = T == 1 && (uint64_t)d_items * I > STAGE_FLOATS && (uint64_t)d_items * I <= WIDE_FLOATS &&
+                      I % 512 == 0 && I >= 1024 && I <= 2048 && H % WIDE_R == 0;
     // two rows per wave; four where two would need several rounds of
     // resident workgroups (large I and H: fewer workgroups, so the routing
     // each of them repeats is done fewer times)
@@ -1184,7 +1345,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
         const uint32_t items = max_items + (ea.has_shared ? 1u : 0u);
         const uint32_t gpr_d = I >> ex.group_shift;
         const uint64_t down_bytes = (uint64_t)items * H * (I / 2 + 4u * gpr_d);
-        if (down_bytes <= (16u << 20) && ea.pf_base < GATEUP_RESIDENT_WGS) {
+        if (!wide && down_bytes <= (16u << 20) && ea.pf_base < GATEUP_RESIDENT_WGS) {
             const uint32_t per_block = (DOWN_R * I / 2 + 127) / 128 + 2 * ((DOWN_R * gpr_d * 2 + 127) / 128);
             const uint64_t lines_xcd = (uint64_t)items * ((H / DOWN_R + 7) / 8) * per_block;
             const uint64_t per_xcd = (lines_xcd + 2 * 256 - 1) / (2 * 256);
@@ -1238,6 +1399,25 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     da.residual = d.residual;
     da.hidden_out = d.hidden_out;
     da.status = d.status;
+    if (wide) {
+        dim3 gw(H / WIDE_R);
+#define PBM_DW(C)                                                                              \
+    hipExtLaunchKernelGGL((down_wide_kernel<SBT, C>), gw, dim3(256), 0, st, phase_event(d, 4), phase_event(d, 5), 0, da)
+        switch (I / 512) {
+        case 2: PBM_DW(2); break;
+        case 3: PBM_DW(3); break;
+        default: PBM_DW(4); break;
+        }
+#undef PBM_DW
+        err = hipGetLastError();
+        if (err != hipSuccess)
+            return err;
+        if (d.next_norm_w && d.next_normed) {
+            next_norm_kernel<<<T, 256, 0, st>>>(d.hidden_out, d.next_norm_w, H, d.eps, d.next_normed);
+            err = hipGetLastError();
+        }
+        return err;
+    }
     dim3 g2(H / DOWN_R);
 #define PBM_DN(L, C, M, S)                                                                     \
     hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M, S>), g2, dim3(256), 0, st, phase_event(d, 4), \
