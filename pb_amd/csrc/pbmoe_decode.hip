@@ -1034,45 +1034,50 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 // 2048 columns).  WIDE_R = 16 output rows per workgroup, so that one staged
 // copy of the activations (72 KB, two workgroups per CU) serves 16 rows of
 // every item and the grid (H / 16 workgroups) is one round of residency.
-// Slot s (16 lanes) owns output row s; pass p takes items 3p .. 3p + 2 for
-// every row at once, so the four slots of a wave read the same activation
-// chunks (LDS broadcast).  Lane gl takes chunks gl + 16c, c < CPL (I = 512
-// CPL).  The activations are stored with float4 j of chunk q at
-// q * 32 + 4 (j ^ (q & 7)), so the 16 lanes of a slot hit distinct banks.
+// Wave w owns rows 4w .. 4w + 3 of the block; lane l owns 32-column chunk l
+// (I <= 2048), reads that chunk of an item's activations from LDS once and
+// applies it to its rows.  Each lane folds the combine weight of the
+// item into its partial sums, so a row needs one wave reduction in all:
+// h = r + sum over lanes of sum_m c_m (s q.x + b sum x), c_m = w_m for a
+// routed item, sigma(shared logit) for the shared one.  Float4 j of staged
+// chunk q sits at q * 32 + 4 (j ^ ((q >> 1) & 7)): 16 consecutive chunks
+// fall on distinct banks.
 // ---------------------------------------------------------------------------
 constexpr int WIDE_R = 16;
+constexpr int WIDE_THREADS = 256;
 constexpr uint32_t WIDE_FLOATS = 18432;
-__device__ __forceinline__ uint32_t wide_f4(uint32_t q, uint32_t j) { return q * 32u + 4u * (j ^ (q & 7u)); }
+__device__ __forceinline__ uint32_t wide_f4(uint32_t q, uint32_t j) { return q * 32u + 4u * (j ^ ((q >> 1) & 7u)); }
 
-template <int SBT, int CPL>
-__global__ __launch_bounds__(256, 2) void down_wide_kernel(DownArgs a)
+template <int SBT>
+__global__ __launch_bounds__(WIDE_THREADS, 2) void down_wide_kernel(DownArgs a)
 {
-    constexpr int LPR = 16, MAXR = 3;
-    constexpr int NST = WIDE_FLOATS / 4 / 256; // staged float4 per thread
+    constexpr int RW = WIDE_R / (WIDE_THREADS / 64); // rows per wave
+    constexpr int MAXI = 3;                          // items per pass
+    constexpr int NST = WIDE_FLOATS / 4 / WIDE_THREADS; // staged float4 per thread
     __shared__ __align__(16) float xst[WIDE_FLOATS];
     __shared__ float xsum[WIDE_FLOATS / 32];
-    __shared__ float yl[MAX_K + 1][WIDE_R];
-    __shared__ float c_w[MAX_K];
-    __shared__ float c_res[WIDE_R];
-    __shared__ float c_sw;
-    const uint32_t tid = threadIdx.x, gl = tid % LPR, slot = tid / LPR;
+    __shared__ float c_m[MAX_K + 1];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform: row addresses stay scalar
     const uint32_t K = a.k, I = a.ex.down.cols, chunks = I / 32;
     const uint32_t n_items = K + (a.has_shared ? 1u : 0u);
-    const uint32_t row = blockIdx.x * WIDE_R + slot;
+    const uint32_t row0 = blockIdx.x * WIDE_R + wv * RW;
+    const uint32_t ch = min(lane, chunks - 1); // lanes past the row read its last chunk, unused
+    const bool lane_on = lane < chunks;
     // loads that need nothing: the routes' expert ids (uniform), the
-    // combine inputs, the residual, then every staged activation
+    // combine weights, the residual, then every staged activation
     uint32_t eid[MAX_K];
 #pragma unroll
     for (int m = 0; m < MAX_K; ++m)
         eid[m] = a.ids[min((uint32_t)m, K - 1)];
     const float cw_v = a.weights[min(tid, K - 1)];
     const float csl_v = (a.has_shared ? a.shared_logit : a.weights)[0];
-    const float res_v = a.residual[row];
+    const float res_v = a.residual[row0 + min(lane, (uint32_t)RW - 1)];
     const uint32_t n4 = K * I / 4, n_st = n_items * I / 4;
     float4 stv[NST];
 #pragma unroll
     for (int q = 0; q < NST; ++q) {
-        const uint32_t i = min(tid + 256u * q, n_st - 1);
+        const uint32_t i = min(tid + (uint32_t)WIDE_THREADS * q, n_st - 1);
         stv[q] = i < n4 ? reinterpret_cast<const float4*>(a.act)[i]
                         : reinterpret_cast<const float4*>(a.act_shared)[i - n4];
     }
@@ -1082,45 +1087,80 @@ __global__ __launch_bounds__(256, 2) void down_wide_kernel(DownArgs a)
     const uint8_t* const sh_base = a.has_shared ? a.sh.base : ex_base;
     const uint64_t sh_w = a.sh.down.w_off, sh_s = a.sh.down.s_off, sh_b = a.sh.down.b_off;
     const uint32_t gsh_e = a.ex.group_shift, gsh_s = a.has_shared ? a.sh.group_shift : gsh_e;
-    // weights of the units of pass p (items 3p + j): no branch, units past
-    // the last item and experts out of range read slot 0 and are not used
-    uint4 w[MAXR][CPL];
-    uint32_t scr[MAXR][CPL], bir[MAXR][CPL];
-    bool live[MAXR];
-    auto load_pass = [&](uint32_t p) {
+    // codes and raw scale/bias of this lane's chunk, four rows, the items of
+    // pass p (3p + j): every address is a uniform base plus the lane's
+    // chunk offset; items past the last (also whole passes) and experts out
+    // of range read the same rows of slot 0 and are not used
+    struct PassRegs {
+        uint4 w[MAXI][RW];
+        uint32_t scr[MAXI][RW], bir[MAXI][RW];
+        bool live[MAXI];
+    };
+    auto load_pass = [&](PassRegs& r, uint32_t p) {
 #pragma unroll
-        for (int j = 0; j < MAXR; ++j) {
-            const uint32_t m = 3u * p + j;
+        for (int j = 0; j < MAXI; ++j) {
+            const uint32_t m = (uint32_t)MAXI * p + j;
             const bool shared = a.has_shared && m == K;
             uint32_t e = 0;
 #pragma unroll
             for (int q = 0; q < MAX_K; ++q)
                 e = (uint32_t)q == m ? eid[q] : e;
-            live[j] = m < n_items && (shared || e < a.ex.count);
-            const bool ok = live[j];
-            const uint8_t* slot_p = shared ? sh_base : ex_base + (uint64_t)(ok ? e : 0u) * ex_stride;
-            const uint64_t w_off = shared ? sh_w : ex_w, s_off = shared ? sh_s : ex_s, b_off = shared ? sh_b : ex_b;
-            const uint32_t gsh = shared ? gsh_s : gsh_e;
-            const uint8_t* dw = slot_p + w_off + (uint64_t)row * (I / 2);
-            const uint16_t* sp = reinterpret_cast<const uint16_t*>(slot_p + s_off) + (uint64_t)row * (I >> gsh);
-            const uint16_t* bp = reinterpret_cast<const uint16_t*>(slot_p + b_off) + (uint64_t)row * (I >> gsh);
+            r.live[j] = m < n_items && (shared || e < a.ex.count);
+            const bool use_sh = shared && m < n_items;
+            const uint8_t* slot_p = use_sh ? sh_base : ex_base + (uint64_t)(r.live[j] ? e : 0u) * ex_stride;
+            const uint64_t w_off = use_sh ? sh_w : ex_w, s_off = use_sh ? sh_s : ex_s, b_off = use_sh ? sh_b : ex_b;
+            const uint32_t gsh = use_sh ? gsh_s : gsh_e;
+            // unused items read the first row of slot 0 for every row, the
+            // same lines in every workgroup (cache hits, not HBM traffic)
+            const uint32_t gpr = r.live[j] ? I >> gsh : 0u, g = (ch * 32u) >> gsh;
+            const uint32_t wstride = r.live[j] ? I / 2 : 0u, rb = r.live[j] ? row0 : 0u;
+            const uint8_t* wrow = slot_p + w_off + (uint64_t)rb * wstride;
+            const uint16_t* srow = reinterpret_cast<const uint16_t*>(slot_p + s_off) + (uint64_t)rb * gpr;
+            const uint16_t* brow = reinterpret_cast<const uint16_t*>(slot_p + b_off) + (uint64_t)rb * gpr;
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const uint32_t ch = gl + LPR * c;
-                const uint32_t g = (ch * 32u) >> gsh;
-                w[j][c] = *reinterpret_cast<const uint4*>(ok ? dw + ch * 16u : ex_base);
-                scr[j][c] = *(ok ? sp + g : reinterpret_cast<const uint16_t*>(ex_base));
-                bir[j][c] = *(ok ? bp + g : reinterpret_cast<const uint16_t*>(ex_base));
+            for (int rr = 0; rr < RW; ++rr) {
+                r.w[j][rr] = *reinterpret_cast<const uint4*>(wrow + (uint64_t)rr * wstride + ch * 16u);
+                r.scr[j][rr] = srow[rr * gpr + g];
+                r.bir[j][rr] = brow[rr * gpr + g];
             }
         }
     };
-    load_pass(0);
-    // stage: every element past n_st goes to padding no read touches (the
-    // last float4 of the buffer is beyond n_st * 4 only when the buffer is
-    // not full; then it is never read)
+    float part[RW];
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr)
+        part[rr] = 0.0f;
+    auto compute_pass = [&](PassRegs& r, uint32_t p) {
+#pragma unroll
+        for (int j = 0; j < MAXI; ++j) {
+            const uint32_t m = (uint32_t)MAXI * p + j;
+            // this lane's chunk of item m (passes past the last read item 0)
+            const uint32_t q = (m < n_items ? m : 0u) * chunks + ch;
+            float xv[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(&xst[wide_f4(q, i)]);
+                xv[4 * i] = v.x, xv[4 * i + 1] = v.y, xv[4 * i + 2] = v.z, xv[4 * i + 3] = v.w;
+            }
+            const float xs = xsum[q];
+            const float cm = r.live[j] && lane_on ? c_m[m < n_items ? m : 0u] : 0.0f;
+#pragma unroll
+            for (int rr = 0; rr < RW; ++rr) {
+                // the nibble conversions of one row at a time (scheduled
+                // together, those of a pass would need 384 registers)
+                asm volatile("" : "+v"(r.w[j][rr].x), "+v"(r.w[j][rr].y), "+v"(r.w[j][rr].z), "+v"(r.w[j][rr].w));
+                const float qx = q4_chunk_qx_reg(r.w[j][rr], xv);
+                const float y = fmaf(sb_bits<SBT>(r.scr[j][rr]), qx, sb_bits<SBT>(r.bir[j][rr]) * xs);
+                part[rr] = fmaf(cm, y, part[rr]);
+            }
+        }
+    };
+    PassRegs ra;
+    load_pass(ra, 0);
+    // stage: elements past n_st go to the last float4 of the buffer, which
+    // no read touches unless the buffer is full (then there are none)
 #pragma unroll
     for (int q = 0; q < NST; ++q) {
-        const uint32_t i = tid + 256u * q;
+        const uint32_t i = tid + (uint32_t)WIDE_THREADS * q;
         const uint32_t d = i < n_st ? wide_f4(i >> 3, i & 7u) : WIDE_FLOATS - 4;
         *reinterpret_cast<float4*>(&xst[d]) = stv[q];
         // chunk sums: the 8 float4 of chunk i >> 3 sit on 8 consecutive lanes
@@ -1132,56 +1172,28 @@ __global__ __launch_bounds__(256, 2) void down_wide_kernel(DownArgs a)
             xsum[i >> 3] = s4;
     }
     if (tid < K)
-        c_w[tid] = cw_v;
-    if (gl == 0)
-        c_res[slot] = res_v;
-    if (tid == 0)
-        c_sw = a.has_shared ? sigmoidf_(csl_v) : 0.0f;
+        c_m[tid] = cw_v;
+    if (tid == K)
+        c_m[K] = a.has_shared ? sigmoidf_(csl_v) : 0.0f;
     __syncthreads();
-    const uint32_t npass = (n_items + MAXR - 1) / MAXR;
+    // passes in turn: a second register set for the next pass's loads
+    // (two items per pass to fit) measured slower, 22.6 against 19.9 us on
+    // C5; the lanes' VALU work, not the load latency, bounds the passes
+    const uint32_t npass = (n_items + MAXI - 1) / MAXI;
     for (uint32_t p = 0; p < npass; ++p) {
         if (p > 0)
-            load_pass(p);
-#pragma unroll
-        for (int j = 0; j < MAXR; ++j) {
-            const uint32_t m = 3u * p + j;
-            float part = 0.0f;
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const uint32_t q = m * chunks + gl + LPR * c; // staged chunk (item m)
-                const uint32_t words[4] = {w[j][c].x, w[j][c].y, w[j][c].z, w[j][c].w};
-                float qx0 = 0.0f, qx1 = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float4 xa = *reinterpret_cast<const float4*>(&xst[wide_f4(q, 2 * i)]);
-                    const float4 xb = *reinterpret_cast<const float4*>(&xst[wide_f4(q, 2 * i + 1)]);
-                    float f[8];
-                    q4_word_to_float(words[i], f);
-                    qx0 = fmaf(f[0], xa.x, qx0);
-                    qx1 = fmaf(f[1], xa.y, qx1);
-                    qx0 = fmaf(f[2], xa.z, qx0);
-                    qx1 = fmaf(f[3], xa.w, qx1);
-                    qx0 = fmaf(f[4], xb.x, qx0);
-                    qx1 = fmaf(f[5], xb.y, qx1);
-                    qx0 = fmaf(f[6], xb.z, qx0);
-                    qx1 = fmaf(f[7], xb.w, qx1);
-                }
-                part = fmaf(sb_bits<SBT>(scr[j][c]), qx0 + qx1, fmaf(sb_bits<SBT>(bir[j][c]), xsum[q], part));
-            }
-            const float y = group_sum<LPR>(live[j] ? part : 0.0f);
-            if (gl == 0 && m < n_items)
-                yl[m][slot] = y;
-        }
+            load_pass(ra, p);
+        compute_pass(ra, p);
     }
-    __syncthreads();
-    if (tid < WIDE_R) {
-        float moe = 0.0f;
-        for (uint32_t k = 0; k < K; ++k)
-            moe = moe + c_w[k] * yl[k][tid];
-        const float rm = c_res[tid] + moe;
-        const float sv = a.has_shared ? yl[K][tid] : 0.0f;
-        a.hidden_out[(uint64_t)blockIdx.x * WIDE_R + tid] = rm + c_sw * sv;
+    // one reduction per row; lane rr writes row rr
+    float out = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+        const float t = wave_sum(part[rr]);
+        out = lane == (uint32_t)rr ? t : out;
     }
+    if (lane < (uint32_t)RW)
+        a.hidden_out[row0 + lane] = res_v + out;
 }
 
 // next-layer RMSNorm: one block per token (rms_norm_reduced)
@@ -1401,13 +1413,9 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     da.status = d.status;
     if (wide) {
         dim3 gw(H / WIDE_R);
-#define PBM_DW(C)                                                                              \
-    hipExtLaunchKernelGGL((down_wide_kernel<SBT, C>), gw, dim3(256), 0, st, phase_event(d, 4), phase_event(d, 5), 0, da)
-        switch (I / 512) {
-        case 2: PBM_DW(2); break;
-        case 3: PBM_DW(3); break;
-        default: PBM_DW(4); break;
-        }
+#define PBM_DW()                                                                               \
+    hipExtLaunchKernelGGL((down_wide_kernel<SBT>), gw, dim3(WIDE_THREADS), 0, st, phase_event(d, 4), phase_event(d, 5), 0, da)
+        PBM_DW();
 #undef PBM_DW
         err = hipGetLastError();
         if (err != hipSuccess)
