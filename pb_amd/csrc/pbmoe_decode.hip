@@ -1310,6 +1310,32 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     return hipGetLastError();
 }
 
+// Rows per wave of the gate/up kernel and its workgroups (without the
+// down-prefetch ones): two rows per wave; four where two would need several
+// rounds of resident workgroups (large I and H: fewer workgroups, so the
+// routing each of them repeats is done fewer times).
+static uint32_t gateup_rpw(const DecodeArgs& d, uint32_t* wgs)
+{
+    const uint32_t T = d.tokens, K = d.rp.k, I = d.ex.gate.rows;
+    const uint32_t max_items = T > 1 ? std::min(d.ex.count, T * K) : T * K;
+    const uint32_t rpw = (max_items * (I / 2) + 3) / 4 > 2 * GATEUP_RESIDENT_WGS && I % 4 == 0 ? 4 : 2;
+    if (wgs)
+        *wgs = (max_items * (I / rpw) + 3) / 4;
+    return rpw;
+}
+
+// Route in a launch of its own (route_topk) when the gate/up grid does not
+// fit one round of residency: every gate/up workgroup would repeat the
+// routing, once per round.  C5 (1024 workgroups, two rounds): 98.0 ->
+// 89.5 us per layer; C2 (640 workgroups, one round): the extra launch
+// costs more than the routing it saves (23.7 -> 25.9 us).
+static bool route_separately(const DecodeArgs& d)
+{
+    uint32_t wgs = 0;
+    gateup_rpw(d, &wgs);
+    return wgs > GATEUP_RESIDENT_WGS;
+}
+
 template <int SBT>
 static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool route_here)
 {
@@ -1339,10 +1365,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     const uint32_t d_items = K + (d.shared ? 1u : 0u);
     const bool wide = T == 1 && (uint64_t)d_items * I > STAGE_FLOATS && (uint64_t)d_items * I <= WIDE_FLOATS &&
                       I % 512 == 0 && I >= 1024 && I <= 2048 && H % WIDE_R == 0;
-    // two rows per wave; four where two would need several rounds of
-    // resident workgroups (large I and H: fewer workgroups, so the routing
-    // each of them repeats is done fewer times)
-    const int RPW = (max_items * (I / 2) + 3) / 4 > 2 * GATEUP_RESIDENT_WGS && I % 4 == 0 ? 4 : 2;
+    const int RPW = (int)gateup_rpw(d, nullptr);
     const uint32_t waves = max_items * (I / RPW);
     const uint32_t cpl = (H / 32 + 63) / 64;
     const uint32_t epl = (d.rp.experts + 63) / 64;
@@ -1529,10 +1552,17 @@ hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mod
     err = launch_router_stage(st, d, full, d.shared != nullptr);
     if (err != hipSuccess)
         return err;
+    bool route_here = full;
+    if (full && route_separately(d)) {
+        err = launch_route_topk(st, d.logits, d.sel_bias, d.tokens, d.rp, d.ids, d.weights, d.status);
+        if (err != hipSuccess)
+            return err;
+        route_here = false;
+    }
     if (d.ex.sb_dtype == 2)
-        err = launch_experts_typed<2>(st, d, full);
+        err = launch_experts_typed<2>(st, d, route_here);
     else
-        err = launch_experts_typed<1>(st, d, full);
+        err = launch_experts_typed<1>(st, d, route_here);
     return err;
 }
 
