@@ -539,7 +539,7 @@ __device__ uint32_t touch_down_lines(const ExpertArgs& a, const RouteLds& s, uin
 }
 
 template <int EPL>
-__device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s)
+__device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s, bool need_w)
 {
     const int wv = threadIdx.x >> 6;
     const uint32_t K = a.rp.k;
@@ -551,7 +551,7 @@ __device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s)
             if (t)
                 __syncthreads(); // scratch reuse
             route_token_block<EPT>(a.logits + (uint64_t)t * a.rp.experts, a.sel_bias, a.rp, s.ids + t * K,
-                                   s.w + t * K, &s.grp[0][0], a.status);
+                                   s.w + t * K, &s.grp[0][0], a.status, need_w);
         }
         return;
     }
@@ -574,7 +574,10 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
     const bool use_plan = T > 1;
 
     if (a.route_here) {
-        route_all_tokens<EPL>(a, s);
+        // only the publishing workgroup needs the route weights (the down
+        // kernel reads them); the others select the ids and move on to
+        // their weight loads sooner
+        route_all_tokens<EPL>(a, s, blockIdx.x == 0);
     } else {
         for (uint32_t r = threadIdx.x; r < routes; r += blockDim.x) {
             s.ids[r] = a.ids[r];

@@ -555,13 +555,15 @@ __device__ inline void route_token_wave(const float* __restrict__ l, const float
 // quarter of the experts (K rounds of a wave max over per-thread sorted
 // heads), then wave 0 merges the <= 4K candidates, one per lane.  Same
 // selection rule (score desc, lower index) and value arithmetic as
-// route_token_wave; every thread of the workgroup must call it.
+// route_token_wave; every thread of the workgroup must call it.  need_w
+// false (the same in every thread): the ids only, no softmax sums, weights
+// or weight checks (callers that publish no weights).
 // lds: >= 1024 + 8 + 144 floats of workgroup scratch.
 // ---------------------------------------------------------------------------
 template <int EPT>
 __device__ inline void route_token_block(const float* __restrict__ l, const float* __restrict__ bias,
                                          const RouteParams& p, uint32_t* ids_out, float* w_out, float* lds,
-                                         uint32_t* status)
+                                         uint32_t* status, bool need_w = true)
 {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t E = p.experts, K = p.k;
@@ -583,7 +585,7 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
         atomicOr(status, ST_NONFINITE);
     float mx = 0.0f;
     float sel[EPT];
-    if (p.kind == 0) {
+    if (p.kind == 0 && need_w) {
         float m = -INFINITY;
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
@@ -602,6 +604,10 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
         sm = wave_sum(sm);
         if (lane == 0)
             red[4 + wv] = sm;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            sel[j] = raw[j];
+    } else if (p.kind == 0) { // selection only: softmax is monotonic, select on the logits
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
             sel[j] = raw[j];
@@ -675,6 +681,11 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
             ck = 0u;
         if ((uint32_t)lane == r)
             myid = win;
+    }
+    if (!need_w) { // the ids only (the caller publishes no weights)
+        if ((uint32_t)lane < K)
+            ids_out[lane] = myid;
+        return;
     }
     // value behind each selected id, renormalisation (as route_token_wave)
     const float v = (uint32_t)lane < K && myid < E ? raw_l[myid] : 0.0f;
