@@ -101,7 +101,9 @@ def test_router_logits_within_summation_bound(ctx, cfg, T):
 
 
 @pytest.mark.parametrize("cfg,T,order", [(C2, 8, abi.ORDER_CANONICAL), (C1, 8, abi.ORDER_REFERENCE_SLOT),
-                                         (C2, 4, abi.ORDER_REFERENCE_SLOT)])
+                                         (C2, 4, abi.ORDER_REFERENCE_SLOT),
+                                         # fewer than 4 tokens: one workgroup per token (bitonic selection)
+                                         (C2, 1, abi.ORDER_CANONICAL), (C1, 3, abi.ORDER_CANONICAL)])
 def test_topk_bit_exact_on_device_logits(ctx, cfg, T, order):
     _say(f"[test] topk exact {cfg.name} T={T} order={order}")
     dl = _layer(ctx, cfg, 0, order)
@@ -294,6 +296,59 @@ def test_decode_layer_matches_oracle(ctx, cfg, T):
     mx, rel = assert_layer_tolerance(out.download(), ref_h, exact=exact)
     _say(f"[result] {cfg.name} T={T} hidden max_abs={mx:.3e} rel_l2={rel:.3e}")
     assert_layer_tolerance(nn.download(), ref_n, "next_normed")
+
+
+# One-token shapes whose routed + shared activations exceed the down
+# kernel's staging buffer (48 KB) but fit the wide down kernel's 72 KB: chunk
+# lanes past the row (I = 1024, 1536), no shared expert, K = 12.  W_K16
+# routes 16 of 200 experts (the bitonic block routing at its largest K).
+W_I1024 = MoeConfig("wide_i1024_k12", hidden=1024, intermediate=1024, experts=64, k=12,
+                    routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    shared_intermediate=1024, shared_gated=True, sb_dtype=abi.DTYPE_F16)
+W_I1536 = MoeConfig("wide_i1536_k8", hidden=2048, intermediate=1536, experts=128, k=8,
+                    routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    shared_intermediate=1536, shared_gated=False, sb_dtype=abi.DTYPE_BF16)
+W_NOSH = MoeConfig("wide_i2048_noshared", hidden=1024, intermediate=2048, experts=32, k=8,
+                   routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                   sb_dtype=abi.DTYPE_F16)
+W_K16 = MoeConfig("route_e200_k16", hidden=1024, intermediate=512, experts=200, k=16,
+                  routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                  shared_intermediate=512, shared_gated=True, sb_dtype=abi.DTYPE_F16)
+
+
+@pytest.mark.parametrize("cfg", [W_I1024, W_I1536, W_NOSH, W_K16], ids=lambda c: c.name)
+def test_wide_down_and_routing_shapes_match_oracle(ctx, cfg):
+    """The expert phase and the full layer (router stage, routing inside the
+    gate/up kernel, down) for one token on the shapes above, against the
+    oracle; the routes bit-exact against the oracle's routing of the
+    device logits."""
+    _say(f"[test] one-token layer {cfg.name}")
+    dl = _layer(ctx, cfg, 0)
+    xh, rh = synth.activations(SEED, 77, 1, cfg.hidden)
+    x, ids, w, logits = _route(ctx, dl, xh)
+    ref_ids, ref_w = orc.route_rows(logits.download(), cfg.k, orc.ROUTING_SOFTMAX, orc.ORDER_CANONICAL)
+    np.testing.assert_array_equal(ids.download().astype(np.int64), ref_ids.astype(np.int64))
+    np.testing.assert_allclose(w.download(), ref_w, rtol=4e-6)
+    res = ctx.to_device(rh)
+    out = ctx.array((1, cfg.hidden), np.float32)
+    dl.moe.submit_scheduled_expert_command(x, res, ids, w, out)
+    ctx.sync()
+    ids_h = ids.download().astype(np.int32)
+    ref_h, _ = dl.oracle_block(xh, rh, ids_h, w.download())
+    # outputs beyond 1e3 (the ungated shared expert): the fp64 evaluation decides
+    exact = dl.exact_block(xh, rh, ids_h, w.download()) if np.max(np.abs(ref_h)) > 1e3 else None
+    mx, rel = assert_layer_tolerance(out.download(), ref_h, exact=exact)
+    _say(f"[result] {cfg.name} hidden max_abs={mx:.3e} rel_l2={rel:.3e}")
+    # the fused layer (routing inside the gate/up kernel) gives the same hidden state
+    out2 = ctx.array((1, cfg.hidden), np.float32)
+    ids2 = ctx.array((1, cfg.k), np.uint32)
+    w2 = ctx.array((1, cfg.k), np.float32)
+    dl.moe.forward(x, res, out2, ids2, w2)
+    ctx.sync()
+    np.testing.assert_array_equal(ids2.download(), ids.download())
+    np.testing.assert_array_equal(w2.download().view(np.uint32), w.download().view(np.uint32))
+    mx2, rel2 = assert_layer_tolerance(out2.download(), ref_h, exact=exact)
+    _say(f"[result] {cfg.name} fused hidden max_abs={mx2:.3e} rel_l2={rel2:.3e}")
 
 
 def test_one_row_prefill_is_bitwise_decode(ctx):
