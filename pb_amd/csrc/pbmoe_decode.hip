@@ -742,10 +742,10 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 
 // ---------------------------------------------------------------------------
 // kernel 3: down projection + combine for R output rows per workgroup.
-// Unit = (item, row) handled by LPR lanes with CPL chunks each.  With one
-// token (direct routes) the activations of every route are staged in LDS by
-// loads that do not wait for the routes; with more tokens they are read from
-// L2 per unit.
+// Unit = (item, row) handled by LPR lanes with CPL chunks each.  When every
+// route's activations fit STAGE_FLOATS (one token, or two of C2's) they are
+// staged in LDS by loads that do not wait for the routes; otherwise they are
+// read from L2 per unit.
 // ---------------------------------------------------------------------------
 constexpr uint32_t STAGE_FLOATS = 12288; // activations staged (54 KB of LDS in XP-padded chunks)
 // Staged chunk q (32 floats) sits at q * XP floats, so that the lanes'
@@ -763,7 +763,7 @@ struct DownArgs {
     const float* weights;
     Plan plan;
     bool use_plan;
-    bool stage; // activations fit STAGE_FLOATS (direct mode)
+    bool stage; // every route's activations fit STAGE_FLOATS
     const float* residual;
     float* hidden_out;
     uint32_t* status;
@@ -1433,7 +1433,9 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     da.weights = d.weights;
     da.plan = d.plan;
     da.use_plan = use_plan;
-    da.stage = !use_plan && (uint64_t)(T * K + (da.has_shared ? T : 0u)) * I <= STAGE_FLOATS;
+    // every route's activations (plan order for several tokens) and the
+    // shared expert's, when they fit the staging buffer
+    da.stage = (uint64_t)(T * K + (da.has_shared ? T : 0u)) * I <= STAGE_FLOATS;
     da.residual = d.residual;
     da.hidden_out = d.hidden_out;
     da.status = d.status;

@@ -276,7 +276,7 @@ def test_sigmoid_noaux_reference_golden_on_device(ctx, order):
 
 
 # ------------------------------------------------------------ expert phase ---
-@pytest.mark.parametrize("cfg,T", [(C1, 1), (C2, 1), (C2, 4), (C2, 8), (C1, 16), (C5, 1), (C5, 4)])
+@pytest.mark.parametrize("cfg,T", [(C1, 1), (C2, 1), (C2, 2), (C2, 4), (C2, 8), (C1, 16), (C5, 1), (C5, 4)])
 def test_decode_layer_matches_oracle(ctx, cfg, T):
     _say(f"[test] decode layer {cfg.name} T={T}")
     dl = _layer(ctx, cfg, 0)
