@@ -49,7 +49,7 @@ struct RowsArgs {
     float* y;              // [total rows]
 };
 
-template <int SBT, int CPL, int RPW>
+template <int SBT, int CPL, int RPW, bool NORM>
 __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
 {
     // x is staged in LDS once per workgroup with coalesced loads (a lane's
@@ -60,51 +60,74 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
     __shared__ __align__(16) float xl[WAVE * CPL * XP];
     __shared__ float red[4];
     const int lane = threadIdx.x & 63;
-    const uint32_t r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    // The wave index is read as a scalar, so that the matrix choice and the
+    // row pointers are scalar too and the weight loads issue at once (a
+    // per-lane choice fetches the matrix descriptor per lane first: one more
+    // memory round trip).
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r0 = (blockIdx.x * 4 + wv) * RPW;
     const bool active = r0 < a.first[a.n_mat];
     const uint32_t rr = active ? r0 : 0u; // idle waves still reach the barrier
-    uint32_t mi = 0;
-    while (mi + 1 < a.n_mat && rr >= a.first[mi + 1])
-        ++mi;
-    const Q4Mat m = a.m[mi];
-    const uint32_t row0 = rr - a.first[mi];
+    const uint32_t mi = (a.n_mat > 1 && rr >= a.first[1]) + (a.n_mat > 2 && rr >= a.first[2]);
+    const uint8_t* codes = mi == 0 ? a.m[0].codes : mi == 1 ? a.m[1].codes : a.m[2].codes;
+    const uint16_t* scales =
+        reinterpret_cast<const uint16_t*>(mi == 0 ? a.m[0].scales : mi == 1 ? a.m[1].scales : a.m[2].scales);
+    const uint16_t* biases =
+        reinterpret_cast<const uint16_t*>(mi == 0 ? a.m[0].biases : mi == 1 ? a.m[1].biases : a.m[2].biases);
+    const uint32_t row0 = rr - (mi == 0 ? 0u : mi == 1 ? a.first[1] : a.first[2]);
     const uint32_t cols = a.m[0].cols; // every matrix of one launch has the same columns
     const uint32_t chunks = cols / 32, gpr = cols >> a.group_shift;
+    // Every load is issued before any is used: lanes past the last chunk
+    // read the last chunk again (clamped, no branch: a load inside a
+    // divergent branch is waited for where the branch ends), and the 16-bit
+    // scales and biases are converted where they are used.
     uint4 w[RPW][CPL];
-    float sc[RPW][CPL], bi[RPW][CPL];
+    uint32_t sr[RPW][CPL], br[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const uint32_t row = row0 + r;
-        const uint4* wp = reinterpret_cast<const uint4*>(m.codes + (uint64_t)row * (cols / 2));
+        const uint4* wp = reinterpret_cast<const uint4*>(codes + (uint64_t)row * (cols / 2));
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const uint32_t ch = lane + WAVE * c;
-            if (ch < chunks) {
-                w[r][c] = wp[ch];
-                const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> a.group_shift);
-                sc[r][c] = sb_at<SBT>(m.scales, gi);
-                bi[r][c] = sb_at<SBT>(m.biases, gi);
-            }
+            const uint32_t ch = min(lane + WAVE * c, chunks - 1);
+            w[r][c] = wp[ch];
+            const uint64_t gi = (uint64_t)row * gpr + ((ch * 32u) >> a.group_shift);
+            sr[r][c] = scales[gi];
+            br[r][c] = biases[gi];
         }
     }
+    // residual of this wave's rows (lane r holds row r's), or y itself as a
+    // harmless stand-in that is not used
+    const float* rsrc = a.residual ? a.residual : a.y;
+    const float resv = rsrc[rr + min(lane, RPW - 1)];
     // Stage x (times the norm weight when the input RMSNorm is fused).  Every
     // row product is linear in the norm's scale, so the sums are multiplied
-    // by 1 / sqrt(mean(x^2) + eps) at the end (math.rs:151-167).
+    // by 1 / sqrt(mean(x^2) + eps) at the end (math.rs:151-167).  The float4
+    // slots past cols / 4 hold zeros in chunks no lane reads.
+    const uint32_t nf = cols / 4;
+    float4 xv4[2 * CPL], nv4[2 * CPL];
+#pragma unroll
+    for (int j = 0; j < 2 * CPL; ++j) {
+        const uint32_t f = min(threadIdx.x + 256u * j, nf - 1);
+        xv4[j] = reinterpret_cast<const float4*>(a.x)[f];
+        if constexpr (NORM)
+            nv4[j] = reinterpret_cast<const float4*>(a.norm_w)[f];
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2 * CPL; ++j) {
-        const uint32_t f = threadIdx.x + 256u * j; // float4 index
-        if (f < cols / 4) {
-            float4 v = reinterpret_cast<const float4*>(a.x)[f];
-            if (a.norm_w) {
-                const float4 nw = reinterpret_cast<const float4*>(a.norm_w)[f];
-                ss = fmaf(v.x, v.x, ss), ss = fmaf(v.y, v.y, ss), ss = fmaf(v.z, v.z, ss), ss = fmaf(v.w, v.w, ss);
-                v.x *= nw.x, v.y *= nw.y, v.z *= nw.z, v.w *= nw.w;
-            }
-            *reinterpret_cast<float4*>(&xl[(f >> 3) * XP + (f & 7) * 4]) = v;
+        const uint32_t f = threadIdx.x + 256u * j;
+        const bool in = f < nf;
+        float4 v = xv4[j];
+        v.x = in ? v.x : 0.0f, v.y = in ? v.y : 0.0f, v.z = in ? v.z : 0.0f, v.w = in ? v.w : 0.0f;
+        if constexpr (NORM) {
+            const float4 nw = nv4[j];
+            ss = fmaf(v.x, v.x, ss), ss = fmaf(v.y, v.y, ss), ss = fmaf(v.z, v.z, ss), ss = fmaf(v.w, v.w, ss);
+            v.x *= nw.x, v.y *= nw.y, v.z *= nw.z, v.w *= nw.w;
         }
+        *reinterpret_cast<float4*>(&xl[(f >> 3) * XP + (f & 7) * 4]) = v;
     }
-    if (a.norm_w) {
+    if constexpr (NORM) {
         ss = wave_sum(ss);
         if (lane == 0)
             red[threadIdx.x >> 6] = ss;
@@ -113,7 +136,7 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
     if (!active)
         return;
     const float inv_rms =
-        a.norm_w ? 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)cols + a.eps) : 1.0f;
+        NORM ? 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)cols + a.eps) : 1.0f;
     float acc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
@@ -135,16 +158,16 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
                 xs += (xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3]);
 #pragma unroll
             for (int r = 0; r < RPW; ++r)
-                acc[r] = fmaf(sc[r][c], q4_chunk_qx_reg(w[r][c], xv), fmaf(bi[r][c], xs, acc[r]));
+                acc[r] = fmaf(sb_bits<SBT>(sr[r][c]), q4_chunk_qx_reg(w[r][c], xv),
+                              fmaf(sb_bits<SBT>(br[r][c]), xs, acc[r]));
         }
     }
+    const float res = a.residual ? resv : 0.0f;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const float s = wave_sum(acc[r]) * inv_rms;
-        if (lane == r) {
-            const uint32_t o = r0 + r;
-            a.y[o] = a.residual ? a.residual[o] + s : s;
-        }
+        if (lane == r)
+            a.y[r0 + r] = res + s;
     }
 }
 
@@ -383,7 +406,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
         out[i] = (h[i] * scale) * w[i];
 }
 
-template <int SBT, int RPW>
+template <int SBT, int RPW, bool NORM>
 static hipError_t launch_rows(hipStream_t st, const RowsArgs& r)
 {
     const uint32_t total = r.first[r.n_mat];
@@ -391,14 +414,20 @@ static hipError_t launch_rows(hipStream_t st, const RowsArgs& r)
     const uint32_t cpl = (cols / 32 + 63) / 64;
     const dim3 grid((total / RPW + 3) / 4);
     if (cpl <= 1)
-        hipLaunchKernelGGL((q4_rows_kernel<SBT, 1, RPW>), grid, dim3(256), 0, st, r);
+        hipLaunchKernelGGL((q4_rows_kernel<SBT, 1, RPW, NORM>), grid, dim3(256), 0, st, r);
     else if (cpl <= 2)
-        hipLaunchKernelGGL((q4_rows_kernel<SBT, 2, RPW>), grid, dim3(256), 0, st, r);
+        hipLaunchKernelGGL((q4_rows_kernel<SBT, 2, RPW, NORM>), grid, dim3(256), 0, st, r);
     else if (cpl <= 4)
-        hipLaunchKernelGGL((q4_rows_kernel<SBT, 4, RPW>), grid, dim3(256), 0, st, r);
+        hipLaunchKernelGGL((q4_rows_kernel<SBT, 4, RPW, NORM>), grid, dim3(256), 0, st, r);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+template <int SBT, int RPW>
+static hipError_t launch_rows(hipStream_t st, const RowsArgs& r)
+{
+    return r.norm_w ? launch_rows<SBT, RPW, true>(st, r) : launch_rows<SBT, RPW, false>(st, r);
 }
 
 // rows per wave: 2 for q/k/v (640 workgroups at C4), 1 for o_proj (512
