@@ -176,13 +176,13 @@ __global__ __launch_bounds__(256) void q4_rows_kernel(RowsArgs a)
 // apply_optional_per_head_rms_norm_and_split_half_rope (math.rs:278-300):
 // value *= (1 / sqrt(mean(v^2) + 1e-6)) * weight, then x0 cos - x1 sin,
 // x0 sin + x1 cos.
-__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const float* w, float sn, float cs)
+// w0, w1: the weights of dims lane and lane + 64.
+__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, float w0, float w1, float sn, float cs)
 {
-    const int lane = threadIdx.x & 63;
     const float ms = wave_sum(x0 * x0 + x1 * x1) / (float)HD;
     const float scale = 1.0f / sqrtf(ms + 1e-6f);
-    const float a0 = x0 * (scale * w[lane]);
-    const float a1 = x1 * (scale * w[lane + HALF]);
+    const float a0 = x0 * (scale * w0);
+    const float a1 = x1 * (scale * w1);
     x0 = a0 * cs - a1 * sn;
     x1 = a0 * sn + a1 * cs;
 }
@@ -202,68 +202,83 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
     __shared__ float ps[NH][CH];
     __shared__ __align__(16) uint16_t knew[HD];
     __shared__ __align__(16) uint16_t vnew[HD];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6); // wave index, scalar
     const uint32_t chunk = blockIdx.x, j = blockIdx.y;
     const uint32_t nq = a.q_heads / a.kv_heads;
-    const uint32_t qh = j * nq + blockIdx.z * NH + wv; // this wave's q head (wv < NH)
+    // this wave's q head (waves past NH read head NH - 1 and store nothing)
+    const uint32_t qh = j * nq + blockIdx.z * NH + min(wv, (uint32_t)NH - 1);
     const uint32_t n = a.position + 1; // attended positions 0..position
     const uint32_t t0 = chunk * CH;
     const uint32_t cnt = min((uint32_t)CH, n - t0);
     const uint32_t chunks = gridDim.x;
     const bool has_new = a.position >= t0 && a.position < t0 + CH;
 
-    // issue the chunk's key/value loads first (16 bytes per thread per step);
-    // this position's row is taken from LDS below, not from the cache
+    // The small loads (rotation frequency, q row, this position's k and v
+    // rows, the q and k norm weights) are issued first and unconditionally: a wave's loads complete in
+    // issue order, so the rotation below waits only for these, while the
+    // chunk's key/value loads (16 bytes per thread per step) stay in flight.
+    const float ifr = a.inv_freq[lane];
+    const float* qr = a.qkv + (uint64_t)qh * HD;
+    const float* kr = a.qkv + (uint64_t)a.q_heads * HD + (uint64_t)j * HD;
+    const float* vr = kr + (uint64_t)a.kv_heads * HD;
+    const float q0 = qr[lane], q1 = qr[lane + HALF];
+    const float k0 = kr[lane], k1 = kr[lane + HALF];
+    const float v0 = vr[lane], v1 = vr[lane + HALF];
+    const float qn0 = a.q_norm[lane], qn1 = a.q_norm[lane + HALF];
+    const float kn0 = a.k_norm[lane], kn1 = a.k_norm[lane + HALF];
+    // Rows past cnt read the chunk's last row (no branch around a load: one
+    // inside a divergent branch is waited for where the branch ends) and are
+    // zeroed when staged; this position's row is taken from LDS below, not
+    // from the cache.
     constexpr int PIECES = CH * (HD / 8) / 256;
     uint4 kk[PIECES], vv[PIECES];
 #pragma unroll
     for (int u = 0; u < PIECES; ++u) {
-        const uint32_t i = tid + 256 * u, t = i / (HD / 8), q = i % (HD / 8);
-        kk[u] = make_uint4(0, 0, 0, 0), vv[u] = make_uint4(0, 0, 0, 0);
-        if (t < cnt && t0 + t != a.position) {
-            const uint64_t o = ((uint64_t)(t0 + t) * a.kv_heads + j) * HD;
-            kk[u] = reinterpret_cast<const uint4*>(a.cache_k + o)[q];
-            vv[u] = reinterpret_cast<const uint4*>(a.cache_v + o)[q];
-        }
+        const uint32_t i = tid + 256 * u, t = min(i / (HD / 8), cnt - 1), q = i % (HD / 8);
+        const uint64_t o = ((uint64_t)(t0 + t) * a.kv_heads + j) * HD;
+        kk[u] = reinterpret_cast<const uint4*>(a.cache_k + o)[q];
+        vv[u] = reinterpret_cast<const uint4*>(a.cache_v + o)[q];
     }
 
     // rotation of the pair (lane, lane + 64) at this position: the f32 angle
     // of split_half_rope_rotations (math.rs:303-325)
     float sn, cs;
-    sincosf((float)a.position * a.inv_freq[lane], &sn, &cs);
+    sincosf((float)a.position * ifr, &sn, &cs);
     if (wv < NH) {
-        const float* qr = a.qkv + (uint64_t)qh * HD;
-        float x0 = qr[lane], x1 = qr[lane + HALF];
-        norm_rope_pair(x0, x1, a.q_norm, sn, cs);
+        float x0 = q0, x1 = q1;
+        norm_rope_pair(x0, x1, qn0, qn1, sn, cs);
         qs[wv][lane] = x0;
         qs[wv][lane + HALF] = x1;
     }
     if (has_new && wv == 0) {
-        const float* kr = a.qkv + (uint64_t)a.q_heads * HD + (uint64_t)j * HD;
-        const float* vr = kr + (uint64_t)a.kv_heads * HD;
-        float x0 = kr[lane], x1 = kr[lane + HALF];
-        norm_rope_pair(x0, x1, a.k_norm, sn, cs);
-        const uint16_t k0 = __half_as_ushort(__float2half(x0)), k1 = __half_as_ushort(__float2half(x1));
-        const uint16_t v0 = __half_as_ushort(__float2half(vr[lane]));
-        const uint16_t v1 = __half_as_ushort(__float2half(vr[lane + HALF]));
-        knew[lane] = k0, knew[lane + HALF] = k1;
-        vnew[lane] = v0, vnew[lane + HALF] = v1;
+        float x0 = k0, x1 = k1;
+        norm_rope_pair(x0, x1, kn0, kn1, sn, cs);
+        const uint16_t nk0 = __half_as_ushort(__float2half(x0)), nk1 = __half_as_ushort(__float2half(x1));
+        const uint16_t nv0 = __half_as_ushort(__float2half(v0));
+        const uint16_t nv1 = __half_as_ushort(__float2half(v1));
+        knew[lane] = nk0, knew[lane + HALF] = nk1;
+        vnew[lane] = nv0, vnew[lane + HALF] = nv1;
         if (blockIdx.z == 0) { // one writer per kv head
             const uint64_t o = ((uint64_t)a.position * a.kv_heads + j) * HD;
-            a.cache_k[o + lane] = k0, a.cache_k[o + lane + HALF] = k1;
-            a.cache_v[o + lane] = v0, a.cache_v[o + lane + HALF] = v1;
+            a.cache_k[o + lane] = nk0, a.cache_k[o + lane + HALF] = nk1;
+            a.cache_v[o + lane] = nv0, a.cache_v[o + lane + HALF] = nv1;
         }
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < PIECES; ++u) {
         const uint32_t i = tid + 256 * u, t = i / (HD / 8), q = i % (HD / 8);
+        const bool live = t < cnt;
+        uint4 kx = kk[u], vx = vv[u];
+        kx.x = live ? kx.x : 0u, kx.y = live ? kx.y : 0u, kx.z = live ? kx.z : 0u, kx.w = live ? kx.w : 0u;
+        vx.x = live ? vx.x : 0u, vx.y = live ? vx.y : 0u, vx.z = live ? vx.z : 0u, vx.w = live ? vx.w : 0u;
         if (t0 + t == a.position) {
-            kk[u] = reinterpret_cast<const uint4*>(knew)[q];
-            vv[u] = reinterpret_cast<const uint4*>(vnew)[q];
+            kx = reinterpret_cast<const uint4*>(knew)[q];
+            vx = reinterpret_cast<const uint4*>(vnew)[q];
         }
-        reinterpret_cast<uint4*>(&kc[t][0])[q] = kk[u];
-        reinterpret_cast<uint4*>(&vc[t][0])[q] = vv[u];
+        reinterpret_cast<uint4*>(&kc[t][0])[q] = kx;
+        reinterpret_cast<uint4*>(&vc[t][0])[q] = vx;
     }
     __syncthreads();
     if (wv >= NH)
