@@ -748,6 +748,10 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 // read from L2 per unit.
 // ---------------------------------------------------------------------------
 constexpr uint32_t STAGE_FLOATS = 12288; // activations staged (54 KB of LDS in XP-padded chunks)
+// Per-token variant (several tokens, grid H / DOWN_R x tokens): one token's
+// routed + shared activations (27 KB of LDS), so that four workgroups fit a CU.
+constexpr uint32_t PT_STAGE_FLOATS = 6144;
+constexpr int PT_R = 8; // output rows per per-token workgroup: 8 x (K + 1) units in one pass
 // Staged chunk q (32 floats) sits at q * XP floats, so that the lanes'
 // 16-byte reads of consecutive chunks fall on distinct banks.
 constexpr int XP = 36;
@@ -774,25 +778,41 @@ struct DownArgs {
 // whose activations never fit STAGE_FLOATS, such as I = 2048 with K = 8).
 // ONE: one token without the dispatch plan only (the token-loop path is not
 // compiled, which keeps the registers of the straight-line path low).
-template <int SBT, int LPR, int CPL, int MAXR, bool STG, bool ONE = false>
+// PT: several tokens, workgroup (row block, token blockIdx.y) does the
+// one-token work for its token: the token's K routes (ids, weights and
+// combine in route order) and shared expert, with the routes' activation
+// rows gathered from the plan-ordered buffer through the plan's output
+// index (a.stage: they fit PT_STAGE_FLOATS).
+template <int SBT, int LPR, int CPL, int MAXR, bool STG, bool ONE = false, bool PT = false>
 __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 {
-    constexpr int R = DOWN_R;
+    constexpr int R = PT ? PT_R : DOWN_R;
     constexpr int SLOTS = 256 / LPR;
-    __shared__ float ylds[DEC_ROUTES][R];
-    __shared__ float yshl[DEC_T][R];
-    __shared__ float c_w[DEC_ROUTES];    // combine inputs, loaded at the start
-    __shared__ uint32_t c_oi[DEC_ROUTES];
-    __shared__ float c_sw[DEC_T];
-    __shared__ __align__(16) float astage[STG ? STAGE_FLOATS / 32 * XP : 4];
-    __shared__ float xsl[STG ? STAGE_FLOATS / 32 : 4]; // per-chunk sums of the staged activations
+    constexpr uint32_t SF = PT ? PT_STAGE_FLOATS : STAGE_FLOATS;
+    constexpr int NT = PT ? 1 : DEC_T;               // tokens of one workgroup
+    constexpr int NR = PT ? DEC_ROUTES / DEC_T : DEC_ROUTES; // routes of one workgroup
+    __shared__ float ylds[NR][R];
+    __shared__ float yshl[NT][R];
+    __shared__ float c_w[NR];    // combine inputs, loaded at the start
+    __shared__ uint32_t c_oi[NR];
+    __shared__ float c_sw[NT];
+    __shared__ __align__(16) float astage[STG ? SF / 32 * XP : 4];
+    __shared__ float xsl[STG ? SF / 32 : 4]; // per-chunk sums of the staged activations
     const bool stage = STG && a.stage;
     const int gl = threadIdx.x % LPR;
     const int slot_id = threadIdx.x / LPR;
     const uint32_t row_base = blockIdx.x * R;
-    const uint32_t T = a.tokens, K = a.k;
+    const uint32_t tk = PT ? blockIdx.y : 0u; // this workgroup's token (PT)
+    const uint32_t T = PT ? 1u : a.tokens, K = a.k;
     const uint32_t I = a.ex.down.cols;
     const uint32_t routes = T * K;
+    const bool use_plan = !PT && a.use_plan;
+    const uint32_t* const ids = a.ids + tk * K;
+    const float* const rweights = a.weights + tk * K;
+    const float* const residual = a.residual + (uint64_t)tk * a.hidden;
+    float* const hidden_out = a.hidden_out + (uint64_t)tk * a.hidden;
+    const float* const act_shared = a.act_shared + (uint64_t)tk * I;
+    const float* const shared_logit = a.has_shared ? a.shared_logit + tk : rweights;
 
     // Load order.  Every load below is issued before anything waits on it,
     // and none sits in a branch (a load inside a divergent branch is waited
@@ -810,10 +830,10 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     // would wait for them
     float res_v = 0.0f, cw_v = 0.0f, csl_v = 0.0f;
     uint32_t coi_v = 0;
-    const uint32_t n_routed = a.use_plan ? a.plan.unique_count[0] : routes;
+    const uint32_t n_routed = use_plan ? a.plan.unique_count[0] : routes;
     const uint32_t n_items = n_routed + (a.has_shared ? 1u : 0u);
     const uint32_t n_units = n_items * R;
-    const uint32_t* id_src = a.use_plan ? a.plan.unique_ids : a.ids;
+    const uint32_t* id_src = use_plan ? a.plan.unique_ids : ids;
     const uint32_t gsh_e = a.ex.group_shift, gsh_s = a.has_shared ? a.sh.group_shift : gsh_e;
 
     // the fields of both sets as plain values (selected per unit below;
@@ -837,11 +857,11 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             rw[m] = unit % R;
             eid[m] = id_src[min(it[m], routes - 1)]; // n_routed <= routes
         }
-        res_v = a.residual[(uint64_t)(ri / R) * a.hidden + row_base + ri % R];
-        cw_v = a.weights[rq];
-        coi_v = (a.use_plan ? a.plan.out_idx : a.ids)[rq];
-        csl_v = (a.has_shared ? a.shared_logit : a.weights)[tq];
-        constexpr int NST = STG ? STAGE_FLOATS / 4 / 256 : 1;
+        res_v = residual[(uint64_t)(ri / R) * a.hidden + row_base + ri % R];
+        cw_v = rweights[rq];
+        coi_v = (use_plan ? a.plan.out_idx : ids)[rq];
+        csl_v = shared_logit[tq];
+        constexpr int NST = STG ? SF / 4 / 256 : 1;
         float4 stv[NST];
         uint32_t n4 = 0, n_st = 0;
         if (stage && u0 == 0) {
@@ -849,13 +869,28 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             n_st = n4 + (a.has_shared ? (T * I) / 4 : 0u);
         }
         if constexpr (STG) {
+            // PT: plan-ordered row of each staged element's route (routes
+            // the plan dropped, out of range, read row 0 and are not used)
+            uint32_t grow[PT ? NST : 1];
+            if constexpr (PT) {
+#pragma unroll
+                for (int q = 0; q < NST; ++q) {
+                    const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
+                    grow[q] = a.plan.out_idx[tk * K + min(i / (I / 4), K - 1)];
+                }
+            }
 #pragma unroll
             for (int q = 0; q < NST; ++q) {
                 // (passes that stage nothing read a.act[0])
                 const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
+                uint32_t ia = i;
+                if constexpr (PT) {
+                    const uint32_t k = i / (I / 4);
+                    ia = (grow[q] < a.tokens * K ? grow[q] : 0u) * (I / 4) + (i - k * (I / 4));
+                }
                 // I % 32 == 0: the shared rows start on a chunk
-                const float4* src = i < n4 || n_st == 0 ? reinterpret_cast<const float4*>(a.act) + i
-                                                        : reinterpret_cast<const float4*>(a.act_shared) + (i - n4);
+                const float4* src = i < n4 || n_st == 0 ? reinterpret_cast<const float4*>(a.act) + ia
+                                                        : reinterpret_cast<const float4*>(act_shared) + (i - n4);
                 stv[q] = *src;
             }
         }
@@ -890,7 +925,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                     // no branch: elements past n_st go to the never-read
                     // padding of the last chunk
                     const uint32_t i = threadIdx.x + 256u * q;
-                    const uint32_t d = i < n_st ? (i >> 3) * XP + (i & 7) * 4 : (STAGE_FLOATS / 32 - 1) * XP + 32;
+                    const uint32_t d = i < n_st ? (i >> 3) * XP + (i & 7) * 4 : (SF / 32 - 1) * XP + 32;
                     *reinterpret_cast<float4*>(&astage[d]) = stv[q];
                 }
             }
@@ -916,7 +951,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                 sc[m][c] = sb_bits<SBT>(scr[m][c]);
                 bi[m][c] = sb_bits<SBT>(bir[m][c]);
             }
-        if (ONE || (!STG && !a.use_plan)) {
+        if (ONE || (!STG && !use_plan)) {
             // one token, activations read from L2: every unit's loads in one
             // straight-line block (no token loop between them), so that they
             // are in flight together instead of one round trip per unit
@@ -927,7 +962,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                 const uint32_t unit = u0 + slot_id + SLOTS * m;
                 if (unit < n_units && live[m]) {
                     const bool shared = a.has_shared && it[m] == n_routed;
-                    const float* av = shared ? a.act_shared : a.act + (uint64_t)it[m] * I;
+                    const float* av = shared ? act_shared : a.act + (uint64_t)it[m] * I;
 #pragma unroll
                     for (int c = 0; c < CPL; ++c) {
                         const uint32_t ch = gl + LPR * c;
@@ -962,7 +997,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             uint32_t g0 = 0, n = 0;
             if (shared) {
                 n = T;
-            } else if (a.use_plan) {
+            } else if (use_plan) {
                 g0 = a.plan.groups[2 * it[m]];
                 n = a.plan.groups[2 * it[m] + 1];
             } else {
@@ -983,7 +1018,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
                             part = fmaf(sc[m][c], qx, fmaf(bi[m][c], xs[ch], part));
                         }
                     } else {
-                        const float* av = shared ? a.act_shared + (uint64_t)j * I : a.act + (uint64_t)(g0 + j) * I;
+                        const float* av = shared ? act_shared + (uint64_t)j * I : a.act + (uint64_t)(g0 + j) * I;
 #pragma unroll
                         for (int c = 0; c < CPL; ++c) {
                             const uint32_t ch = gl + LPR * c;
@@ -1010,7 +1045,7 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
     }
     if (threadIdx.x < routes) {
         c_w[threadIdx.x] = cw_v;
-        c_oi[threadIdx.x] = a.use_plan ? coi_v : threadIdx.x;
+        c_oi[threadIdx.x] = use_plan ? coi_v : threadIdx.x;
     }
     if (threadIdx.x < T)
         c_sw[threadIdx.x] = a.has_shared ? sigmoidf_(csl_v) : 0.0f;
@@ -1021,13 +1056,13 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
         for (uint32_t kk = 0; kk < K; ++kk) {
             const uint32_t route = t * K + kk;
             const uint32_t gi = c_oi[route];
-            const float y = gi < DEC_ROUTES ? ylds[gi][r] : 0.0f;
+            const float y = gi < NR ? ylds[gi][r] : 0.0f;
             moe = moe + c_w[route] * y;
         }
         const float rm = res_v + moe;
         const float sw = c_sw[t];
         const float sv = a.has_shared ? yshl[t][r] : 0.0f;
-        a.hidden_out[(uint64_t)t * a.hidden + row_base + r] = rm + sw * sv;
+        hidden_out[(uint64_t)t * a.hidden + row_base + r] = rm + sw * sv;
     }
 }
 
@@ -1445,6 +1480,36 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     hipExtLaunchKernelGGL((down_wide_kernel<SBT>), gw, dim3(WIDE_THREADS), 0, st, phase_event(d, 4), phase_event(d, 5), 0, da)
         PBM_DW();
 #undef PBM_DW
+        err = hipGetLastError();
+        if (err != hipSuccess)
+            return err;
+        if (d.next_norm_w && d.next_normed) {
+            next_norm_kernel<<<T, 256, 0, st>>>(d.hidden_out, d.next_norm_w, H, d.eps, d.next_normed);
+            err = hipGetLastError();
+        }
+        return err;
+    }
+    // several tokens: one workgroup per (row block, token) when a token's
+    // routed and shared activations fit the per-token staging buffer (the
+    // plan-mode loop over every route of the call runs one dependent round
+    // trip after another)
+    const bool per_token = use_plan && (uint64_t)(K + (da.has_shared ? 1u : 0u)) * I <= PT_STAGE_FLOATS &&
+                           I <= 1536 && H % PT_R == 0;
+    if (per_token) {
+        da.stage = true;
+        dim3 gp(H / PT_R, T);
+#define PBM_DNT(L, C, M)                                                                       \
+    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M, true, false, true>), gp, dim3(256), 0, st, \
+                          phase_event(d, 4), phase_event(d, 5), 0, da)
+        switch (I) {
+        case 256: PBM_DNT(8, 1, 4); break;
+        case 512: PBM_DNT(8, 2, 4); break;
+        case 768: PBM_DNT(8, 3, 4); break;
+        case 1024: PBM_DNT(16, 2, 4); break;
+        case 1536: PBM_DNT(16, 3, 4); break;
+        default: return hipErrorInvalidValue;
+        }
+#undef PBM_DNT
         err = hipGetLastError();
         if (err != hipSuccess)
             return err;
