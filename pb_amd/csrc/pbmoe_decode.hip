@@ -741,6 +741,142 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// kernel 2, several tokens with the routes given (routed by route_topk):
+// persistent waves, each over units (route, RPW consecutive rows) strided
+// by the grid's wave count; activations in route order [T*K][I].  A wave
+// holds two units' weights in registers (buffers A and B, alternating, so
+// no register copies): the next unit's weights load while this unit is
+// computed.  This unit's x row is loaded before the next unit's weights,
+// since a wave's loads complete in issue order: waiting for x then does not
+// wait for them.  Each route is its own unit (a token pair that shares an
+// expert reads its weights twice, mostly from the MALL), so every unit has
+// exactly one token.  The unit's x chunks are loaded with its weights, so
+// that each step waits only for loads issued a whole unit earlier.
+// ---------------------------------------------------------------------------
+template <int CPL, int RPW>
+struct UnitWeights {
+    uint4 wg[RPW][CPL], wu[RPW][CPL];
+    uint32_t sg[RPW][CPL], bg[RPW][CPL], su[RPW][CPL], bu[RPW][CPL]; // raw 16-bit scale / bias
+    float xv[CPL][32];                                                // the unit's x chunk(s)
+};
+
+template <int SBT, int CPL, int RPW>
+__global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
+{
+    __shared__ uint32_t sid[DEC_ROUTES];
+    const int lane = threadIdx.x & 63;
+    const uint32_t K = a.rp.k, H = a.hidden, I = a.ex.gate.rows;
+    const uint32_t routes = a.tokens * K;
+    for (uint32_t r = threadIdx.x; r < routes; r += 256)
+        sid[r] = a.ids[r];
+    __syncthreads();
+    const uint32_t row_tasks = I / RPW;
+    const uint32_t n_units = routes * row_tasks;
+    const uint32_t nw = gridDim.x * 4;
+    const uint32_t chunks = H / 32, gsh = a.ex.group_shift, gpr = H >> gsh;
+    // the expert set's fields as plain values (uniform)
+    const uint8_t* const base = a.ex.base;
+    const uint64_t stride = a.ex.stride;
+    const uint32_t count = a.ex.count;
+    const uint64_t gw_off = a.ex.gate.w_off, gs_off = a.ex.gate.s_off, gb_off = a.ex.gate.b_off;
+    const uint64_t uw_off = a.ex.up.w_off, us_off = a.ex.up.s_off, ub_off = a.ex.up.b_off;
+
+    // unconditional loads: a unit past the end loads the last unit again
+    auto load_w = [&](uint32_t u, UnitWeights<CPL, RPW>& W) {
+        const uint32_t uc = min(u, n_units - 1);
+        const uint32_t route = uc / row_tasks, row0 = (uc % row_tasks) * RPW;
+        uint32_t e = __builtin_amdgcn_readfirstlane(sid[route]);
+        e = e < count ? e : 0u;
+        const uint8_t* slot = base + (uint64_t)e * stride;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const uint32_t row = row0 + r;
+            const uint4* gw = reinterpret_cast<const uint4*>(slot + gw_off + (uint64_t)row * (H / 2));
+            const uint4* uw = reinterpret_cast<const uint4*>(slot + uw_off + (uint64_t)row * (H / 2));
+            const uint16_t* gs = reinterpret_cast<const uint16_t*>(slot + gs_off) + (uint64_t)row * gpr;
+            const uint16_t* gb = reinterpret_cast<const uint16_t*>(slot + gb_off) + (uint64_t)row * gpr;
+            const uint16_t* us = reinterpret_cast<const uint16_t*>(slot + us_off) + (uint64_t)row * gpr;
+            const uint16_t* ub = reinterpret_cast<const uint16_t*>(slot + ub_off) + (uint64_t)row * gpr;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t ch = min((uint32_t)(lane + WAVE * c), chunks - 1);
+                const uint32_t g = (ch * 32u) >> gsh;
+                W.wg[r][c] = gw[ch];
+                W.wu[r][c] = uw[ch];
+                W.sg[r][c] = gs[g];
+                W.bg[r][c] = gb[g];
+                W.su[r][c] = us[g];
+                W.bu[r][c] = ub[g];
+            }
+        }
+    };
+    auto load_x = [&](uint32_t u, UnitWeights<CPL, RPW>& W) {
+        const uint32_t uc = min(u, n_units - 1);
+        const float* xt = a.x + (uint64_t)((uc / row_tasks) / K) * H;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const float4* x4 = reinterpret_cast<const float4*>(xt + min((uint32_t)(lane + WAVE * c), chunks - 1) * 32);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 v = x4[q];
+                W.xv[c][4 * q] = v.x, W.xv[c][4 * q + 1] = v.y, W.xv[c][4 * q + 2] = v.z, W.xv[c][4 * q + 3] = v.w;
+            }
+        }
+    };
+    // branch-free apart from the stores: a load the compiler could sink into
+    // a branch here would be issued after the next unit's weights
+    auto compute = [&](uint32_t u, UnitWeights<CPL, RPW>& W) {
+        const uint32_t route = u / row_tasks, row0 = (u % row_tasks) * RPW;
+        const bool ok = __builtin_amdgcn_readfirstlane(sid[route]) < count;
+        float pg[RPW], pu[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            pg[r] = 0.0f, pu[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            // lanes past the row's last chunk hold a copy of it: weight 0
+            const float on = lane + WAVE * c < chunks ? 1.0f : 0.0f;
+            float xs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 32; q += 4)
+                xs += (W.xv[c][q] + W.xv[c][q + 1]) + (W.xv[c][q + 2] + W.xv[c][q + 3]);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const float qg = q4_chunk_qx_reg<RPW * CPL <= 2>(W.wg[r][c], W.xv[c]);
+                const float qu = q4_chunk_qx_reg<RPW * CPL <= 2>(W.wu[r][c], W.xv[c]);
+                pg[r] = fmaf(on, fmaf(sb_bits<SBT>(W.sg[r][c]), qg, sb_bits<SBT>(W.bg[r][c]) * xs), pg[r]);
+                pu[r] = fmaf(on, fmaf(sb_bits<SBT>(W.su[r][c]), qu, sb_bits<SBT>(W.bu[r][c]) * xs), pu[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const float g = wave_sum(pg[r]);
+            const float up = wave_sum(pu[r]);
+            if (ok && lane == r)
+                a.act[(uint64_t)route * I + row0 + r] = (g / (1.0f + expf(-g))) * up;
+        }
+        if (!ok && lane == 0)
+            atomicOr(a.status, ST_ROUTE_RANGE);
+    };
+    UnitWeights<CPL, RPW> A, B;
+    uint32_t u = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    load_w(u, A);
+    load_x(u, A);
+    while (u < n_units) {
+        load_w(u + nw, B);
+        load_x(u + nw, B);
+        compute(u, A);
+        u += nw;
+        if (u >= n_units)
+            break;
+        load_w(u + nw, A);
+        load_x(u + nw, A);
+        compute(u, B);
+        u += nw;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // kernel 3: down projection + combine for R output rows per workgroup.
 // Unit = (item, row) handled by LPR lanes with CPL chunks each.  When every
 // route's activations fit STAGE_FLOATS (one token, or two of C2's) they are
@@ -752,6 +888,7 @@ constexpr uint32_t STAGE_FLOATS = 12288; // activations staged (54 KB of LDS in 
 // routed + shared activations (27 KB of LDS), so that four workgroups fit a CU.
 constexpr uint32_t PT_STAGE_FLOATS = 6144;
 constexpr int PT_R = 8; // output rows per per-token workgroup: 8 x (K + 1) units in one pass
+constexpr int MULTI_RPW = 2; // rows per unit of gateup_multi_kernel
 // Staged chunk q (32 floats) sits at q * XP floats, so that the lanes'
 // 16-byte reads of consecutive chunks fall on distinct banks.
 constexpr int XP = 36;
@@ -869,14 +1006,23 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             n_st = n4 + (a.has_shared ? (T * I) / 4 : 0u);
         }
         if constexpr (STG) {
-            // PT: plan-ordered row of each staged element's route (routes
-            // the plan dropped, out of range, read row 0 and are not used)
+            // PT: the activation row of each staged element's route: the
+            // plan-ordered row (a.use_plan; routes the plan dropped, out of
+            // range, read row 0 and are not used) or the route itself
             uint32_t grow[PT ? NST : 1];
             if constexpr (PT) {
+                if (a.use_plan) {
 #pragma unroll
-                for (int q = 0; q < NST; ++q) {
-                    const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
-                    grow[q] = a.plan.out_idx[tk * K + min(i / (I / 4), K - 1)];
+                    for (int q = 0; q < NST; ++q) {
+                        const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
+                        grow[q] = a.plan.out_idx[tk * K + min(i / (I / 4), K - 1)];
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < NST; ++q) {
+                        const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
+                        grow[q] = tk * K + min(i / (I / 4), K - 1);
+                    }
                 }
             }
 #pragma unroll
@@ -1367,16 +1513,106 @@ static uint32_t gateup_rpw(const DecodeArgs& d, uint32_t* wgs)
 // routing, once per round.  C5 (1024 workgroups, two rounds): 98.0 ->
 // 89.5 us per layer; C2 (640 workgroups, one round): the extra launch
 // costs more than the routing it saves (23.7 -> 25.9 us).
+// Several tokens whose per-token activations fit the per-token down kernel:
+// routing in its own launch, the persistent gate/up kernel over routes and
+// the per-token down kernel (no dispatch plan).
+static bool multi_token_path(const DecodeArgs& d)
+{
+    const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
+    return T > 1 && (uint64_t)(K + (d.shared ? 1u : 0u)) * I <= PT_STAGE_FLOATS && I <= 1536 && I % 4 == 0 &&
+           H % PT_R == 0 && H <= 64 * 32 * 4;
+}
+
 static bool route_separately(const DecodeArgs& d)
 {
+    if (multi_token_path(d))
+        return true;
     uint32_t wgs = 0;
     gateup_rpw(d, &wgs);
     return wgs > GATEUP_RESIDENT_WGS;
 }
 
+// resident workgroups of gateup_multi_kernel per CU
+constexpr uint32_t MULTI_WGS_PER_CU = 4;
+
+template <int SBT>
+static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
+{
+    const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
+    ExpertArgs ea{};
+    ea.ex = d.ex;
+    ea.rp = d.rp;
+    ea.ids = d.ids;
+    ea.weights = d.weights;
+    ea.x = d.in_norm_w ? d.x_normed : d.x; // normalised by the router stage
+    ea.tokens = T;
+    ea.hidden = H;
+    ea.act = d.act;
+    ea.status = d.status;
+    constexpr int RPW = MULTI_RPW;
+    const uint32_t units = T * K * (I / RPW);
+    const uint32_t cus = 256;
+    const dim3 g1(std::min((units + 3) / 4, cus * MULTI_WGS_PER_CU));
+    const uint32_t cpl = (H / 32 + 63) / 64;
+    if (cpl <= 1)
+        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 1, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
+                              phase_event(d, 3), 0, ea);
+    else if (cpl <= 2)
+        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 2, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
+                              phase_event(d, 3), 0, ea);
+    else
+        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 4, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
+                              phase_event(d, 3), 0, ea);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return err;
+    DownArgs da{};
+    da.ex = d.ex;
+    da.has_shared = d.shared != nullptr;
+    if (da.has_shared)
+        da.sh = *d.shared;
+    da.act = d.act;
+    da.act_shared = d.act_shared;
+    da.shared_logit = d.shared_weight;
+    da.tokens = T;
+    da.k = K;
+    da.hidden = H;
+    da.ids = d.ids;
+    da.weights = d.weights;
+    da.plan = d.plan;
+    da.use_plan = false; // activations in route order
+    da.stage = true;
+    da.residual = d.residual;
+    da.hidden_out = d.hidden_out;
+    da.status = d.status;
+    dim3 gp(H / PT_R, T);
+#define PBM_DNT(L, C, M)                                                                       \
+    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M, true, false, true>), gp, dim3(256), 0, st, \
+                          phase_event(d, 4), phase_event(d, 5), 0, da)
+    switch (I) {
+    case 256: PBM_DNT(8, 1, 4); break;
+    case 512: PBM_DNT(8, 2, 4); break;
+    case 768: PBM_DNT(8, 3, 4); break;
+    case 1024: PBM_DNT(16, 2, 4); break;
+    case 1536: PBM_DNT(16, 3, 4); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef PBM_DNT
+    err = hipGetLastError();
+    if (err != hipSuccess)
+        return err;
+    if (d.next_norm_w && d.next_normed) {
+        next_norm_kernel<<<T, 256, 0, st>>>(d.hidden_out, d.next_norm_w, H, d.eps, d.next_normed);
+        err = hipGetLastError();
+    }
+    return err;
+}
+
 template <int SBT>
 static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool route_here)
 {
+    if (!route_here && multi_token_path(d))
+        return launch_multi_token<SBT>(st, d);
     const ExpertSet& ex = d.ex;
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = ex.gate.rows;
     const bool use_plan = T > 1;
