@@ -742,38 +742,60 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 
 // ---------------------------------------------------------------------------
 // kernel 2, several tokens with the routes given (routed by route_topk):
-// persistent waves, each over units (route, RPW consecutive rows) strided
-// by the grid's wave count; activations in route order [T*K][I].  A wave
-// holds two units' weights in registers (buffers A and B, alternating, so
-// no register copies): the next unit's weights load while this unit is
-// computed.  This unit's x row is loaded before the next unit's weights,
-// since a wave's loads complete in issue order: waiting for x then does not
-// wait for them.  Each route is its own unit (a token pair that shares an
-// expert reads its weights twice, mostly from the MALL), so every unit has
-// exactly one token.  The unit's x chunks are loaded with its weights, so
-// that each step waits only for loads issued a whole unit earlier.
+// grid (workgroups per token, tokens); the workgroups of token t stage its
+// x row in LDS once and their waves run over the token's units (route k,
+// RPW consecutive rows), strided by the waves of the token; activations in
+// route order [T*K][I].  A wave holds two units' weights in registers
+// (buffers A and B, alternating, so no register copies): the next unit's
+// weights load while this unit is computed.  x comes from LDS, so reading
+// it never waits for those loads (and the waves do not all read the same
+// few L2 lines: every unit would otherwise load the whole 8 KB row).  Each
+// route is its own unit (a token pair that shares an expert reads its
+// weights twice, mostly from the MALL).
 // ---------------------------------------------------------------------------
 template <int CPL, int RPW>
 struct UnitWeights {
     uint4 wg[RPW][CPL], wu[RPW][CPL];
     uint32_t sg[RPW][CPL], bg[RPW][CPL], su[RPW][CPL], bu[RPW][CPL]; // raw 16-bit scale / bias
-    float xv[CPL][32];                                                // the unit's x chunk(s)
 };
 
 template <int SBT, int CPL, int RPW>
 __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
 {
-    __shared__ uint32_t sid[DEC_ROUTES];
+    // staged chunk q (32 floats) at q * XQ floats: the lanes' 16-byte reads
+    // of consecutive chunks fall on distinct banks
+    constexpr int XQ = 36;
+    __shared__ __align__(16) float xl[WAVE * CPL * XQ];
+    __shared__ uint32_t sid[MAX_K];
     const int lane = threadIdx.x & 63;
     const uint32_t K = a.rp.k, H = a.hidden, I = a.ex.gate.rows;
-    const uint32_t routes = a.tokens * K;
-    for (uint32_t r = threadIdx.x; r < routes; r += 256)
-        sid[r] = a.ids[r];
+    const uint32_t t = blockIdx.y;
+    const uint32_t chunks = H / 32, gsh = a.ex.group_shift, gpr = H >> gsh;
+    {
+        // the token's route ids and its x row (coalesced), both loaded
+        // before either is stored; float4 slots past H / 4 hold zeros in
+        // chunks no lane reads
+        const uint32_t idv = a.ids[t * K + min((uint32_t)threadIdx.x, K - 1)];
+        const uint32_t nf = H / 4;
+        float4 v[2 * CPL];
+#pragma unroll
+        for (int j = 0; j < 2 * CPL; ++j)
+            v[j] = reinterpret_cast<const float4*>(a.x + (uint64_t)t * H)[min(threadIdx.x + 256u * j, nf - 1)];
+        if (threadIdx.x < K)
+            sid[threadIdx.x] = idv;
+#pragma unroll
+        for (int j = 0; j < 2 * CPL; ++j) {
+            const uint32_t f = threadIdx.x + 256u * j;
+            const bool in = f < nf;
+            float4 w = v[j];
+            w.x = in ? w.x : 0.0f, w.y = in ? w.y : 0.0f, w.z = in ? w.z : 0.0f, w.w = in ? w.w : 0.0f;
+            *reinterpret_cast<float4*>(&xl[(f >> 3) * XQ + (f & 7) * 4]) = w;
+        }
+    }
     __syncthreads();
     const uint32_t row_tasks = I / RPW;
-    const uint32_t n_units = routes * row_tasks;
+    const uint32_t n_units = K * row_tasks; // this token's
     const uint32_t nw = gridDim.x * 4;
-    const uint32_t chunks = H / 32, gsh = a.ex.group_shift, gpr = H >> gsh;
     // the expert set's fields as plain values (uniform)
     const uint8_t* const base = a.ex.base;
     const uint64_t stride = a.ex.stride;
@@ -784,8 +806,8 @@ __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
     // unconditional loads: a unit past the end loads the last unit again
     auto load_w = [&](uint32_t u, UnitWeights<CPL, RPW>& W) {
         const uint32_t uc = min(u, n_units - 1);
-        const uint32_t route = uc / row_tasks, row0 = (uc % row_tasks) * RPW;
-        uint32_t e = __builtin_amdgcn_readfirstlane(sid[route]);
+        const uint32_t k = uc / row_tasks, row0 = (uc % row_tasks) * RPW;
+        uint32_t e = __builtin_amdgcn_readfirstlane(sid[k]);
         e = e < count ? e : 0u;
         const uint8_t* slot = base + (uint64_t)e * stride;
 #pragma unroll
@@ -810,42 +832,35 @@ __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
             }
         }
     };
-    auto load_x = [&](uint32_t u, UnitWeights<CPL, RPW>& W) {
-        const uint32_t uc = min(u, n_units - 1);
-        const float* xt = a.x + (uint64_t)((uc / row_tasks) / K) * H;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const float4* x4 = reinterpret_cast<const float4*>(xt + min((uint32_t)(lane + WAVE * c), chunks - 1) * 32);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 v = x4[q];
-                W.xv[c][4 * q] = v.x, W.xv[c][4 * q + 1] = v.y, W.xv[c][4 * q + 2] = v.z, W.xv[c][4 * q + 3] = v.w;
-            }
-        }
-    };
-    // branch-free apart from the stores: a load the compiler could sink into
-    // a branch here would be issued after the next unit's weights
     auto compute = [&](uint32_t u, UnitWeights<CPL, RPW>& W) {
-        const uint32_t route = u / row_tasks, row0 = (u % row_tasks) * RPW;
-        const bool ok = __builtin_amdgcn_readfirstlane(sid[route]) < count;
+        const uint32_t k = u / row_tasks, row0 = (u % row_tasks) * RPW;
+        const bool ok = __builtin_amdgcn_readfirstlane(sid[k]) < count;
         float pg[RPW], pu[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
             pg[r] = 0.0f, pu[r] = 0.0f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            // lanes past the row's last chunk hold a copy of it: weight 0
-            const float on = lane + WAVE * c < chunks ? 1.0f : 0.0f;
-            float xs = 0.0f;
+            const uint32_t ch = lane + WAVE * c;
+            if (ch < chunks) {
+                const float4* x4 = reinterpret_cast<const float4*>(&xl[ch * XQ]);
+                float xv[32];
 #pragma unroll
-            for (int q = 0; q < 32; q += 4)
-                xs += (W.xv[c][q] + W.xv[c][q + 1]) + (W.xv[c][q + 2] + W.xv[c][q + 3]);
+                for (int q = 0; q < 8; ++q) {
+                    const float4 v = x4[q];
+                    xv[4 * q] = v.x, xv[4 * q + 1] = v.y, xv[4 * q + 2] = v.z, xv[4 * q + 3] = v.w;
+                }
+                float xs = 0.0f;
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                const float qg = q4_chunk_qx_reg<RPW * CPL <= 2>(W.wg[r][c], W.xv[c]);
-                const float qu = q4_chunk_qx_reg<RPW * CPL <= 2>(W.wu[r][c], W.xv[c]);
-                pg[r] = fmaf(on, fmaf(sb_bits<SBT>(W.sg[r][c]), qg, sb_bits<SBT>(W.bg[r][c]) * xs), pg[r]);
-                pu[r] = fmaf(on, fmaf(sb_bits<SBT>(W.su[r][c]), qu, sb_bits<SBT>(W.bu[r][c]) * xs), pu[r]);
+                for (int q = 0; q < 32; q += 4)
+                    xs += (xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3]);
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float qg = q4_chunk_qx_reg<RPW * CPL <= 2>(W.wg[r][c], xv);
+                    const float qu = q4_chunk_qx_reg<RPW * CPL <= 2>(W.wu[r][c], xv);
+                    pg[r] = fmaf(sb_bits<SBT>(W.sg[r][c]), qg, fmaf(sb_bits<SBT>(W.bg[r][c]), xs, pg[r]));
+                    pu[r] = fmaf(sb_bits<SBT>(W.su[r][c]), qu, fmaf(sb_bits<SBT>(W.bu[r][c]), xs, pu[r]));
+                }
             }
         }
 #pragma unroll
@@ -853,7 +868,7 @@ __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
             const float g = wave_sum(pg[r]);
             const float up = wave_sum(pu[r]);
             if (ok && lane == r)
-                a.act[(uint64_t)route * I + row0 + r] = (g / (1.0f + expf(-g))) * up;
+                a.act[(uint64_t)(t * K + k) * I + row0 + r] = (g / (1.0f + expf(-g))) * up;
         }
         if (!ok && lane == 0)
             atomicOr(a.status, ST_ROUTE_RANGE);
@@ -861,16 +876,13 @@ __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
     UnitWeights<CPL, RPW> A, B;
     uint32_t u = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     load_w(u, A);
-    load_x(u, A);
     while (u < n_units) {
         load_w(u + nw, B);
-        load_x(u + nw, B);
         compute(u, A);
         u += nw;
         if (u >= n_units)
             break;
         load_w(u + nw, A);
-        load_x(u + nw, A);
         compute(u, B);
         u += nw;
     }
@@ -1550,9 +1562,11 @@ static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
     ea.act = d.act;
     ea.status = d.status;
     constexpr int RPW = MULTI_RPW;
-    const uint32_t units = T * K * (I / RPW);
-    const uint32_t cus = 256;
-    const dim3 g1(std::min((units + 3) / 4, cus * MULTI_WGS_PER_CU));
+    // workgroups per token: every CU (256 on MI355X) holds MULTI_WGS_PER_CU
+    // workgroups, shared by the tokens (more workgroups than that only wait)
+    const uint32_t units = K * (I / RPW); // per token
+    const uint32_t per_token = std::max(1u, std::min((units + 3) / 4, 256u * MULTI_WGS_PER_CU / T));
+    const dim3 g1(per_token, T);
     const uint32_t cpl = (H / 32 + 63) / 64;
     if (cpl <= 1)
         hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 1, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
