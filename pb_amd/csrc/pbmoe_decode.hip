@@ -125,10 +125,12 @@ __device__ __forceinline__ void dense8_to_float(const uint32_t (&wr)[WDT == 0 ? 
     }
 }
 
+// tscale: null, or the per-token scale 1 / rms of the rows of x (already
+// formed; the sums of squares here are then unused)
 template <int WDT, int CR>
 __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, const float* x,
                                                uint32_t T, uint32_t H, float* out, uint32_t out_stride,
-                                               const float* norm_w, float eps)
+                                               const float* norm_w, float eps, const float* tscale = nullptr)
 {
     const int lane = threadIdx.x & 63;
     // 16-bit weights stay packed in registers until use
@@ -193,7 +195,9 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
             dot_pass(base, t, acc0, acc1, ss);
         }
         float s = wave_sum(acc0 + acc1);
-        if (norm_w)
+        if (tscale)
+            s *= tscale[t];
+        else if (norm_w)
             s *= inv_rms_of(ss, H, eps);
         if (lane == 0)
             out[(uint64_t)t * out_stride] = s;
@@ -205,7 +209,8 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
 // per group, the factored form of the dequantised row.
 template <int SBT, int CS>
 __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const float* x, uint32_t T, uint32_t H,
-                                            float* out, uint32_t out_stride, const float* norm_w, float eps)
+                                            float* out, uint32_t out_stride, const float* norm_w, float eps,
+                                            const float* tscale = nullptr)
 {
     const int lane = threadIdx.x & 63;
     const uint32_t chunks = H / 32, gpr = H >> m.gshift;
@@ -250,14 +255,24 @@ __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const
             }
         }
         float r = wave_sum(p);
-        if (norm_w)
+        if (tscale)
+            r *= tscale[t];
+        else if (norm_w)
             r *= inv_rms_of(ss, H, eps);
         if (lane == 0)
             out[(uint64_t)t * out_stride] = r;
     }
 }
 
-template <int WDT, int GDT, int SBT, int CR, int CS>
+// Several tokens (XL): grid (task workgroups, token groups of XL_FLOATS / H
+// tokens); a workgroup stages its group's rows of x in LDS by coalesced
+// loads (and the norm weight), so that a wave's row runs every token of the
+// group from LDS instead of one L2 round trip per token, and the groups'
+// workgroups run side by side.
+constexpr uint32_t XL_FLOATS = 8192; // staged x floats (32 KB)
+constexpr uint32_t XL_MAX_H = 4096;  // widest row of the staged variant (norm weight buffer)
+
+template <int WDT, int GDT, int SBT, int CR, int CS, bool XL>
 __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
 {
     const int lane = threadIdx.x & 63;
@@ -267,13 +282,17 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
     const uint32_t n_tasks = n_router + (Is ? Is + 1u : 0u);
     const uint32_t wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t n_waves = gridDim.x * 4;
-    for (uint32_t task = wave_id; task < n_tasks; task += n_waves) {
+    // task over tokens t0 .. t0 + nt - 1 with their rows at x (row t at
+    // x + t H); norm_w, tscale as for the row helpers
+    auto run_task = [&](uint32_t task, const float* x, uint32_t t0, uint32_t nt, const float* norm_w,
+                        const float* tscale) {
         if (task < n_router) {
             if constexpr (WDT == (int)DT_Q4)
-                q4_row_dots<SBT, CS>(a.router_q4, task, a.x, T, H, a.logits + task, n_router, a.norm_w, a.eps);
+                q4_row_dots<SBT, CS>(a.router_q4, task, x, nt, H, a.logits + (uint64_t)t0 * n_router + task, n_router,
+                                     norm_w, a.eps, tscale);
             else
-                dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, a.x, T, H, a.logits + task, n_router,
-                                        a.norm_w, a.eps);
+                dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, x, nt, H,
+                                        a.logits + (uint64_t)t0 * n_router + task, n_router, norm_w, a.eps, tscale);
         } else if (task < n_router + Is) {
             const uint32_t i = task - n_router;
             const ExpertSet& s = a.sh;
@@ -295,7 +314,7 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
                     bu[c] = sb_at<SBT>(s.base + s.up.b_off, gi);
                 }
             }
-            for (uint32_t t = 0; t < T; ++t) {
+            for (uint32_t t = 0; t < nt; ++t) {
                 // the nibble conversions do not depend on the token: without
                 // this opaque step the compiler hoists them out of the loop
                 // (32 floats per chunk and matrix: one wave per SIMD at CS = 4)
@@ -313,7 +332,7 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             float4 u, v;
-                            load_x8(a.x, (uint64_t)t * H + ch * 32 + 8 * q, a.norm_w, ch * 32 + 8 * q, u, v, ss);
+                            load_x8(x, (uint64_t)t * H + ch * 32 + 8 * q, norm_w, ch * 32 + 8 * q, u, v, ss);
                             xv[8 * q] = u.x, xv[8 * q + 1] = u.y, xv[8 * q + 2] = u.z, xv[8 * q + 3] = u.w;
                             xv[8 * q + 4] = v.x, xv[8 * q + 5] = v.y, xv[8 * q + 6] = v.z, xv[8 * q + 7] = v.w;
                         }
@@ -330,28 +349,73 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
                 }
                 float g = wave_sum(pg);
                 float u = wave_sum(pu);
-                if (a.norm_w) {
+                if (tscale) {
+                    g *= tscale[t], u *= tscale[t];
+                } else if (norm_w) {
                     const float inv = inv_rms_of(ss, H, a.eps);
                     g *= inv, u *= inv;
                 }
                 if (lane == 0)
-                    a.act_shared[(uint64_t)t * Is + i] = (g / (1.0f + expf(-g))) * u;
+                    a.act_shared[(uint64_t)(t0 + t) * Is + i] = (g / (1.0f + expf(-g))) * u;
             }
         } else if (a.sgate_w) {
             if constexpr (GDT == (int)DT_Q4)
-                q4_row_dots<SBT, CS>(a.sgate_q4, 0, a.x, T, H, a.shared_weight, 1, a.norm_w, a.eps);
+                q4_row_dots<SBT, CS>(a.sgate_q4, 0, x, nt, H, a.shared_weight + t0, 1, norm_w, a.eps, tscale);
             else
-                dense_row_dots<GDT, CR>(a.sgate_w, 0, a.x, T, H, a.shared_weight, 1, a.norm_w, a.eps);
+                dense_row_dots<GDT, CR>(a.sgate_w, 0, x, nt, H, a.shared_weight + t0, 1, norm_w, a.eps, tscale);
             // sigma applied by the consumer: shared_weight holds the gate logit
         } else if (lane == 0) {
-            for (uint32_t t = 0; t < T; ++t)
-                a.shared_weight[t] = 80.0f; // sigma(80) = 1 (metal/mod.rs:4666-4669)
+            for (uint32_t t = 0; t < nt; ++t)
+                a.shared_weight[t0 + t] = 80.0f; // sigma(80) = 1 (metal/mod.rs:4666-4669)
         }
+    };
+    if constexpr (!XL) {
+        for (uint32_t task = wave_id; task < n_tasks; task += n_waves)
+            run_task(task, a.x, 0, T, a.norm_w, nullptr);
+    } else {
+        __shared__ __align__(16) float xsh[XL_FLOATS];
+        __shared__ __align__(16) float nwsh[XL_MAX_H];
+        __shared__ float inv_sh[XL_FLOATS / 256]; // per token of the group (H >= 256)
+        const uint32_t TG = XL_FLOATS / H, H4 = H / 4;
+        const uint32_t g0 = blockIdx.y * TG, nt = min(TG, T - g0), n4 = nt * H4;
+        constexpr int PER = XL_FLOATS / 4 / 256; // float4 per thread
+        constexpr int NPER = XL_MAX_H / 4 / 256;
+        // unconditional loads and stores: slots past the data reload the last
+        // float4 and land in buffer slots nothing reads; without a norm, x
+        // stands in for the norm weight
+        const float4* nsrc = reinterpret_cast<const float4*>(a.norm_w ? a.norm_w : a.x);
+        const float4* src = reinterpret_cast<const float4*>(a.x + (uint64_t)g0 * H);
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            reinterpret_cast<float4*>(xsh)[threadIdx.x + 256u * j] = src[min(threadIdx.x + 256u * j, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < NPER; ++j)
+            reinterpret_cast<float4*>(nwsh)[threadIdx.x + 256u * j] = nsrc[min(threadIdx.x + 256u * j, H4 - 1)];
+        __syncthreads();
+        if (a.norm_w) {
+            // 1 / rms per token: wave w the tokens w, w + 4, ...
+            for (uint32_t t = threadIdx.x >> 6; t < nt; t += 4) {
+                float ss = 0.0f;
+                for (uint32_t i = lane; i < H4; i += 64) {
+                    const float4 q = reinterpret_cast<const float4*>(xsh)[t * H4 + i];
+                    ss = fmaf(q.x, q.x, ss), ss = fmaf(q.y, q.y, ss), ss = fmaf(q.z, q.z, ss), ss = fmaf(q.w, q.w, ss);
+                }
+                const float inv = inv_rms_of(ss, H, a.eps);
+                if (lane == 0)
+                    inv_sh[t] = inv;
+            }
+            __syncthreads();
+        }
+        if (wave_id < n_tasks)
+            run_task(wave_id, xsh, g0, nt, a.norm_w ? nwsh : nullptr, a.norm_w ? inv_sh : nullptr);
     }
     // the extra last workgroup (no tasks) writes the normalised rows for the
     // gate/up kernel, wave w the tokens w, w + 4, ...
     if (a.norm_w && blockIdx.x == gridDim.x - 1) {
-        for (uint32_t t = threadIdx.x >> 6; t < T; t += 4) {
+        // (XL: the tokens of this workgroup's group)
+        const uint32_t tb = XL ? blockIdx.y * (XL_FLOATS / H) : 0u;
+        const uint32_t te = XL ? min(tb + XL_FLOATS / H, T) : T;
+        for (uint32_t t = tb + (threadIdx.x >> 6); t < te; t += 4) {
             const float* xr = a.x + (uint64_t)t * H;
             float ss = 0.0f;
             for (uint32_t i = (uint32_t)lane * 4; i < H; i += 256) {
@@ -1463,14 +1527,25 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     const uint32_t cs = (d.hidden / 32 + 63) / 64;
     if (cr > 16 || cs > 4)
         return hipErrorInvalidValue;
+    // four tokens or more: x staged in LDS per group of tokens (with two, the
+    // staging round trip before the weight loads costs more than it saves:
+    // C2 6.2 -> 7.0 us)
+    const bool xl = d.tokens >= 4 && d.hidden <= XL_MAX_H && d.hidden >= 256 && d.hidden % 4 == 0;
+    const uint32_t xl_groups = xl ? (d.tokens + XL_FLOATS / d.hidden - 1) / (XL_FLOATS / d.hidden) : 1u;
     // router/gate dtypes: the benchmark layers use f16 for both; other
     // combinations share the f16 gate path only when the gate is f16
     const uint32_t gdt = a.sgate_w ? d.sgate_dtype : d.router_dtype;
     const uint32_t wdt = a.experts ? d.router_dtype : gdt;
     const uint32_t sbt = a.shared_rows ? a.sh.sb_dtype : 1u;
 #define PBM_RS(W, G, S, CRV, CSV)                                                              \
-    hipExtLaunchKernelGGL((router_stage_kernel<W, G, S, CRV, CSV>), dim3(blocks), dim3(256), 0, st, \
-                          phase_event(d, 0), phase_event(d, 1), 0, a)
+    do {                                                                                       \
+        if (xl)                                                                                \
+            hipExtLaunchKernelGGL((router_stage_kernel<W, G, S, CRV, CSV, true>), dim3(blocks, xl_groups), \
+                                  dim3(256), 0, st, phase_event(d, 0), phase_event(d, 1), 0, a); \
+        else                                                                                   \
+            hipExtLaunchKernelGGL((router_stage_kernel<W, G, S, CRV, CSV, false>), dim3(blocks), dim3(256), 0, \
+                                  st, phase_event(d, 0), phase_event(d, 1), 0, a);             \
+    } while (0)
 #define PBM_RS_CS(W, G, S, CRV)                                                                \
     do {                                                                                       \
         if (cs <= 1) PBM_RS(W, G, S, CRV, 1);                                                  \
