@@ -1289,6 +1289,142 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// kernel 3, several tokens (routes given, activations in route order):
+// grid (workgroups per token, tokens).  A workgroup stages its token's K
+// routed and shared activation rows in LDS once; each wave then computes
+// whole output rows, strided over the token's workgroups.  Lane l takes
+// the (item, 32-column chunk) slots l, l + 64, ... of a row and folds the
+// item's combine weight (the route weight, or sigma of the shared gate
+// logit) into its partial sum, so one wave reduction gives the row:
+// h = r + sum over lanes of c_m (s q.x + b sum x).  The next row's weights
+// load while this row is computed (buffers A and B, alternating: no
+// register copies).
+// ---------------------------------------------------------------------------
+constexpr uint32_t ROWS_CHUNKS = PT_STAGE_FLOATS / 32; // staged chunks (<= 3 slots per lane)
+
+template <int NCH>
+struct RowWeights {
+    uint4 w[NCH];
+    uint32_t sr[NCH], br[NCH]; // raw 16-bit scale / bias
+    float res;                 // residual of the row
+};
+
+template <int SBT, int NCH>
+__global__ __launch_bounds__(256) void down_rows_kernel(DownArgs a)
+{
+    __shared__ __align__(16) float astage[ROWS_CHUNKS * XP];
+    __shared__ float xsl[ROWS_CHUNKS]; // per-chunk sums of the staged activations
+    __shared__ float cwl[MAX_K + 1];   // combine weight per item
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.y, K = a.k, H = a.hidden, I = a.ex.down.cols;
+    const uint32_t cpi = I / 32; // chunks per item
+    const uint32_t n_items = K + (a.has_shared ? 1u : 0u);
+    const uint32_t n_ch = n_items * cpi;
+    const uint32_t n4 = n_ch * 8, r4 = K * (I / 4); // staged float4, routed ones
+    constexpr int NST = PT_STAGE_FLOATS / 4 / 256;
+    // every load issued before any is used, none in a branch: activations,
+    // combine inputs, the slots' expert ids
+    float4 stv[NST];
+#pragma unroll
+    for (int q = 0; q < NST; ++q) {
+        const uint32_t i = min(threadIdx.x + 256u * q, n4 - 1);
+        stv[q] = i < r4 ? reinterpret_cast<const float4*>(a.act + (uint64_t)t * K * I)[i]
+                        : reinterpret_cast<const float4*>(a.act_shared + (uint64_t)t * I)[i - r4];
+    }
+    const uint32_t mi = min((uint32_t)threadIdx.x, n_items - 1);
+    const float rw = a.weights[t * K + min(mi, K - 1)];
+    const float lg = (a.has_shared ? a.shared_logit : a.weights)[a.has_shared ? t : 0u];
+    uint32_t eid[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        const uint32_t m = min((uint32_t)(lane + 64 * j) / cpi, n_items - 1);
+        eid[j] = a.ids[t * K + min(m, K - 1)];
+    }
+#pragma unroll
+    for (int q = 0; q < NST; ++q) {
+        // elements past n4 go to the never-read padding of the last chunk
+        const uint32_t i = threadIdx.x + 256u * q;
+        const uint32_t d = i < n4 ? (i >> 3) * XP + (i & 7) * 4 : (ROWS_CHUNKS - 1) * XP + 32;
+        *reinterpret_cast<float4*>(&astage[d]) = stv[q];
+    }
+    if (threadIdx.x < n_items)
+        cwl[threadIdx.x] = mi < K ? rw : sigmoidf_(lg);
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < n_ch; q += 256) {
+        const float4* c4 = reinterpret_cast<const float4*>(astage + q * XP);
+        float sum = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float4 f = c4[v];
+            sum += (f.x + f.y) + (f.z + f.w);
+        }
+        xsl[q] = sum;
+    }
+    __syncthreads();
+
+    // this lane's slots: item, chunk, expert base and offsets, combine weight
+    // (0 for slots past the last chunk and for out-of-range routes, whose
+    // weights are read from expert 0 and not used)
+    const uint8_t* sbase[NCH];
+    uint64_t s_w[NCH], s_s[NCH], s_b[NCH];
+    uint32_t s_gsh[NCH], s_ch[NCH], s_q[NCH];
+    float s_cw[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        const uint32_t f = lane + 64 * j;
+        const uint32_t m = min(f / cpi, n_items - 1);
+        const bool sh = a.has_shared && m == K;
+        const bool ok = f < n_ch && (sh || eid[j] < a.ex.count);
+        sbase[j] = sh ? a.sh.base : a.ex.base + (uint64_t)(ok ? eid[j] : 0u) * a.ex.stride;
+        s_w[j] = sh ? a.sh.down.w_off : a.ex.down.w_off;
+        s_s[j] = sh ? a.sh.down.s_off : a.ex.down.s_off;
+        s_b[j] = sh ? a.sh.down.b_off : a.ex.down.b_off;
+        s_gsh[j] = sh ? a.sh.group_shift : a.ex.group_shift;
+        s_ch[j] = f < n_ch ? f % cpi : 0u;
+        s_q[j] = f < n_ch ? f : 0u;
+        s_cw[j] = ok ? cwl[m] : 0.0f;
+    }
+    const float* res_row = a.residual + (uint64_t)t * H;
+    auto load_row = [&](uint32_t r, RowWeights<NCH>& W) {
+        const uint32_t rc = min(r, H - 1);
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            const uint32_t gpr = I >> s_gsh[j];
+            const uint32_t g = (s_ch[j] * 32u) >> s_gsh[j];
+            W.w[j] = *reinterpret_cast<const uint4*>(sbase[j] + s_w[j] + (uint64_t)rc * (I / 2) + s_ch[j] * 16u);
+            W.sr[j] = reinterpret_cast<const uint16_t*>(sbase[j] + s_s[j])[(uint64_t)rc * gpr + g];
+            W.br[j] = reinterpret_cast<const uint16_t*>(sbase[j] + s_b[j])[(uint64_t)rc * gpr + g];
+        }
+        W.res = res_row[rc];
+    };
+    auto compute = [&](uint32_t r, RowWeights<NCH>& W) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            const float qx = q4_chunk_q(W.w[j], astage + s_q[j] * XP);
+            acc = fmaf(s_cw[j], fmaf(sb_bits<SBT>(W.sr[j]), qx, sb_bits<SBT>(W.br[j]) * xsl[s_q[j]]), acc);
+        }
+        const float y = wave_sum(acc);
+        if (lane == 0)
+            a.hidden_out[(uint64_t)t * H + r] = W.res + y;
+    };
+    RowWeights<NCH> A, B;
+    const uint32_t step = gridDim.x * 4;
+    uint32_t r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    load_row(r, A);
+    while (r < H) {
+        load_row(r + step, B);
+        compute(r, A);
+        r += step;
+        if (r >= H)
+            break;
+        load_row(r + step, A);
+        compute(r, B);
+        r += step;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // kernel 3, wide variant: one token whose routed + shared activations are
 // too large for the staging buffer of down_combine_kernel (C5: 9 items x
 // 2048 columns).  WIDE_R = 16 output rows per workgroup, so that one staged
@@ -1621,6 +1757,8 @@ static bool route_separately(const DecodeArgs& d)
 
 // resident workgroups of gateup_multi_kernel per CU
 constexpr uint32_t MULTI_WGS_PER_CU = 4;
+// resident workgroups of down_rows_kernel per CU
+constexpr uint32_t ROWS_WGS_PER_CU = 2;
 
 template <int SBT>
 static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
@@ -1674,19 +1812,18 @@ static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
     da.residual = d.residual;
     da.hidden_out = d.hidden_out;
     da.status = d.status;
-    dim3 gp(H / PT_R, T);
-#define PBM_DNT(L, C, M)                                                                       \
-    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M, true, false, true>), gp, dim3(256), 0, st, \
-                          phase_event(d, 4), phase_event(d, 5), 0, da)
-    switch (I) {
-    case 256: PBM_DNT(8, 1, 4); break;
-    case 512: PBM_DNT(8, 2, 4); break;
-    case 768: PBM_DNT(8, 3, 4); break;
-    case 1024: PBM_DNT(16, 2, 4); break;
-    case 1536: PBM_DNT(16, 3, 4); break;
-    default: return hipErrorInvalidValue;
-    }
-#undef PBM_DNT
+    // rows: workgroups per token so that the grid is about four per CU
+    const uint32_t nch = ((K + (da.has_shared ? 1u : 0u)) * (I / 32) + 63) / 64;
+    const dim3 gr(std::max(1u, std::min(H / 4, 256u * ROWS_WGS_PER_CU / T)), T);
+    if (nch <= 1)
+        hipExtLaunchKernelGGL((down_rows_kernel<SBT, 1>), gr, dim3(256), 0, st, phase_event(d, 4), phase_event(d, 5),
+                              0, da);
+    else if (nch <= 2)
+        hipExtLaunchKernelGGL((down_rows_kernel<SBT, 2>), gr, dim3(256), 0, st, phase_event(d, 4), phase_event(d, 5),
+                              0, da);
+    else
+        hipExtLaunchKernelGGL((down_rows_kernel<SBT, 3>), gr, dim3(256), 0, st, phase_event(d, 4), phase_event(d, 5),
+                              0, da);
     err = hipGetLastError();
     if (err != hipSuccess)
         return err;
