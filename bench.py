@@ -507,6 +507,31 @@ def stack_bytes_per_token(acfg, mcfg, layers: int, position: int) -> dict:
     return {"attention": attn * layers, "moe": moe * layers, "total": (attn + moe) * layers}
 
 
+STACK_KERNELS = ("qkv_rows", "attn_chunk", "attn_merge", "o_rows", "router_stage", "route_gateup", "down_combine")
+
+
+def stack_kernel_times(ctx, ev, token, layers: int, tokens: int = 4) -> dict:
+    """Mean duration of each kernel of a stack layer over `tokens` eager
+    tokens: 14 hipEvents per layer call attached to the dispatch packets
+    (pbmoe_set_phase_events; the first 6 time the MoE layer's three kernels,
+    the other 8 the four attention kernels)."""
+    from pb_amd import abi
+    sets = [[ev.create() for _ in range(14)] for _ in range(tokens * layers)]
+    it = iter(sets)
+
+    def arm():
+        arr = (C.c_void_p * 14)(*[e.value for e in next(it)])
+        abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 14))
+
+    for _ in range(tokens):
+        token(arm=arm)
+    abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, None, 0))
+    ctx.sync()
+    order = (6, 8, 10, 12, 0, 2, 4)  # start event of each kernel in STACK_KERNELS order
+    return {nm: float(np.mean([ev.elapsed_ms(e[i], e[i + 1]) * 1e3 for e in sets]))
+            for nm, i in zip(STACK_KERNELS, order)}
+
+
 def bench_stack(args, ctx, ev) -> dict:
     """Workload C4: one token through the 48-layer decode stack —
     per layer the GQA attention block (pbmoe_attention_decode: input RMSNorm
@@ -550,10 +575,12 @@ def bench_stack(args, ctx, ev) -> dict:
 
     fused = args.stack_norms == "fused"
 
-    def token(parts=("attn", "moe")):
+    def token(parts=("attn", "moe"), arm=None):
         bufs = ((x_a, h_a), (x_b, h_b))
         for l in range(L):
             (x, h), (xn, hn) = bufs[l % 2], bufs[(l + 1) % 2]
+            if arm is not None:
+                arm()
             if fused:
                 if "attn" in parts:
                     atts[l].decode(h, h, pos, mid, input_norm=atts[l].input_norm)
@@ -590,6 +617,9 @@ def bench_stack(args, ctx, ev) -> dict:
     gbps = nbytes["total"] / (ms * 1e-3) / 1e9
     print(f"[bench] stack: {ms:.3f} ms/token ({1e3 / ms:.1f} tokens/s); attention-only {res['attention']:.3f} ms, "
           f"MoE-only {res['moe']:.3f} ms; {gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    kernels_us = stack_kernel_times(ctx, ev, token, L)
+    print("[bench] stack kernels (us, eager, per layer): "
+          + ", ".join(f"{k} {v:.2f}" for k, v in kernels_us.items()), file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_stack_baseline(acfg, mcfg, [h for _, h in moes[:2]], pos, keys, vals, args.cpu_seconds)
@@ -615,6 +645,7 @@ def bench_stack(args, ctx, ev) -> dict:
                    "quant": "q4 affine g64 f16 scale/bias (zero-mean)"},
         "tokens_per_s": round(1e3 / ms, 2),
         "phase_ms": {"attention_only": round(res["attention"], 4), "moe_only": round(res["moe"], 4)},
+        "kernels_us": {k: round(v, 3) for k, v in kernels_us.items()},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "whole token (all kernels of the 48 layers)", "bytes_per_token": nbytes["total"],

@@ -204,7 +204,10 @@ int pbmoe_sync(pbmoe_ctx* ctx);
  * calls attach events[2i] / events[2i+1] (hipEvent_t) as the start / stop
  * events of kernel i's dispatch packet.  Decode and whole-layer calls:
  * 0 router stage, 1 gate/up, 2 down + combine.  Grouped prefill (more than
- * 16 tokens): 0 gate/up GEMM, 1 down GEMM, 2 combine.  count == 0 disables. */
+ * 16 tokens): 0 gate/up GEMM, 1 down GEMM, 2 combine.  With count == 14,
+ * events[6 + 2i] / events[7 + 2i] also time pbmoe_attention_decode's kernel
+ * i: 0 q/k/v projections, 1 chunk partials, 2 merge, 3 o_proj + residual.
+ * count == 0 disables.  Timed calls are not for graph capture. */
 int pbmoe_set_phase_events(pbmoe_ctx* ctx, void* const* events, uint32_t count);
 /* Measurement reference (no counterpart in the reference): read the device
  * buffer src[0, bytes) once with one 16-byte load per lane, the access shape

@@ -115,6 +115,7 @@ struct pbmoe_ctx {
     uint32_t cus = 0;            // compute units of the device
     hipEvent_t phase_ev[6] = {};
     bool phase_timing = false;
+    hipEvent_t attn_ev[8] = {}; // null unless 14 phase events were set
 };
 
 namespace {
@@ -534,22 +535,26 @@ PBMOE_API int pbmoe_sync(pbmoe_ctx* ctx)
 // reference's FlashMoeTimingBuckets / record_detailed_timing, types.rs:600-619,
 // runtime/mod.rs:1470): events (hipEvent_t) 2i / 2i+1 are the start / stop
 // events of kernel i (router stage, gate/up, down+combine), attached to the
-// dispatch packets.
+// dispatch packets; 8 more time the attention decode kernels.
 PBMOE_API int pbmoe_set_phase_events(pbmoe_ctx* ctx, void* const* events, uint32_t count)
 {
     if (!ctx)
         return fail(PBMOE_ERR_INVALID_ARGUMENT, "ctx is null");
     if (count == 0) {
         ctx->phase_timing = false;
+        for (hipEvent_t& e : ctx->attn_ev)
+            e = nullptr;
         return ok();
     }
-    if (count != 6 || !events)
-        return fail(PBMOE_ERR_INVALID_ARGUMENT, "phase timing takes exactly 6 events (or 0 to disable)");
-    for (uint32_t i = 0; i < 6; ++i) {
+    if ((count != 6 && count != 14) || !events)
+        return fail(PBMOE_ERR_INVALID_ARGUMENT, "phase timing takes 6 or 14 events (or 0 to disable)");
+    for (uint32_t i = 0; i < count; ++i)
         if (!events[i])
             return fail(PBMOE_ERR_INVALID_ARGUMENT, "phase event %u is null", i);
+    for (uint32_t i = 0; i < 6; ++i)
         ctx->phase_ev[i] = static_cast<hipEvent_t>(events[i]);
-    }
+    for (uint32_t i = 0; i < 8; ++i)
+        ctx->attn_ev[i] = count == 14 ? static_cast<hipEvent_t>(events[6 + i]) : nullptr;
     ctx->phase_timing = true;
     return ok();
 }
@@ -1958,6 +1963,8 @@ PBMOE_API int pbmoe_attention_decode(pbmoe_ctx* ctx, uint32_t layer, const float
     a.qkv = reinterpret_cast<float*>(base);
     a.part = reinterpret_cast<float*>(base + qkv_bytes);
     a.attn_out = attn_out ? attn_out : reinterpret_cast<float*>(base + qkv_bytes + part_bytes);
+    for (int i = 0; i < 8; ++i)
+        a.ev[i] = ctx->phase_timing ? ctx->attn_ev[i] : nullptr;
     HIP_TRY(pbmoe::launch_attention_decode(ctx->stream, a));
     return ok();
 }

@@ -421,28 +421,29 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
         out[i] = (h[i] * scale) * w[i];
 }
 
+// e0, e1: start / stop events of the dispatch, or null
 template <int SBT, int RPW, bool NORM>
-static hipError_t launch_rows(hipStream_t st, const RowsArgs& r)
+static hipError_t launch_rows(hipStream_t st, const RowsArgs& r, hipEvent_t e0, hipEvent_t e1)
 {
     const uint32_t total = r.first[r.n_mat];
     const uint32_t cols = r.m[0].cols;
     const uint32_t cpl = (cols / 32 + 63) / 64;
     const dim3 grid((total / RPW + 3) / 4);
     if (cpl <= 1)
-        hipLaunchKernelGGL((q4_rows_kernel<SBT, 1, RPW, NORM>), grid, dim3(256), 0, st, r);
+        hipExtLaunchKernelGGL((q4_rows_kernel<SBT, 1, RPW, NORM>), grid, dim3(256), 0, st, e0, e1, 0, r);
     else if (cpl <= 2)
-        hipLaunchKernelGGL((q4_rows_kernel<SBT, 2, RPW, NORM>), grid, dim3(256), 0, st, r);
+        hipExtLaunchKernelGGL((q4_rows_kernel<SBT, 2, RPW, NORM>), grid, dim3(256), 0, st, e0, e1, 0, r);
     else if (cpl <= 4)
-        hipLaunchKernelGGL((q4_rows_kernel<SBT, 4, RPW, NORM>), grid, dim3(256), 0, st, r);
+        hipExtLaunchKernelGGL((q4_rows_kernel<SBT, 4, RPW, NORM>), grid, dim3(256), 0, st, e0, e1, 0, r);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 template <int SBT, int RPW>
-static hipError_t launch_rows(hipStream_t st, const RowsArgs& r)
+static hipError_t launch_rows(hipStream_t st, const RowsArgs& r, hipEvent_t e0, hipEvent_t e1)
 {
-    return r.norm_w ? launch_rows<SBT, RPW, true>(st, r) : launch_rows<SBT, RPW, false>(st, r);
+    return r.norm_w ? launch_rows<SBT, RPW, true>(st, r, e0, e1) : launch_rows<SBT, RPW, false>(st, r, e0, e1);
 }
 
 // rows per wave: 2 for q/k/v (640 workgroups at C4), 1 for o_proj (512
@@ -467,16 +468,29 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
     r.eps = a.post_eps;
     r.residual = nullptr;
     r.y = a.qkv;
-    hipError_t e = a.sb_dtype == 2 ? launch_rows<2, RPW_QKV>(st, r) : launch_rows<1, RPW_QKV>(st, r);
+    hipError_t e = a.sb_dtype == 2 ? launch_rows<2, RPW_QKV>(st, r, a.ev[0], a.ev[1])
+                                  : launch_rows<1, RPW_QKV>(st, r, a.ev[0], a.ev[1]);
     if (e != hipSuccess)
         return e;
     // 2. chunk partials
     const uint32_t chunks = (a.position + 1 + CH - 1) / CH;
     switch (nq) {
-    case 1: hipLaunchKernelGGL((attn_chunk_kernel<1>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((attn_chunk_kernel<2>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 2), dim3(256), 0, st, a); break;
+    case 1:
+        hipExtLaunchKernelGGL((attn_chunk_kernel<1>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a.ev[2], a.ev[3],
+                              0, a);
+        break;
+    case 2:
+        hipExtLaunchKernelGGL((attn_chunk_kernel<2>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a.ev[2], a.ev[3],
+                              0, a);
+        break;
+    case 4:
+        hipExtLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 1), dim3(256), 0, st, a.ev[2], a.ev[3],
+                              0, a);
+        break;
+    case 8:
+        hipExtLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 2), dim3(256), 0, st, a.ev[2], a.ev[3],
+                              0, a);
+        break;
     default: return hipErrorInvalidValue;
     }
     if ((e = hipGetLastError()) != hipSuccess)
@@ -484,8 +498,8 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
     // 3. merge
     if (chunks > MERGE_MAX_CHUNKS)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads), dim3(256), 0, st, (const float*)a.part, chunks,
-                       a.attn_out);
+    hipExtLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads), dim3(256), 0, st, a.ev[4], a.ev[5], 0,
+                          (const float*)a.part, chunks, a.attn_out);
     if ((e = hipGetLastError()) != hipSuccess)
         return e;
     // 4. o_proj + residual
@@ -498,7 +512,8 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
     o.norm_w = nullptr;
     o.residual = a.residual;
     o.y = a.hidden_out;
-    e = a.sb_dtype == 2 ? launch_rows<2, RPW_O>(st, o) : launch_rows<1, RPW_O>(st, o);
+    e = a.sb_dtype == 2 ? launch_rows<2, RPW_O>(st, o, a.ev[6], a.ev[7])
+                          : launch_rows<1, RPW_O>(st, o, a.ev[6], a.ev[7]);
     if (e != hipSuccess)
         return e;
     // 5. post-attention RMSNorm

@@ -254,6 +254,9 @@ struct AttnArgs {
     // scratch
     float* qkv;            // [(q_heads + 2 kv_heads) * head_dim]
     float* part;           // [q_heads][chunks][head_dim + 2]
+    // start/stop events of q/k/v, chunk partials, merge, o_proj (all null:
+    // untimed)
+    hipEvent_t ev[8];
 };
 
 constexpr uint32_t ATTN_CHUNK = 64; // positions per attention workgroup
