@@ -960,10 +960,9 @@ __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
 // read from L2 per unit.
 // ---------------------------------------------------------------------------
 constexpr uint32_t STAGE_FLOATS = 12288; // activations staged (54 KB of LDS in XP-padded chunks)
-// Per-token variant (several tokens, grid H / DOWN_R x tokens): one token's
-// routed + shared activations (27 KB of LDS), so that four workgroups fit a CU.
+// Several tokens (down_rows_kernel): one token's routed + shared activations
+// (27 KB of LDS).
 constexpr uint32_t PT_STAGE_FLOATS = 6144;
-constexpr int PT_R = 8; // output rows per per-token workgroup: 8 x (K + 1) units in one pass
 constexpr int MULTI_RPW = 2; // rows per unit of gateup_multi_kernel
 // Staged chunk q (32 floats) sits at q * XP floats, so that the lanes'
 // 16-byte reads of consecutive chunks fall on distinct banks.
@@ -991,41 +990,34 @@ struct DownArgs {
 // whose activations never fit STAGE_FLOATS, such as I = 2048 with K = 8).
 // ONE: one token without the dispatch plan only (the token-loop path is not
 // compiled, which keeps the registers of the straight-line path low).
-// PT: several tokens, workgroup (row block, token blockIdx.y) does the
-// one-token work for its token: the token's K routes (ids, weights and
-// combine in route order) and shared expert, with the routes' activation
-// rows gathered from the plan-ordered buffer through the plan's output
-// index (a.stage: they fit PT_STAGE_FLOATS).
-template <int SBT, int LPR, int CPL, int MAXR, bool STG, bool ONE = false, bool PT = false>
+template <int SBT, int LPR, int CPL, int MAXR, bool STG, bool ONE = false>
 __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
 {
-    constexpr int R = PT ? PT_R : DOWN_R;
+    constexpr int R = DOWN_R;
     constexpr int SLOTS = 256 / LPR;
-    constexpr uint32_t SF = PT ? PT_STAGE_FLOATS : STAGE_FLOATS;
-    constexpr int NT = PT ? 1 : DEC_T;               // tokens of one workgroup
-    constexpr int NR = PT ? DEC_ROUTES / DEC_T : DEC_ROUTES; // routes of one workgroup
+    constexpr uint32_t SF = STAGE_FLOATS;
+    constexpr int NR = DEC_ROUTES;
     __shared__ float ylds[NR][R];
-    __shared__ float yshl[NT][R];
+    __shared__ float yshl[DEC_T][R];
     __shared__ float c_w[NR];    // combine inputs, loaded at the start
     __shared__ uint32_t c_oi[NR];
-    __shared__ float c_sw[NT];
+    __shared__ float c_sw[DEC_T];
     __shared__ __align__(16) float astage[STG ? SF / 32 * XP : 4];
     __shared__ float xsl[STG ? SF / 32 : 4]; // per-chunk sums of the staged activations
     const bool stage = STG && a.stage;
     const int gl = threadIdx.x % LPR;
     const int slot_id = threadIdx.x / LPR;
     const uint32_t row_base = blockIdx.x * R;
-    const uint32_t tk = PT ? blockIdx.y : 0u; // this workgroup's token (PT)
-    const uint32_t T = PT ? 1u : a.tokens, K = a.k;
+    const uint32_t T = a.tokens, K = a.k;
     const uint32_t I = a.ex.down.cols;
     const uint32_t routes = T * K;
-    const bool use_plan = !PT && a.use_plan;
-    const uint32_t* const ids = a.ids + tk * K;
-    const float* const rweights = a.weights + tk * K;
-    const float* const residual = a.residual + (uint64_t)tk * a.hidden;
-    float* const hidden_out = a.hidden_out + (uint64_t)tk * a.hidden;
-    const float* const act_shared = a.act_shared + (uint64_t)tk * I;
-    const float* const shared_logit = a.has_shared ? a.shared_logit + tk : rweights;
+    const bool use_plan = a.use_plan;
+    const uint32_t* const ids = a.ids;
+    const float* const rweights = a.weights;
+    const float* const residual = a.residual;
+    float* const hidden_out = a.hidden_out;
+    const float* const act_shared = a.act_shared;
+    const float* const shared_logit = a.has_shared ? a.shared_logit : rweights;
 
     // Load order.  Every load below is issued before anything waits on it,
     // and none sits in a branch (a load inside a divergent branch is waited
@@ -1082,36 +1074,12 @@ __global__ __launch_bounds__(256) void down_combine_kernel(DownArgs a)
             n_st = n4 + (a.has_shared ? (T * I) / 4 : 0u);
         }
         if constexpr (STG) {
-            // PT: the activation row of each staged element's route: the
-            // plan-ordered row (a.use_plan; routes the plan dropped, out of
-            // range, read row 0 and are not used) or the route itself
-            uint32_t grow[PT ? NST : 1];
-            if constexpr (PT) {
-                if (a.use_plan) {
-#pragma unroll
-                    for (int q = 0; q < NST; ++q) {
-                        const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
-                        grow[q] = a.plan.out_idx[tk * K + min(i / (I / 4), K - 1)];
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < NST; ++q) {
-                        const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
-                        grow[q] = tk * K + min(i / (I / 4), K - 1);
-                    }
-                }
-            }
 #pragma unroll
             for (int q = 0; q < NST; ++q) {
                 // (passes that stage nothing read a.act[0])
                 const uint32_t i = min(threadIdx.x + 256u * q, n_st > 0 ? n_st - 1 : 0u);
-                uint32_t ia = i;
-                if constexpr (PT) {
-                    const uint32_t k = i / (I / 4);
-                    ia = (grow[q] < a.tokens * K ? grow[q] : 0u) * (I / 4) + (i - k * (I / 4));
-                }
                 // I % 32 == 0: the shared rows start on a chunk
-                const float4* src = i < n4 || n_st == 0 ? reinterpret_cast<const float4*>(a.act) + ia
+                const float4* src = i < n4 || n_st == 0 ? reinterpret_cast<const float4*>(a.act) + i
                                                         : reinterpret_cast<const float4*>(act_shared) + (i - n4);
                 stv[q] = *src;
             }
@@ -1365,9 +1333,12 @@ __global__ __launch_bounds__(256) void down_rows_kernel(DownArgs a)
     // this lane's slots: item, chunk, expert base and offsets, combine weight
     // (0 for slots past the last chunk and for out-of-range routes, whose
     // weights are read from expert 0 and not used)
-    const uint8_t* sbase[NCH];
-    uint64_t s_w[NCH], s_s[NCH], s_b[NCH];
-    uint32_t s_gsh[NCH], s_ch[NCH], s_q[NCH];
+    // per slot: its chunk's code bytes in row 0 and its group's scale and
+    // bias in row 0 (row r adds r * I / 2 bytes, r * gpr entries)
+    const uint8_t* p_w[NCH];
+    const uint16_t* p_s[NCH];
+    const uint16_t* p_b[NCH];
+    uint32_t s_gpr[NCH], s_q[NCH];
     float s_cw[NCH];
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -1375,12 +1346,13 @@ __global__ __launch_bounds__(256) void down_rows_kernel(DownArgs a)
         const uint32_t m = min(f / cpi, n_items - 1);
         const bool sh = a.has_shared && m == K;
         const bool ok = f < n_ch && (sh || eid[j] < a.ex.count);
-        sbase[j] = sh ? a.sh.base : a.ex.base + (uint64_t)(ok ? eid[j] : 0u) * a.ex.stride;
-        s_w[j] = sh ? a.sh.down.w_off : a.ex.down.w_off;
-        s_s[j] = sh ? a.sh.down.s_off : a.ex.down.s_off;
-        s_b[j] = sh ? a.sh.down.b_off : a.ex.down.b_off;
-        s_gsh[j] = sh ? a.sh.group_shift : a.ex.group_shift;
-        s_ch[j] = f < n_ch ? f % cpi : 0u;
+        const uint8_t* base = sh ? a.sh.base : a.ex.base + (uint64_t)(ok ? eid[j] : 0u) * a.ex.stride;
+        const uint32_t gsh = sh ? a.sh.group_shift : a.ex.group_shift;
+        const uint32_t ch = f < n_ch ? f % cpi : 0u;
+        p_w[j] = base + (sh ? a.sh.down.w_off : a.ex.down.w_off) + ch * 16u;
+        p_s[j] = reinterpret_cast<const uint16_t*>(base + (sh ? a.sh.down.s_off : a.ex.down.s_off)) + ((ch * 32u) >> gsh);
+        p_b[j] = reinterpret_cast<const uint16_t*>(base + (sh ? a.sh.down.b_off : a.ex.down.b_off)) + ((ch * 32u) >> gsh);
+        s_gpr[j] = I >> gsh;
         s_q[j] = f < n_ch ? f : 0u;
         s_cw[j] = ok ? cwl[m] : 0.0f;
     }
@@ -1389,11 +1361,9 @@ __global__ __launch_bounds__(256) void down_rows_kernel(DownArgs a)
         const uint32_t rc = min(r, H - 1);
 #pragma unroll
         for (int j = 0; j < NCH; ++j) {
-            const uint32_t gpr = I >> s_gsh[j];
-            const uint32_t g = (s_ch[j] * 32u) >> s_gsh[j];
-            W.w[j] = *reinterpret_cast<const uint4*>(sbase[j] + s_w[j] + (uint64_t)rc * (I / 2) + s_ch[j] * 16u);
-            W.sr[j] = reinterpret_cast<const uint16_t*>(sbase[j] + s_s[j])[(uint64_t)rc * gpr + g];
-            W.br[j] = reinterpret_cast<const uint16_t*>(sbase[j] + s_b[j])[(uint64_t)rc * gpr + g];
+            W.w[j] = *reinterpret_cast<const uint4*>(p_w[j] + (uint64_t)rc * (I / 2));
+            W.sr[j] = p_s[j][(uint64_t)rc * s_gpr[j]];
+            W.br[j] = p_b[j][(uint64_t)rc * s_gpr[j]];
         }
         W.res = res_row[rc];
     };
@@ -1743,7 +1713,7 @@ static bool multi_token_path(const DecodeArgs& d)
 {
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
     return T > 1 && (uint64_t)(K + (d.shared ? 1u : 0u)) * I <= PT_STAGE_FLOATS && I <= 1536 && I % 4 == 0 &&
-           H % PT_R == 0 && H <= 64 * 32 * 4;
+           H % 4 == 0 && H <= 64 * 32 * 4;
 }
 
 static bool route_separately(const DecodeArgs& d)
@@ -1942,36 +1912,6 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     hipExtLaunchKernelGGL((down_wide_kernel<SBT>), gw, dim3(WIDE_THREADS), 0, st, phase_event(d, 4), phase_event(d, 5), 0, da)
         PBM_DW();
 #undef PBM_DW
-        err = hipGetLastError();
-        if (err != hipSuccess)
-            return err;
-        if (d.next_norm_w && d.next_normed) {
-            next_norm_kernel<<<T, 256, 0, st>>>(d.hidden_out, d.next_norm_w, H, d.eps, d.next_normed);
-            err = hipGetLastError();
-        }
-        return err;
-    }
-    // several tokens: one workgroup per (row block, token) when a token's
-    // routed and shared activations fit the per-token staging buffer (the
-    // plan-mode loop over every route of the call runs one dependent round
-    // trip after another)
-    const bool per_token = use_plan && (uint64_t)(K + (da.has_shared ? 1u : 0u)) * I <= PT_STAGE_FLOATS &&
-                           I <= 1536 && H % PT_R == 0;
-    if (per_token) {
-        da.stage = true;
-        dim3 gp(H / PT_R, T);
-#define PBM_DNT(L, C, M)                                                                       \
-    hipExtLaunchKernelGGL((down_combine_kernel<SBT, L, C, M, true, false, true>), gp, dim3(256), 0, st, \
-                          phase_event(d, 4), phase_event(d, 5), 0, da)
-        switch (I) {
-        case 256: PBM_DNT(8, 1, 4); break;
-        case 512: PBM_DNT(8, 2, 4); break;
-        case 768: PBM_DNT(8, 3, 4); break;
-        case 1024: PBM_DNT(16, 2, 4); break;
-        case 1536: PBM_DNT(16, 3, 4); break;
-        default: return hipErrorInvalidValue;
-        }
-#undef PBM_DNT
         err = hipGetLastError();
         if (err != hipSuccess)
             return err;
