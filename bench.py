@@ -176,7 +176,7 @@ def cpu_baselines(cfg, host_layers, tokens: int, budget_s: float) -> dict:
     return rec
 
 
-KERNEL_NAMES = {"stage": "router_stage_kernel", "gateup": "route_gateup_kernel", "down": "down_combine_kernel"}
+KERNEL_NAMES = {"stage": "router_stage_kernel", "gateup": "route_gateup_kernel", "down": "down_rows_kernel"}
 
 
 def load_traffic(phase: str, workload: str):
