@@ -846,7 +846,7 @@ def main() -> int:
     dom_gbps = kernels[dominant]["GBps"]
     traffic, traffic_src = load_traffic(dominant, cfg.name)
     # route_gateup_kernel also touches the down weights of the selected
-    # experts (prefetch for down_combine_kernel); its traffic includes them
+    # experts (prefetch for the down kernel); its traffic includes them
     pf_bytes = down_prefetch_bytes(cfg, int(round(u_mean)), T) if dominant == "gateup" else 0
 
     cpu = None

@@ -545,10 +545,11 @@ constexpr uint32_t GATEUP_RESIDENT_WGS = 768;
 
 // Down-weight prefetch: touch every 128-byte line of the down codes, scales
 // and biases of the selected experts (and the shared expert) while the
-// gate/up workgroups run, so that down_combine_kernel finds them in the L2 /
+// gate/up workgroups run, so that the down kernel finds them in the L2 /
 // MALL instead of HBM.  Row block rb (DOWN_R output rows) is read by down
-// workgroup rb, which the dispatcher places on XCD rb % 8; a prefetch
-// workgroup on XCD x touches only the blocks rb = x + 8j.
+// workgroup rb (down_combine_kernel), or rb mod the grid (down_rows_kernel:
+// its grid is a multiple of 8), which the dispatcher places on XCD rb % 8;
+// a prefetch workgroup on XCD x touches only the blocks rb = x + 8j.
 // lane0/lanes: this lane's index among the lanes of this XCD that share the
 // work, and their number.  Returns a value that depends on every load.
 __device__ uint32_t touch_down_lines(const ExpertArgs& a, const RouteLds& s, uint32_t n_routed, bool use_plan,
