@@ -351,6 +351,59 @@ def test_wide_down_and_routing_shapes_match_oracle(ctx, cfg):
     _say(f"[result] {cfg.name} fused hidden max_abs={mx2:.3e} rel_l2={rel2:.3e}")
 
 
+# Several-token shapes of the multi-token decode kernels (router stage by
+# token groups, persistent gate/up over routes, row-wise down + combine):
+# two chunks per lane (H = 4096, two-token groups), one / two / three
+# (item, chunk) slots per lane, bf16 scale/bias, gated and ungated shared
+# experts, groups of 32 and 128, odd token counts.
+M_H4096 = MoeConfig("multi_h4096_bf16", hidden=4096, intermediate=512, experts=64, k=6,
+                    routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    shared_intermediate=512, shared_gated=True, sb_dtype=abi.DTYPE_BF16)
+M_I256 = MoeConfig("multi_i256_g32", hidden=1024, intermediate=256, experts=96, k=8,
+                   routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                   shared_intermediate=256, shared_gated=False, group=32, sb_dtype=abi.DTYPE_F16)
+M_I1024 = MoeConfig("multi_i1024_g128", hidden=2048, intermediate=1024, experts=64, k=4,
+                    routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    shared_intermediate=1024, shared_gated=True, group=128, sb_dtype=abi.DTYPE_F16)
+M_I1536 = MoeConfig("multi_i1536_noshared", hidden=1024, intermediate=1536, experts=32, k=3,
+                    routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    sb_dtype=abi.DTYPE_F16)
+M_SMALL = MoeConfig("multi_h512_one_slot", hidden=512, intermediate=256, experts=16, k=4,
+                    routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
+                    sb_dtype=abi.DTYPE_F16)
+
+
+@pytest.mark.parametrize("cfg,T", [(M_H4096, 6), (M_I256, 5), (M_I1024, 4), (M_I1536, 7), (M_SMALL, 2),
+                                   (M_SMALL, 9), (C2, 3), (C2, 16)], ids=lambda v: getattr(v, "name", str(v)))
+def test_multi_token_decode_shapes_match_oracle(ctx, cfg, T):
+    _say(f"[test] multi-token decode {cfg.name} T={T}")
+    dl = _layer(ctx, cfg, 0)
+    xh, rh = synth.activations(SEED, 70 + T, T, cfg.hidden)
+    x, ids, w, _ = _route(ctx, dl, xh)
+    res = ctx.to_device(rh)
+    nw_h = synth.uniform_f32(SEED, 98, 0, 0, 0, cfg.hidden, 0.5, 1.0)
+    nw = ctx.to_device(nw_h)
+    out = ctx.array((T, cfg.hidden), np.float32)
+    nn = ctx.array((T, cfg.hidden), np.float32)
+    dl.moe.submit_scheduled_expert_command(x, res, ids, w, out, nw, nn)
+    ctx.sync()
+    ids_h = ids.download().astype(np.int32)
+    w_h = w.download()
+    ref_h, ref_n = dl.oracle_block(xh, rh, ids_h, w_h, next_norm=nw_h)
+    exact = dl.exact_block(xh, rh, ids_h, w_h) if np.max(np.abs(ref_h)) > 1e3 else None
+    mx, rel = assert_layer_tolerance(out.download(), ref_h, exact=exact)
+    _say(f"[result] {cfg.name} T={T} hidden max_abs={mx:.3e} rel_l2={rel:.3e}")
+    assert_layer_tolerance(nn.download(), ref_n, "next_normed")
+    # the fused layer (router stage by token groups from T = 4) on the same rows
+    out2 = ctx.array((T, cfg.hidden), np.float32)
+    ids2 = ctx.array((T, cfg.k), np.uint32)
+    w2 = ctx.array((T, cfg.k), np.float32)
+    dl.moe.forward(x, res, out2, ids2, w2)
+    ctx.sync()
+    np.testing.assert_array_equal(ids2.download(), ids.download())
+    assert_layer_tolerance(out2.download(), ref_h, exact=exact)
+
+
 def test_one_row_prefill_is_bitwise_decode(ctx):
     _say("[test] one-row parity")
     dl = _layer(ctx, C2, 0)
