@@ -964,7 +964,6 @@ constexpr uint32_t STAGE_FLOATS = 12288; // activations staged (54 KB of LDS in 
 // Several tokens (down_rows_kernel): one token's routed + shared activations
 // (27 KB of LDS).
 constexpr uint32_t PT_STAGE_FLOATS = 6144;
-constexpr int MULTI_RPW = 2; // rows per unit of gateup_multi_kernel
 // Staged chunk q (32 floats) sits at q * XP floats, so that the lanes'
 // 16-byte reads of consecutive chunks fall on distinct banks.
 constexpr int XP = 36;
@@ -1731,8 +1730,11 @@ constexpr uint32_t MULTI_WGS_PER_CU = 4;
 // resident workgroups of down_rows_kernel per CU
 constexpr uint32_t ROWS_WGS_PER_CU = 2;
 
+// gateup_multi_kernel with the routes in d.ids: two rows per unit (one with
+// four chunks per lane, for the registers) and about the resident number of
+// workgroups, shared by the tokens (more workgroups than that only wait)
 template <int SBT>
-static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
+static hipError_t launch_gateup_multi(hipStream_t st, const DecodeArgs& d)
 {
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
     ExpertArgs ea{};
@@ -1745,23 +1747,31 @@ static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
     ea.hidden = H;
     ea.act = d.act;
     ea.status = d.status;
-    constexpr int RPW = MULTI_RPW;
-    // workgroups per token: every CU (256 on MI355X) holds MULTI_WGS_PER_CU
-    // workgroups, shared by the tokens (more workgroups than that only wait)
-    const uint32_t units = K * (I / RPW); // per token
-    const uint32_t per_token = std::max(1u, std::min((units + 3) / 4, 256u * MULTI_WGS_PER_CU / T));
-    const dim3 g1(per_token, T);
     const uint32_t cpl = (H / 32 + 63) / 64;
+    const uint32_t rpw = cpl <= 2 ? 2u : 1u;
+    const uint32_t wgs_cu = cpl <= 2 ? MULTI_WGS_PER_CU : 3u;
+    const uint32_t units = K * (I / rpw); // per token
+    const uint32_t per_token = std::max(1u, std::min((units + 3) / 4, 256u * wgs_cu / T));
+    const dim3 g1(per_token, T);
     if (cpl <= 1)
-        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 1, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
+        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 1, 2>), g1, dim3(256), 0, st, phase_event(d, 2),
                               phase_event(d, 3), 0, ea);
     else if (cpl <= 2)
-        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 2, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
+        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 2, 2>), g1, dim3(256), 0, st, phase_event(d, 2),
+                              phase_event(d, 3), 0, ea);
+    else if (cpl <= 4)
+        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 4, 1>), g1, dim3(256), 0, st, phase_event(d, 2),
                               phase_event(d, 3), 0, ea);
     else
-        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 4, RPW>), g1, dim3(256), 0, st, phase_event(d, 2),
-                              phase_event(d, 3), 0, ea);
-    hipError_t err = hipGetLastError();
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+template <int SBT>
+static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
+{
+    const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
+    hipError_t err = launch_gateup_multi<SBT>(st, d);
     if (err != hipSuccess)
         return err;
     DownArgs da{};
@@ -1813,6 +1823,12 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     const ExpertSet& ex = d.ex;
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = ex.gate.rows;
     const bool use_plan = T > 1;
+    // one token on the wide down kernel with the routes given (C5): the
+    // persistent gate/up kernel (C5 gate/up 44.7 -> 35.0 us)
+    const bool multi_gu = !route_here && T == 1 &&
+                          (uint64_t)(K + (d.shared ? 1u : 0u)) * I > STAGE_FLOATS &&
+                          (uint64_t)(K + (d.shared ? 1u : 0u)) * I <= WIDE_FLOATS && I % 512 == 0 && I >= 1024 &&
+                          I <= 2048 && H % WIDE_R == 0 && H <= 64 * 32 * 4;
     const uint32_t max_items = use_plan ? std::min(ex.count, T * K) : T * K;
     ExpertArgs ea{};
     ea.ex = ex;
@@ -1876,13 +1892,18 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
         else if (epl <= 8) PBM_GU(C, 8);                                                       \
         else PBM_GU(C, 16);                                                                    \
     } while (0)
-    if (cpl <= 1) PBM_GU_E(1);
-    else if (cpl <= 2) PBM_GU_E(2);
-    else if (cpl <= 4) PBM_GU_E(4);
-    else return hipErrorInvalidValue;
+    hipError_t err;
+    if (multi_gu) {
+        err = launch_gateup_multi<SBT>(st, d);
+    } else {
+        if (cpl <= 1) PBM_GU_E(1);
+        else if (cpl <= 2) PBM_GU_E(2);
+        else if (cpl <= 4) PBM_GU_E(4);
+        else return hipErrorInvalidValue;
+        err = hipGetLastError();
+    }
 #undef PBM_GU
 #undef PBM_GU_E
-    hipError_t err = hipGetLastError();
     if (err != hipSuccess)
         return err;
 
