@@ -507,7 +507,7 @@ def stack_bytes_per_token(acfg, mcfg, layers: int, position: int) -> dict:
     return {"attention": attn * layers, "moe": moe * layers, "total": (attn + moe) * layers}
 
 
-STACK_KERNELS = ("qkv_rows", "attn_chunk", "attn_merge", "o_rows", "router_stage", "route_gateup", "down_combine")
+STACK_KERNELS = ("qkv_rows", "attn_chunk", "attn_merge", "o_rows", "router_stage", "route_gateup", "down")
 
 
 def stack_kernel_times(ctx, ev, token, layers: int, tokens: int = 4) -> dict:
