@@ -608,9 +608,8 @@ __device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s, bool need_w)
 {
     const int wv = threadIdx.x >> 6;
     const uint32_t K = a.rp.k;
-    const bool grouped = a.rp.kind == 2 && a.rp.n_group > 1;
-    if (a.tokens < 4 && a.rp.order == 0 && !grouped) {
-        // few tokens: all four waves route each token in turn
+    if (block_routing(a.tokens, a.rp)) {
+        // decode tokens: all four waves route each token in turn
         constexpr int EPT = EPL <= 4 ? 1 : (EPL <= 8 ? 2 : 4); // ceil(E / 256) bucket
         for (uint32_t t = 0; t < a.tokens; ++t) {
             if (t)
@@ -824,30 +823,53 @@ struct UnitWeights {
     uint32_t sg[RPW][CPL], bg[RPW][CPL], su[RPW][CPL], bu[RPW][CPL]; // raw 16-bit scale / bias
 };
 
-template <int SBT, int CPL, int RPW>
+template <int SBT, int CPL, int RPW, int EPL>
 __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
 {
     // staged chunk q (32 floats) at q * XQ floats: the lanes' 16-byte reads
     // of consecutive chunks fall on distinct banks
     constexpr int XQ = 36;
+    constexpr int EPT = EPL <= 4 ? 1 : (EPL <= 8 ? 2 : 4); // ceil(E / 256) bucket of the block routing
+    constexpr int RSCR = 2 * EPL * WAVE + 192 > 1176 ? 2 * EPL * WAVE + 192 : 1176;
     __shared__ __align__(16) float xl[WAVE * CPL * XQ];
     __shared__ uint32_t sid[MAX_K];
+    __shared__ float sw[MAX_K];
+    __shared__ float rscr[RSCR]; // routing scratch
     const int lane = threadIdx.x & 63;
     const uint32_t K = a.rp.k, H = a.hidden, I = a.ex.gate.rows;
     const uint32_t t = blockIdx.y;
     const uint32_t chunks = H / 32, gsh = a.ex.group_shift, gpr = H >> gsh;
     {
-        // the token's route ids and its x row (coalesced), both loaded
-        // before either is stored; float4 slots past H / 4 hold zeros in
-        // chunks no lane reads
-        const uint32_t idv = a.ids[t * K + min((uint32_t)threadIdx.x, K - 1)];
+        // the token's x row (coalesced), loaded before the routes are known
+        // and stored after; float4 slots past H / 4 hold zeros in chunks no
+        // lane reads
         const uint32_t nf = H / 4;
         float4 v[2 * CPL];
 #pragma unroll
         for (int j = 0; j < 2 * CPL; ++j)
             v[j] = reinterpret_cast<const float4*>(a.x + (uint64_t)t * H)[min(threadIdx.x + 256u * j, nf - 1)];
-        if (threadIdx.x < K)
-            sid[threadIdx.x] = idv;
+        if (a.route_here) {
+            // every workgroup routes its token (the routing launch's own
+            // device routines, so the ids agree bitwise); workgroup 0 of
+            // the token publishes the routes for the down kernel and the
+            // caller
+            const float* lt = a.logits + (uint64_t)t * a.rp.experts;
+            if (block_routing(a.tokens, a.rp)) {
+                route_token_block<EPT>(lt, a.sel_bias, a.rp, sid, sw, rscr, a.status, blockIdx.x == 0);
+            } else if (threadIdx.x < 64) {
+                uint32_t* sel = reinterpret_cast<uint32_t*>(xl); // (x is stored after the routing)
+                route_token_wave<EPL>(lt, a.sel_bias, a.rp, sid, sw, sel, rscr, a.status);
+            }
+            __syncthreads();
+            if (blockIdx.x == 0 && threadIdx.x < K) {
+                a.ids[t * K + threadIdx.x] = sid[threadIdx.x];
+                a.weights[t * K + threadIdx.x] = sw[threadIdx.x];
+            }
+        } else {
+            const uint32_t idv = a.ids[t * K + min((uint32_t)threadIdx.x, K - 1)];
+            if (threadIdx.x < K)
+                sid[threadIdx.x] = idv;
+        }
 #pragma unroll
         for (int j = 0; j < 2 * CPL; ++j) {
             const uint32_t f = threadIdx.x + 256u * j;
@@ -1706,9 +1728,9 @@ static uint32_t gateup_rpw(const DecodeArgs& d, uint32_t* wgs)
 // routing, once per round.  C5 (1024 workgroups, two rounds): 98.0 ->
 // 89.5 us per layer; C2 (640 workgroups, one round): the extra launch
 // costs more than the routing it saves (23.7 -> 25.9 us).
-// Several tokens whose per-token activations fit the per-token down kernel:
-// routing in its own launch, the persistent gate/up kernel over routes and
-// the per-token down kernel (no dispatch plan).
+// Several tokens whose per-token activations fit down_rows_kernel: the
+// persistent gate/up kernel over routes (each workgroup routing its token)
+// and the row kernel for down + combine (no dispatch plan).
 static bool multi_token_path(const DecodeArgs& d)
 {
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
@@ -1719,7 +1741,7 @@ static bool multi_token_path(const DecodeArgs& d)
 static bool route_separately(const DecodeArgs& d)
 {
     if (multi_token_path(d))
-        return true;
+        return false; // gateup_multi_kernel routes
     uint32_t wgs = 0;
     gateup_rpw(d, &wgs);
     return wgs > GATEUP_RESIDENT_WGS;
@@ -1734,12 +1756,15 @@ constexpr uint32_t ROWS_WGS_PER_CU = 2;
 // four chunks per lane, for the registers) and about the resident number of
 // workgroups, shared by the tokens (more workgroups than that only wait)
 template <int SBT>
-static hipError_t launch_gateup_multi(hipStream_t st, const DecodeArgs& d)
+static hipError_t launch_gateup_multi(hipStream_t st, const DecodeArgs& d, bool route_here)
 {
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
     ExpertArgs ea{};
     ea.ex = d.ex;
     ea.rp = d.rp;
+    ea.logits = d.logits;
+    ea.sel_bias = d.sel_bias;
+    ea.route_here = route_here;
     ea.ids = d.ids;
     ea.weights = d.weights;
     ea.x = d.in_norm_w ? d.x_normed : d.x; // normalised by the router stage
@@ -1753,25 +1778,39 @@ static hipError_t launch_gateup_multi(hipStream_t st, const DecodeArgs& d)
     const uint32_t units = K * (I / rpw); // per token
     const uint32_t per_token = std::max(1u, std::min((units + 3) / 4, 256u * wgs_cu / T));
     const dim3 g1(per_token, T);
+    const uint32_t epl = (d.rp.experts + 63) / 64;
+#define PBM_GM(C, R)                                                                           \
+    do {                                                                                       \
+        if (epl <= 2)                                                                          \
+            hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, C, R, 2>), g1, dim3(256), 0, st,   \
+                                  phase_event(d, 2), phase_event(d, 3), 0, ea);                \
+        else if (epl <= 4)                                                                     \
+            hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, C, R, 4>), g1, dim3(256), 0, st,   \
+                                  phase_event(d, 2), phase_event(d, 3), 0, ea);                \
+        else if (epl <= 8)                                                                     \
+            hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, C, R, 8>), g1, dim3(256), 0, st,   \
+                                  phase_event(d, 2), phase_event(d, 3), 0, ea);                \
+        else                                                                                   \
+            hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, C, R, 16>), g1, dim3(256), 0, st,  \
+                                  phase_event(d, 2), phase_event(d, 3), 0, ea);                \
+    } while (0)
     if (cpl <= 1)
-        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 1, 2>), g1, dim3(256), 0, st, phase_event(d, 2),
-                              phase_event(d, 3), 0, ea);
+        PBM_GM(1, 2);
     else if (cpl <= 2)
-        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 2, 2>), g1, dim3(256), 0, st, phase_event(d, 2),
-                              phase_event(d, 3), 0, ea);
+        PBM_GM(2, 2);
     else if (cpl <= 4)
-        hipExtLaunchKernelGGL((gateup_multi_kernel<SBT, 4, 1>), g1, dim3(256), 0, st, phase_event(d, 2),
-                              phase_event(d, 3), 0, ea);
+        PBM_GM(4, 1);
     else
         return hipErrorInvalidValue;
+#undef PBM_GM
     return hipGetLastError();
 }
 
 template <int SBT>
-static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
+static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d, bool route_here)
 {
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = d.ex.gate.rows;
-    hipError_t err = launch_gateup_multi<SBT>(st, d);
+    hipError_t err = launch_gateup_multi<SBT>(st, d, route_here);
     if (err != hipSuccess)
         return err;
     DownArgs da{};
@@ -1818,8 +1857,8 @@ static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d)
 template <int SBT>
 static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool route_here)
 {
-    if (!route_here && multi_token_path(d))
-        return launch_multi_token<SBT>(st, d);
+    if (multi_token_path(d))
+        return launch_multi_token<SBT>(st, d, route_here);
     const ExpertSet& ex = d.ex;
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = ex.gate.rows;
     const bool use_plan = T > 1;
@@ -1894,7 +1933,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     } while (0)
     hipError_t err;
     if (multi_gu) {
-        err = launch_gateup_multi<SBT>(st, d);
+        err = launch_gateup_multi<SBT>(st, d, false);
     } else {
         if (cpl <= 1) PBM_GU_E(1);
         else if (cpl <= 2) PBM_GU_E(2);

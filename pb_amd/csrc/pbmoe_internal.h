@@ -54,6 +54,15 @@ struct RouteParams {
     float routed_scale;
 };
 
+// One token routed by a whole workgroup (route_token_block) rather than one
+// wave (route_token_wave): decode token counts, canonical order, no expert
+// groups.  Every entry point that routes decode tokens uses this choice, so
+// that they agree bitwise on the route weights.
+__host__ __device__ inline bool block_routing(uint32_t tokens, const RouteParams& p)
+{
+    return tokens <= 16 && p.order == 0 && !(p.kind == 2 && p.n_group > 1);
+}
+
 // Dispatch plan buffers (device), layout documented in pbmoe.h.
 struct Plan {
     uint32_t* unique_ids;  // [experts]

@@ -179,8 +179,9 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                           weights + (uint64_t)t * p.k, sel[wv], grp[wv], status);
 }
 
-// few tokens: one workgroup per token (route_token_block), the same routing
-// the fused decode layer performs, so both entry points agree bitwise
+// decode token counts (block_routing): one workgroup per token
+// (route_token_block), the same routing the fused decode layer performs, so
+// both entry points agree bitwise
 template <int EPT>
 __global__ __launch_bounds__(256) void route_block_kernel(const float* __restrict__ logits,
                                                          const float* __restrict__ bias, RouteParams p,
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(256) void route_block_kernel(const float* __restric
 hipError_t launch_route_topk(hipStream_t s, const float* logits, const float* bias, uint32_t tokens,
                              const RouteParams& p, uint32_t* ids, float* weights, uint32_t* status)
 {
-    if (tokens < 4 && p.order == 0 && !(p.kind == 2 && p.n_group > 1)) {
+    if (block_routing(tokens, p)) {
         if (p.experts <= 256)
             route_block_kernel<1><<<tokens, 256, 0, s>>>(logits, bias, p, ids, weights, status);
         else if (p.experts <= 512)
