@@ -188,14 +188,20 @@ __device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, float w0, f
 }
 
 // ---------------------------------------------------------------------------
-// attention partials: workgroup (chunk c, kv head j, head group z), NH <= 4
+// attention partials: workgroup (chunk c, kv head j, head group z), NH <= 8
 // q heads per workgroup (heads j*NQ + z*NH .. +NH), wave w handles head w.
 // Partial record per (q head, chunk): sum_t exp(s_t - m) v_t [HD], m,
 // sum_t exp(s_t - m).
 // ---------------------------------------------------------------------------
+// CHUNK_THREADS: four waves, or one per q head for eight heads (the kv
+// head's keys and values are then loaded by one workgroup, not two)
 template <int NH>
-__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
+constexpr int CHUNK_THREADS = NH <= 4 ? 256 : 64 * NH;
+
+template <int NH>
+__global__ __launch_bounds__(CHUNK_THREADS<NH>) void attn_chunk_kernel(AttnArgs a)
 {
+    constexpr int NT = CHUNK_THREADS<NH>;
     __shared__ float qs[NH][HD];
     __shared__ __align__(16) uint16_t kc[CH][KPITCH];
     __shared__ __align__(16) uint16_t vc[CH][HD];
@@ -231,11 +237,11 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
     // inside a divergent branch is waited for where the branch ends) and are
     // zeroed when staged; this position's row is taken from LDS below, not
     // from the cache.
-    constexpr int PIECES = CH * (HD / 8) / 256;
+    constexpr int PIECES = CH * (HD / 8) / NT;
     uint4 kk[PIECES], vv[PIECES];
 #pragma unroll
     for (int u = 0; u < PIECES; ++u) {
-        const uint32_t i = tid + 256 * u, t = min(i / (HD / 8), cnt - 1), q = i % (HD / 8);
+        const uint32_t i = tid + NT * u, t = min(i / (HD / 8), cnt - 1), q = i % (HD / 8);
         const uint64_t o = ((uint64_t)(t0 + t) * a.kv_heads + j) * HD;
         kk[u] = reinterpret_cast<const uint4*>(a.cache_k + o)[q];
         vv[u] = reinterpret_cast<const uint4*>(a.cache_v + o)[q];
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a)
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < PIECES; ++u) {
-        const uint32_t i = tid + 256 * u, t = i / (HD / 8), q = i % (HD / 8);
+        const uint32_t i = tid + NT * u, t = i / (HD / 8), q = i % (HD / 8);
         const bool live = t < cnt;
         uint4 kx = kk[u], vx = vv[u];
         kx.x = live ? kx.x : 0u, kx.y = live ? kx.y : 0u, kx.z = live ? kx.z : 0u, kx.w = live ? kx.w : 0u;
@@ -488,8 +494,8 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
                               0, a);
         break;
     case 8:
-        hipExtLaunchKernelGGL((attn_chunk_kernel<4>), dim3(chunks, a.kv_heads, 2), dim3(256), 0, st, a.ev[2], a.ev[3],
-                              0, a);
+        hipExtLaunchKernelGGL((attn_chunk_kernel<8>), dim3(chunks, a.kv_heads, 1), dim3(CHUNK_THREADS<8>), 0, st,
+                              a.ev[2], a.ev[3], 0, a);
         break;
     default: return hipErrorInvalidValue;
     }
