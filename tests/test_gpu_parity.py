@@ -355,7 +355,9 @@ def test_wide_down_and_routing_shapes_match_oracle(ctx, cfg):
 # token groups, persistent gate/up over routes, row-wise down + combine):
 # two chunks per lane (H = 4096, two-token groups), one / two / three
 # (item, chunk) slots per lane, bf16 scale/bias, gated and ungated shared
-# experts, groups of 32 and 128, odd token counts.
+# experts, groups of 32 and 128, odd token counts; and one token of the
+# same shapes (the row kernel for down + combine with one and two slots per
+# lane).
 M_H4096 = MoeConfig("multi_h4096_bf16", hidden=4096, intermediate=512, experts=64, k=6,
                     routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
                     shared_intermediate=512, shared_gated=True, sb_dtype=abi.DTYPE_BF16)
@@ -374,7 +376,8 @@ M_SMALL = MoeConfig("multi_h512_one_slot", hidden=512, intermediate=256, experts
 
 
 @pytest.mark.parametrize("cfg,T", [(M_H4096, 6), (M_I256, 5), (M_I1024, 4), (M_I1536, 7), (M_SMALL, 2),
-                                   (M_SMALL, 9), (C2, 3), (C2, 16)], ids=lambda v: getattr(v, "name", str(v)))
+                                   (M_SMALL, 9), (C2, 3), (C2, 16), (M_H4096, 1), (M_I256, 1), (M_SMALL, 1)],
+                         ids=lambda v: getattr(v, "name", str(v)))
 def test_multi_token_decode_shapes_match_oracle(ctx, cfg, T):
     _say(f"[test] multi-token decode {cfg.name} T={T}")
     dl = _layer(ctx, cfg, 0)
