@@ -1749,7 +1749,8 @@ static bool route_separately(const DecodeArgs& d)
 
 // resident workgroups of gateup_multi_kernel per CU
 constexpr uint32_t MULTI_WGS_PER_CU = 4;
-// resident workgroups of down_rows_kernel per CU
+// workgroups of down_rows_kernel per CU (its registers allow two; more only
+// wait)
 constexpr uint32_t ROWS_WGS_PER_CU = 2;
 
 // gateup_multi_kernel with the routes in d.ids: two rows per unit (one with
@@ -1824,15 +1825,12 @@ static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d, bool r
     da.tokens = T;
     da.k = K;
     da.hidden = H;
-    da.ids = d.ids;
+    da.ids = d.ids; // activations in route order
     da.weights = d.weights;
-    da.plan = d.plan;
-    da.use_plan = false; // activations in route order
-    da.stage = true;
     da.residual = d.residual;
     da.hidden_out = d.hidden_out;
     da.status = d.status;
-    // rows: workgroups per token so that the grid is about four per CU
+    // rows: workgroups per token, ROWS_WGS_PER_CU per CU in all
     const uint32_t nch = ((K + (da.has_shared ? 1u : 0u)) * (I / 32) + 63) / 64;
     const dim3 gr(std::max(1u, std::min(H / 4, 256u * ROWS_WGS_PER_CU / T)), T);
     if (nch <= 1)
