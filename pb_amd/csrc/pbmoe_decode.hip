@@ -1417,9 +1417,10 @@ __global__ __launch_bounds__(256) void down_rows_kernel(DownArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// kernel 3, wide variant: one token whose routed + shared activations are
+// kernel 3, wide variant: tokens whose routed + shared activations are
 // too large for the staging buffer of down_combine_kernel (C5: 9 items x
-// 2048 columns).  WIDE_R = 16 output rows per workgroup, so that one staged
+// 2048 columns), one token per grid row (blockIdx.y), activations in route
+// order.  WIDE_R = 16 output rows per workgroup, so that one staged
 // copy of the activations (72 KB, two workgroups per CU) serves 16 rows of
 // every item and the grid (H / 16 workgroups) is one round of residency.
 // Wave w owns rows 4w .. 4w + 3 of the block; lane l owns 32-column chunk l
@@ -1450,6 +1451,12 @@ __global__ __launch_bounds__(WIDE_THREADS, 2) void down_wide_kernel(DownArgs a)
     const uint32_t K = a.k, I = a.ex.down.cols, chunks = I / 32;
     const uint32_t n_items = K + (a.has_shared ? 1u : 0u);
     const uint32_t row0 = blockIdx.x * WIDE_R + wv * RW;
+    // token blockIdx.y (grid H / WIDE_R x tokens; activations in route order)
+    const uint32_t t = blockIdx.y, H = a.hidden;
+    const uint32_t* const ids = a.ids + t * K;
+    const float* const rweights = a.weights + t * K;
+    const float* const act = a.act + (uint64_t)t * K * I;
+    const float* const act_sh = a.act_shared + (uint64_t)t * I;
     const uint32_t ch = min(lane, chunks - 1); // lanes past the row read its last chunk, unused
     const bool lane_on = lane < chunks;
     // loads that need nothing: the routes' expert ids (uniform), the
@@ -1457,17 +1464,16 @@ __global__ __launch_bounds__(WIDE_THREADS, 2) void down_wide_kernel(DownArgs a)
     uint32_t eid[MAX_K];
 #pragma unroll
     for (int m = 0; m < MAX_K; ++m)
-        eid[m] = a.ids[min((uint32_t)m, K - 1)];
-    const float cw_v = a.weights[min(tid, K - 1)];
-    const float csl_v = (a.has_shared ? a.shared_logit : a.weights)[0];
-    const float res_v = a.residual[row0 + min(lane, (uint32_t)RW - 1)];
+        eid[m] = ids[min((uint32_t)m, K - 1)];
+    const float cw_v = rweights[min(tid, K - 1)];
+    const float csl_v = (a.has_shared ? a.shared_logit + t : rweights)[0];
+    const float res_v = a.residual[(uint64_t)t * H + row0 + min(lane, (uint32_t)RW - 1)];
     const uint32_t n4 = K * I / 4, n_st = n_items * I / 4;
     float4 stv[NST];
 #pragma unroll
     for (int q = 0; q < NST; ++q) {
         const uint32_t i = min(tid + (uint32_t)WIDE_THREADS * q, n_st - 1);
-        stv[q] = i < n4 ? reinterpret_cast<const float4*>(a.act)[i]
-                        : reinterpret_cast<const float4*>(a.act_shared)[i - n4];
+        stv[q] = i < n4 ? reinterpret_cast<const float4*>(act)[i] : reinterpret_cast<const float4*>(act_sh)[i - n4];
     }
     const uint8_t* const ex_base = a.ex.base;
     const uint64_t ex_stride = a.ex.stride;
@@ -1581,7 +1587,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 2) void down_wide_kernel(DownArgs a)
         out = lane == (uint32_t)rr ? t : out;
     }
     if (lane < (uint32_t)RW)
-        a.hidden_out[row0 + lane] = res_v + out;
+        a.hidden_out[(uint64_t)t * H + row0 + lane] = res_v + out;
 }
 
 // next-layer RMSNorm: one block per token (rms_norm_reduced)
@@ -1860,12 +1866,16 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     const ExpertSet& ex = d.ex;
     const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = ex.gate.rows;
     const bool use_plan = T > 1;
-    // one token on the wide down kernel with the routes given (C5): the
-    // persistent gate/up kernel (C5 gate/up 44.7 -> 35.0 us)
-    const bool multi_gu = !route_here && T == 1 &&
-                          (uint64_t)(K + (d.shared ? 1u : 0u)) * I > STAGE_FLOATS &&
-                          (uint64_t)(K + (d.shared ? 1u : 0u)) * I <= WIDE_FLOATS && I % 512 == 0 && I >= 1024 &&
-                          I <= 2048 && H % WIDE_R == 0 && H <= 64 * 32 * 4;
+    // Activations of a token too large for the down kernel's staging buffer
+    // but within the wide kernel's (C5: 9 x 2048 floats): the wide down
+    // kernel, one token per grid row.  Its gate/up runs in the persistent
+    // kernel (activations in route order; C5 one token 44.7 -> 35.0 us)
+    // unless one token is routed inside route_gateup_kernel.
+    const bool wide_shape = (uint64_t)(K + (d.shared ? 1u : 0u)) * I > STAGE_FLOATS &&
+                            (uint64_t)(K + (d.shared ? 1u : 0u)) * I <= WIDE_FLOATS && I % 512 == 0 &&
+                            I >= 1024 && I <= 2048 && H % WIDE_R == 0;
+    const bool multi_gu = wide_shape && H <= 64 * 32 * 4 && (T > 1 || !route_here);
+    const bool wide = wide_shape && (T == 1 || multi_gu);
     const uint32_t max_items = use_plan ? std::min(ex.count, T * K) : T * K;
     ExpertArgs ea{};
     ea.ex = ex;
@@ -1884,11 +1894,6 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     ea.has_shared = d.shared != nullptr;
     if (ea.has_shared)
         ea.sh = *d.shared;
-    // one token whose activations do not fit the down kernel's staging
-    // buffer: the wide down kernel (16 rows per workgroup, 72 KB staged)
-    const uint32_t d_items = K + (d.shared ? 1u : 0u);
-    const bool wide = T == 1 && (uint64_t)d_items * I > STAGE_FLOATS && (uint64_t)d_items * I <= WIDE_FLOATS &&
-                      I % 512 == 0 && I >= 1024 && I <= 2048 && H % WIDE_R == 0;
     const int RPW = (int)gateup_rpw(d, nullptr);
     const uint32_t waves = max_items * (I / RPW);
     const uint32_t cpl = (H / 32 + 63) / 64;
@@ -1931,7 +1936,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     } while (0)
     hipError_t err;
     if (multi_gu) {
-        err = launch_gateup_multi<SBT>(st, d, false);
+        err = launch_gateup_multi<SBT>(st, d, route_here);
     } else {
         if (cpl <= 1) PBM_GU_E(1);
         else if (cpl <= 2) PBM_GU_E(2);
@@ -1966,7 +1971,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     da.hidden_out = d.hidden_out;
     da.status = d.status;
     if (wide) {
-        dim3 gw(H / WIDE_R);
+        dim3 gw(H / WIDE_R, T);
 #define PBM_DW()                                                                               \
     hipExtLaunchKernelGGL((down_wide_kernel<SBT>), gw, dim3(WIDE_THREADS), 0, st, phase_event(d, 4), phase_event(d, 5), 0, da)
         PBM_DW();
