@@ -270,7 +270,10 @@ __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const
 // group from LDS instead of one L2 round trip per token, and the groups'
 // workgroups run side by side.
 constexpr uint32_t XL_FLOATS = 8192; // staged x floats (32 KB)
-constexpr uint32_t XL_MAX_H = 4096;  // widest row of the staged variant (norm weight buffer)
+constexpr uint32_t XL_MAX_H = 8192;  // widest row of the staged variant
+// dynamic LDS of the staged variant: the x rows, then the norm weight (H
+// floats) when the norm is fused
+inline size_t xl_lds_bytes(uint32_t hidden, bool norm) { return (XL_FLOATS + (norm ? hidden : 0u)) * sizeof(float); }
 
 template <int WDT, int GDT, int SBT, int CR, int CS, bool XL>
 __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
@@ -373,24 +376,32 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
         for (uint32_t task = wave_id; task < n_tasks; task += n_waves)
             run_task(task, a.x, 0, T, a.norm_w, nullptr);
     } else {
-        __shared__ __align__(16) float xsh[XL_FLOATS];
-        __shared__ __align__(16) float nwsh[XL_MAX_H];
+        extern __shared__ __align__(16) float xl_dyn[]; // xl_lds_bytes
+        float* const xsh = xl_dyn;
+        float* const nwsh = xl_dyn + XL_FLOATS; // (with a fused norm only)
         __shared__ float inv_sh[XL_FLOATS / 256]; // per token of the group (H >= 256)
         const uint32_t TG = XL_FLOATS / H, H4 = H / 4;
         const uint32_t g0 = blockIdx.y * TG, nt = min(TG, T - g0), n4 = nt * H4;
         constexpr int PER = XL_FLOATS / 4 / 256; // float4 per thread
         constexpr int NPER = XL_MAX_H / 4 / 256;
-        // unconditional loads and stores: slots past the data reload the last
-        // float4 and land in buffer slots nothing reads; without a norm, x
-        // stands in for the norm weight
+        // unconditional loads: slots past the data reload the last float4 (x
+        // slots land in buffer slots nothing reads); without a norm, x stands
+        // in for the norm weight, whose stores are then skipped
         const float4* nsrc = reinterpret_cast<const float4*>(a.norm_w ? a.norm_w : a.x);
         const float4* src = reinterpret_cast<const float4*>(a.x + (uint64_t)g0 * H);
+        float4 nv[NPER];
+#pragma unroll
+        for (int j = 0; j < NPER; ++j)
+            nv[j] = nsrc[min(threadIdx.x + 256u * j, H4 - 1)];
 #pragma unroll
         for (int j = 0; j < PER; ++j)
             reinterpret_cast<float4*>(xsh)[threadIdx.x + 256u * j] = src[min(threadIdx.x + 256u * j, n4 - 1)];
+        if (a.norm_w) {
 #pragma unroll
-        for (int j = 0; j < NPER; ++j)
-            reinterpret_cast<float4*>(nwsh)[threadIdx.x + 256u * j] = nsrc[min(threadIdx.x + 256u * j, H4 - 1)];
+            for (int j = 0; j < NPER; ++j)
+                if (threadIdx.x + 256u * j < H4)
+                    reinterpret_cast<float4*>(nwsh)[threadIdx.x + 256u * j] = nv[j];
+        }
         __syncthreads();
         if (a.norm_w) {
             // 1 / rms per token: wave w the tokens w, w + 4, ...
@@ -1661,10 +1672,13 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     const uint32_t cs = (d.hidden / 32 + 63) / 64;
     if (cr > 16 || cs > 4)
         return hipErrorInvalidValue;
-    // four tokens or more: x staged in LDS per group of tokens (with two, the
-    // staging round trip before the weight loads costs more than it saves:
-    // C2 6.2 -> 7.0 us)
-    const bool xl = d.tokens >= 4 && d.hidden <= XL_MAX_H && d.hidden >= 256 && d.hidden % 4 == 0;
+    // four tokens or more, or rows past 4096 columns: x staged in LDS per
+    // group of tokens (with two tokens of C2 the staging round trip before
+    // the weight loads costs more than it saves: 6.2 -> 7.0 us; C5's
+    // 7168-column rows, whose every task would read 28 KB of x from L2,
+    // gain at any token count)
+    const bool xl = (d.tokens >= 4 || d.hidden > 4096) && d.hidden <= XL_MAX_H && d.hidden >= 256 &&
+                    d.hidden % 4 == 0;
     const uint32_t xl_groups = xl ? (d.tokens + XL_FLOATS / d.hidden - 1) / (XL_FLOATS / d.hidden) : 1u;
     // router/gate dtypes: the benchmark layers use f16 for both; other
     // combinations share the f16 gate path only when the gate is f16
@@ -1675,7 +1689,8 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     do {                                                                                       \
         if (xl)                                                                                \
             hipExtLaunchKernelGGL((router_stage_kernel<W, G, S, CRV, CSV, true>), dim3(blocks, xl_groups), \
-                                  dim3(256), 0, st, phase_event(d, 0), phase_event(d, 1), 0, a); \
+                                  dim3(256), xl_lds_bytes(d.hidden, a.norm_w != nullptr), st,  \
+                                  phase_event(d, 0), phase_event(d, 1), 0, a);                 \
         else                                                                                   \
             hipExtLaunchKernelGGL((router_stage_kernel<W, G, S, CRV, CSV, false>), dim3(blocks), dim3(256), 0, \
                                   st, phase_event(d, 0), phase_event(d, 1), 0, a);             \
