@@ -179,6 +179,47 @@ def test_attention_rejects_position_beyond_cache(ctx):
     abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
 
 
+def test_attention_phase_events_time_each_kernel(ctx):
+    """pbmoe_set_phase_events with 14 events also times the attention
+    kernels (q/k/v, chunk partials, merge, o_proj): every pair brackets a
+    dispatch of positive duration; counts other than 0, 6 and 14 are
+    rejected."""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    hip.hipEventSynchronize.argtypes = [C.c_void_p]
+    hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    hip.hipEventDestroy.argtypes = [C.c_void_p]
+    evs = []
+    for _ in range(14):
+        e = C.c_void_p()
+        assert hip.hipEventCreate(C.byref(e)) == 0
+        evs.append(e)
+    arr = (C.c_void_p * 14)(*[e.value for e in evs])
+    assert abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 7) == abi.ERR_INVALID_ARGUMENT
+    acfg = synth.AttnConfig("t_events", hidden=512, q_heads=16, kv_heads=4, max_context=200)
+    layer = 54
+    dev = AttentionLayer(ctx, layer, acfg).bind_synth(SEED, layer)
+    H = acfg.hidden
+    rng = np.random.default_rng(11)
+    x_d, r_d, h_d = ctx.array((H,), F), ctx.array((H,), F), ctx.array((H,), F)
+    x_d.upload(rng.standard_normal(H).astype(F))
+    r_d.upload(rng.standard_normal(H).astype(F))
+    abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 14))
+    try:
+        dev.decode(x_d, r_d, 150, h_d)
+        ctx.sync()
+    finally:
+        abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, None, 0))
+    for i in range(4):
+        ms = C.c_float()
+        assert hip.hipEventSynchronize(evs[7 + 2 * i]) == 0
+        assert hip.hipEventElapsedTime(C.byref(ms), evs[6 + 2 * i], evs[7 + 2 * i]) == 0
+        assert ms.value > 0.0, f"attention kernel {i}"
+    for e in evs:
+        hip.hipEventDestroy(e)
+    abi.check(abi.lib().pbmoe_unbind_attention(ctx.handle, layer))
+
+
 def test_attention_rejects_unsupported_shapes(ctx):
     d = abi.AttnDesc()
     d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.rotary_dim = 512, 8, 3, 128, 128
