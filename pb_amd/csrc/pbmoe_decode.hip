@@ -816,9 +816,11 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// kernel 2, several tokens with the routes given (routed by route_topk):
-// grid (workgroups per token, tokens); the workgroups of token t stage its
-// x row in LDS once and their waves run over the token's units (route k,
+// kernel 2, persistent variant (several tokens; one token of a wide layer):
+// grid (workgroups per token, tokens); every workgroup first routes its
+// token from the logits (route_here; workgroup 0 of the token publishes
+// the routes) or loads the given routes; the workgroups of token t stage
+// its x row in LDS once and their waves run over the token's units (route k,
 // RPW consecutive rows), strided by the waves of the token; activations in
 // route order [T*K][I].  A wave holds two units' weights in registers
 // (buffers A and B, alternating, so no register copies): the next unit's
