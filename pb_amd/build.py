@@ -19,7 +19,7 @@ ROOT = os.path.dirname(HERE)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["pbmoe_kernels.hip", "pbmoe_decode.hip", "pbmoe_persist.hip", "pbmoe_prefill.hip", "pbmoe_attn.hip",
+HIP_SOURCES = ["pbmoe_kernels.hip", "pbmoe_decode.hip", "pbmoe_prefill.hip", "pbmoe_attn.hip",
                "pbmoe_abi.cpp", "pbmoe_pack.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",

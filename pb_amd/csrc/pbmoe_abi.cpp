@@ -110,8 +110,6 @@ struct pbmoe_ctx {
     DeviceBuf plan_work; // multi-workgroup plan scratch of pbmoe_dispatch_plan
     DeviceBuf attn_scratch; // q/k/v, chunk partials and attention values of one decode step
     DeviceBuf x_normed;     // [T][H] input RMSNorm rows of pbmoe_moe_layer_norm
-    DeviceBuf persist;      // tagged-word scratch of the one-launch batch-1 decode (zeroed on allocation)
-    bool persist_enabled = false; // PBMOE_DECODE_KERNELS=1 selects the one-launch decode for one token
     uint32_t cus = 0;            // compute units of the device
     hipEvent_t phase_ev[6] = {};
     bool phase_timing = false;
@@ -137,20 +135,6 @@ int ensure(pbmoe_ctx* ctx, DeviceBuf& b, size_t bytes)
     size_t want = bytes < 256 ? 256 : bytes;
     HIP_TRY(hipMalloc(&b.ptr, want));
     b.bytes = want;
-    return ok();
-}
-
-// ensure() for buffers whose contents must start at zero: a new allocation
-// is cleared by a fill kernel before first use.
-int ensure_zeroed(pbmoe_ctx* ctx, DeviceBuf& b, size_t bytes)
-{
-    if (b.bytes >= bytes && b.ptr)
-        return ok();
-    int rc = ensure(ctx, b, bytes);
-    if (rc)
-        return rc;
-    HIP_TRY(pbmoe::launch_fill_u32(ctx->stream, static_cast<uint32_t*>(b.ptr), 0u, b.bytes / 4));
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
     return ok();
 }
 
@@ -432,8 +416,6 @@ PBMOE_API int pbmoe_ctx_create(int device, pbmoe_ctx** out)
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess)
         e = pbmoe::static_scratch_init(device); // device address of the static scratch, once per device
-    if (const char* k = std::getenv("PBMOE_DECODE_KERNELS"))
-        ctx->persist_enabled = std::strcmp(k, "1") == 0;
     if (e == hipSuccess)
         e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess)
@@ -519,10 +501,6 @@ PBMOE_API int pbmoe_sync(pbmoe_ctx* ctx)
         if (st & (pbmoe::ST_BAD_SUM | pbmoe::ST_NEGATIVE))
             return fail(PBMOE_ERR_ROUTE,
                         "selected expert probabilities must have a positive finite sum");
-        if (st & pbmoe::ST_TIMEOUT)
-            return fail(PBMOE_ERR_TIMEOUT,
-                        "a workgroup of the one-launch decode waited too long for another (the grid was "
-                        "not resident at once); the call's results are invalid");
         if (st & pbmoe::ST_F16_RANGE)
             return fail(PBMOE_ERR_NONFINITE,
                         "a prefill SwiGLU activation exceeded the f16 operand range (|a| > 65504)");
@@ -988,6 +966,7 @@ static void drop_router(pbmoe_ctx* ctx, LayerBinding* b)
     b->router = nullptr;
     b->router_dtype = 0;
     b->router_q4 = pbmoe::Q4Rows{};
+    b->sel_bias = nullptr; // its copy may have been replaced by the failed bind
 }
 
 static void drop_gate(pbmoe_ctx* ctx, LayerBinding* b)
@@ -998,6 +977,31 @@ static void drop_gate(pbmoe_ctx* ctx, LayerBinding* b)
     b->shared_gate = nullptr;
     b->shared_gate_dtype = 0;
     b->gate_q4 = pbmoe::Q4Rows{};
+}
+
+// The selection bias of a router bind, adopted before the router itself so
+// that a failed copy leaves no new router without its bias.  No bias: an
+// owned copy from an earlier bind is freed.  On failure the layer keeps no
+// bias (a sigmoid-routed call then reports it as not bound).
+static int adopt_selection_bias(pbmoe_ctx* ctx, LayerBinding* b, const float* selection_bias, uint32_t flags,
+                                const float** out)
+{
+    *out = nullptr;
+    if (!selection_bias) {
+        if (b->bias_owned.ptr) {
+            HIP_TRY(hipStreamSynchronize(ctx->stream));
+            free_buf(b->bias_owned);
+        }
+        return ok();
+    }
+    const void* dev = nullptr;
+    int rc = adopt(ctx, selection_bias, (size_t)b->desc.experts * 4, flags, b->bias_owned, &dev);
+    if (rc) {
+        b->sel_bias = nullptr;
+        return rc;
+    }
+    *out = static_cast<const float*>(dev);
+    return ok();
 }
 
 PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weight, uint32_t dtype,
@@ -1020,6 +1024,9 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
     if (rc)
         return rc;
     size_t esz = dtype == PBMOE_DTYPE_F32 ? 4 : 2;
+    const float* bias = nullptr;
+    if ((rc = adopt_selection_bias(ctx, b, selection_bias, flags, &bias)))
+        return rc;
     const void* dev = nullptr;
     rc = adopt(ctx, weight, (size_t)b->desc.experts * b->desc.hidden * esz, flags, b->router_owned,
                &dev);
@@ -1032,13 +1039,7 @@ PBMOE_API int pbmoe_bind_router(pbmoe_ctx* ctx, uint32_t layer, const void* weig
     b->router_q4 = pbmoe::Q4Rows{};
     free_buf(b->router_s_owned); // a Q4 router bound before (the stream was synchronised by adopt)
     free_buf(b->router_b_owned);
-    b->sel_bias = nullptr;
-    if (selection_bias) {
-        rc = adopt(ctx, selection_bias, (size_t)b->desc.experts * 4, flags, b->bias_owned, &dev);
-        if (rc)
-            return rc;
-        b->sel_bias = static_cast<const float*>(dev);
-    }
+    b->sel_bias = bias;
     return ok();
 }
 
@@ -1097,6 +1098,9 @@ PBMOE_API int pbmoe_bind_router_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q
                     "sigmoid routing requires the per-expert selection bias");
     if ((rc = check_q4(weight, b->desc.hidden, group_size, flags)) || (rc = set_device(ctx)))
         return rc;
+    const float* bias = nullptr;
+    if ((rc = adopt_selection_bias(ctx, b, selection_bias, flags, &bias)))
+        return rc;
     pbmoe::Q4Rows q{};
     if ((rc = adopt_q4(ctx, weight, b->desc.experts, b->desc.hidden, group_size, flags, b->router_owned,
                        b->router_s_owned, b->router_b_owned, &q))) {
@@ -1106,14 +1110,7 @@ PBMOE_API int pbmoe_bind_router_q4(pbmoe_ctx* ctx, uint32_t layer, const pbmoe_q
     b->router_q4 = q;
     b->router = q.codes;
     b->router_dtype = pbmoe::DT_Q4;
-    b->sel_bias = nullptr;
-    if (selection_bias) {
-        const void* dev = nullptr;
-        rc = adopt(ctx, selection_bias, (size_t)b->desc.experts * 4, flags, b->bias_owned, &dev);
-        if (rc)
-            return rc;
-        b->sel_bias = static_cast<const float*>(dev);
-    }
+    b->sel_bias = bias;
     return ok();
 }
 
@@ -1343,22 +1340,6 @@ static int decode_args(pbmoe_ctx* ctx, LayerBinding* b, const float* x, const fl
     a->phase_timing = ctx->phase_timing;
     for (int i = 0; i < 6; ++i)
         a->phase_ev[i] = ctx->phase_ev[i];
-    // one token: the whole layer in one persistent launch where the shape allows
-    a->persist = nullptr;
-    pbmoe::PersistPlan pp{};
-    if (ctx->persist_enabled && pbmoe::persist_plan(*a, ctx->cus, &pp)) {
-        const size_t bytes = pp.words * 8;
-        if (fixed) {
-            uint8_t* region = fixed - pbmoe::STATIC_PERSIST_BYTES;
-            if (bytes <= pbmoe::STATIC_PERSIST_BYTES)
-                a->persist = reinterpret_cast<uint64_t*>(region);
-        } else {
-            if ((rc = ensure_zeroed(ctx, ctx->persist, bytes)))
-                return rc;
-            a->persist = static_cast<uint64_t*>(ctx->persist.ptr);
-        }
-        a->pplan = pp;
-    }
     return ok();
 }
 
@@ -1468,10 +1449,6 @@ static int expert_phase(pbmoe_ctx* ctx, uint32_t layer, const float* x, const fl
         fixed = static_cast<uint8_t*>(pbmoe::static_scratch(ctx->device, &cap));
         if (!fixed)
             return fail(PBMOE_ERR_DEVICE, "static scratch of device %d was not set up", ctx->device);
-        // the first STATIC_PERSIST_BYTES hold the one-launch path's tagged
-        // words; the rest the three-kernel path's buffers
-        fixed += pbmoe::STATIC_PERSIST_BYTES;
-        cap -= pbmoe::STATIC_PERSIST_BYTES;
         const DecodeScratchLayout l = decode_scratch_layout(d, tokens);
         if (l.total > cap)
             return fail(PBMOE_ERR_UNSUPPORTED,

@@ -2090,10 +2090,6 @@ hipError_t static_scratch_init(int device)
         return e;
     if (!p)
         return hipErrorInvalidSymbol;
-    // the tagged words of the one-launch decode start from zero (epoch 0)
-    e = hipMemset(p, 0, STATIC_PERSIST_BYTES);
-    if (e != hipSuccess)
-        return e;
     g_scratch_ptr[device] = p;
     return hipSuccess;
 }
@@ -2123,8 +2119,6 @@ hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mod
         return launch_route_topk(st, d.logits, d.sel_bias, d.tokens, d.rp, d.ids, d.weights, d.status);
     }
     const bool full = mode == DECODE_FULL_LAYER;
-    if (d.persist) // one token: the whole layer in one persistent launch
-        return launch_persist_decode(st, d, full, d.pplan, d.persist);
     err = launch_router_stage(st, d, full, d.shared != nullptr);
     if (err != hipSuccess)
         return err;

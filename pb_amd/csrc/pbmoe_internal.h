@@ -15,8 +15,7 @@ enum : uint32_t {
     ST_BAD_SUM = 1u << 2,      // renormalisation sum not positive/finite
     ST_NEGATIVE = 1u << 3,     // negative selected probability
     ST_PLAN_OVERFLOW = 1u << 4, // more routes than the plan buffers hold
-    ST_F16_RANGE = 1u << 5,     // prefill activation outside the f16 operand range
-    ST_TIMEOUT = 1u << 6        // a bounded wait of the one-launch decode ran out
+    ST_F16_RANGE = 1u << 5      // prefill activation outside the f16 operand range
 };
 
 // One projection inside a fixed expert slot.
@@ -86,16 +85,6 @@ uint32_t plan_work_words(uint32_t routes, uint32_t experts);
 hipError_t launch_dispatch_plan(hipStream_t s, const uint32_t* ids, uint32_t routes,
                                 uint32_t experts, uint32_t k, const Plan& plan,
                                 uint32_t* status);
-// Grid and scratch of the one-launch batch-1 decode (pbmoe_persist.hip).
-struct PersistPlan {
-    uint32_t nw;      // workgroups (all resident at once)
-    uint32_t ngroups; // unused (0)
-    uint32_t nci;     // 32-row gate/up units per expert
-    uint32_t nunits;  // gate/up units (routed slots and shared expert x chunks)
-    uint32_t rpw;     // combine rows per workgroup
-    size_t words;     // 64-bit scratch words: epoch, arrivals, logits, activations, norm sums, flags
-};
-
 // Decode path (tokens <= 16).  Modes: the full layer (router + routing +
 // experts), the expert phase for given routes, or routing only.
 enum : uint32_t { DECODE_FULL_LAYER = 0, DECODE_EXPERTS = 1, DECODE_ROUTE_ONLY = 2 };
@@ -131,56 +120,16 @@ struct DecodeArgs {
     hipEvent_t phase_ev[6];    // start/stop per kernel when phase_timing
     bool phase_timing;
     uint32_t* status;
-    uint64_t* persist;         // scratch of the one-launch path (zeroed when allocated), or null
-    PersistPlan pplan;         // its plan (valid when persist is set)
 };
 
 hipError_t launch_decode_layer(hipStream_t s, const DecodeArgs& d, uint32_t mode);
 
-// Arguments of persist_decode_kernel.
-struct PersistArgs {
-    const void* router_w;
-    const float* sel_bias;
-    RouteParams rp;
-    const void* sgate_w;
-    ExpertSet ex, sh;
-    uint32_t has_shared;
-    const float* x;
-    const float* in_norm_w;
-    float eps;
-    const float* residual;
-    float* hidden_out;
-    const float* next_norm_w;
-    float* next_normed;
-    uint32_t* ids;    // [K] routes out (full) or in
-    float* weights;   // [K]
-    uint32_t full;    // 1: router + routing in the kernel
-    uint32_t hidden, nunits, rpw;
-    uint32_t* epoch;  // call counter (its own 64-bit word)
-    uint64_t* arrive; // [nw] tagged arrivals
-    uint64_t* tl;     // [E + 1] tagged logits + shared gate logit
-    uint64_t* ta;     // [items][I] tagged SwiGLU activations
-    uint64_t* tn;     // [nw] tagged sums of squares (next-layer norm)
-    uint64_t* tfr;    // [nw] tagged "router rows published" flag per workgroup
-    uint64_t* tfu;    // [nunits] tagged "partials published" flag per unit
-    uint32_t* status;
-    uint32_t spin_max;
-};
-// true when the one-launch path covers the call (tokens == 1, the shape
-// limits, a grid of at most max_wgs workgroups = the device's CUs); fills
-// the plan
-bool persist_plan(const DecodeArgs& d, uint32_t max_wgs, PersistPlan* p);
-hipError_t launch_persist_decode(hipStream_t s, const DecodeArgs& d, bool full, const PersistPlan& p,
-                                 uint64_t* scratch);
 // Static scratch of the allocation-free decode entry point: a file-scope
 // device array in pbmoe_decode.hip.  static_scratch_init looks up its address
 // on `device` (which must be current) once; static_scratch returns it (null
 // before init) and its size.
 hipError_t static_scratch_init(int device);
 void* static_scratch(int device, size_t* bytes);
-// the first bytes of the static scratch: the one-launch decode's tagged words
-// (cleared once at set-up); the rest holds the three-kernel decode buffers
-constexpr size_t STATIC_PERSIST_BYTES = 4u << 20;
 // Prefill path (grouped GEMM on the matrix cores, any token count).
 struct PrefillArgs {
     ExpertSet ex;              // routed experts

@@ -5,7 +5,6 @@ tokens, so stale scratch from the first call would show), with and without
 caller-provided route buffers and the next-layer norm."""
 from __future__ import annotations
 
-import os
 import sys
 
 import numpy as np
@@ -23,21 +22,9 @@ def _say(msg):
     sys.stdout.flush()
 
 
-@pytest.fixture(scope="module", params=["three-kernel", "one-launch"])
-def ctx(request):
-    """Both decode paths: the default three kernels, and the one-launch
-    batch-1 kernel (PBMOE_DECODE_KERNELS=1), whose tagged words live in the
-    static scratch too."""
-    old = os.environ.get("PBMOE_DECODE_KERNELS")
-    if request.param == "one-launch":
-        os.environ["PBMOE_DECODE_KERNELS"] = "1"
-    try:
-        c = abi.Context(0)
-    finally:
-        if old is None:
-            os.environ.pop("PBMOE_DECODE_KERNELS", None)
-        else:
-            os.environ["PBMOE_DECODE_KERNELS"] = old
+@pytest.fixture(scope="module")
+def ctx():
+    c = abi.Context(0)
     yield c
     c.close()
 
