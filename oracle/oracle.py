@@ -311,6 +311,22 @@ def combine(residual, ys, weights, shared=None, shared_weight: float = 0.0) -> n
     return out
 
 
+def _gate_arg(shared_gate_w, shared_gate_dtype: int):
+    """The shared-gate argument of or_moe_block[_f64]: a dense row, or for
+    DT_Q4 a (codes, scales, biases, group, sb_dtype) tuple passed as an
+    or_q4_rows struct; plus the arrays it points into (kept alive)."""
+    if shared_gate_w is None:
+        return None, []
+    if shared_gate_dtype == DT_Q4:
+        codes, scales, biases, group, sbt = shared_gate_w
+        keep = [np.ascontiguousarray(codes, dtype=np.uint8), _sb(scales, sbt), _sb(biases, sbt)]
+        q = _Q4Rows(keep[0].ctypes.data, keep[1].ctypes.data, keep[2].ctypes.data, group, sbt)
+        keep.append(q)
+        return C.byref(q), keep
+    keep = [np.ascontiguousarray(shared_gate_w)]
+    return _p(keep[0]), keep
+
+
 def moe_block(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarray, residual: np.ndarray,
               ids: np.ndarray, weights: np.ndarray, shared_layout: Q4Layout | None = None,
               shared_slot: np.ndarray | None = None, shared_gate_w: np.ndarray | None = None,
@@ -327,18 +343,7 @@ def moe_block(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarray, 
     out = np.empty((rows, hidden), np.float32)
     nn = np.empty((rows, hidden), np.float32) if next_norm_w is not None else None
     nw = _f32(next_norm_w) if next_norm_w is not None else None
-    keep = []
-    if shared_gate_w is None:
-        gate_arg = None
-    elif shared_gate_dtype == DT_Q4:  # (codes, scales, biases, group, sb_dtype)
-        codes, scales, biases, group, sbt = shared_gate_w
-        keep = [np.ascontiguousarray(codes, dtype=np.uint8), _sb(scales, sbt), _sb(biases, sbt)]
-        q = _Q4Rows(keep[0].ctypes.data, keep[1].ctypes.data, keep[2].ctypes.data, group, sbt)
-        keep.append(q)
-        gate_arg = C.byref(q)
-    else:
-        keep = [np.ascontiguousarray(shared_gate_w)]
-        gate_arg = _p(keep[0])
+    gate_arg, keep = _gate_arg(shared_gate_w, shared_gate_dtype)
     rc = lib().or_moe_block(
         C.byref(layout), _p(slots), C.c_int(experts),
         C.byref(shared_layout) if shared_layout is not None else None,
@@ -356,19 +361,20 @@ def moe_block_f64(layout: Q4Layout, slots: np.ndarray, experts: int, x: np.ndarr
                   ids: np.ndarray, weights: np.ndarray, shared_layout: Q4Layout | None = None,
                   shared_slot: np.ndarray | None = None, shared_gate_w: np.ndarray | None = None,
                   shared_gate_dtype: int = DT_F16, threads: int = 1) -> np.ndarray:
-    """fp64 evaluation of the block (the exact value the f32 paths round)."""
+    """fp64 evaluation of the block (the exact value the f32 paths round);
+    the shared gate as for moe_block (dense row, or a DT_Q4 tuple)."""
     xx = _f32(x)
     rr = _f32(residual)
     rows, hidden = xx.shape
     ii = np.ascontiguousarray(ids, dtype=np.int32)
     ww = _f32(weights)
     out = np.empty((rows, hidden), np.float64)
-    sg = np.ascontiguousarray(shared_gate_w) if shared_gate_w is not None else None
+    gate_arg, keep = _gate_arg(shared_gate_w, shared_gate_dtype)
     rc = lib().or_moe_block_f64(
         C.byref(layout), _p(slots), C.c_int(experts),
         C.byref(shared_layout) if shared_layout is not None else None,
         _p(shared_slot) if shared_slot is not None else None,
-        _p(sg) if sg is not None else None, C.c_int(shared_gate_dtype),
+        gate_arg, C.c_int(shared_gate_dtype),
         _p(xx), _p(rr), C.c_int(rows), C.c_int(ii.shape[1]), _p(ii), _p(ww), _p(out), C.c_int(threads))
     if rc:
         raise ValueError(f"oracle moe_block_f64 failed: {rc}")

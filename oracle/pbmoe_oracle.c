@@ -32,6 +32,9 @@
  *     of the two largest biased scores, keep topk_group groups, top-k among
  *     their experts; ties to the lower index), exact ties included.
  */
+#ifdef __FMA__
+#include <immintrin.h>
+#endif
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -434,7 +437,59 @@ int or_q4_fma_matvec(const uint8_t* packed, const float* x, const void* scales,
         return OR_ERR_ARG;
     int gpr = (cols + group - 1) / group;
     size_t stride = (size_t)(cols + 1) / 2;
-    for (int r = 0; r < rows; ++r) {
+    /* Eight rows side by side: each row's sum is the same sequential chain of
+     * operations as one row alone (bitwise equal); the eight chains run in
+     * the lanes of one vector, so that their additions overlap.  A group's
+     * codes of the eight rows are decoded into q8 first. */
+    int r = 0;
+    float q8[128 * 8];
+    if (group <= 128)
+        for (; r + 8 <= rows; r += 8) {
+            float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            for (int g = 0; g < gpr; ++g) {
+                float s[8], b[8];
+                for (int j = 0; j < 8; ++j) {
+                    s[j] = or_load(scales, sb_dtype, (size_t)(r + j) * gpr + g);
+                    b[j] = or_load(biases, sb_dtype, (size_t)(r + j) * gpr + g);
+                }
+                int c0 = g * group, end = (g + 1) * group < cols ? (g + 1) * group : cols;
+                if ((c0 & 1) == 0 && ((end - c0) & 1) == 0) {
+                    for (int j = 0; j < 8; ++j) {
+                        const uint8_t* row = packed + (size_t)(r + j) * stride + c0 / 2;
+                        for (int i = 0; i < (end - c0) / 2; ++i) {
+                            q8[(2 * i) * 8 + j] = (float)(row[i] & 0x0F);
+                            q8[(2 * i + 1) * 8 + j] = (float)(row[i] >> 4);
+                        }
+                    }
+                } else {
+                    for (int c = c0; c < end; ++c)
+                        for (int j = 0; j < 8; ++j)
+                            q8[(c - c0) * 8 + j] = or_nibble(packed, stride, r + j, c);
+                }
+#ifdef __FMA__
+                /* lane j = row r + j: mul, mul, fused multiply-add, add, the
+                 * operations (and roundings) of the scalar loop below */
+                __m256 va = _mm256_loadu_ps(acc);
+                const __m256 vs = _mm256_loadu_ps(s), vb = _mm256_loadu_ps(b);
+                for (int c = c0; c < end; ++c) {
+                    const __m256 xc = _mm256_set1_ps(x[c]);
+                    const __m256 q = _mm256_loadu_ps(q8 + (c - c0) * 8);
+                    va = _mm256_add_ps(va, _mm256_fmadd_ps(q, _mm256_mul_ps(vs, xc), _mm256_mul_ps(vb, xc)));
+                }
+                _mm256_storeu_ps(acc, va);
+#else
+                for (int c = c0; c < end; ++c) {
+                    const float xc = x[c];
+                    const float* q = q8 + (c - c0) * 8;
+                    for (int j = 0; j < 8; ++j)
+                        acc[j] = acc[j] + fmaf(q[j], s[j] * xc, b[j] * xc);
+                }
+#endif
+            }
+            for (int j = 0; j < 8; ++j)
+                out[r + j] = acc[j];
+        }
+    for (; r < rows; ++r) {
         float acc = 0.0f;
         for (int g = 0; g < gpr; ++g) {
             float s = or_load(scales, sb_dtype, (size_t)r * gpr + g);
@@ -760,83 +815,150 @@ int or_route_rows(const float* logits, const float* bias, int rows, int experts,
  * f32 rounding error where outputs are large enough that a fixed absolute
  * tolerance falls below f32 resolution.
  * ---------------------------------------------------------------------- */
-static void or_projection_f64(const or_q4_layout* l, const uint8_t* slot, int proj,
-                              const double* x, double* out)
+/* Row r of a Q4 projection [rows][cols] as exact f64 weights q*s + b. */
+static void or_q4_row_f64(const uint8_t* packed, const void* sc, const void* bi, int sb_dtype, int cols, int g,
+                          int r, double* w)
 {
-    int rows = proj == 2 ? (int)l->hidden : (int)l->intermediate;
-    int cols = proj == 2 ? (int)l->intermediate : (int)l->hidden;
-    int g = (int)l->group_size, gpr = cols / g;
-    const uint8_t* packed = slot + l->offset[3 * proj];
-    const void* sc = slot + l->offset[3 * proj + 1];
-    const void* bi = slot + l->offset[3 * proj + 2];
-    size_t stride = (size_t)(cols + 1) / 2;
-    for (int r = 0; r < rows; ++r) {
-        double acc = 0.0;
-        for (int c = 0; c < cols; ++c) {
-            double s = or_load(sc, (int)l->sb_dtype, (size_t)r * gpr + c / g);
-            double b = or_load(bi, (int)l->sb_dtype, (size_t)r * gpr + c / g);
-            acc += ((double)or_nibble(packed, stride, r, c) * s + b) * x[c];
+    const int gpr = cols / g;
+    const uint8_t* row = packed + (size_t)r * (size_t)(cols / 2);
+    for (int k = 0; k < gpr; ++k) {
+        const double s = or_load(sc, sb_dtype, (size_t)r * gpr + k);
+        const double b = or_load(bi, sb_dtype, (size_t)r * gpr + k);
+        for (int i = k * g / 2; i < (k + 1) * g / 2; ++i) {
+            w[2 * i] = (double)(row[i] & 0x0F) * s + b;
+            w[2 * i + 1] = (double)(row[i] >> 4) * s + b;
         }
-        out[r] = acc;
     }
 }
 
-static void or_expert_f64(const or_q4_layout* l, const uint8_t* slot, const double* x, double* y)
+static double or_dot_f64(const double* a, const double* b, int n)
 {
-    int I = (int)l->intermediate;
-    double* g = (double*)malloc(sizeof(double) * 3 * (size_t)I);
-    double* u = g + I;
-    double* a = g + 2 * I;
-    or_projection_f64(l, slot, 0, x, g);
-    or_projection_f64(l, slot, 1, x, u);
-    for (int i = 0; i < I; ++i)
-        a[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
-    or_projection_f64(l, slot, 2, a, y);
-    free(g);
+    double acc = 0.0;
+#ifdef _OPENMP
+#pragma omp simd reduction(+ : acc)
+#endif
+    for (int i = 0; i < n; ++i)
+        acc += a[i] * b[i];
+    return acc;
 }
 
+/* One expert's SwiGLU MLP in f64 for n input rows x[n][H] -> y[n][H]: every
+ * weight row is decoded once and applied to all n rows. */
+static void or_expert_f64_rows(const or_q4_layout* l, const uint8_t* slot, const double* x, int n, double* y)
+{
+    const int H = (int)l->hidden, I = (int)l->intermediate, g = (int)l->group_size, sbt = (int)l->sb_dtype;
+    double* w = (double*)malloc(sizeof(double) * (size_t)(H > I ? H : I));
+    double* gu = (double*)malloc(sizeof(double) * 2 * (size_t)n * I);
+    double* act = (double*)malloc(sizeof(double) * (size_t)n * I);
+    for (int m = 0; m < 2; ++m) /* gate, up */
+        for (int i = 0; i < I; ++i) {
+            or_q4_row_f64(slot + l->offset[3 * m], slot + l->offset[3 * m + 1], slot + l->offset[3 * m + 2], sbt,
+                          H, g, i, w);
+            for (int t = 0; t < n; ++t)
+                gu[((size_t)m * n + t) * I + i] = or_dot_f64(w, x + (size_t)t * H, H);
+        }
+    for (size_t e = 0; e < (size_t)n * I; ++e) {
+        const double gg = gu[e], uu = gu[(size_t)n * I + e];
+        act[e] = gg / (1.0 + exp(-gg)) * uu;
+    }
+    for (int r = 0; r < H; ++r) {
+        or_q4_row_f64(slot + l->offset[6], slot + l->offset[7], slot + l->offset[8], sbt, I, g, r, w);
+        for (int t = 0; t < n; ++t)
+            y[(size_t)t * H + r] = or_dot_f64(w, act + (size_t)t * I, I);
+    }
+    free(w);
+    free(gu);
+    free(act);
+}
+
+/* Expert-major: the routes of each expert (and the shared expert over all
+ * rows) form one job; then the combine in f64. */
 int or_moe_block_f64(const or_q4_layout* lay, const uint8_t* slots, int experts,
                      const or_q4_layout* shared_lay, const uint8_t* shared_slot,
                      const void* shared_gate_w, int shared_gate_dtype, const float* x,
                      const float* residual, int rows, int k, const int32_t* ids,
                      const float* weights, double* hidden, int threads)
 {
-    int H = (int)lay->hidden;
-    for (int i = 0; i < rows * k; ++i)
+    const int H = (int)lay->hidden;
+    const int R = rows * k;
+    for (int i = 0; i < R; ++i)
         if (ids[i] < 0 || ids[i] >= experts)
             return OR_ERR_ROUTE;
+    if (shared_lay && (int)shared_lay->hidden != H)
+        return OR_ERR_SHAPE;
+    /* routes grouped by expert (stable) */
+    int* start = (int*)calloc((size_t)experts + 1, sizeof(int));
+    int* order = (int*)malloc(sizeof(int) * (size_t)(R > 0 ? R : 1));
+    double* xd = (double*)malloc(sizeof(double) * (size_t)rows * H);
+    double* y = (double*)malloc(sizeof(double) * (size_t)(R > 0 ? R : 1) * H);
+    double* S = shared_lay ? (double*)malloc(sizeof(double) * (size_t)rows * H) : NULL;
+    for (int i = 0; i < R; ++i)
+        start[ids[i] + 1]++;
+    for (int e = 0; e < experts; ++e)
+        start[e + 1] += start[e];
+    {
+        int* fill = (int*)malloc(sizeof(int) * (size_t)experts);
+        memcpy(fill, start, sizeof(int) * (size_t)experts);
+        for (int i = 0; i < R; ++i)
+            order[fill[ids[i]]++] = i;
+        free(fill);
+    }
+    for (size_t i = 0; i < (size_t)rows * H; ++i)
+        xd[i] = x[i];
+    const int jobs = experts + (shared_lay ? 1 : 0);
     (void)threads;
 #ifdef _OPENMP
 #pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(dynamic, 1)
 #endif
+    for (int j = 0; j < jobs; ++j) {
+        if (j == experts) { /* the shared expert over every row */
+            or_expert_f64_rows(shared_lay, shared_slot, xd, rows, S);
+            continue;
+        }
+        const int n = start[j + 1] - start[j];
+        if (n == 0)
+            continue;
+        double* xin = (double*)malloc(sizeof(double) * (size_t)n * H);
+        double* yo = (double*)malloc(sizeof(double) * (size_t)n * H);
+        for (int q = 0; q < n; ++q)
+            memcpy(xin + (size_t)q * H, xd + (size_t)(order[start[j] + q] / k) * H, sizeof(double) * (size_t)H);
+        or_expert_f64_rows(lay, slots + (size_t)j * lay->expert_bytes, xin, n, yo);
+        for (int q = 0; q < n; ++q)
+            memcpy(y + (size_t)order[start[j] + q] * H, yo + (size_t)q * H, sizeof(double) * (size_t)H);
+        free(xin);
+        free(yo);
+    }
     for (int t = 0; t < rows; ++t) {
-        double* xd = (double*)malloc(sizeof(double) * (size_t)H);
-        double* y = (double*)malloc(sizeof(double) * (size_t)H);
         double* h = hidden + (size_t)t * H;
-        for (int c = 0; c < H; ++c) {
-            xd[c] = x[(size_t)t * H + c];
+        for (int c = 0; c < H; ++c)
             h[c] = residual[(size_t)t * H + c];
-        }
-        for (int j = 0; j < k; ++j) {
-            or_expert_f64(lay, slots + (size_t)ids[t * k + j] * lay->expert_bytes, xd, y);
+        for (int j = 0; j < k; ++j)
             for (int c = 0; c < H; ++c)
-                h[c] += (double)weights[t * k + j] * y[c];
-        }
+                h[c] += (double)weights[t * k + j] * y[((size_t)t * k + j) * H + c];
         if (shared_lay) {
-            or_expert_f64(shared_lay, shared_slot, xd, y);
             double g = 80.0;
-            if (shared_gate_w) {
+            const double* xt = xd + (size_t)t * H;
+            if (shared_gate_w && shared_gate_dtype == OR_DT_Q4) {
+                const or_q4_rows* q = (const or_q4_rows*)shared_gate_w;
+                double* w = (double*)malloc(sizeof(double) * (size_t)H);
+                or_q4_row_f64(q->codes, q->scales, q->biases, q->sb_dtype, H, q->group, 0, w);
+                g = or_dot_f64(w, xt, H);
+                free(w);
+            } else if (shared_gate_w) {
                 g = 0.0;
                 for (int c = 0; c < H; ++c)
-                    g += (double)or_load(shared_gate_w, shared_gate_dtype, (size_t)c) * xd[c];
+                    g += (double)or_load(shared_gate_w, shared_gate_dtype, (size_t)c) * xt[c];
             }
-            double sw = 1.0 / (1.0 + exp(-g));
+            const double sw = 1.0 / (1.0 + exp(-g));
             for (int c = 0; c < H; ++c)
-                h[c] += sw * y[c];
+                h[c] += sw * S[(size_t)t * H + c];
         }
-        free(xd);
-        free(y);
     }
+    free(start);
+    free(order);
+    free(xd);
+    free(y);
+    free(S);
     return OR_OK;
 }
 

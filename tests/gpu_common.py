@@ -86,13 +86,30 @@ class DeviceLayer:
                                int(sl.expert_bytes))
 
     def compact_slots(self, ids: np.ndarray):
-        """Host slots of just the experts in `ids`, and ids remapped onto them."""
+        """Host slots of just the experts in `ids`, and ids remapped onto them
+        (the last result is kept: the f32 and fp64 blocks of one check ask
+        for the same experts)."""
+        key = np.ascontiguousarray(ids, dtype=np.int64).tobytes()
+        cached = getattr(self, "_compact", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        res = self._compact_slots(ids)
+        self._compact = (key, res)
+        return res
+
+    def _compact_slots(self, ids: np.ndarray):
         uniq = sorted(set(int(e) for e in ids.ravel()))
         lay, cfg = self.layout, self.cfg
-        parts = [synth.q4_experts(SEED, synth.T_EXPERT, self.layer, e, 1, cfg.hidden, cfg.intermediate, cfg.group,
-                                  cfg.sb_dtype, lay.offsets, int(lay.expert_bytes)) for e in uniq]
+        runs = []  # consecutive expert ids generated in one call
+        for e in uniq:
+            if runs and runs[-1][0] + runs[-1][1] == e:
+                runs[-1][1] += 1
+            else:
+                runs.append([e, 1])
+        parts = [synth.q4_experts(SEED, synth.T_EXPERT, self.layer, e0, n, cfg.hidden, cfg.intermediate, cfg.group,
+                                  cfg.sb_dtype, lay.offsets, int(lay.expert_bytes)) for e0, n in runs]
         if self.centred:
-            parts = [synth.center_q4_slots(p_, lay, 1, cfg.sb_dtype) for p_ in parts]
+            parts = [synth.center_q4_slots(p_, lay, n, cfg.sb_dtype) for p_, (_, n) in zip(parts, runs)]
         remap = {e: i for i, e in enumerate(uniq)}
         return np.concatenate(parts), np.vectorize(remap.get)(ids).astype(np.int32), len(uniq)
 
@@ -110,12 +127,12 @@ class DeviceLayer:
                              shared_gate_w=gw, shared_gate_dtype=gdt, next_norm_w=next_norm, threads=threads)
 
     def exact_block(self, x, residual, ids, weights, threads=8):
-        assert self.q4_gate is None, "the fp64 block takes a dense shared gate row"
         slots, rid, n = self.compact_slots(ids)
         h = self.host
+        gw, gdt = self._oracle_gate()
         return orc.moe_block_f64(self.oracle_layout(), slots, n, x, residual, rid, weights,
                                  shared_layout=self.oracle_shared_layout(), shared_slot=h.shared_slot,
-                                 shared_gate_w=h.shared_gate_f16, shared_gate_dtype=orc.DT_F16, threads=threads)
+                                 shared_gate_w=gw, shared_gate_dtype=gdt, threads=threads)
 
     def oracle_logits(self, x):
         if self.q4_router is not None:

@@ -170,9 +170,8 @@ def test_prefill_c5_shape(ctx):
 
 def test_prefill_c5_full_chunk(ctx):
     """C5 at its benchmark size: 1024 tokens through the DeepSeek-V3-shaped
-    layer (group-limited sigmoid routing on the device); sampled rows (every
-    16th plus rows of the most and least loaded experts) against the oracle
-    and its fp64 evaluation, and a second call bitwise identical."""
+    layer (group-limited sigmoid routing on the device); every row against
+    the oracle and its fp64 evaluation, and a second call bitwise identical."""
     _say("[test] prefill C5 1024 tokens")
     dl = _layer(ctx, C5)
     T = 1024
@@ -183,11 +182,8 @@ def test_prefill_c5_full_chunk(ctx):
     np.testing.assert_array_equal(got.view(np.uint32), again.view(np.uint32))
     ids_h, w_h = ids.download().astype(np.int32), w.download()
     counts = np.bincount(ids_h.ravel(), minlength=C5.experts)
-    heavy, light = int(np.argmax(counts)), int(np.argmin(np.where(counts > 0, counts, 1 << 30)))
-    rows = set(range(0, T, 16))
-    rows |= set(np.nonzero((ids_h == light).any(1))[0][:4].tolist())
-    rows |= set(np.nonzero((ids_h == heavy).any(1))[0][-4:].tolist())
-    _check_rows(dl, xh, rh, ids_h, w_h, got, np.array(sorted(rows)), tag="C5 1024")
+    _say(f"[info] C5 expert load max={counts.max()} min={counts.min()} used={np.count_nonzero(counts)}")
+    _check_rows(dl, xh, rh, ids_h, w_h, got, np.arange(T), tag="C5 1024")
 
 
 def test_prefill_out_of_range_route_is_reported(ctx):

@@ -307,3 +307,112 @@ def test_two_layer_deferred_handoff_golden():
     ids, vals = orc.top_k_sorted(logits, 2)
     assert ids == [0, 3]
     assert abs(vals[0] - 3.3762858) <= 1e-5 and abs(vals[1] - 1.4731821) <= 1e-5
+
+
+# ------------------------------------------- fp64 block, shared branch ---
+def _pin_layer(gated: bool, sbt: int, seed: int):
+    from pb_amd import abi, synth
+    from pb_amd.synth import MoeConfig
+    cfg = MoeConfig("pin_shared", hidden=256, intermediate=128, experts=6, k=3, shared_intermediate=192,
+                    shared_gated=gated, sb_dtype=sbt)
+    host = synth.make_layer(cfg, seed, 0, abi.q4_layout_fixed)
+    lay = orc.make_layout(cfg.hidden, cfg.intermediate, cfg.group, sbt, host.layout.offsets,
+                          int(host.layout.expert_bytes))
+    sl = orc.make_layout(cfg.hidden, cfg.shared_intermediate, cfg.group, sbt, host.shared_layout.offsets,
+                         int(host.shared_layout.expert_bytes))
+    T = 5
+    x, r = synth.activations(seed, 1, T, cfg.hidden)
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(cfg.experts, cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.1, 0.5, (T, cfg.k)).astype(F)
+    return cfg, host, lay, sl, x, r, ids, w
+
+
+@pytest.mark.parametrize("gate", ["none", "dense", "q4"])
+@pytest.mark.parametrize("sbt", [1, 2])
+def test_fp64_block_shared_branch_agrees_with_f32(gate, sbt):
+    """or_moe_block_f64 (the exact value that decides max-abs for large
+    outputs) against the pinned f32 oracle on small random layers with an
+    ungated shared expert, a dense f16 gate row and a Q4 gate row: the two
+    agree to f32 rounding, while dropping the shared term or leaving the gate
+    out (sigma = 1) moves the result by far more than that, so the check
+    can tell those mistakes apart."""
+    from pb_amd import abi, synth
+    cfg, host, lay, sl, x, r, ids, w = _pin_layer(gate != "none", sbt, 31 + sbt)
+    gw, gdt = None, orc.DT_F16
+    if gate == "dense":
+        gw = host.shared_gate_f16
+    elif gate == "q4":
+        gw = synth.q4_matrix(31, synth.T_SHARED_GATE_Q4, 0, 1, cfg.hidden, cfg.group, sbt,
+                             abi.q4_layout_fixed) + (cfg.group, sbt)
+        gdt = orc.DT_Q4
+    kw = dict(shared_layout=sl, shared_slot=host.shared_slot, shared_gate_w=gw, shared_gate_dtype=gdt)
+    h32, _ = orc.moe_block(lay, host.slots, cfg.experts, x, r, ids, w, **kw)
+    h64 = orc.moe_block_f64(lay, host.slots, cfg.experts, x, r, ids, w, **kw)
+    # f32 rounding of these rows: about 1e-6 of the row's largest output
+    # (measured 3e-7 .. 1.4e-6); the bar is 1e-5 of it
+    tol = 1e-5 * (np.max(np.abs(h64), axis=1, keepdims=True) + 1.0)
+    err = np.abs(h32.astype(np.float64) - h64)
+    assert np.all(err <= tol), float(np.max(err / tol))
+    # the shared expert's contribution, and what the plausible mistakes change
+    no_sh = orc.moe_block_f64(lay, host.slots, cfg.experts, x, r, ids, w)
+    assert np.all(np.max(np.abs(h64 - no_sh), axis=1) > 100 * tol[:, 0])
+    if gate != "none":
+        # the gate applied (sigma(g)) against no gate (sigma = 1)
+        ones = orc.moe_block_f64(lay, host.slots, cfg.experts, x, r, ids, w, shared_layout=sl,
+                                 shared_slot=host.shared_slot)
+        assert np.all(np.max(np.abs(ones - h64), axis=1) > 10 * tol[:, 0])
+
+
+def test_fp64_block_dense_and_q4_gate_read_different_rows():
+    """The fp64 block reads a Q4 gate as codes/scales/biases, not as raw
+    16-bit values: with the dense row and the Q4 row of the same layer the
+    results differ, and each agrees with the f32 oracle given the same gate."""
+    from pb_amd import abi, synth
+    cfg, host, lay, sl, x, r, ids, w = _pin_layer(True, 1, 41)
+    q4 = synth.q4_matrix(41, synth.T_SHARED_GATE_Q4, 0, 1, cfg.hidden, cfg.group, 1, abi.q4_layout_fixed)
+    kw = dict(shared_layout=sl, shared_slot=host.shared_slot)
+    a = orc.moe_block_f64(lay, host.slots, cfg.experts, x, r, ids, w, shared_gate_w=q4 + (cfg.group, 1),
+                          shared_gate_dtype=orc.DT_Q4, **kw)
+    b = orc.moe_block_f64(lay, host.slots, cfg.experts, x, r, ids, w, shared_gate_w=host.shared_gate_f16,
+                          shared_gate_dtype=orc.DT_F16, **kw)
+    assert np.max(np.abs(a - b)) > 1e-3
+    a32, _ = orc.moe_block(lay, host.slots, cfg.experts, x, r, ids, w, shared_gate_w=q4 + (cfg.group, 1),
+                           shared_gate_dtype=orc.DT_Q4, **kw)
+    assert np.max(np.abs(a32 - a)) < 1e-4 * max(1.0, float(np.max(np.abs(a))))
+
+
+# ------------------------------------------------- multi-thread helpers ---
+@pytest.mark.parametrize("dtype", [orc.DT_F32, orc.DT_F16, orc.DT_BF16])
+@pytest.mark.parametrize("threads", [1, 2, 3, 8])
+def test_router_logits_mt_bitwise_equals_router_logits(dtype, threads):
+    """or_router_logits_mt (the all-cores CPU baseline's router) splits the
+    rows over threads; every logit is bitwise the sequential one."""
+    rng = np.random.default_rng(7 + dtype)
+    E, H = 77, 520
+    w = (rng.standard_normal((E, H)) * 0.02).astype(F)
+    if dtype == orc.DT_F16:
+        w = w.astype(np.float16)
+    elif dtype == orc.DT_BF16:
+        w = (w.view(np.uint32) >> 16).astype(np.uint16)
+    x = rng.standard_normal(H).astype(F)
+    ref = orc.router_logits(w, x, dtype)
+    got = orc.router_logits_mt(w, x, dtype, threads)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q4_matvec_rows_bitwise_equal_one_row_at_a_time():
+    """or_q4_fma_matvec takes rows four at a time (interleaved chains); each
+    row must equal the same row computed alone, including the rows left
+    over after the last block of four."""
+    rng = np.random.default_rng(3)
+    rows, cols, g = 11, 320, 64
+    packed = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+    sc = rng.uniform(0.005, 0.02, rows * cols // g).astype(np.float16)
+    bi = rng.uniform(-0.1, 0.1, rows * cols // g).astype(np.float16)
+    x = rng.standard_normal(cols).astype(F)
+    allr = orc.q4_fma_matvec(packed, x, sc, bi, rows, cols, g, orc.DT_F16)
+    for r in range(rows):
+        one = orc.q4_fma_matvec(packed[r * cols // 2:(r + 1) * cols // 2], x, sc[r * cols // g:(r + 1) * cols // g],
+                                bi[r * cols // g:(r + 1) * cols // g], 1, cols, g, orc.DT_F16)
+        assert one.view(np.uint32)[0] == allr.view(np.uint32)[r]
