@@ -155,24 +155,33 @@ def cpu_baseline(cfg, host_layers, tokens: int, budget_s: float, threads: int):
 
 
 def host_cores() -> int:
-    """Cores the all-cores baseline uses: OMP_NUM_THREADS where set (the GPU
-    box sets it to its CPU share), else the visible CPUs; at most 16."""
-    n = os.cpu_count() or 1
+    """Threads of the all-cores baseline: OMP_NUM_THREADS where set (the GPU
+    box sets it to the CPU share one GPU's job may use), else every CPU this
+    process may run on."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     env = os.environ.get("OMP_NUM_THREADS", "")
     if env.isdigit() and int(env) > 0:
-        n = min(n, int(env))
-    return max(1, min(n, 16))
+        n = int(env)
+    return max(1, n)
 
 
 def cpu_baselines(cfg, host_layers, tokens: int, budget_s: float) -> dict:
-    """The oracle on all cores (the reported baseline) and on one core (the
-    reference's own sequential path), each on about `budget_s` of work."""
+    """The oracle on all the job's cores (the reported baseline) and on one
+    core (the reference's own sequential path), each on about `budget_s` of
+    work; the record names the host's CPU count beside the threads used."""
     cores = host_cores()
     one = cpu_baseline(cfg, host_layers, tokens, budget_s, 1)
+    host = {"nproc": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "threads_rule": "OMP_NUM_THREADS where set (the CPU share of one GPU's job on the GPU box), "
+                            "else every CPU of the process's affinity mask"}
     if cores == 1:
+        one["host"] = host
         return one
     rec = cpu_baseline(cfg, host_layers, tokens, budget_s, cores)
     rec["single_core"] = one
+    rec["host"] = host
     return rec
 
 
@@ -503,7 +512,7 @@ def stack_bytes_per_token(acfg, mcfg, layers: int, position: int) -> dict:
     H, g = acfg.hidden, acfg.group
     attn = (q4_proj_bytes(acfg.q_width, H, g) + 2 * q4_proj_bytes(acfg.kv_width, H, g)
             + q4_proj_bytes(H, acfg.q_width, g) + (position + 1) * acfg.kv_width * 2 * 2 + 6 * H * 4)
-    moe = algorithmic_bytes(mcfg, mcfg.k, 1)
+    moe = algorithmic_bytes(mcfg, mcfg.k, 1, fused_norm=True)
     return {"attention": attn * layers, "moe": moe * layers, "total": (attn + moe) * layers}
 
 
@@ -684,6 +693,98 @@ def cpu_stack_baseline(acfg, mcfg, host_layers, pos: int, keys, vals, budget_s: 
                       f"per token = {C4_LAYERS} x {per_layer_us:.0f} us"}
 
 
+NORM_SEED_TENSOR = 9001  # seeded input-RMSNorm weight of the chained decode bench
+
+
+def decode_leg(ctx, ev, cfg, layers, T: int, K: int, R: int, warmup: int, phases: bool) -> dict:
+    """Chained decode steps: step i runs the MoE layer on copy i mod L from
+    the un-normalised hidden state h_i (pbmoe_moe_layer_norm: the input
+    RMSNorm inside the router stage, h_i also the residual) and writes
+    h_{i+1}, which step i + 1 reads, so every step waits for the one before
+    it as a decode loop does.  Timed: a hipGraph of K chained steps replayed
+    R times back to back (median replay); also the same K steps as one ABI
+    call each, and (phases) the mean per-kernel durations from hipEvents on
+    the dispatch packets over min(K, 512) eager steps."""
+    from pb_amd import abi, synth
+    H, L = cfg.hidden, len(layers)
+    stream = ctx.stream()
+    _, h0 = synth.activations(SEED, 999, T, H)
+    nw = synth.uniform_f32(SEED, NORM_SEED_TENSOR, 0, 0, 0, H, 0.5, 1.0)
+    hb = [ctx.to_device(h0), ctx.array((T, H), np.float32)]
+    norm_w = ctx.to_device(nw)
+    ids = ctx.array((T, cfg.k), np.uint32)
+    w = ctx.array((T, cfg.k), np.float32)
+    state = {"i": 0}  # global step index: buffer parity and layer copy
+
+    def step():
+        i = state["i"]
+        layers[i % L][0].forward_norm(hb[i % 2], norm_w, hb[(i + 1) % 2], ids, w)
+        state["i"] = i + 1
+
+    for _ in range(warmup):
+        step()
+    ctx.sync()
+    a, b = ev.create(), ev.create()
+    ev.record(a, stream)
+    for _ in range(K):
+        step()
+    ev.record(b, stream)
+    us_stream = ev.elapsed_ms(a, b) * 1e3 / K
+    ctx.sync()
+    # one graph per (layer copy, buffer parity) a replay starts from; the
+    # replays continue the chain where the previous one stopped
+    i0 = state["i"]
+    starts = [(i0 + r * K) for r in range(R)]
+    graphs = {}
+    for st in starts:
+        key = (st % L, st % 2)
+        if key not in graphs:
+            state["i"] = st
+            graphs[key] = ev.capture(stream, lambda: [step() for _ in range(K)])
+    state["i"] = i0
+    marks = [ev.create() for _ in range(R + 1)]
+    ev.record(marks[0], stream)
+    for r in range(R):
+        ev.launch_graph(graphs[(starts[r] % L, starts[r] % 2)], stream)
+        ev.record(marks[r + 1], stream)
+    ctx.sync()
+    state["i"] = i0 + R * K
+    per_step = np.asarray([ev.elapsed_ms(marks[r], marks[r + 1]) * 1e3 / K for r in range(R)])
+    us = float(np.median(per_step))
+    spread = {"median_us": round(us, 3), "min_us": round(float(per_step.min()), 3),
+              "max_us": round(float(per_step.max()), 3), "replays": R, "steps_per_replay": K}
+    out = {"us": us, "us_stream": us_stream, "spread": spread,
+           "timing": f"median over {R} back-to-back hipGraph replays of {K} chained layer steps each (step i on "
+                     f"layer copy i mod {L}, its input the hidden state step i - 1 wrote; pbmoe_moe_layer_norm, "
+                     "the input RMSNorm fused); stream_us_per_layer: the same chained steps as one ABI call each"}
+    # per-kernel durations (events attached to the dispatch packets) and
+    # the distinct experts the chained steps select
+    n_ph = max(min(K, 512), 48) if phases else 16
+    evs = [[ev.create() for _ in range(6)] for _ in range(n_ph)]
+    uniq = []
+    for j in range(n_ph):
+        if phases:
+            arr = (C.c_void_p * 6)(*[e.value for e in evs[j]])
+            abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 6))
+        step()
+        if j < 16:
+            ctx.sync()
+            uniq.append(len(set(ids.download().ravel().tolist())))
+    abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, None, 0))
+    ctx.sync()
+    out["unique"] = float(np.mean(uniq))
+    out["phase_steps"] = n_ph
+    if phases:
+        out["phase_us"] = {name: float(np.mean([ev.elapsed_ms(e[2 * j], e[2 * j + 1]) * 1e3 for e in evs]))
+                           for j, name in enumerate(("stage", "gateup", "down"))}
+    print(f"[bench] {cfg.name} T={T}: {us:.2f} us/layer (graph, median of {R} replays of {K} chained steps; "
+          f"min {per_step.min():.2f}, max {per_step.max():.2f}), {us_stream:.2f} us/layer (stream); "
+          f"unique experts {out['unique']:.1f}"
+          + ("; kernels (us): " + ", ".join(f"{k} {v:.2f}" for k, v in out["phase_us"].items()) if phases else ""),
+          file=sys.stderr, flush=True)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -700,6 +801,8 @@ def main() -> int:
                     help="c4_stack: RMSNorms inside the projection/router kernels, or as separate passes")
     ap.add_argument("--prefill", action="store_true",
                     help="layer-major prefill of --tokens (default: the config's) instead of decode")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="decode: time the headline shape only (no C2 4/8-token and C3 prefill legs)")
     ap.add_argument("--expert-phase", action="store_true",
                     help="also time pbmoe_moe_decode alone (routes fixed)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -731,7 +834,7 @@ def main() -> int:
               "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
         return 2
 
-    from pb_amd import abi
+    from pb_amd import abi, synth
     from pb_amd.configs import CONFIGS, algorithmic_bytes, decode_phase_bytes, down_prefetch_bytes
 
     if args.config in ("c4_stack", "c4_stack_decode"):
@@ -743,7 +846,6 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     T = args.tokens
     ctx = abi.Context(0)
-    stream = ctx.stream()
     ev = HipEvents()
     if args.prefill or cfg.name.startswith("c3"):
         rec = bench_prefill(args, cfg, ctx, ev)
@@ -752,94 +854,15 @@ def main() -> int:
         return 0
     t_setup = time.perf_counter()
     lay, layers = build_layers(ctx, cfg, args.layers, T)
-    from pb_amd import synth
-    xh, rh = synth.activations(SEED, 999, T, cfg.hidden)
-    x, res = ctx.to_device(xh), ctx.to_device(rh)
-    ids = ctx.array((T, cfg.k), np.uint32)
-    w = ctx.array((T, cfg.k), np.float32)
-    out = ctx.array((T, cfg.hidden), np.float32)
     print(f"[bench] setup {time.perf_counter() - t_setup:.1f} s, {args.layers} layers bound", file=sys.stderr,
           flush=True)
-
-    L = len(layers)
     K, R = args.steps, max(20, args.replays)
-
-    def step(i):
-        # one MoE layer for the batch: router + routing + experts + combine
-        layers[i % L][0].forward(x, res, out, ids, w)
-
-    for i in range(args.warmup):
-        step(i)
-    ctx.sync()
-    a, b = ev.create(), ev.create()
-    # plain stream: one ABI call per step
-    ev.record(a, stream)
-    for i in range(K):
-        step(i)
-    ev.record(b, stream)
-    us_stream = ev.elapsed_ms(a, b) * 1e3 / K
-    ctx.sync()
-    # production decode loop: K steps captured as a hipGraph (step i on layer
-    # copy i % L, the next replay continuing where the last one stopped) and
-    # replayed R times back to back; the median replay is the headline
-    starts = [(r * K) % L for r in range(R)]
-    graphs = {s0: ev.capture(stream, lambda s0=s0: [step(s0 + i) for i in range(K)]) for s0 in sorted(set(starts))}
-    for s0 in graphs:
-        ev.launch_graph(graphs[s0], stream)
-    ctx.sync()
-    marks = [ev.create() for _ in range(R + 1)]
-    ev.record(marks[0], stream)
-    for r in range(R):
-        ev.launch_graph(graphs[starts[r]], stream)
-        ev.record(marks[r + 1], stream)
-    ctx.sync()
-    per_step = np.asarray([ev.elapsed_ms(marks[r], marks[r + 1]) * 1e3 / K for r in range(R)])
-    us_step = float(np.median(per_step))
-    spread = {"median_us": round(us_step, 3), "min_us": round(float(per_step.min()), 3),
-              "max_us": round(float(per_step.max()), 3), "replays": R, "steps_per_replay": K}
-
-    us_expert = None
-    if args.expert_phase:
-        # expert phase alone (routes fixed, pbmoe_moe_decode)
-        for i in range(L):
-            layers[i][0].route(x, ids, w)
-        ctx.sync()
-        ev.record(a, stream)
-        for i in range(args.steps):
-            layers[i % L][0].submit_scheduled_expert_command(x, res, ids, w, out)
-        ev.record(b, stream)
-        us_expert = round(ev.elapsed_ms(a, b) * 1e3 / args.steps, 3)
-        ctx.sync()
-    print(f"[bench] {us_step:.2f} us/layer (graph, median of {R} replays of {K} steps; min {per_step.min():.2f}, "
-          f"max {per_step.max():.2f}), {us_stream:.2f} us/layer (stream), expert phase {us_expert} us",
-          file=sys.stderr, flush=True)
-
-    # per-kernel durations of the same steps (stream mode): the library
-    # records hipEvents between its three kernels (pbmoe_set_phase_events)
-    # (start/stop events attached to each kernel's dispatch packet)
-    n_ph = max(min(K, 512), 48)
-    evs = [[ev.create() for _ in range(6)] for _ in range(n_ph)]
-    for i in range(n_ph):
-        arr = (C.c_void_p * 6)(*[e.value for e in evs[i]])
-        abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, arr, 6))
-        step(i)
-    abi.check(abi.lib().pbmoe_set_phase_events(ctx.handle, None, 0))
-    ctx.sync()
-    phase_us = {name: float(np.mean([ev.elapsed_ms(e[2 * j], e[2 * j + 1]) * 1e3 for e in evs]))
-                for j, name in enumerate(("stage", "gateup", "down"))}
-    print(f"[bench] phases (us): " + ", ".join(f"{k} {v:.2f}" for k, v in phase_us.items()), file=sys.stderr,
-          flush=True)
-
-    # unique experts per step (decode: distinct ids of the batch)
-    uniq = []
-    for i in range(min(L, 16)):
-        layers[i][0].route(x, ids, w)
-        ctx.sync()
-        uniq.append(len(set(ids.download().ravel().tolist())))
-    u_mean = float(np.mean(uniq))
-    bytes_layer = algorithmic_bytes(cfg, int(round(u_mean)), T)
+    head = decode_leg(ctx, ev, cfg, layers, T, K, R, args.warmup, phases=True)
+    us_step = head["us"]
+    bytes_layer = algorithmic_bytes(cfg, int(round(head["unique"])), T, fused_norm=True)
     gbps = bytes_layer / (us_step * 1e-6) / 1e9
-    ph_bytes = decode_phase_bytes(cfg, int(round(u_mean)), T)
+    ph_bytes = decode_phase_bytes(cfg, int(round(head["unique"])), T, fused_norm=True)
+    phase_us = head["phase_us"]
     kernels = {k: {"us": round(phase_us[k], 3), "bytes": ph_bytes[k],
                    "GBps": round(ph_bytes[k] / (phase_us[k] * 1e-6) / 1e9, 1)} for k in phase_us}
     dominant = max(phase_us, key=phase_us.get)
@@ -847,7 +870,58 @@ def main() -> int:
     traffic, traffic_src = load_traffic(dominant, cfg.name)
     # route_gateup_kernel also touches the down weights of the selected
     # experts (prefetch for the down kernel); its traffic includes them
-    pf_bytes = down_prefetch_bytes(cfg, int(round(u_mean)), T) if dominant == "gateup" else 0
+    pf_bytes = down_prefetch_bytes(cfg, int(round(head["unique"])), T) if dominant == "gateup" else 0
+
+    us_expert = None
+    if args.expert_phase:
+        # expert phase alone (routes fixed, pbmoe_moe_decode)
+        xh, rh = synth.activations(SEED, 999, T, cfg.hidden)
+        x, res = ctx.to_device(xh), ctx.to_device(rh)
+        ids = ctx.array((T, cfg.k), np.uint32)
+        w = ctx.array((T, cfg.k), np.float32)
+        out = ctx.array((T, cfg.hidden), np.float32)
+        L = len(layers)
+        for i in range(L):
+            layers[i][0].route(x, ids, w)
+        ctx.sync()
+        a, b = ev.create(), ev.create()
+        ev.record(a, ctx.stream())
+        for i in range(args.steps):
+            layers[i % L][0].submit_scheduled_expert_command(x, res, ids, w, out)
+        ev.record(b, ctx.stream())
+        us_expert = round(ev.elapsed_ms(a, b) * 1e3 / args.steps, 3)
+        ctx.sync()
+
+    # the other BASELINE shapes in the same run: C2 with 4 and 8 tokens on the
+    # same resident layer copies, and the C3 prefill of 2048 tokens
+    extra = {}
+    if not args.headline_only and T == 1 and cfg.name == "c2_qwen3next_decode":
+        for t_extra in (4, 8):
+            leg = decode_leg(ctx, ev, cfg, layers, t_extra, K, R, args.warmup, phases=True)
+            u = leg["unique"]
+            nb = algorithmic_bytes(cfg, int(round(u)), t_extra, fused_norm=True)
+            extra[f"c2_t{t_extra}"] = {
+                "tokens": t_extra, "us_per_layer": round(leg["us"], 3),
+                "us_per_token_layer": round(leg["us"] / t_extra, 3),
+                "tokens_per_s": round(t_extra / (leg["us"] * 1e-6), 1),
+                "unique_experts_mean": round(u, 2), "algorithmic_bytes": nb,
+                "achieved_GBps": round(nb / (leg["us"] * 1e-6) / 1e9, 1),
+                "hbm_frac": round(nb / (leg["us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                "kernels_us": {k: round(v, 3) for k, v in leg["phase_us"].items()},
+                "spread": leg["spread"], "timing": leg["timing"]}
+        pargs = argparse.Namespace(**vars(args))
+        pargs.tokens, pargs.steps, pargs.warmup = 1, 20, 3
+        pargs.cpu_seconds = min(args.cpu_seconds, 4.0)
+        from pb_amd.configs import C3
+        prec = bench_prefill(pargs, C3, ctx, ev)
+        extra["c3_prefill"] = {
+            "tokens": prec["config"]["tokens"], "us_per_layer": round(prec["ms_per_step"] * 1e3, 2),
+            "us_per_token_layer": prec["value"], "tokens_per_s": prec["tokens_per_s"],
+            "layer_TFLOPs": prec["expert_TFLOPs"],
+            "layer_mfma_frac": round(prec["expert_TFLOPs"] / MFMA_PEAK_TFLOPS, 4),
+            "gateup": prec["kernels"]["gateup"], "down": prec["kernels"]["down"],
+            "combine": prec["kernels"]["combine"], "roofline": prec["roofline"],
+            "spread": prec["spread"], "cpu_baseline": prec["cpu_baseline"], "timing": prec["timing"]}
 
     cpu = None
     if not args.no_cpu:
@@ -868,23 +942,26 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden, "experts": cfg.experts, "k": cfg.k,
                    "intermediate": cfg.intermediate, "shared_intermediate": cfg.shared_intermediate,
-                   "quant": "q4 affine g64 f16 scale/bias", "layers_cycled": L},
+                   "quant": "q4 affine g64 f16 scale/bias", "layers_cycled": len(layers)},
         "tokens_per_s": round(T / (us_step * 1e-6), 1),
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "expert_phase_us": us_expert,
-        "stream_us_per_layer": round(us_stream, 3),
-        "timing": f"median over {R} back-to-back hipGraph replays of {K} layer steps each (step i on layer copy "
-                  f"i mod {L}); stream_us_per_layer: the same {K} steps as one ABI call each",
-        "spread": spread,
+        "stream_us_per_layer": round(head["us_stream"], 3),
+        "timing": head["timing"],
+        "spread": head["spread"],
         "roofline": {"bound": "hbm", "achieved": dom_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": KERNEL_NAMES[dominant], "bytes_per_launch": ph_bytes[dominant],
                      "launch_us": kernels[dominant]["us"], "traffic_source": traffic_src,
+                     "launch_us_source": "mean of hipEvents attached to this kernel's dispatch packets "
+                                         f"(pbmoe_set_phase_events) over {head['phase_steps']} chained eager steps "
+                                         "on the library stream",
                      "prefetch_bytes": pf_bytes},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
+    rec.update(extra)
     if args.copy_calibration_mb:
         copy_calibration(ctx, args.copy_calibration_mb, 3)
     if args.read_calibration_mb:

@@ -36,10 +36,11 @@ C4_ATTN = AttnConfig("c4_attention", hidden=2048, q_heads=32, kv_heads=4, head_d
 C4_LAYERS = 48
 
 
-def algorithmic_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:
+def algorithmic_bytes(cfg: MoeConfig, unique_experts: int, tokens: int, fused_norm: bool = False) -> int:
     """HBM bytes a decode call must move at minimum: each selected expert's
     Q4 slot once, the shared slot, the router (f16) and shared gate, and the
-    f32 activations in (x, residual) and out (hidden)."""
+    f32 activations in (x, residual) and out (hidden); with the fused input
+    RMSNorm (pbmoe_moe_layer_norm) also its f32 weight."""
     def slot(h, i):
         return 3 * (h * i // 2) + 3 * 2 * (h * i // cfg.group) * 2
     b = unique_experts * slot(cfg.hidden, cfg.intermediate)
@@ -49,6 +50,8 @@ def algorithmic_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:
             b += cfg.hidden * 2
     b += cfg.experts * cfg.hidden * 2
     b += tokens * cfg.hidden * 4 * 3
+    if fused_norm:
+        b += cfg.hidden * 4
     return b
 
 
@@ -57,16 +60,20 @@ def q4_proj_bytes(rows: int, cols: int, group: int) -> int:
     return rows * cols // 2 + 2 * (rows * cols // group) * 2
 
 
-def decode_phase_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> dict:
+def decode_phase_bytes(cfg: MoeConfig, unique_experts: int, tokens: int, fused_norm: bool = False) -> dict:
     """Algorithmic HBM bytes of each decode kernel (pbmoe_moe_layer):
     stage   router rows (f16), shared gate/up + gate row, x in, logits and
-            shared activations out;
+            shared activations out; with the fused input RMSNorm
+            (pbmoe_moe_layer_norm) also the norm weight in and the
+            normalised rows out (the gate/up kernel's x);
     gateup  gate/up of the selected experts, logits and x in, act out;
     down    down of the selected experts + shared down, act in, residual
             in, hidden out."""
     H, I, Is, E, K, g, T = (cfg.hidden, cfg.intermediate, cfg.shared_intermediate, cfg.experts, cfg.k,
                             cfg.group, tokens)
     stage = E * H * 2 + T * H * 4 + T * E * 4
+    if fused_norm:
+        stage += H * 4 + T * H * 4
     if Is:
         stage += 2 * q4_proj_bytes(Is, H, g) + T * Is * 4
         if cfg.shared_gated:
