@@ -157,9 +157,10 @@ def lib() -> C.CDLL:
     """Load libpbmoe.so (raises if it is not built: no fallback exists)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"native library missing: {LIB_PATH}; run __graft_entry__.build()")
-        L = C.CDLL(LIB_PATH)
+        path = os.environ.get("PBMOE_LIB", LIB_PATH)  # another build of the library (comparisons)
+        if not os.path.exists(path):
+            raise RuntimeError(f"native library missing: {path}; run __graft_entry__.build()")
+        L = C.CDLL(path)
         for name, (args, res) in _SIG.items():
             fn = getattr(L, name)
             fn.argtypes = args
