@@ -36,6 +36,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "pbmoe_device.h"
@@ -96,11 +98,15 @@ __device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 }
 
 // ---------------------------------------------------------------------------
-// tile table: for every used expert ceil(count / 64) tiles (item, start);
-// the shared expert, when present, is item U with all T tokens.  One wave:
-// a scan of per-item tile counts, then each lane writes its item's tiles.
-// Runs in the last workgroup of the split launch (both follow the plan and
-// precede the GEMMs).
+// tile table: for every used expert ceil(count / tok) tiles (item, start);
+// the shared expert, when present, is item U with all T tokens.  Order:
+// the full tiles of all items, then the partial ones (the last tile of an
+// item whose count is not a multiple of tok) by their 32-token fragments,
+// most first, so that the GEMMs (which deal the list to the XCDs in turn)
+// start the longest workgroups first and end on the shortest.  One wave:
+// per class, a scan of the per-item tile counts, then each lane writes its
+// item's tiles.  Runs in the last workgroup of the split launch (both follow
+// the plan and precede the GEMMs).
 // ---------------------------------------------------------------------------
 struct TileArgs {
     const uint32_t* unique_count;
@@ -109,6 +115,7 @@ struct TileArgs {
     uint32_t tokens;
     uint32_t* tiles;
     uint32_t* tile_count;
+    uint32_t tok; // tokens per tile (64 or 128)
 };
 
 __device__ void tile_table_wave(const TileArgs& a)
@@ -119,31 +126,57 @@ __device__ void tile_table_wave(const TileArgs& a)
     uint32_t* tiles = a.tiles;
     const uint32_t U = a.unique_count[0];
     const uint32_t items = U + has_shared;
+    const uint32_t nfrag = a.tok / 32;
     uint32_t base = 0;
-    for (uint32_t u0 = 0; u0 < items; u0 += 64) {
-        const uint32_t u = u0 + lane;
-        uint32_t cnt = 0;
-        if (u < U)
-            cnt = groups[2 * u + 1];
-        else if (u < items)
-            cnt = tokens;
-        const uint32_t nt = (cnt + TOK - 1) / TOK;
-        uint32_t inc = nt; // inclusive scan over the wave
+    // class 0: full tiles; class c = 1 .. nfrag: the partial tile with
+    // nfrag + 1 - c fragments
+    for (uint32_t c = 0; c <= nfrag; ++c) {
+        for (uint32_t u0 = 0; u0 < items; u0 += 64) {
+            const uint32_t u = u0 + lane;
+            uint32_t cnt = 0;
+            if (u < U)
+                cnt = groups[2 * u + 1];
+            else if (u < items)
+                cnt = tokens;
+            const uint32_t full = cnt / a.tok, rest = cnt % a.tok;
+            uint32_t nt;
+            if (c == 0)
+                nt = full;
+            else
+                nt = rest != 0 && (rest + 31) / 32 == nfrag + 1 - c ? 1u : 0u;
+            uint32_t inc = nt; // inclusive scan over the wave
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t v = __shfl_up(inc, o);
-            if ((int)lane >= o)
-                inc += v;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_up(inc, o);
+                if ((int)lane >= o)
+                    inc += v;
+            }
+            const uint32_t first = base + inc - nt;
+            for (uint32_t j = 0; j < nt; ++j) {
+                tiles[2 * (first + j)] = u;
+                tiles[2 * (first + j) + 1] = c == 0 ? j * a.tok : full * a.tok;
+            }
+            base += __shfl(inc, 63);
         }
-        const uint32_t first = base + inc - nt;
-        for (uint32_t j = 0; j < nt; ++j) {
-            tiles[2 * (first + j)] = u;
-            tiles[2 * (first + j) + 1] = j * TOK;
-        }
-        base += __shfl(inc, 63);
     }
     if (lane == 0)
         a.tile_count[0] = base;
+}
+
+// Work unit of a GEMM workgroup: the tiles are dealt to the 8 XCDs in turn
+// (tile t on XCD t % 8: workgroup b runs on XCD b % 8), and the row blocks
+// of one tile are consecutive on its XCD, so they share that XCD's L2 for
+// the tile's activation rows.  In tile-table order, each XCD meets its
+// largest tiles first.  Grid: 8 * RB * ceil(max_tiles / 8) (gemm_units).
+__device__ __forceinline__ bool gemm_unit(uint32_t ntiles, uint32_t RB, uint32_t& tile, uint32_t& rb)
+{
+    const uint32_t j = blockIdx.x >> 3, xcd = blockIdx.x & 7;
+    const uint32_t t = 8 * (j / RB) + xcd;
+    if (t >= ntiles)
+        return false;
+    tile = t;
+    rb = j % RB;
+    return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -241,6 +274,7 @@ struct GemmArgs {
     const uint32_t* b_lo_any; // per B row: lo part not all zero (null: assume it is not)
     uint32_t kdim;            // H (gate/up) or I (down)
     uint32_t b_rows;          // rows of the B operand buffers
+    uint32_t lo_delta;        // bytes from b_hi to b_lo (one allocation)
     // outputs
     uint16_t* act_hi;         // [routes + T][I]
     uint16_t* act_lo;
@@ -324,11 +358,9 @@ __device__ __forceinline__ float sb_buf(rsrc_t r, uint32_t voff, uint32_t soff)
 // s[row][g] * P after each group; the bias term sum_g b[row][g] * xsum_g
 // runs on the matrix cores after the loop.
 //
-// Work mapping: the flat list (tile major, row block minor; tiles are grouped
-// by expert) is cut into 8 contiguous ranges, one per XCD (workgroup ids are
-// dealt to the XCDs round-robin): the row blocks of one token tile run back
-// to back on one XCD and share the activation tile in its L2, and the next
-// tiles of the same expert find the expert's weights there.
+// Work mapping (gemm_unit): tile t on XCD t % 8, its row blocks back to
+// back there, sharing the activation tile in that XCD's L2; largest tiles
+// first.
 template <int SBT, bool GATEUP, int KS>
 __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs a)
 {
@@ -344,15 +376,9 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     const uint32_t ntiles = a.tile_count[0];
     const uint32_t rows_total = GATEUP ? a.ex.gate.rows : a.ex.down.rows;
     const uint32_t RB = rows_total / WG_ROWS;
-    const uint32_t total = ntiles * RB;
-    const uint32_t chunk = (total + 7) / 8;
-    const uint32_t j8 = blockIdx.x >> 3, xcd = blockIdx.x & 7;
-    if (j8 >= chunk)
+    uint32_t tile, rb;
+    if (!gemm_unit(ntiles, RB, tile, rb))
         return;
-    const uint32_t widx = xcd * chunk + j8;
-    if (widx >= total)
-        return;
-    const uint32_t tile = widx / RB, rb = widx % RB;
     const uint32_t item = a.tiles[2 * tile], n0 = a.tiles[2 * tile + 1];
     const bool shared = a.has_shared && item == a.unique_count[0];
     uint32_t g0, cnt;
@@ -899,6 +925,568 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     }
 }
 
+// ---------------------------------------------------------------------------
+// grouped GEMM, 128-token tiles
+//
+// One workgroup: 128 tokens of one item x WGR weight rows, four waves (one
+// per SIMD), two workgroups per CU.  Wave w owns two sets of 32 rows (set
+// 0/1 = gate/up rows 32w .. 32w+31 of the block, or down rows 64w + 32m ..
+// +32) and all four 32-token fragments: every unpacked code fragment feeds
+// four MFMAs (one per token fragment), so the unpack costs a quarter of an
+// MFMA's issue time instead of half.  Per quantisation group and (fragment,
+// set): a chain of 2KS (x2 with lo) MFMAs into a fresh partial P, then
+// acc += s * P (the group scale, in f32).  The activation tile of a group is
+// staged by buffer loads straight into LDS ([128 tokens][CH chunks], hi
+// only when no row of the tile has a lo part, else hi and lo interleaved;
+// chunk c of row r at position c ^ (r % CH)), NBUF groups resident; the
+// codes come two groups ahead into registers.  The bias term runs on the
+// matrix cores after the loop, as in the 64-token kernel.
+// ---------------------------------------------------------------------------
+constexpr int TOK_L = 128;
+constexpr int GL_THREADS = 256;
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane,
+// written out so that the compiler does not see an LDS write it cannot tell
+// apart from the LDS reads of other staging buffers (it would wait for the
+// load before each of them).  The caller waits for completion (vmcnt)
+// before the barrier that publishes the buffer.  M0 is written here and
+// read by the load only; no compiler-generated code of the kernels that
+// call it uses M0.
+// Address: a scalar base plus a 32-bit per-lane offset; LDS destination: a
+// wave-uniform LDS address (M0).
+__device__ __forceinline__ void load_lds16(const uint8_t* sbase, uint32_t voff, uint32_t lds_addr)
+{
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_addr)
+                 : "memory");
+}
+
+// f16 bits to f32 through an explicit conversion: left to itself the
+// compiler keeps the group scales packed and runs out of registers
+__device__ __forceinline__ float cvt_f16_bits(uint16_t v)
+{
+    float f;
+    asm("v_cvt_f32_f16 %0, %1" : "=v"(f) : "v"((uint32_t)v));
+    return f;
+}
+
+template <int KS, int WPC>
+struct GemmLLds {
+    static constexpr int CH_HI = 4 * KS; // 16-byte chunks of a token row per group, hi only
+    static constexpr int CH_LO = 8 * KS; // hi and lo interleaved
+    static constexpr int TILE_HI = TOK_L * CH_HI * 16;
+    static constexpr int TILE_LO = TOK_L * CH_LO * 16;
+    static constexpr int NBUF_HI = 4, NBUF_LO = 2; // hi tiles: one quarter each; hi + lo tiles: two
+    static constexpr int OPITCH = 128 + 4; // gate/up epilogue tile: 4 x [32 tokens][OPITCH] f32
+    // LDS as four separate arrays ("quarters"): a hi tile fills one, a
+    // hi + lo tile two (token rows 0-63, 64-127), an epilogue block of 32
+    // tokens one.  Being distinct objects, the compiler can tell the reads
+    // of one staging buffer from the direct loads into another, and does not
+    // wait for those loads before every LDS read.
+    static constexpr int QBYTES_ = TILE_HI > TILE_LO / 2 ? TILE_HI : TILE_LO / 2;
+    static constexpr int QBYTES = QBYTES_ > 32 * OPITCH * 4 ? QBYTES_ : 32 * OPITCH * 4;
+    static_assert(WPC == 2 && KS == 2, "the quarter layout is sized for group 64, two workgroups per CU");
+};
+
+template <int SBT, bool GATEUP, int KS, int WPC>
+__global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs a)
+{
+    using L = GemmLLds<KS, WPC>;
+    constexpr int NSTEP = 2 * KS;          // 16-column K-steps per quantisation group
+    constexpr int WGR = GATEUP ? 128 : 256; // output rows per workgroup
+    constexpr int WL = 2 * KS == 8 ? 2 : 1; // load instructions per code fragment
+    __shared__ __align__(16) uint8_t q0[L::QBYTES];
+    __shared__ __align__(16) uint8_t q1[L::QBYTES];
+    __shared__ __align__(16) uint8_t q2[L::QBYTES];
+    __shared__ __align__(16) uint8_t q3[L::QBYTES];
+    __shared__ uint32_t row_lds[TOK_L];
+    __shared__ float rs_lds[TOK_L];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t wvs = __builtin_amdgcn_readfirstlane(wv); // the wave index as a scalar
+    auto lds_addr = [](const uint8_t* p) __attribute__((always_inline)) -> uint32_t {
+        return (uint32_t)(uintptr_t)p;
+    };
+    // quarter Q (compile-time, so each access names its array)
+    auto quarter = [&](auto q_tag) __attribute__((always_inline)) -> uint8_t* {
+        constexpr int Q = decltype(q_tag)::value;
+        if constexpr (Q == 0)
+            return q0;
+        else if constexpr (Q == 1)
+            return q1;
+        else if constexpr (Q == 2)
+            return q2;
+        else
+            return q3;
+    };
+
+    // ---- work item (gemm_unit: tile t on XCD t % 8, its row blocks back to
+    //      back there) ----
+    const uint32_t ntiles = a.tile_count[0];
+    const uint32_t rows_total = GATEUP ? a.ex.gate.rows : a.ex.down.rows;
+    const uint32_t RB = rows_total / WGR;
+    uint32_t tile, rb;
+    if (!gemm_unit(ntiles, RB, tile, rb))
+        return;
+    const uint32_t item = a.tiles[2 * tile], n0 = a.tiles[2 * tile + 1];
+    const bool shared = a.has_shared && item == a.unique_count[0];
+    uint32_t g0, cnt;
+    const uint8_t* slot;
+    if (shared) {
+        g0 = a.routes;
+        cnt = a.tokens;
+        slot = a.sh.base;
+    } else {
+        const uint32_t e = a.unique_ids[item];
+        g0 = a.groups[2 * item];
+        cnt = a.groups[2 * item + 1];
+        if (e >= a.ex.count) {
+            if (tid == 0)
+                atomicOr(a.status, ST_ROUTE_RANGE);
+            return;
+        }
+        slot = a.ex.base + (uint64_t)e * a.ex.stride;
+    }
+    const ExpertSet& set = shared ? a.sh : a.ex;
+    const uint32_t K = a.kdim;
+    const uint32_t G = K / (32 * KS), C32 = K / 32, WPR = K / 8;
+    auto tok_row = [&](uint32_t n) __attribute__((always_inline)) -> uint32_t {
+        return GATEUP ? (shared ? n : a.src_rows[g0 + n]) : g0 + n;
+    };
+    int lo_flag = 0;
+    if (tid < TOK_L) {
+        const uint32_t n = n0 + tid;
+        const bool v = n < cnt;
+        const uint32_t r = v ? tok_row(n) : 0u;
+        row_lds[tid] = v ? r : 0xFFFFFFFFu;
+        if (GATEUP)
+            rs_lds[tid] = v ? a.rowscale[r] : 1.0f;
+        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[r] != 0u);
+    }
+    const bool tile_lo = __syncthreads_or(lo_flag) != 0;
+    const uint32_t first_row = row_lds[0];
+    const uint32_t nvalid = cnt - n0 < (uint32_t)TOK_L ? cnt - n0 : (uint32_t)TOK_L;
+
+    // ---- this lane's weight rows: set m, row (lane & 31), lane half h takes
+    //      the K-steps' upper 8 columns ----
+    const uint32_t n32 = lane & 31, h = lane >> 5;
+    uint32_t rowm[2];
+    if constexpr (GATEUP) {
+        rowm[0] = rowm[1] = rb * WGR + wv * 32 + n32;
+    } else {
+        rowm[0] = rb * WGR + wv * 64 + n32;
+        rowm[1] = rowm[0] + 32;
+    }
+    const Q4Proj pm0 = GATEUP ? set.gate : set.down;
+    const Q4Proj pm1 = GATEUP ? set.up : set.down;
+    const rsrc_t wr = make_rsrc(slot, (uint32_t)set.stride);
+    const uint32_t w_voff[2] = {(rowm[0] * WPR + h * 2 * KS) * 4, (rowm[1] * WPR + h * 2 * KS) * 4};
+    const uint32_t sb_voff[2] = {rowm[0] * G * 2, rowm[1] * G * 2};
+    const uint32_t w_soff[2] = {(uint32_t)pm0.w_off, (uint32_t)pm1.w_off};
+    const uint32_t s_soff[2] = {(uint32_t)pm0.s_off, (uint32_t)pm1.s_off};
+    const uint32_t b_soff[2] = {(uint32_t)pm0.b_off, (uint32_t)pm1.b_off};
+    const uint32_t magic = 0x64006400u;
+    typedef uint32_t Words[2][2 * KS];
+    auto w_load = [&](uint32_t g, Words& w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            load_words<2 * KS>(wr, w_voff[m], w_soff[m] + g * 16 * KS, w[m]);
+    };
+    auto s_load = [&](uint32_t g, uint32_t (&sp)[2]) { // scales of groups g, g + 1 (g even)
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            sp[m] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff[m], s_soff[m] + g * 2, 0);
+    };
+    auto s_of = [&](uint32_t pair, uint32_t g) __attribute__((always_inline)) -> float {
+        const uint16_t v = (uint16_t)(pair >> ((g & 1) * 16));
+        if constexpr (SBT == 2)
+            return __uint_as_float((uint32_t)v << 16);
+        else
+            return cvt_f16_bits(v);
+    };
+
+    // accumulators: set by the bias term (fragments holding tokens) and
+    // after the group loop (the others, zero)
+    float16_t acc[4][2];
+
+    // ---- bias term on the matrix cores: acc = sum_g b[row][g] * xsum[token][g]
+    //      (K' = groups in slices of 16, lane half h: groups k0 + 8h .. +8;
+    //      sums split into f16 hi + lo).  Run before the group loop, with the
+    //      loop's first loads in flight: acc is the only live state then ----
+    const rsrc_t sum_r = make_rsrc(a.b_sum32, a.b_rows * C32 * 4);
+    auto bias_term = [&](auto ntf_tag) __attribute__((always_inline)) {
+        constexpr int NTF = decltype(ntf_tag)::value;
+        uint32_t rrow[NTF];
+        bool bvalid[NTF];
+#pragma unroll
+        for (int tf = 0; tf < NTF; ++tf) {
+            const uint32_t brow = row_lds[32 * tf + n32];
+            bvalid[tf] = brow != 0xFFFFFFFFu;
+            rrow[tf] = bvalid[tf] ? brow : 0u;
+        }
+        // slice k00 for fragments T0 .. T1 - 1 (FIRST: k00 = 0, which sets acc)
+        auto slice = [&](uint32_t k00, auto first_tag, auto t0_tag, auto t1_tag) __attribute__((always_inline)) {
+            constexpr bool FIRST = decltype(first_tag)::value;
+            constexpr int T0 = decltype(t0_tag)::value, T1 = decltype(t1_tag)::value;
+            const uint32_t gb = k00 + 8 * h;
+            uint32_t b2[2][4];
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    b2[m][q] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff[m], b_soff[m] + gb * 2 + 4 * q, 0);
+            u32x4 v4[T1 - T0][2 * KS];
+#pragma unroll
+            for (int tf = T0; tf < T1; ++tf)
+#pragma unroll
+                for (int q = 0; q < 2 * KS; ++q)
+                    v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(sum_r, rrow[tf] * C32 * 4,
+                                                                           (gb * KS + 4 * q) * 4, 0);
+            half8_t bw[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint16_t raw = (uint16_t)(b2[m][j / 2] >> (16 * (j & 1)));
+                    float bv;
+                    if constexpr (SBT == 2)
+                        bv = __uint_as_float((uint32_t)raw << 16);
+                    else
+                        bv = (float)__builtin_bit_cast(_Float16, raw);
+                    bw[m][j] = gb + j < G ? (_Float16)bv : (_Float16)0.0f;
+                }
+#pragma unroll
+            for (int tf = T0; tf < T1; ++tf) {
+                half8_t xh, xl;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < KS; ++c)
+                        v += __uint_as_float(v4[tf - T0][(j * KS + c) / 4][(j * KS + c) % 4]);
+                    if (!bvalid[tf] || gb + j >= G)
+                        v = 0.0f;
+                    const _Float16 hv = (_Float16)v;
+                    xh[j] = hv;
+                    xl[j] = (_Float16)(v - (float)hv);
+                }
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    float16_t c;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        c[j] = 0.0f;
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, bw[m], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, bw[m], c, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        acc[tf][m][j] = FIRST ? 0.0f + c[j] : acc[tf][m][j] + c[j];
+                }
+            }
+        };
+        using F0 = std::integral_constant<int, 0>;
+        using FH = std::integral_constant<int, NTF < 2 ? NTF : 2>;
+        using FN = std::integral_constant<int, NTF>;
+        // the first slice: every fragment's loads at once (acc is not live yet);
+        // the others two fragments at a time
+        slice(0u, std::true_type{}, F0{}, FN{});
+        for (uint32_t k00 = 16; k00 < G; k00 += 16) {
+            slice(k00, std::false_type{}, F0{}, FH{});
+            if constexpr (NTF > 2)
+                slice(k00, std::false_type{}, FH{}, FN{});
+        }
+    };
+
+    // staging source: b_hi, b_lo at b_hi + lo_delta; 32-bit byte offsets.
+    // (Direct-to-LDS loads through a buffer resource measured 4-6x slower
+    // than these global ones on this part.)
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(a.b_hi);
+    auto run = [&](auto lo_tag, auto ntf_tag) __attribute__((always_inline)) {
+        constexpr bool LO = decltype(lo_tag)::value;
+        constexpr int NTF = decltype(ntf_tag)::value; // token fragments holding tokens of the item
+        constexpr int NHL = LO ? 2 : 1;
+        constexpr int CH = LO ? L::CH_LO : L::CH_HI;
+        constexpr int NBUF = LO ? L::NBUF_LO : L::NBUF_HI;
+        constexpr int PF = NBUF - 1;
+        constexpr int TILE = TOK_L * CH * 16;
+        constexpr int DW = TOK_L * CH / 64 / 4; // staging instructions per wave and group
+        // staging: instruction i of wave wv fills positions 64(wv + 4i) .. +63
+        uint32_t st_off[DW];
+#pragma unroll
+        for (int i = 0; i < DW; ++i) {
+            const uint32_t pos = 64 * (wv + 4 * i) + lane;
+            const uint32_t r = pos / CH, c = (pos % CH) ^ (r % CH);
+            const uint32_t rr = row_lds[r];
+            const uint32_t trow = rr != 0xFFFFFFFFu ? rr : first_row; // rows past the item: any valid row
+            if constexpr (LO)
+                st_off[i] = (c & 1) * a.lo_delta + trow * K * 2 + (c >> 1) * 16;
+            else
+                st_off[i] = trow * K * 2 + c * 16;
+        }
+        // buffer b: quarter b (hi), quarters 2b, 2b + 1 (hi + lo; instructions
+        // 0-3 fill token rows 0-63, 4-7 rows 64-127)
+        auto stage = [&](uint32_t g, auto buf_tag) __attribute__((always_inline)) {
+            constexpr int BUF = decltype(buf_tag)::value;
+            const uint8_t* sb = xbase + g * 64 * KS;
+#pragma unroll
+            for (int i = 0; i < DW; ++i) {
+                uint32_t dst;
+                if constexpr (LO)
+                    dst = i < DW / 2 ? lds_addr(quarter(std::integral_constant<int, 2 * BUF>{})) + 1024 * (wvs + 4 * i)
+                                     : lds_addr(quarter(std::integral_constant<int, 2 * BUF + 1>{})) +
+                                           1024 * (wvs + 4 * (i - DW / 2));
+                else
+                    dst = lds_addr(quarter(std::integral_constant<int, BUF>{})) + 1024 * (wvs + 4 * i);
+                load_lds16(sb, st_off[i], dst);
+            }
+        };
+        // fragment reads: row 32tf + n32, chunk (NSTEP h + k) (x2 + hl with lo)
+        // at position chunk ^ (n32 % CH)
+        uint32_t rd_off[NSTEP][NHL];
+#pragma unroll
+        for (int k = 0; k < NSTEP; ++k)
+#pragma unroll
+            for (int hl = 0; hl < NHL; ++hl) {
+                const uint32_t c = LO ? 2 * (h * NSTEP + k) + hl : h * NSTEP + k;
+                rd_off[k][hl] = (n32 * CH + (c ^ (n32 % CH))) * 16;
+            }
+        Words wA, wB;
+        half8_t wf[2][NSTEP];
+        uint32_t spa[2], spb[2];
+        auto unpack_all = [&](Words& w) __attribute__((always_inline)) {
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int k = 0; k < NSTEP; ++k) {
+                    asm volatile("" : "+v"(w[m][k]));
+                    wf[m][k] = unpack8(w[m][k], magic);
+                }
+        };
+        // one quantisation group: B = g % NBUF; TAIL: among the last NBUF groups
+        auto step = [&](uint32_t g, auto b_tag, auto tail_tag) __attribute__((always_inline)) {
+            constexpr int B = decltype(b_tag)::value;
+            constexpr bool TAIL = decltype(tail_tag)::value;
+            constexpr bool ST = !TAIL || B + PF < NBUF;            // stage group g + PF
+            constexpr bool WLD = !TAIL || B + 2 < NBUF;            // codes of group g + 2
+            constexpr bool SLD = B % 2 == 0 && WLD;                // scales of groups g + 2, g + 3
+            constexpr bool NEXT = !TAIL || B + 1 < NBUF;           // a group g + 1 exists
+            // vmcnt at the wait: the loads issued in this step after the
+            // staging of group g + 1 and the codes of group g + 1 may stay in
+            // flight (PF = 1: the staging of g + 1 is this step's own, issued
+            // last; else an earlier step's)
+            constexpr int WAIT = PF == 1 ? 0 : (WLD ? 2 * WL : 0) + (SLD ? 2 : 0) + (ST ? DW : 0);
+            Words& wcur = B % 2 == 0 ? wA : wB; // codes of group g (unpacked in wf)
+            Words& wnext = B % 2 == 0 ? wB : wA;
+            // register loads first: the compiler counts only those, so its
+            // own waits for them never wait for the staging issued after
+            if constexpr (WLD)
+                w_load(g + 2, wcur);
+            if constexpr (SLD)
+                s_load(g + 2, spb);
+            if constexpr (ST)
+                stage(g + PF, std::integral_constant<int, (B + PF) % NBUF>{});
+            float sa[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                sa[m] = s_of(spa[m], g);
+            // token fragment tf of buffer B
+            auto frag = [&](int tf) __attribute__((always_inline)) -> const uint8_t* {
+                if constexpr (LO)
+                    return tf < 2 ? quarter(std::integral_constant<int, 2 * B>{}) + tf * 32 * CH * 16
+                                  : quarter(std::integral_constant<int, 2 * B + 1>{}) + (tf - 2) * 32 * CH * 16;
+                else
+                    return quarter(std::integral_constant<int, B>{}) + tf * 32 * CH * 16;
+            };
+#pragma unroll
+            for (int tf = 0; tf < NTF; ++tf) {
+                if (tf == NTF - 1) {
+                    // codes of group g + 1 (loaded a step earlier) and its
+                    // staged tile: in place before the last fragment, so the
+                    // unpack can run beside its MFMAs
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
+                }
+                // K-step outer: the two sets' chains alternate, and a
+                // K-step's activation fragments are live only for its MFMAs
+                float16_t pp[2];
+#pragma unroll
+                for (int k = 0; k < NSTEP; ++k) {
+                    half8_t ax[NHL];
+#pragma unroll
+                    for (int hl = 0; hl < NHL; ++hl)
+                        ax[hl] = *reinterpret_cast<const half8_t*>(frag(tf) + rd_off[k][hl]);
+#pragma unroll
+                    for (int hl = 0; hl < NHL; ++hl)
+#pragma unroll
+                        for (int m = 0; m < 2; ++m) {
+                            float16_t c;
+                            if (k == 0 && hl == 0) {
+#pragma unroll
+                                for (int j = 0; j < 16; ++j)
+                                    c[j] = 0.0f;
+                            } else {
+                                c = pp[m];
+                            }
+                            pp[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[hl], wf[m][k], c, 0, 0, 0);
+                        }
+                }
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        acc[tf][m][j] = fmaf(sa[m], pp[m][j], acc[tf][m][j]);
+            }
+            if constexpr (NEXT)
+                unpack_all(wnext);
+            __syncthreads();
+            if constexpr (B % 2 == 1) {
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+                    spa[m] = spb[m];
+            }
+        };
+        // prologue: the first PF tiles, codes of groups 0 and 1, scales of 0 and 1
+        stage(0, std::integral_constant<int, 0>{});
+        if constexpr (PF >= 2)
+            stage(1, std::integral_constant<int, 1>{});
+        if constexpr (PF >= 3)
+            stage(2, std::integral_constant<int, 2>{});
+        w_load(0, wA);
+        w_load(1, wB);
+        s_load(0, spa);
+        bias_term(ntf_tag); // waits for its loads, and so for the prologue's
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        unpack_all(wA);
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        auto iter = [&](uint32_t g, auto tail_tag) __attribute__((always_inline)) {
+            step(g, I0{}, tail_tag);
+            step(g + 1, I1{}, tail_tag);
+            if constexpr (NBUF == 4) {
+                step(g + 2, I2{}, tail_tag);
+                step(g + 3, I3{}, tail_tag);
+            }
+        };
+        uint32_t g = 0;
+        for (; g + NBUF < G; g += NBUF) // G is a multiple of NBUF
+            iter(g, std::false_type{});
+        iter(g, std::true_type{});
+#pragma unroll
+        for (int tf = NTF; tf < 4; ++tf)
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    acc[tf][m][j] = 0.0f;
+    };
+    using T1 = std::integral_constant<int, 1>;
+    using T2 = std::integral_constant<int, 2>;
+    using T3 = std::integral_constant<int, 3>;
+    using T4 = std::integral_constant<int, 4>;
+    auto run_lo = [&](auto lo_tag) __attribute__((always_inline)) {
+        if (nvalid > 96)
+            run(lo_tag, T4{});
+        else if (nvalid > 64)
+            run(lo_tag, T3{});
+        else if (nvalid > 32)
+            run(lo_tag, T2{});
+        else
+            run(lo_tag, T1{});
+    };
+    if (tile_lo)
+        run_lo(std::true_type{});
+    else
+        run_lo(std::false_type{});
+    // the last step waited for every load and met the other waves: the
+    // staging buffers are free for the epilogue
+    // ---- epilogue ----
+    if constexpr (GATEUP) {
+        // accumulator element (token 32tf + 8(j/4) + 4h + (j%4), row wv*32 + n32)
+        // -> SiLU(g) * u in an f32 tile in LDS -> each thread (token, 32-row
+        // chunk) writes act hi/lo in K order and the chunk's sum
+        // token block b of the tile: quarter b
+        auto ot = [&](uint32_t b) __attribute__((always_inline)) -> float* {
+            return reinterpret_cast<float*>(b == 0 ? q0 : b == 1 ? q1 : b == 2 ? q2 : q3);
+        };
+        const uint32_t col = wv * 32 + n32;
+#pragma unroll
+        for (int tf = 0; tf < 4; ++tf)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t tl = 8 * (j / 4) + 4 * h + (j % 4); // token within fragment tf
+                const float rs = rs_lds[32 * tf + tl];
+                const float gg = acc[tf][0][j] * rs, uu = acc[tf][1][j] * rs;
+                // SiLU with the hardware exponential and reciprocal (relative
+                // error ~1e-6, far inside the layer tolerance)
+                ot(tf)[tl * L::OPITCH + col] = __fdividef(gg, 1.0f + __expf(-gg)) * uu;
+            }
+        __syncthreads();
+        const uint32_t I = rows_total;
+#pragma unroll
+        for (int rep = 0; rep < 2; ++rep) {
+            const uint32_t task = tid + 256 * rep; // (token, chunk of 32 rows)
+            const uint32_t c_tok = task >> 2, c_chunk = task & 3;
+            const uint32_t n = n0 + c_tok;
+            if (n >= cnt)
+                continue;
+            const float* src = ot(c_tok / 32) + (c_tok % 32) * L::OPITCH + 32 * c_chunk;
+            float v[32];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = reinterpret_cast<const float4*>(src)[q];
+                v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+            }
+            float sum = 0.0f;
+            bool overflow = false;
+            uint16_t hv[32], lv[32];
+#pragma unroll
+            for (int q = 0; q < 32; ++q) {
+                // K order inside every 8-row block: c0 c4 c1 c5 c2 c6 c3 c7
+                const int cb = (q & ~7) + ((q & 1) ? 4 + ((q & 7) >> 1) : ((q & 7) >> 1));
+                const float x = v[cb];
+                sum += v[q];
+                overflow |= !(fabsf(x) <= 65504.0f);
+                const _Float16 hh = (_Float16)x;
+                hv[q] = __builtin_bit_cast(uint16_t, hh);
+                lv[q] = __builtin_bit_cast(uint16_t, (_Float16)(x - (float)hh));
+            }
+            if (overflow)
+                atomicOr(a.status, ST_F16_RANGE);
+            const uint64_t o = (uint64_t)(g0 + n) * I + rb * WGR + 32 * c_chunk;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint4 hq, lq;
+                hq.x = hv[8 * q] | ((uint32_t)hv[8 * q + 1] << 16);
+                hq.y = hv[8 * q + 2] | ((uint32_t)hv[8 * q + 3] << 16);
+                hq.z = hv[8 * q + 4] | ((uint32_t)hv[8 * q + 5] << 16);
+                hq.w = hv[8 * q + 6] | ((uint32_t)hv[8 * q + 7] << 16);
+                lq.x = lv[8 * q] | ((uint32_t)lv[8 * q + 1] << 16);
+                lq.y = lv[8 * q + 2] | ((uint32_t)lv[8 * q + 3] << 16);
+                lq.z = lv[8 * q + 4] | ((uint32_t)lv[8 * q + 5] << 16);
+                lq.w = lv[8 * q + 6] | ((uint32_t)lv[8 * q + 7] << 16);
+                reinterpret_cast<uint4*>(a.act_hi + o)[q] = hq;
+                reinterpret_cast<uint4*>(a.act_lo + o)[q] = lq;
+            }
+            a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + rb * (WGR / 32) + c_chunk] = sum;
+        }
+    } else {
+        // y [grouped row][H] f32 straight from the accumulators: a store
+        // instruction writes 32 consecutive rows of two tokens
+        const uint32_t H = rows_total;
+#pragma unroll
+        for (int tf = 0; tf < 4; ++tf)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t tk = 32 * tf + 8 * (j / 4) + 4 * h + (j % 4);
+                if (n0 + tk < cnt) {
+#pragma unroll
+                    for (int m = 0; m < 2; ++m)
+                        a.y[(uint64_t)(g0 + n0 + tk) * H + rowm[m]] = acc[tf][m][j];
+                }
+            }
+    }
+}
+
 // shared-expert gate logit per token: one wave per token, f32 accumulation
 template <int WDT>
 __global__ __launch_bounds__(256) void gate_row_kernel(const void* __restrict__ w, const float* __restrict__ x,
@@ -1006,11 +1594,31 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(
     }
 }
 
-uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared)
+static uint32_t max_tiles_of(uint32_t tok, uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared)
 {
     const uint32_t routes = tokens * k;
-    return routes / TOK + std::min(experts, routes) +
-           (has_shared ? (tokens + TOK - 1) / TOK : 0u) + 1;
+    return routes / tok + std::min(experts, routes) + (has_shared ? (tokens + tok - 1) / tok : 0u) + 1;
+}
+
+uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared)
+{
+    return max_tiles_of(TOK, tokens, k, experts, has_shared); // the larger count: 64-token tiles
+}
+
+// The 128-token kernels take group 64, rows in blocks of 256 (down) and
+// operand buffers addressed with 32-bit offsets; PBMOE_PREFILL_TILE=64 in
+// the environment keeps the 64-token kernels (for comparison).
+static bool use_t128(const PrefillArgs& p, uint32_t routes)
+{
+    static const bool forced64 = [] {
+        const char* v = std::getenv("PBMOE_PREFILL_TILE");
+        return v && std::strcmp(v, "64") == 0;
+    }();
+    const uint64_t I = p.ex.gate.rows, H = p.hidden, T = p.tokens;
+    const uint64_t x_bytes = (uint64_t)((const uint8_t*)p.x_lo - (const uint8_t*)p.x_hi) + T * H * 2;
+    const uint64_t a_bytes = (uint64_t)((const uint8_t*)p.act_lo - (const uint8_t*)p.act_hi) + (routes + T) * I * 2;
+    return !forced64 && p.ex.group == 64 && H % 256 == 0 && I % 128 == 0 && p.x_lo > p.x_hi &&
+           p.act_lo > p.act_hi && x_bytes < (1ull << 32) && a_bytes < (1ull << 32);
 }
 
 // start/stop events of kernel i/2 (gate/up GEMM, down GEMM, combine) when
@@ -1021,10 +1629,21 @@ static inline hipEvent_t phase_event(const PrefillArgs& p, int i)
 }
 
 // 8 x ceil(work / 8) workgroups for the XCD-split work list (see the kernel)
+static dim3 grid_of(uint32_t max_tiles, uint32_t row_blocks)
+{
+    return dim3((uint32_t)(8 * (uint64_t)row_blocks * ((max_tiles + 7) / 8)));
+}
+
 static dim3 gemm_grid(uint32_t max_tiles, uint32_t rows)
 {
-    const uint64_t work = (uint64_t)max_tiles * (rows / WG_ROWS);
-    return dim3((uint32_t)(8 * ((work + 7) / 8)));
+    return grid_of(max_tiles, rows / WG_ROWS);
+}
+
+// the 128-token kernels (group 64: KS = 2), two workgroups per CU
+template <int SBT, bool GATEUP>
+static void launch_gemm_t128(hipStream_t st, dim3 grid, hipEvent_t e0, hipEvent_t e1, const GemmArgs& a)
+{
+    hipExtLaunchKernelGGL((q4_gemm_t128_kernel<SBT, GATEUP, 2, 2>), grid, dim3(GL_THREADS), 0, st, e0, e1, 0, a);
 }
 
 template <int SBT, int KS>
@@ -1037,7 +1656,9 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     hipError_t err = launch_dispatch_plan(st, p.ids, routes, ex.count, K, p.plan, p.status);
     if (err != hipSuccess)
         return err;
-    const TileArgs ta{p.plan.unique_count, p.plan.groups, has_shared, T, p.tiles, p.tile_count};
+    const bool t128 = KS == 2 && use_t128(p, routes);
+    const TileArgs ta{p.plan.unique_count, p.plan.groups, has_shared, T, p.tiles, p.tile_count,
+                      t128 ? (uint32_t)TOK_L : (uint32_t)TOK};
     split_rows_kernel<<<T + 1, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any, ta);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
@@ -1081,8 +1702,13 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.act_hi = p.act_hi;
     a.act_lo = p.act_lo;
     a.act_sum32 = p.act_sum32;
-    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(GEMM_THREADS), 0, st,
-                          phase_event(p, 0), phase_event(p, 1), 0, a);
+    a.lo_delta = (uint32_t)((const uint8_t*)p.x_lo - (const uint8_t*)p.x_hi);
+    const uint32_t tiles128 = max_tiles_of(TOK_L, T, K, ex.count, has_shared != 0);
+    if (t128)
+        launch_gemm_t128<SBT, true>(st, grid_of(tiles128, I / 128), phase_event(p, 0), phase_event(p, 1), a);
+    else
+        hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, true, KS>), gemm_grid(max_tiles, I), dim3(GEMM_THREADS), 0,
+                              st, phase_event(p, 0), phase_event(p, 1), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     a.b_hi = p.act_hi;
@@ -1093,8 +1719,12 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.kdim = I;
     a.b_rows = routes + T;
     a.y = p.y;
-    hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(GEMM_THREADS), 0, st,
-                          phase_event(p, 2), phase_event(p, 3), 0, a);
+    a.lo_delta = (uint32_t)((const uint8_t*)p.act_lo - (const uint8_t*)p.act_hi);
+    if (t128)
+        launch_gemm_t128<SBT, false>(st, grid_of(tiles128, H / 256), phase_event(p, 2), phase_event(p, 3), a);
+    else
+        hipExtLaunchKernelGGL((q4_group_gemm_kernel<SBT, false, KS>), gemm_grid(max_tiles, H), dim3(GEMM_THREADS), 0,
+                              st, phase_event(p, 2), phase_event(p, 3), 0, a);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     hipExtLaunchKernelGGL(prefill_combine_kernel, dim3(T), dim3(256), 0, st, phase_event(p, 4), phase_event(p, 5), 0,
