@@ -459,7 +459,9 @@ struct RouteLds {
     uint32_t start[1024];
     uint32_t unique_count;
     uint32_t sel[4][MAX_K];
-    float grp[4][2048 + 192];
+    // 16-byte aligned: the routing code reads and writes 64-bit keys here
+    // (an LDS access of 8 bytes at an address that is 4 mod 8 runs far slower)
+    alignas(16) float grp[4][2048 + 192];
 };
 
 // Stable plan of `routes` routes from s.ids (block-wide, routes <= 256):
@@ -847,7 +849,7 @@ __global__ __launch_bounds__(256) void gateup_multi_kernel(ExpertArgs a)
     __shared__ __align__(16) float xl[WAVE * CPL * XQ];
     __shared__ uint32_t sid[MAX_K];
     __shared__ float sw[MAX_K];
-    __shared__ float rscr[RSCR]; // routing scratch
+    __shared__ __align__(16) float rscr[RSCR]; // routing scratch (64-bit keys: 8-byte aligned)
     const int lane = threadIdx.x & 63;
     const uint32_t K = a.rp.k, H = a.hidden, I = a.ex.gate.rows;
     const uint32_t t = blockIdx.y;

@@ -648,7 +648,8 @@ __device__ __forceinline__ void wave_sort64_desc(uint64_t& a)
 // route_token_wave; every thread of the workgroup must call it.  need_w
 // false (the same in every thread): the ids only, no softmax sums, weights
 // or weight checks (callers that publish no weights).
-// lds: >= 1024 + 8 + 144 floats of workgroup scratch.
+// lds: >= 1024 + 8 + 144 floats of workgroup scratch, 8-byte aligned (64-bit
+// keys are stored at lds + 512 and lds + 1032).
 // ---------------------------------------------------------------------------
 template <int EPT>
 __device__ inline void route_token_block(const float* __restrict__ l, const float* __restrict__ bias,
@@ -710,10 +711,10 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
     }
     uint32_t myid = 0;
     if constexpr (EPT <= 2) {
-        // E <= 512: each wave sorts its 128 keys (bitonic, across lanes by
-        // DPP), writes its top 16, and wave 0 sorts the 64 candidates; lane r
-        // < K then holds the r-th selected expert.  Same rule as the rounds
-        // below, 4,700 shader cycles against 7,000 for E = 512, K = 10.
+        // E <= 512: keys above a threshold (below), else each wave sorts its
+        // 128 keys (bitonic, across lanes by DPP), writes its top 16, and
+        // wave 0 sorts the 64 candidates; lane r < K then holds the r-th
+        // selected expert.  Same rule as the rounds below.
         uint64_t c2[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -721,18 +722,77 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
             const uint32_t kj = j < EPT && e < E ? total_key(sel[j < EPT ? j : 0]) : 0u;
             c2[j] = ((uint64_t)kj << 32) | (uint32_t)~e;
         }
-        wave_sort128_desc(c2[0], c2[1]);
-        uint64_t* cand = reinterpret_cast<uint64_t*>(cand_k); // [4][16]
-        if (lane < 8) {
-            cand[wv * 16 + 2 * lane] = c2[0];
-            cand[wv * 16 + 2 * lane + 1] = c2[1];
+        uint64_t* cand = reinterpret_cast<uint64_t*>(cand_k); // [64]
+        bool done = false;
+        if (K <= 16) {
+            // Threshold first: the 16 groups of 16 threads (32 keys each)
+            // publish their maxima; tau, the K-th largest of them, is at most
+            // the K-th largest key (K distinct keys are >= tau), so the keys
+            // >= tau hold the top K.  They are few for any spread of scores:
+            // when they fit one wave (64), wave 0 sorts just them.
+            uint64_t* gmax = reinterpret_cast<uint64_t*>(lds + 512);  // [16] (raw_l holds E <= 512)
+            uint32_t* ncand = reinterpret_cast<uint32_t*>(lds + 544); // candidate count
+            uint64_t gm = c2[0] > c2[1] ? c2[0] : c2[1];
+            uint64_t o = xor_lane64<1>(gm);
+            gm = o > gm ? o : gm;
+            o = xor_lane64<2>(gm);
+            gm = o > gm ? o : gm;
+            o = xor_lane64<4>(gm);
+            gm = o > gm ? o : gm;
+            o = xor_lane64<8>(gm);
+            gm = o > gm ? o : gm;
+            if ((lane & 15) == 0)
+                gmax[wv * 4 + (lane >> 4)] = gm;
+            if (tid == 0)
+                *ncand = 0;
+            __syncthreads();
+            // the maxima are distinct (distinct keys): one rank K - 1 among them
+            const uint64_t v = gmax[lane & 15];
+            uint32_t above = 0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                above += gmax[j] > v ? 1u : 0u;
+            const uint64_t hit = __ballot(above == K - 1);
+            const int src = __ffsll((unsigned long long)hit) - 1;
+            const uint64_t tau = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
+            const bool f0 = c2[0] >= tau, f1 = c2[1] >= tau;
+            const uint64_t b0 = __ballot(f0), b1 = __ballot(f1);
+            const uint32_t n0 = (uint32_t)__popcll(b0), nw = n0 + (uint32_t)__popcll(b1);
+            uint32_t base = 0;
+            if (lane == 0)
+                base = atomicAdd(ncand, nw);
+            base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+            const uint32_t p0 = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
+            const uint32_t p1 = base + n0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
+            if (f0 && p0 < 64)
+                cand[p0] = c2[0];
+            if (f1 && p1 < 64)
+                cand[p1] = c2[1];
+            __syncthreads();
+            const uint32_t n = *ncand;
+            if (n <= 64) {
+                if (wv != 0)
+                    return;
+                uint64_t c = (uint32_t)lane < n ? cand[lane] : 0ull;
+                wave_sort64_desc(c);
+                myid = ~(uint32_t)c;
+                done = true;
+            }
         }
-        __syncthreads();
-        if (wv != 0)
-            return;
-        uint64_t c = (uint32_t)(lane & 15) < K ? cand[(lane >> 4) * 16 + (lane & 15)] : 0ull;
-        wave_sort64_desc(c);
-        myid = ~(uint32_t)c;
+        if (!done) { // every wave sorts its 128 keys, wave 0 sorts the 4 x 16 heads
+            wave_sort128_desc(c2[0], c2[1]);
+            if (lane < 8) {
+                cand[wv * 16 + 2 * lane] = c2[0];
+                cand[wv * 16 + 2 * lane + 1] = c2[1];
+            }
+            __syncthreads();
+            if (wv != 0)
+                return;
+            uint64_t c = (uint32_t)(lane & 15) < K ? cand[(lane >> 4) * 16 + (lane & 15)] : 0ull;
+            wave_sort64_desc(c);
+            myid = ~(uint32_t)c;
+        }
     } else {
     // per-thread keys sorted descending (ascending index on equal keys)
     uint32_t key[EPT], idx[EPT];

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                                                          float* __restrict__ weights,
                                                          uint32_t* __restrict__ status)
 {
-    __shared__ float grp[4][2 * EPL * WAVE + 192];
+    __shared__ __align__(16) float grp[4][2 * EPL * WAVE + 192];
     __shared__ uint32_t sel[4][MAX_K];
     const int wv = threadIdx.x >> 6;
     const uint32_t t = blockIdx.x * 4 + wv;
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void route_block_kernel(const float* __restric
                                                          float* __restrict__ weights,
                                                          uint32_t* __restrict__ status)
 {
-    __shared__ float scratch[1024 + 8 + 144];
+    __shared__ __align__(16) float scratch[1024 + 8 + 144];
     const uint32_t t = blockIdx.x;
     route_token_block<EPT>(logits + (uint64_t)t * p.experts, bias, p, ids + (uint64_t)t * p.k,
                            weights + (uint64_t)t * p.k, scratch, status);
