@@ -1594,8 +1594,8 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     // scratch layout, each part 256-byte aligned
     size_t off[12], total = 0;
     const size_t part[12] = {
-        (size_t)max_tiles * 8, 4,      T * H * 2, T * H * 2, T * (H / 32) * 4, T * 4, T * 4,
-        rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, T * 4};
+        (size_t)max_tiles * 32, 4,     T * H * 2, T * H * 2, T * (H / 32) * 4, rows * 4, T * 4,
+        rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, rows * 4};
     for (int i = 0; i < 12; ++i) {
         off[i] = total;
         total += align256(part[i]);

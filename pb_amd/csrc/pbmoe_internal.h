@@ -148,13 +148,13 @@ struct PrefillArgs {
     float* next_normed;        // [T][H] or null
     Plan plan;                 // [routes] plan scratch
     // scratch (sizes from prefill_scratch_bytes)
-    uint32_t* tiles;           // [max_tiles][2]
+    uint32_t* tiles;           // [max_tiles][8] tile records
     uint32_t* tile_count;      // [1]
     uint16_t* x_hi;            // [T][H] f16
     uint16_t* x_lo;            // [T][H] f16
     float* x_sum32;            // [T][H/32]
-    float* rowscale;           // [T]
-    uint32_t* x_lo_any;        // [T] nonzero when the row's lo part is not all zero
+    float* rowscale;           // [T*K + T] per grouped row: its token's x scale
+    uint32_t* x_lo_any;        // [T*K + T] per grouped row: nonzero when its token's lo part is not all zero
     float* shared_logit;       // [T]
     uint16_t* act_hi;          // [T*K + T][I] f16
     uint16_t* act_lo;          // [T*K + T][I] f16

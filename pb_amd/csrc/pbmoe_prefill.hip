@@ -98,8 +98,9 @@ __device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 }
 
 // ---------------------------------------------------------------------------
-// tile table: for every used expert ceil(count / tok) tiles (item, start);
-// the shared expert, when present, is item U with all T tokens.  Order:
+// tile table: for every used expert ceil(count / tok) tiles (records of
+// TILE_REC words); the shared expert, when present, is item U with all T
+// tokens.  Order:
 // the full tiles of all items, then the partial ones (the last tile of an
 // item whose count is not a multiple of tok) by their 32-token fragments,
 // most first, so that the GEMMs (which deal the list to the XCDs in turn)
@@ -111,12 +112,17 @@ __device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 struct TileArgs {
     const uint32_t* unique_count;
     const uint32_t* groups;
+    const uint32_t* unique_ids;
     uint32_t has_shared;
     uint32_t tokens;
+    uint32_t routes; // T*K: the shared expert's rows start here in grouped order
     uint32_t* tiles;
     uint32_t* tile_count;
     uint32_t tok; // tokens per tile (64 or 128)
 };
+// one tile record: item, first token of the item, the item's first grouped
+// row and token count, the expert slot (all ones: the shared expert), 3 unused
+constexpr int TILE_REC = 8;
 
 __device__ void tile_table_wave(const TileArgs& a)
 {
@@ -152,9 +158,14 @@ __device__ void tile_table_wave(const TileArgs& a)
                     inc += v;
             }
             const uint32_t first = base + inc - nt;
-            for (uint32_t j = 0; j < nt; ++j) {
-                tiles[2 * (first + j)] = u;
-                tiles[2 * (first + j) + 1] = c == 0 ? j * a.tok : full * a.tok;
+            if (nt) {
+                const uint32_t g0 = u < U ? groups[2 * u] : a.routes;
+                const uint32_t e = u < U ? a.unique_ids[u] : 0xFFFFFFFFu;
+                for (uint32_t j = 0; j < nt; ++j) {
+                    uint4* rec = reinterpret_cast<uint4*>(tiles + TILE_REC * (first + j));
+                    rec[0] = make_uint4(u, c == 0 ? j * a.tok : full * a.tok, g0, cnt);
+                    rec[1] = make_uint4(e, 0u, 0u, 0u);
+                }
             }
             base += __shfl(inc, 63);
         }
@@ -186,14 +197,19 @@ __device__ __forceinline__ bool gemm_unit(uint32_t ntiles, uint32_t RB, uint32_t
 // rowscale = 2^e (e > 0 only for rows whose magnitude would leave the f16
 // range), and whether any lo is nonzero (rows of f16-valued inputs have
 // lo == 0 throughout; the gate/up GEMM then skips the lo products, which
-// would add exact zeros).  cols is a multiple of 64.
+// would add exact zeros).  The row scale and the lo flag are written in
+// grouped order, once per route of the token (out_idx) and for the shared
+// expert's row (routes + t), where the GEMMs read them beside the token
+// rows.  cols is a multiple of 64.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, uint32_t cols,
                                                          uint16_t* __restrict__ hi,
                                                          uint16_t* __restrict__ lo,
                                                          float* __restrict__ sum32,
                                                          float* __restrict__ rowscale,
-                                                         uint32_t* __restrict__ lo_any, TileArgs ta)
+                                                         uint32_t* __restrict__ lo_any,
+                                                         const uint32_t* __restrict__ out_idx, uint32_t k,
+                                                         TileArgs ta)
 {
     if (blockIdx.x == gridDim.x - 1) { // the tile table
         if (threadIdx.x < 64)
@@ -220,8 +236,6 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     if (amax > F16_SAFE)
         (void)frexpf(amax / F16_SAFE, &e); // amax * 2^-e <= F16_SAFE
     const float f = ldexpf(1.0f, -e);
-    if (threadIdx.x == 0)
-        rowscale[t] = ldexpf(1.0f, e);
     int any_lo = 0;
     // nb is a multiple of 4: the four blocks of 32 columns are on four
     // consecutive lanes, all present or all absent
@@ -248,8 +262,16 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
             sum32[(uint64_t)t * (cols / 32) + b / 4] = s;
     }
     any_lo = __syncthreads_or(any_lo);
-    if (threadIdx.x == 0)
-        lo_any[t] = any_lo ? 1u : 0u;
+    const uint32_t j = threadIdx.x;
+    if (j < k + (ta.has_shared ? 1u : 0u)) {
+        // a route the plan rejected (expert out of range) has no grouped row:
+        // out_idx all ones
+        const uint32_t pos = j < k ? out_idx[(uint64_t)t * k + j] : ta.routes + t;
+        if (pos < ta.routes + ta.tokens) {
+            rowscale[pos] = ldexpf(1.0f, e);
+            lo_any[pos] = any_lo ? 1u : 0u;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -270,8 +292,8 @@ struct GemmArgs {
     const uint16_t* b_hi;
     const uint16_t* b_lo;
     const float* b_sum32;
-    const float* rowscale;    // gate/up: per token; down: unused
-    const uint32_t* b_lo_any; // per B row: lo part not all zero (null: assume it is not)
+    const float* rowscale;    // gate/up: per grouped row; down: unused
+    const uint32_t* b_lo_any; // gate/up: per grouped row, its B row's lo part is not all zero (null: assume it is not)
     uint32_t kdim;            // H (gate/up) or I (down)
     uint32_t b_rows;          // rows of the B operand buffers
     uint32_t lo_delta;        // bytes from b_hi to b_lo (one allocation)
@@ -379,25 +401,17 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     uint32_t tile, rb;
     if (!gemm_unit(ntiles, RB, tile, rb))
         return;
-    const uint32_t item = a.tiles[2 * tile], n0 = a.tiles[2 * tile + 1];
-    const bool shared = a.has_shared && item == a.unique_count[0];
-    uint32_t g0, cnt;
-    const uint8_t* slot;
-    if (shared) {
-        g0 = a.routes;
-        cnt = a.tokens;
-        slot = a.sh.base;
-    } else {
-        const uint32_t e = a.unique_ids[item];
-        g0 = a.groups[2 * item];
-        cnt = a.groups[2 * item + 1];
-        if (e >= a.ex.count) {
-            if (tid == 0)
-                atomicOr(a.status, ST_ROUTE_RANGE);
-            return;
-        }
-        slot = a.ex.base + (uint64_t)e * a.ex.stride;
+    // the tile record: item, first token, the item's first grouped row and
+    // token count, expert slot (all ones: the shared expert)
+    const uint4 rec = *reinterpret_cast<const uint4*>(a.tiles + TILE_REC * tile);
+    const uint32_t n0 = rec.y, g0 = rec.z, cnt = rec.w, e = a.tiles[TILE_REC * tile + 4];
+    const bool shared = e == 0xFFFFFFFFu;
+    if (shared ? a.has_shared == 0u : e >= a.ex.count) {
+        if (tid == 0)
+            atomicOr(a.status, ST_ROUTE_RANGE);
+        return;
     }
+    const uint8_t* const slot = shared ? a.sh.base : a.ex.base + (uint64_t)e * a.ex.stride;
     const ExpertSet& set = shared ? a.sh : a.ex;
     const Q4Proj p0 = GATEUP ? set.gate : set.down;
     const Q4Proj p1 = set.up;
@@ -418,8 +432,8 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
         const uint32_t r = v ? tok_row(n) : 0u;
         row_lds[tid] = v ? r : 0xFFFFFFFFu;
         if (GATEUP)
-            rs_lds[tid] = v ? a.rowscale[r] : 1.0f;
-        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[r] != 0u);
+            rs_lds[tid] = v ? a.rowscale[g0 + n] : 1.0f;
+        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[g0 + n] != 0u);
     }
     // whether any token row of the tile has a nonzero lo part; if none has,
     // the lo products would all be exact zeros and are skipped
@@ -1026,25 +1040,17 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
     uint32_t tile, rb;
     if (!gemm_unit(ntiles, RB, tile, rb))
         return;
-    const uint32_t item = a.tiles[2 * tile], n0 = a.tiles[2 * tile + 1];
-    const bool shared = a.has_shared && item == a.unique_count[0];
-    uint32_t g0, cnt;
-    const uint8_t* slot;
-    if (shared) {
-        g0 = a.routes;
-        cnt = a.tokens;
-        slot = a.sh.base;
-    } else {
-        const uint32_t e = a.unique_ids[item];
-        g0 = a.groups[2 * item];
-        cnt = a.groups[2 * item + 1];
-        if (e >= a.ex.count) {
-            if (tid == 0)
-                atomicOr(a.status, ST_ROUTE_RANGE);
-            return;
-        }
-        slot = a.ex.base + (uint64_t)e * a.ex.stride;
+    // the tile record: item, first token, the item's first grouped row and
+    // token count, expert slot (all ones: the shared expert)
+    const uint4 rec = *reinterpret_cast<const uint4*>(a.tiles + TILE_REC * tile);
+    const uint32_t n0 = rec.y, g0 = rec.z, cnt = rec.w, e = a.tiles[TILE_REC * tile + 4];
+    const bool shared = e == 0xFFFFFFFFu;
+    if (shared ? a.has_shared == 0u : e >= a.ex.count) {
+        if (tid == 0)
+            atomicOr(a.status, ST_ROUTE_RANGE);
+        return;
     }
+    const uint8_t* const slot = shared ? a.sh.base : a.ex.base + (uint64_t)e * a.ex.stride;
     const ExpertSet& set = shared ? a.sh : a.ex;
     const uint32_t K = a.kdim;
     const uint32_t G = K / (32 * KS), C32 = K / 32, WPR = K / 8;
@@ -1058,8 +1064,8 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         const uint32_t r = v ? tok_row(n) : 0u;
         row_lds[tid] = v ? r : 0xFFFFFFFFu;
         if (GATEUP)
-            rs_lds[tid] = v ? a.rowscale[r] : 1.0f;
-        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[r] != 0u);
+            rs_lds[tid] = v ? a.rowscale[g0 + n] : 1.0f;
+        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[g0 + n] != 0u);
     }
     const bool tile_lo = __syncthreads_or(lo_flag) != 0;
     const uint32_t first_row = row_lds[0];
@@ -1657,9 +1663,10 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     if (err != hipSuccess)
         return err;
     const bool t128 = KS == 2 && use_t128(p, routes);
-    const TileArgs ta{p.plan.unique_count, p.plan.groups, has_shared, T, p.tiles, p.tile_count,
-                      t128 ? (uint32_t)TOK_L : (uint32_t)TOK};
-    split_rows_kernel<<<T + 1, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any, ta);
+    const TileArgs ta{p.plan.unique_count, p.plan.groups, p.plan.unique_ids, has_shared, T, routes, p.tiles,
+                      p.tile_count, t128 ? (uint32_t)TOK_L : (uint32_t)TOK};
+    split_rows_kernel<<<T + 1, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any,
+                                             p.plan.out_idx, K, ta);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     if (has_shared && p.sgate_w) {
