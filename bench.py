@@ -471,7 +471,7 @@ def bench_prefill(args, cfg, ctx, ev) -> dict:
         "expert_TFLOPs": round(total_tf, 1),
         "roofline": {"bound": "mfma", "achieved": g["TFLOPs"], "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(g["TFLOPs"] / MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "q4_group_gemm_kernel (gate/up)", "flops_per_launch": g["flops"],
+                     "kernel": "q4_gemm_t128_kernel (gate/up)", "flops_per_launch": g["flops"],
                      "launch_us": g["us"], "mfma_issued_frac": round(g["mfma_issued_TFLOPs"] / MFMA_PEAK_TFLOPS, 4),
                      "activations_f16_valued": x_f16},
         "kernels": kernels,
