@@ -548,6 +548,7 @@ struct ExpertArgs {
     bool has_shared;
     uint32_t pf_base;         // first down-prefetch workgroup (multiple of 8)
     uint32_t pf_wgs;          // down-prefetch workgroups (multiple of 8, 0: none)
+    bool pf_paired;           // the down kernel maps row blocks by down_row_block
 };
 
 constexpr int PF_LINES = 4; // cache lines touched per prefetch lane per round
@@ -556,13 +557,26 @@ constexpr int PF_LINES = 4; // cache lines touched per prefetch lane per round
 // added only while the whole grid fits in that one round
 constexpr uint32_t GATEUP_RESIDENT_WGS = 768;
 
+// Row block of down_rows_kernel workgroup b in a grid of a multiple of 16
+// workgroups: the 64-byte scale and bias runs of blocks 2m and 2m + 1 share
+// 128-byte lines, so the pair goes to one XCD (workgroup b runs on XCD
+// b % 8): workgroups b and b + 8 of XCD x take blocks 16j + 2x and
+// 16j + 2x + 1.  Other grids: block b.
+__host__ __device__ inline uint32_t down_row_block(uint32_t b, uint32_t grid)
+{
+    if (grid % 16)
+        return b;
+    const uint32_t x = b & 7, q = b >> 3;
+    return 16 * (q >> 1) + 2 * x + (q & 1);
+}
+
 // Down-weight prefetch: touch every 128-byte line of the down codes, scales
 // and biases of the selected experts (and the shared expert) while the
 // gate/up workgroups run, so that the down kernel finds them in the L2 /
 // MALL instead of HBM.  Row block rb (DOWN_R output rows) is read by down
-// workgroup rb (down_combine_kernel), or rb mod the grid (down_rows_kernel:
-// its grid is a multiple of 8), which the dispatcher places on XCD rb % 8;
-// a prefetch workgroup on XCD x touches only the blocks rb = x + 8j.
+// workgroup rb (down_combine_kernel: XCD rb % 8), or by the workgroup
+// down_row_block assigns it (down_rows_kernel, pf_paired: XCD (rb / 2) % 8);
+// a prefetch workgroup on XCD x touches only that XCD's blocks.
 // lane0/lanes: this lane's index among the lanes of this XCD that share the
 // work, and their number.  Returns a value that depends on every load.
 __device__ uint32_t touch_down_lines(const ExpertArgs& a, const RouteLds& s, uint32_t n_routed, bool use_plan,
@@ -576,7 +590,8 @@ __device__ uint32_t touch_down_lines(const ExpertArgs& a, const RouteLds& s, uin
     const uint32_t w_lines = (blk_w + 127) / 128, s_lines = (blk_sb + 127) / 128;
     const uint32_t per_block = w_lines + 2 * s_lines;
     const uint32_t n_blocks = a.hidden / DOWN_R;
-    const uint32_t per_item = n_blocks > xcd ? (n_blocks - xcd + 7) / 8 : 0u;
+    // this XCD's blocks: xcd + 8i, or (pf_paired) 16 (i / 2) + 2 xcd + i % 2
+    const uint32_t per_item = a.pf_paired ? (n_blocks / 16) * 2 : (n_blocks > xcd ? (n_blocks - xcd + 7) / 8 : 0u);
     const uint32_t n_items = n_routed + (a.has_shared ? 1u : 0u);
     const uint32_t total = n_items * per_item * per_block;
     uint32_t acc = 0;
@@ -590,7 +605,8 @@ __device__ uint32_t touch_down_lines(const ExpertArgs& a, const RouteLds& s, uin
                 continue;
             const uint32_t b = L / per_block, off = L % per_block;
             const uint32_t item = b / per_item;
-            const uint32_t rb = xcd + 8 * (b % per_item);
+            const uint32_t i = b % per_item;
+            const uint32_t rb = a.pf_paired ? 16 * (i >> 1) + 2 * xcd + (i & 1) : xcd + 8 * i;
             const bool shared = item == n_routed;
             const ExpertSet& set = shared ? a.sh : a.ex;
             const uint8_t* slot = set.base;
@@ -1417,7 +1433,7 @@ __global__ __launch_bounds__(256) void down_rows_kernel(DownArgs a)
     };
     RowWeights<NCH> A, B;
     const uint32_t step = gridDim.x * 4;
-    uint32_t r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t r = down_row_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     load_row(r, A);
     while (r < H) {
         load_row(r + step, B);
@@ -1777,6 +1793,13 @@ constexpr uint32_t MULTI_WGS_PER_CU = 4;
 // workgroups of down_rows_kernel per CU (its registers allow two; more only
 // wait)
 constexpr uint32_t ROWS_WGS_PER_CU = 2;
+// one token whose routed + shared activations (items x I floats) fit the
+// row kernel's staging: the down kernel is down_rows_kernel, on this grid
+static bool one_token_rows(uint32_t tokens, uint32_t items, uint32_t I)
+{
+    return tokens == 1 && (uint64_t)items * I <= PT_STAGE_FLOATS && I <= 1536;
+}
+static uint32_t rows_grid_one_token(uint32_t H) { return std::min(H / 4, 256u * ROWS_WGS_PER_CU); }
 
 // gateup_multi_kernel with the routes in d.ids: two rows per unit (one with
 // four chunks per lane, for the registers) and about the resident number of
@@ -1924,6 +1947,7 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     // C2 batch 1: down kernel 10.5 -> 9.2 us, gate/up +0.4 us.
     ea.pf_base = ((waves + 3) / 4 + 7) / 8 * 8;
     ea.pf_wgs = 0;
+    ea.pf_paired = one_token_rows(T, K + (d.shared ? 1u : 0u), I) && rows_grid_one_token(H) % 16 == 0;
     {
         const uint32_t items = max_items + (ea.has_shared ? 1u : 0u);
         const uint32_t gpr_d = I >> ex.group_shift;
@@ -2006,9 +2030,9 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     }
     // one token whose routed + shared activations fit: the row kernel (no
     // LDS combine and barrier; C2 down 7.8 -> 6.0 us per layer)
-    if (T == 1 && (uint64_t)(K + (da.has_shared ? 1u : 0u)) * I <= PT_STAGE_FLOATS && I <= 1536) {
+    if (one_token_rows(T, K + (da.has_shared ? 1u : 0u), I)) {
         const uint32_t nch = ((K + (da.has_shared ? 1u : 0u)) * (I / 32) + 63) / 64;
-        const dim3 gr(std::min(H / 4, 256u * ROWS_WGS_PER_CU), 1);
+        const dim3 gr(rows_grid_one_token(H), 1);
         if (nch <= 1)
             hipExtLaunchKernelGGL((down_rows_kernel<SBT, 1>), gr, dim3(256), 0, st, phase_event(d, 4),
                                   phase_event(d, 5), 0, da);
