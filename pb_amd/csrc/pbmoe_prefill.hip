@@ -1476,20 +1476,34 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
             a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + rb * (WGR / 32) + c_chunk] = sum;
         }
     } else {
-        // y [grouped row][H] f32 straight from the accumulators: a store
-        // instruction writes 32 consecutive rows of two tokens
+        // y [grouped row][H] f32: each wave turns its 64 rows of one 32-token
+        // fragment around in its own staging quarter ([token][YP floats]),
+        // then stores 16 bytes per lane, 256 contiguous bytes per token row
+        // (4-byte stores straight from the accumulators took four times the
+        // store instructions).  A wave reads back only what it wrote, in
+        // order, so no barrier is needed.
+        constexpr int YP = 72; // 64 rows + 8: the two lane halves' rows land on distinct banks
         const uint32_t H = rows_total;
+        float* const tb = reinterpret_cast<float*>(wv == 0 ? q0 : wv == 1 ? q1 : wv == 2 ? q2 : q3);
+        float* const yb = a.y + rb * WGR + wv * 64;
 #pragma unroll
-        for (int tf = 0; tf < 4; ++tf)
+        for (int tf = 0; tf < 4; ++tf) {
+            if (n0 + 32 * tf >= cnt)
+                break;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const uint32_t tk = 32 * tf + 8 * (j / 4) + 4 * h + (j % 4);
-                if (n0 + tk < cnt) {
+            for (int j = 0; j < 16; ++j)
 #pragma unroll
-                    for (int m = 0; m < 2; ++m)
-                        a.y[(uint64_t)(g0 + n0 + tk) * H + rowm[m]] = acc[tf][m][j];
-                }
+                for (int m = 0; m < 2; ++m)
+                    tb[(8 * (j / 4) + 4 * h + (j % 4)) * YP + 32 * m + n32] = acc[tf][m][j];
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const uint32_t idx = 64 * it + lane, t = idx >> 4, c = idx & 15;
+                const uint32_t tk = n0 + 32 * tf + t;
+                if (tk < cnt)
+                    *reinterpret_cast<float4*>(yb + (uint64_t)(g0 + tk) * H + 4 * c) =
+                        *reinterpret_cast<const float4*>(tb + t * YP + 4 * c);
             }
+        }
     }
 }
 
