@@ -266,14 +266,14 @@ __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const
 
 // Several tokens (XL): grid (task workgroups, token groups of XL_FLOATS / H
 // tokens); a workgroup stages its group's rows of x in LDS by coalesced
-// loads (and the norm weight), so that a wave's row runs every token of the
-// group from LDS instead of one L2 round trip per token, and the groups'
-// workgroups run side by side.
+// loads (times the norm weight when the norm is fused), so that a wave's row
+// runs every token of the group from LDS instead of one L2 round trip per
+// token, and the groups' workgroups run side by side.
 constexpr uint32_t XL_FLOATS = 8192; // staged x floats (32 KB)
 constexpr uint32_t XL_MAX_H = 8192;  // widest row of the staged variant
-// dynamic LDS of the staged variant: the x rows, then the norm weight (H
-// floats) when the norm is fused
-inline size_t xl_lds_bytes(uint32_t hidden, bool norm) { return (XL_FLOATS + (norm ? hidden : 0u)) * sizeof(float); }
+// dynamic LDS of the staged variant: the x rows (32 KB, four workgroups per
+// CU with or without a fused norm)
+inline size_t xl_lds_bytes(uint32_t, bool) { return XL_FLOATS * sizeof(float); }
 
 template <int WDT, int GDT, int SBT, int CR, int CS, bool XL>
 __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
@@ -378,47 +378,60 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
     } else {
         extern __shared__ __align__(16) float xl_dyn[]; // xl_lds_bytes
         float* const xsh = xl_dyn;
-        float* const nwsh = xl_dyn + XL_FLOATS; // (with a fused norm only)
-        __shared__ float inv_sh[XL_FLOATS / 256]; // per token of the group (H >= 256)
+        __shared__ float inv_sh[XL_FLOATS / 256];     // per token of the group (H >= 256)
+        __shared__ float ss_sh[XL_FLOATS / 256][4];   // per token and wave: partial sums of squares
         const uint32_t TG = XL_FLOATS / H, H4 = H / 4;
         const uint32_t g0 = blockIdx.y * TG, nt = min(TG, T - g0), n4 = nt * H4;
         constexpr int PER = XL_FLOATS / 4 / 256; // float4 per thread
-        constexpr int NPER = XL_MAX_H / 4 / 256;
-        // unconditional loads: slots past the data reload the last float4 (x
-        // slots land in buffer slots nothing reads); without a norm, x stands
-        // in for the norm weight, whose stores are then skipped
-        const float4* nsrc = reinterpret_cast<const float4*>(a.norm_w ? a.norm_w : a.x);
         const float4* src = reinterpret_cast<const float4*>(a.x + (uint64_t)g0 * H);
-        float4 nv[NPER];
-#pragma unroll
-        for (int j = 0; j < NPER; ++j)
-            nv[j] = nsrc[min(threadIdx.x + 256u * j, H4 - 1)];
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-            reinterpret_cast<float4*>(xsh)[threadIdx.x + 256u * j] = src[min(threadIdx.x + 256u * j, n4 - 1)];
         if (a.norm_w) {
+            // the staged rows are x times the norm weight (one buffer: the
+            // workgroup's LDS stays at 32 KB); the sums of squares of x are
+            // taken from the loaded values, per slot, then per token
+            const float4* nsrc = reinterpret_cast<const float4*>(a.norm_w);
+            float4 xv[PER], wv4[PER];
 #pragma unroll
-            for (int j = 0; j < NPER; ++j)
-                if (threadIdx.x + 256u * j < H4)
-                    reinterpret_cast<float4*>(nwsh)[threadIdx.x + 256u * j] = nv[j];
-        }
-        __syncthreads();
-        if (a.norm_w) {
-            // 1 / rms per token: wave w the tokens w, w + 4, ...
-            for (uint32_t t = threadIdx.x >> 6; t < nt; t += 4) {
-                float ss = 0.0f;
-                for (uint32_t i = lane; i < H4; i += 64) {
-                    const float4 q = reinterpret_cast<const float4*>(xsh)[t * H4 + i];
-                    ss = fmaf(q.x, q.x, ss), ss = fmaf(q.y, q.y, ss), ss = fmaf(q.z, q.z, ss), ss = fmaf(q.w, q.w, ss);
-                }
-                const float inv = inv_rms_of(ss, H, a.eps);
+            for (int j = 0; j < PER; ++j) { // unconditional loads: slots past the data reload the last float4
+                const uint32_t i = min(threadIdx.x + 256u * j, n4 - 1);
+                xv[j] = src[i];
+                wv4[j] = nsrc[i % H4];
+            }
+            float ssp[PER];
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const float4 q = xv[j], w = wv4[j];
+                reinterpret_cast<float4*>(xsh)[threadIdx.x + 256u * j] =
+                    make_float4(q.x * w.x, q.y * w.y, q.z * w.z, q.w * w.w);
+                float sq = 0.0f;
+                sq = fmaf(q.x, q.x, sq), sq = fmaf(q.y, q.y, sq), sq = fmaf(q.z, q.z, sq), sq = fmaf(q.w, q.w, sq);
+                ssp[j] = threadIdx.x + 256u * j < n4 ? sq : 0.0f;
+            }
+            const int wv = threadIdx.x >> 6;
+            for (uint32_t t = 0; t < nt; ++t) {
+                float p = 0.0f;
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                    p += (threadIdx.x + 256u * j) / H4 == t ? ssp[j] : 0.0f;
+                p = wave_sum(p);
                 if (lane == 0)
-                    inv_sh[t] = inv;
+                    ss_sh[t][wv] = p;
             }
             __syncthreads();
+            if (threadIdx.x < nt) {
+                const float ss = (ss_sh[threadIdx.x][0] + ss_sh[threadIdx.x][1]) +
+                                 (ss_sh[threadIdx.x][2] + ss_sh[threadIdx.x][3]);
+                inv_sh[threadIdx.x] = 1.0f / sqrtf(ss / (float)H + a.eps);
+            }
+            __syncthreads();
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+                reinterpret_cast<float4*>(xsh)[threadIdx.x + 256u * j] = src[min(threadIdx.x + 256u * j, n4 - 1)];
+            __syncthreads();
         }
+        // with a norm: x already times its weight, the 1 / rms per token as tscale
         if (wave_id < n_tasks)
-            run_task(wave_id, xsh, g0, nt, a.norm_w ? nwsh : nullptr, a.norm_w ? inv_sh : nullptr);
+            run_task(wave_id, xsh, g0, nt, nullptr, a.norm_w ? inv_sh : nullptr);
     }
     // the extra last workgroup (no tasks) writes the normalised rows for the
     // gate/up kernel, wave w the tokens w, w + 4, ...
