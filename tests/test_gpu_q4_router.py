@@ -29,9 +29,10 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 C1_BF = replace(C1, name="c1_bf16_scale_bias", sb_dtype=abi.DTYPE_BF16)
 C2_SIG = replace(C2, name="c2_sigmoid_noaux", routing=abi.ROUTING_SIGMOID_NOAUX)
-# the C5 row width (7168 columns: the router stage stages x, and with the
-# fused norm the norm weight, in dynamic LDS sized per launch) with a small
-# expert intermediate to keep the resident slots small
+# the C5 row width (7168 columns: the router stage stages x in LDS, times
+# the norm weight when the norm is fused, with each token's sum of squares
+# reduced across the workgroup) with a small expert intermediate to keep the
+# resident slots small
 C5W = MoeConfig("c5_width_q4_router", hidden=7168, intermediate=256, experts=256, k=8,
                 routing=abi.ROUTING_SOFTMAX_TOPK, normalization=abi.NORM_RENORMALIZE_SELECTED,
                 sb_dtype=abi.DTYPE_F16)
@@ -143,7 +144,8 @@ def test_q4_router_and_gate_fused_layer(ctx, T):
 @pytest.mark.parametrize("cfg,T", [(C5W, 1), (C5W_BF, 2)])
 def test_q4_router_fused_norm_at_c5_width(ctx, cfg, T):
     """pbmoe_moe_layer_norm with a Q4 router of 7168 columns: the router
-    stage stages x and the norm weight side by side in dynamic LDS.  Routes
+    stage stages x times the norm weight in LDS (one token per workgroup at
+    this width) and reduces each token's sum of squares there.  Routes
     equal those of pbmoe_moe_layer on the host-normalised rows wherever the
     K/K+1 logit gap exceeds the summation bound; hidden and next-normed rows
     within the bar of the oracle on rows normalised in f64."""
