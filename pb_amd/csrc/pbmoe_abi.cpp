@@ -1591,10 +1591,13 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     if ((rc = plan_buffers(ctx, d.experts, (uint32_t)routes, &plan)))
         return rc;
     const uint32_t max_tiles = pbmoe::prefill_max_tiles(tokens, K, d.experts, b->has_shared);
-    // scratch layout, each part 256-byte aligned
+    // scratch layout, each part 256-byte aligned; the tile table holds a
+    // multiple of 8 records (the GEMM workgroups read their record before
+    // checking it against the tile count, and the grid covers max_tiles
+    // rounded up to 8)
     size_t off[12], total = 0;
     const size_t part[12] = {
-        (size_t)max_tiles * 32, 4,     T * H * 2, T * H * 2, T * (H / 32) * 4, rows * 4, T * 4,
+        (size_t)((max_tiles + 7) / 8 * 8) * 32, 4,     T * H * 2, T * H * 2, T * (H / 32) * 4, rows * 4, T * 4,
         rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, rows * 4};
     for (int i = 0; i < 12; ++i) {
         off[i] = total;

@@ -179,15 +179,16 @@ __device__ void tile_table_wave(const TileArgs& a)
 // of one tile are consecutive on its XCD, so they share that XCD's L2 for
 // the tile's activation rows.  In tile-table order, each XCD meets its
 // largest tiles first.  Grid: 8 * RB * ceil(max_tiles / 8) (gemm_units).
-__device__ __forceinline__ bool gemm_unit(uint32_t ntiles, uint32_t RB, uint32_t& tile, uint32_t& rb)
+__device__ __forceinline__ void gemm_unit_of(uint32_t RB, uint32_t& tile, uint32_t& rb)
 {
     const uint32_t j = blockIdx.x >> 3, xcd = blockIdx.x & 7;
-    const uint32_t t = 8 * (j / RB) + xcd;
-    if (t >= ntiles)
-        return false;
-    tile = t;
+    tile = 8 * (j / RB) + xcd;
     rb = j % RB;
-    return true;
+}
+__device__ __forceinline__ bool gemm_unit(uint32_t ntiles, uint32_t RB, uint32_t& tile, uint32_t& rb)
+{
+    gemm_unit_of(RB, tile, rb);
+    return tile < ntiles;
 }
 
 // ---------------------------------------------------------------------------
@@ -1034,16 +1035,24 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
 
     // ---- work item (gemm_unit: tile t on XCD t % 8, its row blocks back to
     //      back there) ----
-    const uint32_t ntiles = a.tile_count[0];
     const uint32_t rows_total = GATEUP ? a.ex.gate.rows : a.ex.down.rows;
     const uint32_t RB = rows_total / WGR;
     uint32_t tile, rb;
-    if (!gemm_unit(ntiles, RB, tile, rb))
-        return;
+    gemm_unit_of(RB, tile, rb);
     // the tile record: item, first token, the item's first grouped row and
-    // token count, expert slot (all ones: the shared expert)
+    // token count, expert slot (all ones: the shared expert).  Loaded beside
+    // the tile count, not after it (the table holds the grid's tiles rounded
+    // up to 8 records, so the read is in bounds for every workgroup; a record
+    // past the count is never used)
     const uint4 rec = *reinterpret_cast<const uint4*>(a.tiles + TILE_REC * tile);
-    const uint32_t n0 = rec.y, g0 = rec.z, cnt = rec.w, e = a.tiles[TILE_REC * tile + 4];
+    const uint32_t e = a.tiles[TILE_REC * tile + 4];
+    const uint32_t ntiles = a.tile_count[0];
+    // the record's values in registers before the check (the compiler
+    // would otherwise load them after it, a second round trip)
+    asm volatile("" ::"s"(rec.y), "s"(rec.z), "s"(rec.w), "s"(e), "s"(ntiles));
+    if (tile >= ntiles)
+        return;
+    const uint32_t n0 = rec.y, g0 = rec.z, cnt = rec.w;
     const bool shared = e == 0xFFFFFFFFu;
     if (shared ? a.has_shared == 0u : e >= a.ex.count) {
         if (tid == 0)
@@ -1057,15 +1066,27 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
     auto tok_row = [&](uint32_t n) __attribute__((always_inline)) -> uint32_t {
         return GATEUP ? (shared ? n : a.src_rows[g0 + n]) : g0 + n;
     };
+    // the tile's token rows, row scales and lo flags: the three loads first,
+    // then their LDS writes (one round trip, not one per load)
     int lo_flag = 0;
-    if (tid < TOK_L) {
+    {
         const uint32_t n = n0 + tid;
-        const bool v = n < cnt;
-        const uint32_t r = v ? tok_row(n) : 0u;
-        row_lds[tid] = v ? r : 0xFFFFFFFFu;
-        if (GATEUP)
-            rs_lds[tid] = v ? a.rowscale[g0 + n] : 1.0f;
-        lo_flag = v && (a.b_lo_any == nullptr || a.b_lo_any[g0 + n] != 0u);
+        const bool v = tid < TOK_L && n < cnt;
+        uint32_t r = 0xFFFFFFFFu, lo = 1u;
+        float rs = 1.0f;
+        if (v) {
+            r = tok_row(n);
+            if (GATEUP)
+                rs = a.rowscale[g0 + n];
+            if (a.b_lo_any != nullptr)
+                lo = a.b_lo_any[g0 + n];
+        }
+        if (tid < TOK_L) {
+            row_lds[tid] = r;
+            if (GATEUP)
+                rs_lds[tid] = rs;
+            lo_flag = v && lo != 0u;
+        }
     }
     const bool tile_lo = __syncthreads_or(lo_flag) != 0;
     const uint32_t first_row = row_lds[0];
@@ -1108,6 +1129,7 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         else
             return cvt_f16_bits(v);
     };
+
 
     // accumulators: set by the bias term (fragments holding tokens) and
     // after the group loop (the others, zero)
@@ -1257,6 +1279,21 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         Words wA, wB;
         half8_t wf[2][NSTEP];
         uint32_t spa[2], spb[2];
+        constexpr bool PIPE = GATEUP && !LO; // the pipelined scaling below
+        // chain results (PIPE): the MFMA chain (tf, m) of a group
+        // accumulates its products in pp[m], and its scaling acc[tf][m] +=
+        // s * pp[m] is issued between the MFMAs of the next chain (tf, 1) or
+        // (tf + 1, 0), which write the other one, so that the scale FMAs
+        // co-execute with the MFMAs instead of waiting for their own chain
+        // (the order of the FMAs per element is unchanged).  The group's
+        // last chain (NTF - 1, 1) is scaled during the next group's first
+        // chain, with scale s_carry; before the first group pp[1] and
+        // s_carry are zero (the first group's carried scaling adds 0).
+        float16_t pp[2];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            pp[1][j] = 0.0f;
+        float s_carry = 0.0f;
         auto unpack_all = [&](Words& w) __attribute__((always_inline)) {
 #pragma unroll
             for (int m = 0; m < 2; ++m)
@@ -1309,19 +1346,63 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
                     // unpack can run beside its MFMAs
                     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
                 }
-                // K-step outer: the two sets' chains alternate, and a
-                // K-step's activation fragments are live only for its MFMAs
-                float16_t pp[2];
+                if constexpr (!PIPE) {
+                    // hi + lo: twice the MFMAs per scale FMA, and the
+                    // pipelined order below would hold all eight activation
+                    // fragments of the token fragment (spills); the down
+                    // GEMM measured slower with it.  K-step outer, the two
+                    // sets' chains alternating, the scaling after them
+                    float16_t qq[2];
 #pragma unroll
-                for (int k = 0; k < NSTEP; ++k) {
-                    half8_t ax[NHL];
+                    for (int k = 0; k < NSTEP; ++k) {
+                        half8_t ax[NHL];
+#pragma unroll
+                        for (int hl = 0; hl < NHL; ++hl)
+                            ax[hl] = *reinterpret_cast<const half8_t*>(frag(tf) + rd_off[k][hl]);
+#pragma unroll
+                        for (int hl = 0; hl < NHL; ++hl)
+#pragma unroll
+                            for (int m = 0; m < 2; ++m) {
+                                float16_t c;
+                                if (k == 0 && hl == 0) {
+#pragma unroll
+                                    for (int j = 0; j < 16; ++j)
+                                        c[j] = 0.0f;
+                                } else {
+                                    c = qq[m];
+                                }
+                                qq[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[hl], wf[m][k], c, 0, 0, 0);
+                            }
+                    }
+#pragma unroll
+                    for (int m = 0; m < 2; ++m)
+#pragma unroll
+                        for (int j = 0; j < 16; ++j)
+                            acc[tf][m][j] = fmaf(sa[m], qq[m][j], acc[tf][m][j]);
+                    continue;
+                }
+                half8_t ax[NSTEP][NHL];
+#pragma unroll
+                for (int k = 0; k < NSTEP; ++k)
 #pragma unroll
                     for (int hl = 0; hl < NHL; ++hl)
-                        ax[hl] = *reinterpret_cast<const half8_t*>(frag(tf) + rd_off[k][hl]);
+                        ax[k][hl] = *reinterpret_cast<const half8_t*>(frag(tf) + rd_off[k][hl]);
 #pragma unroll
-                    for (int hl = 0; hl < NHL; ++hl)
+                for (int m = 0; m < 2; ++m) {
+                    // the previous chain: (tf, 0) for m = 1, else (tf - 1, 1),
+                    // for tf = 0 the previous group's last
+                    const int ptf = m == 1 ? tf : (tf == 0 ? NTF - 1 : tf - 1);
+                    const float ps = m == 1 ? sa[0] : (tf == 0 ? s_carry : sa[1]);
+                    // each MFMA followed by its share of the previous
+                    // chain's scale FMAs, in this order (a scheduling
+                    // barrier after each pair: left alone, the compiler
+                    // issues the FMAs as one block behind the chain)
+                    constexpr int F = 16 / (NSTEP * NHL);
+                    const float16_t prev = pp[1 - m];
 #pragma unroll
-                        for (int m = 0; m < 2; ++m) {
+                    for (int k = 0; k < NSTEP; ++k)
+#pragma unroll
+                        for (int hl = 0; hl < NHL; ++hl) {
                             float16_t c;
                             if (k == 0 && hl == 0) {
 #pragma unroll
@@ -1330,15 +1411,16 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
                             } else {
                                 c = pp[m];
                             }
-                            pp[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[hl], wf[m][k], c, 0, 0, 0);
+                            pp[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[k][hl], wf[m][k], c, 0, 0, 0);
+                            const int i = k * NHL + hl;
+#pragma unroll
+                            for (int j = F * i; j < F * (i + 1); ++j)
+                                acc[ptf][1 - m][j] = fmaf(ps, prev[j], acc[ptf][1 - m][j]);
+                            __builtin_amdgcn_sched_barrier(0x3F4); // memory and scalar instructions may cross
                         }
                 }
-#pragma unroll
-                for (int m = 0; m < 2; ++m)
-#pragma unroll
-                    for (int j = 0; j < 16; ++j)
-                        acc[tf][m][j] = fmaf(sa[m], pp[m][j], acc[tf][m][j]);
             }
+            s_carry = sa[1];
             if constexpr (NEXT)
                 unpack_all(wnext);
             __syncthreads();
@@ -1348,7 +1430,9 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
                     spa[m] = spb[m];
             }
         };
-        // prologue: the first PF tiles, codes of groups 0 and 1, scales of 0 and 1
+        // prologue: the first PF tiles, codes of groups 0 and 1, scales of
+        // 0 and 1 (loaded here, not before the token rows' round trip: held
+        // through the bias term, the codes were spilled)
         stage(0, std::integral_constant<int, 0>{});
         if constexpr (PF >= 2)
             stage(1, std::integral_constant<int, 1>{});
@@ -1377,6 +1461,11 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         for (; g + NBUF < G; g += NBUF) // G is a multiple of NBUF
             iter(g, std::false_type{});
         iter(g, std::true_type{});
+        if constexpr (PIPE) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                acc[NTF - 1][1][j] = fmaf(s_carry, pp[1][j], acc[NTF - 1][1][j]);
+        }
 #pragma unroll
         for (int tf = NTF; tf < 4; ++tf)
 #pragma unroll
