@@ -106,7 +106,7 @@ __device__ __forceinline__ half8_t unpack8(uint32_t w, uint32_t magic)
 // most first, so that the GEMMs (which deal the list to the XCDs in turn)
 // start the longest workgroups first and end on the shortest.  One wave:
 // per class, a scan of the per-item tile counts, then each lane writes its
-// item's tiles.  Runs in the last workgroup of the split launch (both follow
+// item's tiles.  Runs in the first workgroup of the split launch (both follow
 // the plan and precede the GEMMs).
 // ---------------------------------------------------------------------------
 struct TileArgs {
@@ -212,13 +212,15 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
                                                          const uint32_t* __restrict__ out_idx, uint32_t k,
                                                          TileArgs ta)
 {
-    if (blockIdx.x == gridDim.x - 1) { // the tile table
+    // the tile table in the first workgroup, which starts before the token
+    // rows' workgroups and runs beside them (it needs the plan only)
+    if (blockIdx.x == 0) {
         if (threadIdx.x < 64)
             tile_table_wave(ta);
         return;
     }
     __shared__ float red[4];
-    const uint32_t t = blockIdx.x;
+    const uint32_t t = blockIdx.x - 1;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const float4* xr = reinterpret_cast<const float4*>(x + (uint64_t)t * cols);
     const uint32_t nb = cols / 8;
