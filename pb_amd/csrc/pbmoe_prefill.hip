@@ -1236,7 +1236,6 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         constexpr int CH = LO ? L::CH_LO : L::CH_HI;
         constexpr int NBUF = LO ? L::NBUF_LO : L::NBUF_HI;
         constexpr int PF = NBUF - 1;
-        constexpr int TILE = TOK_L * CH * 16;
         constexpr int DW = TOK_L * CH / 64 / 4; // staging instructions per wave and group
         // staging: instruction i of wave wv fills positions 64(wv + 4i) .. +63
         uint32_t st_off[DW];
