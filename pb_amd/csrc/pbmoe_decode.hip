@@ -40,7 +40,8 @@ struct RouterArgs {
     Q4Rows sgate_q4;      // GDT == DT_Q4
     uint32_t experts;     // 0: no router rows
     ExpertSet sh;
-    uint32_t shared_rows; // 0: no shared expert
+    uint32_t shared_rows; // shared gate/up rows computed here (0: none, or computed by the gate/up kernel)
+    uint32_t gate_task;   // 1: a shared expert, whose gate logit (or the 80.0 constant) is a task here
     const void* sgate_w;
     uint32_t sgate_dtype;
     const float* x;
@@ -58,14 +59,17 @@ struct RouterArgs {
 // dots W with x * w and multiplies the wave sum by inv_rms, which it forms
 // from sum(x^2) over the same x registers: no extra loads, no barrier.
 //
-// x [t][col .. col+8) as two float4; with norm_w: the squares go to ss and
-// the values are multiplied by the weight.
+// x [t][col .. col+8) as two float4; with NORM: the squares go to ss and
+// the values are multiplied by the weight.  NORM is a template argument, not
+// a test of norm_w: a runtime branch around the multiply made the compiler
+// wait for every call's loads inside the branch, one round trip per call.
+template <bool NORM>
 __device__ __forceinline__ void load_x8(const float* __restrict__ x, uint64_t off, const float* norm_w,
                                         uint32_t col, float4& u, float4& v, float& ss)
 {
     const float4* xp = reinterpret_cast<const float4*>(x + off);
     u = xp[0], v = xp[1];
-    if (norm_w) {
+    if constexpr (NORM) {
         ss = fmaf(u.x, u.x, ss), ss = fmaf(u.y, u.y, ss), ss = fmaf(u.z, u.z, ss), ss = fmaf(u.w, u.w, ss);
         ss = fmaf(v.x, v.x, ss), ss = fmaf(v.y, v.y, ss), ss = fmaf(v.z, v.z, ss), ss = fmaf(v.w, v.w, ss);
         const float4 w0 = *reinterpret_cast<const float4*>(norm_w + col);
@@ -127,7 +131,7 @@ __device__ __forceinline__ void dense8_to_float(const uint32_t (&wr)[WDT == 0 ? 
 
 // tscale: null, or the per-token scale 1 / rms of the rows of x (already
 // formed; the sums of squares here are then unused)
-template <int WDT, int CR>
+template <int WDT, int CR, bool NORM>
 __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, const float* x,
                                                uint32_t T, uint32_t H, float* out, uint32_t out_stride,
                                                const float* norm_w, float eps, const float* tscale = nullptr)
@@ -165,7 +169,7 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
                 float wvc[8];
                 dense8_to_float<WDT>(wr[c], wvc);
                 float4 u, v;
-                load_x8(x, (uint64_t)t * H + col, norm_w, col, u, v, ss);
+                load_x8<NORM>(x, (uint64_t)t * H + col, norm_w, col, u, v, ss);
                 acc0 = fmaf(wvc[0], u.x, acc0);
                 acc1 = fmaf(wvc[1], u.y, acc1);
                 acc0 = fmaf(wvc[2], u.z, acc0);
@@ -197,7 +201,7 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
         float s = wave_sum(acc0 + acc1);
         if (tscale)
             s *= tscale[t];
-        else if (norm_w)
+        else if constexpr (NORM)
             s *= inv_rms_of(ss, H, eps);
         if (lane == 0)
             out[(uint64_t)t * out_stride] = s;
@@ -207,7 +211,7 @@ __device__ __forceinline__ void dense_row_dots(const void* w, uint64_t row_off, 
 // Q4 row . x for every token (a Q4 router row or shared gate row): lane l
 // takes the 32-column chunks l + 64 c; the row is s . sum(q x) + b . sum(x)
 // per group, the factored form of the dequantised row.
-template <int SBT, int CS>
+template <int SBT, int CS, bool NORM>
 __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const float* x, uint32_t T, uint32_t H,
                                             float* out, uint32_t out_stride, const float* norm_w, float eps,
                                             const float* tscale = nullptr)
@@ -242,7 +246,7 @@ __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     float4 u, v;
-                    load_x8(x, (uint64_t)t * H + ch * 32 + 8 * q, norm_w, ch * 32 + 8 * q, u, v, ss);
+                    load_x8<NORM>(x, (uint64_t)t * H + ch * 32 + 8 * q, norm_w, ch * 32 + 8 * q, u, v, ss);
                     xv[8 * q] = u.x, xv[8 * q + 1] = u.y, xv[8 * q + 2] = u.z, xv[8 * q + 3] = u.w;
                     xv[8 * q + 4] = v.x, xv[8 * q + 5] = v.y, xv[8 * q + 6] = v.z, xv[8 * q + 7] = v.w;
                 }
@@ -257,7 +261,7 @@ __device__ __forceinline__ void q4_row_dots(const Q4Rows& m, uint64_t row, const
         float r = wave_sum(p);
         if (tscale)
             r *= tscale[t];
-        else if (norm_w)
+        else if constexpr (NORM)
             r *= inv_rms_of(ss, H, eps);
         if (lane == 0)
             out[(uint64_t)t * out_stride] = r;
@@ -282,79 +286,121 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
     const uint32_t H = a.hidden, T = a.tokens;
     const uint32_t n_router = a.experts;
     const uint32_t Is = a.shared_rows;
-    const uint32_t n_tasks = n_router + (Is ? Is + 1u : 0u);
+    const uint32_t n_tasks = n_router + Is + (a.gate_task ? 1u : 0u);
     const uint32_t wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t n_waves = gridDim.x * 4;
     // task over tokens t0 .. t0 + nt - 1 with their rows at x (row t at
-    // x + t H); norm_w, tscale as for the row helpers
-    auto run_task = [&](uint32_t task, const float* x, uint32_t t0, uint32_t nt, const float* norm_w,
+    // x + t H); norm_w (used when NORM), tscale as for the row helpers
+    auto run_task = [&](auto norm_tag, uint32_t task, const float* x, uint32_t t0, uint32_t nt, const float* norm_w,
                         const float* tscale) {
+        constexpr bool NORM = decltype(norm_tag)::value;
         if (task < n_router) {
             if constexpr (WDT == (int)DT_Q4)
-                q4_row_dots<SBT, CS>(a.router_q4, task, x, nt, H, a.logits + (uint64_t)t0 * n_router + task, n_router,
-                                     norm_w, a.eps, tscale);
+                q4_row_dots<SBT, CS, NORM>(a.router_q4, task, x, nt, H, a.logits + (uint64_t)t0 * n_router + task,
+                                           n_router, norm_w, a.eps, tscale);
             else
-                dense_row_dots<WDT, CR>(a.router_w, (uint64_t)task * H, x, nt, H,
-                                        a.logits + (uint64_t)t0 * n_router + task, n_router, norm_w, a.eps, tscale);
+                dense_row_dots<WDT, CR, NORM>(a.router_w, (uint64_t)task * H, x, nt, H,
+                                              a.logits + (uint64_t)t0 * n_router + task, n_router, norm_w, a.eps,
+                                              tscale);
         } else if (task < n_router + Is) {
             const uint32_t i = task - n_router;
             const ExpertSet& s = a.sh;
             const uint32_t chunks = H / 32, gpr = H >> s.group_shift;
             const uint4* gw = reinterpret_cast<const uint4*>(s.base + s.gate.w_off + (uint64_t)i * (H / 2));
             const uint4* uw = reinterpret_cast<const uint4*>(s.base + s.up.w_off + (uint64_t)i * (H / 2));
+            // unconditional loads (a lane's chunk past the row reloads the
+            // last chunk; its products are masked below): a load inside a
+            // per-lane branch is waited for at the end of the branch
             uint4 wg[CS], wu[CS];
             float sg[CS], bg[CS], su[CS], bu[CS];
 #pragma unroll
             for (int c = 0; c < CS; ++c) {
-                const uint32_t ch = lane + WAVE * c;
-                if (ch < chunks) {
-                    wg[c] = gw[ch];
-                    wu[c] = uw[ch];
-                    const uint64_t gi = (uint64_t)i * gpr + ((ch * 32u) >> s.group_shift);
-                    sg[c] = sb_at<SBT>(s.base + s.gate.s_off, gi);
-                    bg[c] = sb_at<SBT>(s.base + s.gate.b_off, gi);
-                    su[c] = sb_at<SBT>(s.base + s.up.s_off, gi);
-                    bu[c] = sb_at<SBT>(s.base + s.up.b_off, gi);
-                }
+                const uint32_t ch = min((uint32_t)(lane + WAVE * c), chunks - 1);
+                wg[c] = gw[ch];
+                wu[c] = uw[ch];
+                const uint64_t gi = (uint64_t)i * gpr + ((ch * 32u) >> s.group_shift);
+                sg[c] = sb_at<SBT>(s.base + s.gate.s_off, gi);
+                bg[c] = sb_at<SBT>(s.base + s.gate.b_off, gi);
+                su[c] = sb_at<SBT>(s.base + s.up.s_off, gi);
+                bu[c] = sb_at<SBT>(s.base + s.up.b_off, gi);
             }
             for (uint32_t t = 0; t < nt; ++t) {
-                // the nibble conversions do not depend on the token: without
-                // this opaque step the compiler hoists them out of the loop
-                // (32 floats per chunk and matrix: one wave per SIMD at CS = 4)
-#pragma unroll
-                for (int c = 0; c < CS; ++c) {
-                    asm volatile("" : "+v"(wg[c].x), "+v"(wg[c].y), "+v"(wg[c].z), "+v"(wg[c].w));
-                    asm volatile("" : "+v"(wu[c].x), "+v"(wu[c].y), "+v"(wu[c].z), "+v"(wu[c].w));
-                }
                 float pg = 0.0f, pu = 0.0f, ss = 0.0f;
+                // x of one chunk (times the norm weight), its sum and the
+                // two products
+                auto chunk = [&](int c, const float(&xc)[32]) __attribute__((always_inline)) {
+                    float xs = 0.0f;
 #pragma unroll
-                for (int c = 0; c < CS; ++c) {
-                    const uint32_t ch = lane + WAVE * c;
-                    if (ch < chunks) {
-                        float xv[32];
+                    for (int q = 0; q < 32; q += 8)
+                        xs += ((xc[q] + xc[q + 1]) + (xc[q + 2] + xc[q + 3])) +
+                              ((xc[q + 4] + xc[q + 5]) + (xc[q + 6] + xc[q + 7]));
+                    const float qg = q4_chunk_qx_reg(wg[c], xc);
+                    const float qu = q4_chunk_qx_reg(wu[c], xc);
+                    pg = fmaf(sg[c], qg, fmaf(bg[c], xs, pg));
+                    pu = fmaf(su[c], qu, fmaf(bu[c], xs, pu));
+                };
+                auto load_chunk = [&](int c, float(&xc)[32], float& ssc) __attribute__((always_inline)) {
+                    const uint32_t ch = min((uint32_t)(lane + WAVE * c), chunks - 1);
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            float4 u, v;
-                            load_x8(x, (uint64_t)t * H + ch * 32 + 8 * q, norm_w, ch * 32 + 8 * q, u, v, ss);
-                            xv[8 * q] = u.x, xv[8 * q + 1] = u.y, xv[8 * q + 2] = u.z, xv[8 * q + 3] = u.w;
-                            xv[8 * q + 4] = v.x, xv[8 * q + 5] = v.y, xv[8 * q + 6] = v.z, xv[8 * q + 7] = v.w;
+                    for (int q = 0; q < 4; ++q) {
+                        float4 u4, v4;
+                        load_x8<NORM>(x, (uint64_t)t * H + ch * 32 + 8 * q, norm_w, ch * 32 + 8 * q, u4, v4, ssc);
+                        xc[8 * q] = u4.x, xc[8 * q + 1] = u4.y, xc[8 * q + 2] = u4.z, xc[8 * q + 3] = u4.w;
+                        xc[8 * q + 4] = v4.x, xc[8 * q + 5] = v4.y, xc[8 * q + 6] = v4.z, xc[8 * q + 7] = v4.w;
+                    }
+                };
+                if constexpr (CS <= 2) {
+                    // the token's x first, so that its loads are in flight
+                    // with the weights' (one round trip), then the opaque
+                    // step, which waits for the weights
+                    float xv[CS][32];
+                    float ssc[CS];
+#pragma unroll
+                    for (int c = 0; c < CS; ++c) {
+                        ssc[c] = 0.0f;
+                        load_chunk(c, xv[c], ssc[c]);
+                    }
+                    asm volatile("" ::: "memory");
+                    // the nibble conversions do not depend on the token:
+                    // without this opaque step the compiler hoists them out
+                    // of the loop
+#pragma unroll
+                    for (int c = 0; c < CS; ++c) {
+                        asm volatile("" : "+v"(wg[c].x), "+v"(wg[c].y), "+v"(wg[c].z), "+v"(wg[c].w));
+                        asm volatile("" : "+v"(wu[c].x), "+v"(wu[c].y), "+v"(wu[c].z), "+v"(wu[c].w));
+                    }
+#pragma unroll
+                    for (int c = 0; c < CS; ++c)
+                        if (lane + WAVE * c < chunks) {
+                            ss += ssc[c];
+                            chunk(c, xv[c]);
                         }
-                        float xs = 0.0f;
+                } else {
+                    // four chunks per lane: 128 floats of x would cost waves
+                    // per SIMD; x one chunk at a time (32 floats per chunk
+                    // and matrix in the conversions: one wave per SIMD if
+                    // hoisted, hence the opaque step)
 #pragma unroll
-                        for (int q = 0; q < 32; q += 8)
-                            xs += ((xv[q] + xv[q + 1]) + (xv[q + 2] + xv[q + 3])) +
-                                  ((xv[q + 4] + xv[q + 5]) + (xv[q + 6] + xv[q + 7]));
-                        const float qg = q4_chunk_qx_reg(wg[c], xv);
-                        const float qu = q4_chunk_qx_reg(wu[c], xv);
-                        pg = fmaf(sg[c], qg, fmaf(bg[c], xs, pg));
-                        pu = fmaf(su[c], qu, fmaf(bu[c], xs, pu));
+                    for (int c = 0; c < CS; ++c) {
+                        asm volatile("" : "+v"(wg[c].x), "+v"(wg[c].y), "+v"(wg[c].z), "+v"(wg[c].w));
+                        asm volatile("" : "+v"(wu[c].x), "+v"(wu[c].y), "+v"(wu[c].z), "+v"(wu[c].w));
+                    }
+#pragma unroll
+                    for (int c = 0; c < CS; ++c) {
+                        float xc[32];
+                        float ssc = 0.0f;
+                        load_chunk(c, xc, ssc);
+                        if (lane + WAVE * c < chunks) {
+                            ss += ssc;
+                            chunk(c, xc);
+                        }
                     }
                 }
                 float g = wave_sum(pg);
                 float u = wave_sum(pu);
                 if (tscale) {
                     g *= tscale[t], u *= tscale[t];
-                } else if (norm_w) {
+                } else if constexpr (NORM) {
                     const float inv = inv_rms_of(ss, H, a.eps);
                     g *= inv, u *= inv;
                 }
@@ -363,9 +409,9 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
             }
         } else if (a.sgate_w) {
             if constexpr (GDT == (int)DT_Q4)
-                q4_row_dots<SBT, CS>(a.sgate_q4, 0, x, nt, H, a.shared_weight + t0, 1, norm_w, a.eps, tscale);
+                q4_row_dots<SBT, CS, NORM>(a.sgate_q4, 0, x, nt, H, a.shared_weight + t0, 1, norm_w, a.eps, tscale);
             else
-                dense_row_dots<GDT, CR>(a.sgate_w, 0, x, nt, H, a.shared_weight + t0, 1, norm_w, a.eps, tscale);
+                dense_row_dots<GDT, CR, NORM>(a.sgate_w, 0, x, nt, H, a.shared_weight + t0, 1, norm_w, a.eps, tscale);
             // sigma applied by the consumer: shared_weight holds the gate logit
         } else if (lane == 0) {
             for (uint32_t t = 0; t < nt; ++t)
@@ -373,8 +419,13 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
         }
     };
     if constexpr (!XL) {
-        for (uint32_t task = wave_id; task < n_tasks; task += n_waves)
-            run_task(task, a.x, 0, T, a.norm_w, nullptr);
+        if (a.norm_w) {
+            for (uint32_t task = wave_id; task < n_tasks; task += n_waves)
+                run_task(std::true_type{}, task, a.x, 0, T, a.norm_w, nullptr);
+        } else {
+            for (uint32_t task = wave_id; task < n_tasks; task += n_waves)
+                run_task(std::false_type{}, task, a.x, 0, T, nullptr, nullptr);
+        }
     } else {
         extern __shared__ __align__(16) float xl_dyn[]; // xl_lds_bytes
         float* const xsh = xl_dyn;
@@ -431,12 +482,55 @@ __global__ __launch_bounds__(256) void router_stage_kernel(RouterArgs a)
         }
         // with a norm: x already times its weight, the 1 / rms per token as tscale
         if (wave_id < n_tasks)
-            run_task(wave_id, xsh, g0, nt, nullptr, a.norm_w ? inv_sh : nullptr);
+            run_task(std::false_type{}, wave_id, xsh, g0, nt, nullptr, a.norm_w ? inv_sh : nullptr);
     }
     // the extra last workgroup (no tasks) writes the normalised rows for the
-    // gate/up kernel, wave w the tokens w, w + 4, ...
-    if (a.norm_w && blockIdx.x == gridDim.x - 1) {
-        // (XL: the tokens of this workgroup's group)
+    // gate/up kernel
+    if constexpr (!XL) {
+        // all four waves on each token: every thread's x and norm-weight
+        // loads (H <= 8192: at most 8 float4 each) issued at once, the sum
+        // of squares through LDS, the row written from registers (one round
+        // trip; one wave per token paid two dependent passes)
+        if (a.norm_w && blockIdx.x == gridDim.x - 1) {
+            __shared__ float nrm[4];
+            constexpr int NF = 8;
+            const uint32_t H4 = H / 4;
+            const float4* wr4 = reinterpret_cast<const float4*>(a.norm_w);
+            for (uint32_t t = 0; t < T; ++t) {
+                const float4* xr = reinterpret_cast<const float4*>(a.x + (uint64_t)t * H);
+                float4 v[NF], w[NF];
+#pragma unroll
+                for (int j = 0; j < NF; ++j) { // unconditional: slots past the row reload its last float4
+                    const uint32_t i = min(threadIdx.x + 256u * j, H4 - 1);
+                    v[j] = xr[i];
+                    w[j] = wr4[i];
+                }
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NF; ++j)
+                    if (threadIdx.x + 256u * j < H4) {
+                        const float4 q = v[j];
+                        ss = fmaf(q.x, q.x, ss), ss = fmaf(q.y, q.y, ss), ss = fmaf(q.z, q.z, ss), ss = fmaf(q.w, q.w, ss);
+                    }
+                ss = wave_sum(ss);
+                if (lane == 0)
+                    nrm[threadIdx.x >> 6] = ss;
+                __syncthreads();
+                const float inv = 1.0f / sqrtf(((nrm[0] + nrm[1]) + (nrm[2] + nrm[3])) / (float)H + a.eps);
+#pragma unroll
+                for (int j = 0; j < NF; ++j) {
+                    const uint32_t i = threadIdx.x + 256u * j;
+                    if (i < H4) {
+                        const float4 q = v[j], ww = w[j];
+                        reinterpret_cast<float4*>(a.x_out + (uint64_t)t * H)[i] =
+                            make_float4((q.x * inv) * ww.x, (q.y * inv) * ww.y, (q.z * inv) * ww.z, (q.w * inv) * ww.w);
+                    }
+                }
+                __syncthreads(); // nrm is read before the next token writes it
+            }
+        }
+    } else if (a.norm_w && blockIdx.x == gridDim.x - 1) {
+        // XL: the tokens of this workgroup's group, wave w the tokens w, w + 4, ...
         const uint32_t tb = XL ? blockIdx.y * (XL_FLOATS / H) : 0u;
         const uint32_t te = XL ? min(tb + XL_FLOATS / H, T) : T;
         for (uint32_t t = tb + (threadIdx.x >> 6); t < te; t += 4) {
@@ -562,6 +656,9 @@ struct ExpertArgs {
     uint32_t pf_base;         // first down-prefetch workgroup (multiple of 8)
     uint32_t pf_wgs;          // down-prefetch workgroups (multiple of 8, 0: none)
     bool pf_paired;           // the down kernel maps row blocks by down_row_block
+    uint32_t shared_rows;     // one token: the shared expert's gate/up rows, computed by the
+                              // prefetch workgroups before they route (0: by the router stage)
+    float* act_shared;        // [Is]
 };
 
 constexpr int PF_LINES = 4; // cache lines touched per prefetch lane per round
@@ -670,6 +767,62 @@ __device__ void route_all_tokens(const ExpertArgs& a, RouteLds& s, bool need_w)
 // kernel 2: routing (every workgroup) + routed gate/up with SiLU(g)*u.
 // Task = (work item, RPW consecutive rows) per wave.
 // ---------------------------------------------------------------------------
+// One shared-expert gate/up row of one token (x already normalised):
+// SiLU(g) * u into *out (lane 0).  Lane l takes the 32-column chunks
+// l + 64 c; every load is issued before the first wait (chunks past the row
+// reload the last one and are masked).
+template <int SBT, int CPL>
+__device__ __forceinline__ void shared_row_one_token(const ExpertSet& sh, uint32_t i, const float* __restrict__ x,
+                                                     uint32_t H, float* out)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t chunks = H / 32, gpr = H >> sh.group_shift;
+    const uint4* gw = reinterpret_cast<const uint4*>(sh.base + sh.gate.w_off + (uint64_t)i * (H / 2));
+    const uint4* uw = reinterpret_cast<const uint4*>(sh.base + sh.up.w_off + (uint64_t)i * (H / 2));
+    const uint16_t* gs = reinterpret_cast<const uint16_t*>(sh.base + sh.gate.s_off) + (uint64_t)i * gpr;
+    const uint16_t* gb = reinterpret_cast<const uint16_t*>(sh.base + sh.gate.b_off) + (uint64_t)i * gpr;
+    const uint16_t* us = reinterpret_cast<const uint16_t*>(sh.base + sh.up.s_off) + (uint64_t)i * gpr;
+    const uint16_t* ub = reinterpret_cast<const uint16_t*>(sh.base + sh.up.b_off) + (uint64_t)i * gpr;
+    uint4 wg[CPL], wu[CPL];
+    uint32_t sg[CPL], bg[CPL], su[CPL], bu[CPL];
+    float xv[CPL][32];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const uint32_t ch = min((uint32_t)(lane + WAVE * c), chunks - 1);
+        const uint32_t g = (ch * 32u) >> sh.group_shift;
+        wg[c] = gw[ch];
+        wu[c] = uw[ch];
+        sg[c] = gs[g];
+        bg[c] = gb[g];
+        su[c] = us[g];
+        bu[c] = ub[g];
+        const float4* x4 = reinterpret_cast<const float4*>(x + ch * 32);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 v = x4[q];
+            xv[c][4 * q] = v.x, xv[c][4 * q + 1] = v.y, xv[c][4 * q + 2] = v.z, xv[c][4 * q + 3] = v.w;
+        }
+    }
+    float pg = 0.0f, pu = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        if (lane + WAVE * c < chunks) {
+            float xs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 32; q += 4)
+                xs += (xv[c][q] + xv[c][q + 1]) + (xv[c][q + 2] + xv[c][q + 3]);
+            const float qg = q4_chunk_qx_reg(wg[c], xv[c]);
+            const float qu = q4_chunk_qx_reg(wu[c], xv[c]);
+            pg = fmaf(sb_bits<SBT>(sg[c]), qg, fmaf(sb_bits<SBT>(bg[c]), xs, pg));
+            pu = fmaf(sb_bits<SBT>(su[c]), qu, fmaf(sb_bits<SBT>(bu[c]), xs, pu));
+        }
+    }
+    const float g = wave_sum(pg);
+    const float u = wave_sum(pu);
+    if (lane == 0)
+        *out = (g / (1.0f + expf(-g))) * u;
+}
+
 template <int SBT, int CPL, int RPW, int EPL>
 __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
 {
@@ -678,6 +831,16 @@ __global__ __launch_bounds__(256) void route_gateup_kernel(ExpertArgs a)
     const uint32_t T = a.tokens, K = a.rp.k, H = a.hidden, I = a.ex.gate.rows;
     const uint32_t routes = T * K;
     const bool use_plan = T > 1;
+
+    if (a.shared_rows && blockIdx.x >= a.pf_base) {
+        // the shared expert's rows of the one token need no routes: the
+        // prefetch workgroups take them first (in the router stage their
+        // weights arrived last and held back this launch), wave w of
+        // prefetch workgroup b the rows 4 b + w, + 4 pf_wgs, ...
+        const uint32_t w0 = (blockIdx.x - a.pf_base) * 4 + (threadIdx.x >> 6);
+        for (uint32_t i = w0; i < a.shared_rows; i += a.pf_wgs * 4)
+            shared_row_one_token<SBT, CPL>(a.sh, i, a.x, H, a.act_shared + i);
+    }
 
     if (a.route_here) {
         // only the publishing workgroup needs the route weights (the down
@@ -1667,14 +1830,15 @@ static inline hipEvent_t phase_event(const DecodeArgs& d, int i)
 }
 
 static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool do_router,
-                                      bool do_shared)
+                                      bool do_shared, bool shared_rows_here = true)
 {
     RouterArgs a{};
     a.router_w = d.router_w;
     a.experts = do_router ? d.rp.experts : 0u;
     if (do_shared && d.shared)
         a.sh = *d.shared;
-    a.shared_rows = do_shared && d.shared ? d.shared->gate.rows : 0u;
+    a.shared_rows = do_shared && d.shared && shared_rows_here ? d.shared->gate.rows : 0u;
+    a.gate_task = do_shared && d.shared ? 1u : 0u;
     a.sgate_w = do_shared ? d.sgate_w : nullptr;
     a.sgate_dtype = d.sgate_dtype;
     a.router_q4 = d.router_q4;
@@ -1688,7 +1852,7 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     a.logits = d.logits;
     a.act_shared = d.act_shared;
     a.shared_weight = d.shared_weight;
-    const uint32_t tasks = a.experts + (a.shared_rows ? a.shared_rows + 1u : 0u);
+    const uint32_t tasks = a.experts + a.shared_rows + a.gate_task;
     if (tasks == 0) {
         if (d.phase_timing) {
             hipError_t e = hipEventRecord(d.phase_ev[0], st);
@@ -1717,7 +1881,7 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
     // combinations share the f16 gate path only when the gate is f16
     const uint32_t gdt = a.sgate_w ? d.sgate_dtype : d.router_dtype;
     const uint32_t wdt = a.experts ? d.router_dtype : gdt;
-    const uint32_t sbt = a.shared_rows ? a.sh.sb_dtype : 1u;
+    const uint32_t sbt = a.gate_task ? a.sh.sb_dtype : 1u;
 #define PBM_RS(W, G, S, CRV, CSV)                                                              \
     do {                                                                                       \
         if (xl)                                                                                \
@@ -1743,7 +1907,7 @@ static hipError_t launch_router_stage(hipStream_t st, const DecodeArgs& d, bool 
         return hipErrorInvalidValue; // bind validates matching dtypes
     // a Q4 router or gate row carries the layer's scale/bias dtype
     const uint32_t qsb = wdt == DT_Q4 ? d.ex.sb_dtype : sbt;
-    if (wdt == DT_Q4 && a.shared_rows && sbt != qsb)
+    if (wdt == DT_Q4 && a.gate_task && sbt != qsb)
         return hipErrorInvalidValue;
     if (wdt == DT_Q4) {
         if (qsb == 2) PBM_RS_CS(DT_Q4, DT_Q4, 2, 4);
@@ -1913,6 +2077,62 @@ static hipError_t launch_multi_token(hipStream_t st, const DecodeArgs& d, bool r
     return err;
 }
 
+// Launch shape of route_gateup_kernel outside the several-token path: its
+// gate/up workgroups (pf_base, a multiple of 8) and the down-weight prefetch
+// workgroups appended after them.  Down-weight prefetch by extra workgroups
+// while gate/up runs, when the down bytes of the selected experts fit
+// comfortably in the L2s (8 x 4 MB): about two touched lines per prefetch
+// lane, at most 16 workgroups per XCD (more than that no longer fit beside
+// the gate/up workgroups).  Measured on C2 batch 1: down kernel 10.5 -> 9.2
+// us, gate/up +0.4 us.  Returns false when the gate/up phase runs another
+// kernel (the persistent one).
+static bool gateup_prefetch(const DecodeArgs& d, bool route_here, uint32_t& pf_base, uint32_t& pf_wgs)
+{
+    const ExpertSet& ex = d.ex;
+    const uint32_t T = d.tokens, K = d.rp.k, H = d.hidden, I = ex.gate.rows;
+    const bool use_plan = T > 1;
+    const bool wide_shape = (uint64_t)(K + (d.shared ? 1u : 0u)) * I > STAGE_FLOATS &&
+                            (uint64_t)(K + (d.shared ? 1u : 0u)) * I <= WIDE_FLOATS && I % 512 == 0 &&
+                            I >= 1024 && I <= 2048 && H % WIDE_R == 0;
+    const uint32_t max_items = use_plan ? std::min(ex.count, T * K) : T * K;
+    const uint32_t RPW = gateup_rpw(d, nullptr);
+    const uint32_t waves = max_items * (I / RPW);
+    pf_base = ((waves + 3) / 4 + 7) / 8 * 8;
+    pf_wgs = 0;
+    const bool multi_gu = wide_shape && H <= 64 * 32 * 4 && (T > 1 || !route_here);
+    const bool wide = wide_shape && (T == 1 || multi_gu); // the wide down kernel takes no prefetch
+    const uint32_t items = max_items + (d.shared ? 1u : 0u);
+    const uint32_t gpr_d = I >> ex.group_shift;
+    const uint64_t down_bytes = (uint64_t)items * H * (I / 2 + 4u * gpr_d);
+    if (!wide && down_bytes <= (16u << 20) && pf_base < GATEUP_RESIDENT_WGS) {
+        const uint32_t per_block = (DOWN_R * I / 2 + 127) / 128 + 2 * ((DOWN_R * gpr_d * 2 + 127) / 128);
+        const uint64_t lines_xcd = (uint64_t)items * ((H / DOWN_R + 7) / 8) * per_block;
+        const uint64_t per_xcd = (lines_xcd + 2 * 256 - 1) / (2 * 256);
+        pf_wgs = 8u * (uint32_t)std::min<uint64_t>(per_xcd, 16);
+        pf_wgs = std::min(pf_wgs, (GATEUP_RESIDENT_WGS - pf_base) / 8 * 8);
+    }
+    return !multi_gu;
+}
+
+// One token through route_gateup_kernel with down-prefetch workgroups and a
+// shared expert of the routed experts' scale/bias type: the prefetch
+// workgroups compute the shared gate/up rows (no routes needed) instead of
+// the router stage, whose launch their weight loads held back (C2: the
+// shared rows' workgroups ended 1.3 us after the router rows').
+static bool shared_rows_in_gateup(const DecodeArgs& d, bool route_here)
+{
+    if (!d.shared || d.tokens != 1 || multi_token_path(d) || d.shared->sb_dtype != d.ex.sb_dtype ||
+        d.shared->gate.cols != d.hidden || d.shared->up.cols != d.hidden)
+        return false;
+    const uint32_t K = d.rp.k, I = d.ex.gate.rows, H = d.hidden;
+    const bool wide_shape = (uint64_t)(K + 1u) * I > STAGE_FLOATS && (uint64_t)(K + 1u) * I <= WIDE_FLOATS &&
+                            I % 512 == 0 && I >= 1024 && I <= 2048 && H % WIDE_R == 0;
+    if (wide_shape)
+        return false;
+    uint32_t pf_base, pf_wgs;
+    return gateup_prefetch(d, route_here, pf_base, pf_wgs) && pf_wgs >= 8 && (H / 32 + 63) / 64 <= 4;
+}
+
 template <int SBT>
 static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool route_here)
 {
@@ -1950,28 +2170,18 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
     if (ea.has_shared)
         ea.sh = *d.shared;
     const int RPW = (int)gateup_rpw(d, nullptr);
-    const uint32_t waves = max_items * (I / RPW);
     const uint32_t cpl = (H / 32 + 63) / 64;
     const uint32_t epl = (d.rp.experts + 63) / 64;
-    // Down-weight prefetch by extra workgroups while gate/up runs, when the
-    // down bytes of the selected experts fit comfortably in the L2s (8 x 4 MB):
-    // about two touched lines per prefetch lane, at most 16 workgroups per XCD
-    // (more than that no longer fit beside the gate/up workgroups).  Measured on
-    // C2 batch 1: down kernel 10.5 -> 9.2 us, gate/up +0.4 us.
-    ea.pf_base = ((waves + 3) / 4 + 7) / 8 * 8;
-    ea.pf_wgs = 0;
+    gateup_prefetch(d, route_here, ea.pf_base, ea.pf_wgs);
     ea.pf_paired = one_token_rows(T, K + (d.shared ? 1u : 0u), I) && rows_grid_one_token(H) % 16 == 0;
-    {
-        const uint32_t items = max_items + (ea.has_shared ? 1u : 0u);
-        const uint32_t gpr_d = I >> ex.group_shift;
-        const uint64_t down_bytes = (uint64_t)items * H * (I / 2 + 4u * gpr_d);
-        if (!wide && down_bytes <= (16u << 20) && ea.pf_base < GATEUP_RESIDENT_WGS) {
-            const uint32_t per_block = (DOWN_R * I / 2 + 127) / 128 + 2 * ((DOWN_R * gpr_d * 2 + 127) / 128);
-            const uint64_t lines_xcd = (uint64_t)items * ((H / DOWN_R + 7) / 8) * per_block;
-            const uint64_t per_xcd = (lines_xcd + 2 * 256 - 1) / (2 * 256);
-            ea.pf_wgs = 8u * (uint32_t)std::min<uint64_t>(per_xcd, 16);
-            ea.pf_wgs = std::min(ea.pf_wgs, (GATEUP_RESIDENT_WGS - ea.pf_base) / 8 * 8);
-        }
+    if (shared_rows_in_gateup(d, route_here)) {
+        ea.shared_rows = d.shared->gate.rows;
+        ea.act_shared = d.act_shared;
+        // one shared row per prefetch wave where the single round of
+        // resident workgroups allows (a wave with two paid two round trips
+        // before routing and became the launch's tail)
+        const uint32_t want = (ea.shared_rows + 31) / 32 * 8;
+        ea.pf_wgs = std::max(ea.pf_wgs, std::min(want, (GATEUP_RESIDENT_WGS - ea.pf_base) / 8 * 8));
     }
     dim3 g1(ea.pf_base + ea.pf_wgs);
 #define PBM_GU(C, EP)                                                                          \
@@ -2158,15 +2368,14 @@ hipError_t launch_decode_layer(hipStream_t st, const DecodeArgs& d, uint32_t mod
         return launch_route_topk(st, d.logits, d.sel_bias, d.tokens, d.rp, d.ids, d.weights, d.status);
     }
     const bool full = mode == DECODE_FULL_LAYER;
-    err = launch_router_stage(st, d, full, d.shared != nullptr);
+    const bool route_here = full && !route_separately(d);
+    err = launch_router_stage(st, d, full, d.shared != nullptr, !shared_rows_in_gateup(d, route_here));
     if (err != hipSuccess)
         return err;
-    bool route_here = full;
-    if (full && route_separately(d)) {
+    if (full && !route_here) {
         err = launch_route_topk(st, d.logits, d.sel_bias, d.tokens, d.rp, d.ids, d.weights, d.status);
         if (err != hipSuccess)
             return err;
-        route_here = false;
     }
     if (d.ex.sb_dtype == 2)
         err = launch_experts_typed<2>(st, d, route_here);
