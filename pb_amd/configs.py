@@ -62,11 +62,13 @@ def q4_proj_bytes(rows: int, cols: int, group: int) -> int:
 
 def decode_phase_bytes(cfg: MoeConfig, unique_experts: int, tokens: int, fused_norm: bool = False) -> dict:
     """Algorithmic HBM bytes of each decode kernel (pbmoe_moe_layer):
-    stage   router rows (f16), shared gate/up + gate row, x in, logits and
-            shared activations out; with the fused input RMSNorm
+    stage   router rows (f16), shared gate/up (see below) + gate row, x in,
+            logits and shared activations out; with the fused input RMSNorm
             (pbmoe_moe_layer_norm) also the norm weight in and the
             normalised rows out (the gate/up kernel's x);
-    gateup  gate/up of the selected experts, logits and x in, act out;
+    gateup  gate/up of the selected experts, logits and x in, act out; the
+            shared gate/up rows and shared activations instead of the stage
+            when shared_rows_in_gateup;
     down    down of the selected experts + shared down, act in, residual
             in, hidden out."""
     H, I, Is, E, K, g, T = (cfg.hidden, cfg.intermediate, cfg.shared_intermediate, cfg.experts, cfg.k,
@@ -74,15 +76,34 @@ def decode_phase_bytes(cfg: MoeConfig, unique_experts: int, tokens: int, fused_n
     stage = E * H * 2 + T * H * 4 + T * E * 4
     if fused_norm:
         stage += H * 4 + T * H * 4
+    shared_gu = 2 * q4_proj_bytes(Is, H, g) + T * Is * 4 if Is else 0
+    gateup = unique_experts * 2 * q4_proj_bytes(I, H, g) + T * E * 4 + T * H * 4 + T * K * I * 4
     if Is:
-        stage += 2 * q4_proj_bytes(Is, H, g) + T * Is * 4
+        if shared_rows_in_gateup(cfg, T):
+            gateup += shared_gu
+        else:
+            stage += shared_gu
         if cfg.shared_gated:
             stage += H * 2
-    gateup = unique_experts * 2 * q4_proj_bytes(I, H, g) + T * E * 4 + T * H * 4 + T * K * I * 4
     down = unique_experts * q4_proj_bytes(H, I, g) + T * K * I * 4 + 2 * T * H * 4
     if Is:
         down += q4_proj_bytes(H, Is, g) + T * Is * 4
     return {"stage": stage, "gateup": gateup, "down": down}
+
+
+def shared_rows_in_gateup(cfg: MoeConfig, tokens: int) -> bool:
+    """Whether one token's shared-expert gate/up rows run in the gate/up
+    kernel's down-prefetch workgroups instead of the router stage (the host
+    rule shared_rows_in_gateup in pbmoe_decode.hip): one token, a shared
+    expert, not the wide-activation shape, prefetch workgroups present and at
+    most four 32-column chunks per lane."""
+    if tokens != 1 or not cfg.shared_intermediate:
+        return False
+    H, I, K = cfg.hidden, cfg.intermediate, cfg.k
+    wide = (K + 1) * I > 12288 and (K + 1) * I <= 18432 and I % 512 == 0 and 1024 <= I <= 2048 and H % 16 == 0
+    if wide:
+        return False
+    return down_prefetch_bytes(cfg, K, 1) > 0 and (H // 32 + 63) // 64 <= 4
 
 
 def down_prefetch_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:
