@@ -95,15 +95,19 @@ def shared_rows_in_gateup(cfg: MoeConfig, tokens: int) -> bool:
     """Whether one token's shared-expert gate/up rows run in the gate/up
     kernel's down-prefetch workgroups instead of the router stage (the host
     rule shared_rows_in_gateup in pbmoe_decode.hip): one token, a shared
-    expert, not the wide-activation shape, prefetch workgroups present and at
-    most four 32-column chunks per lane."""
+    expert, not the wide-activation shape, prefetch workgroups present, at
+    most four 32-column chunks per lane, and room in the one round of 768
+    resident workgroups for one shared row per prefetch wave."""
     if tokens != 1 or not cfg.shared_intermediate:
         return False
     H, I, K = cfg.hidden, cfg.intermediate, cfg.k
     wide = (K + 1) * I > 12288 and (K + 1) * I <= 18432 and I % 512 == 0 and 1024 <= I <= 2048 and H % 16 == 0
     if wide:
         return False
-    return down_prefetch_bytes(cfg, K, 1) > 0 and (H // 32 + 63) // 64 <= 4
+    pf_base = ((K * (I // 2) + 3) // 4 + 7) // 8 * 8  # the gate/up workgroups before the prefetch ones
+    room = (768 - pf_base) // 8 * 8 if pf_base < 768 else 0
+    return (down_prefetch_bytes(cfg, K, 1) > 0 and (H // 32 + 63) // 64 <= 4
+            and room * 4 >= cfg.shared_intermediate)
 
 
 def down_prefetch_bytes(cfg: MoeConfig, unique_experts: int, tokens: int) -> int:

@@ -2129,8 +2129,11 @@ static bool shared_rows_in_gateup(const DecodeArgs& d, bool route_here)
                             I % 512 == 0 && I >= 1024 && I <= 2048 && H % WIDE_R == 0;
     if (wide_shape)
         return false;
+    // room in the single round of resident workgroups for one shared row
+    // per prefetch wave (with two rows a wave became the launch's tail)
     uint32_t pf_base, pf_wgs;
-    return gateup_prefetch(d, route_here, pf_base, pf_wgs) && pf_wgs >= 8 && (H / 32 + 63) / 64 <= 4;
+    return gateup_prefetch(d, route_here, pf_base, pf_wgs) && pf_wgs >= 8 && (H / 32 + 63) / 64 <= 4 &&
+           pf_base < GATEUP_RESIDENT_WGS && (GATEUP_RESIDENT_WGS - pf_base) / 8 * 8 * 4 >= d.shared->gate.rows;
 }
 
 template <int SBT>
