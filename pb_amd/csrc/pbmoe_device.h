@@ -729,7 +729,7 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
             // publish their maxima; tau, the K-th largest of them, is at most
             // the K-th largest key (K distinct keys are >= tau), so the keys
             // >= tau hold the top K.  They are few for any spread of scores:
-            // when they fit one wave (64), wave 0 sorts just them.
+            // when they fit one wave (64), wave 0 ranks just them.
             uint64_t* gmax = reinterpret_cast<uint64_t*>(lds + 512);  // [16] (raw_l holds E <= 512)
             uint32_t* ncand = reinterpret_cast<uint32_t*>(lds + 544); // candidate count
             uint64_t gm = c2[0] > c2[1] ? c2[0] : c2[1];
@@ -774,9 +774,19 @@ __device__ inline void route_token_block(const float* __restrict__ l, const floa
             if (n <= 64) {
                 if (wv != 0)
                     return;
-                uint64_t c = (uint32_t)lane < n ? cand[lane] : 0ull;
-                wave_sort64_desc(c);
-                myid = ~(uint32_t)c;
+                // the keys are distinct: a candidate's rank is the number of
+                // larger keys, counted over the candidates read from LDS as
+                // broadcasts (n steps; a bitonic sort of 64 lanes took
+                // 1,900 cycles, the largest part of the routing); the K
+                // first land in rank order, lane r then holds the r-th
+                const uint64_t c = (uint32_t)lane < n ? cand[lane] : 0ull;
+                uint32_t rank = 0;
+                for (uint32_t j = 0; j < n; ++j)
+                    rank += cand[j] > c ? 1u : 0u;
+                uint32_t* sel = reinterpret_cast<uint32_t*>(cand); // the candidates are read
+                if ((uint32_t)lane < n && rank < K)
+                    sel[rank] = ~(uint32_t)c;
+                myid = (uint32_t)lane < K ? sel[lane] : 0u;
                 done = true;
             }
         }
