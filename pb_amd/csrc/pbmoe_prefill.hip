@@ -955,9 +955,9 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
 // acc += s * P (the group scale, in f32).  The activation tile of a group is
 // staged by buffer loads straight into LDS ([128 tokens][CH chunks], hi
 // only when no row of the tile has a lo part, else hi and lo interleaved;
-// chunk c of row r at position c ^ (r % CH)), NBUF groups resident; the
+// chunks of a row in an XOR-swizzled order), NBUF groups resident; the
 // codes come two groups ahead into registers.  The bias term runs on the
-// matrix cores after the loop, as in the 64-token kernel.
+// matrix cores before the loop.
 // ---------------------------------------------------------------------------
 constexpr int TOK_L = 128;
 constexpr int GL_THREADS = 256;
@@ -993,7 +993,10 @@ struct GemmLLds {
     static constexpr int TILE_HI = TOK_L * CH_HI * 16;
     static constexpr int TILE_LO = TOK_L * CH_LO * 16;
     static constexpr int NBUF_HI = 4, NBUF_LO = 2; // hi tiles: one quarter each; hi + lo tiles: two
-    static constexpr int OPITCH = 128 + 4; // gate/up epilogue tile: 4 x [32 tokens][OPITCH] f32
+    // gate/up epilogue tile: 4 x [32 tokens][OPITCH] f32, the 32-row chunk
+    // c of a token at 36c (a row's four chunk reads by four lanes, and the
+    // rows of neighbouring lanes, fall on distinct banks)
+    static constexpr int OCH = 36, OPITCH = 4 * OCH;
     // LDS as four separate arrays ("quarters"): a hi tile fills one, a
     // hi + lo tile two (token rows 0-63, 64-127), an epilogue block of 32
     // tokens one.  Being distinct objects, the compiler can tell the reads
@@ -1237,12 +1240,19 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         constexpr int NBUF = LO ? L::NBUF_LO : L::NBUF_HI;
         constexpr int PF = NBUF - 1;
         constexpr int DW = TOK_L * CH / 64 / 4; // staging instructions per wave and group
+        // chunk c of token row r sits at position c ^ swz(r) of the row, so
+        // that the 16 rows one cycle of 16-byte LDS reads serves (64 banks)
+        // fall on distinct banks, and any 8 consecutive rows (32 banks); with
+        // 8 chunks per row (hi only) r % 8 would repeat after 8 rows
+        auto swz = [](uint32_t r) __attribute__((always_inline)) -> uint32_t {
+            return LO ? r % CH : (r & 7u) ^ ((r >> 3) & 3u); // period 32: a fragment's rows
+        };
         // staging: instruction i of wave wv fills positions 64(wv + 4i) .. +63
         uint32_t st_off[DW];
 #pragma unroll
         for (int i = 0; i < DW; ++i) {
             const uint32_t pos = 64 * (wv + 4 * i) + lane;
-            const uint32_t r = pos / CH, c = (pos % CH) ^ (r % CH);
+            const uint32_t r = pos / CH, c = (pos % CH) ^ swz(r);
             const uint32_t rr = row_lds[r];
             const uint32_t trow = rr != 0xFFFFFFFFu ? rr : first_row; // rows past the item: any valid row
             if constexpr (LO)
@@ -1268,14 +1278,14 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
             }
         };
         // fragment reads: row 32tf + n32, chunk (NSTEP h + k) (x2 + hl with lo)
-        // at position chunk ^ (n32 % CH)
+        // at position chunk ^ swz(n32)
         uint32_t rd_off[NSTEP][NHL];
 #pragma unroll
         for (int k = 0; k < NSTEP; ++k)
 #pragma unroll
             for (int hl = 0; hl < NHL; ++hl) {
                 const uint32_t c = LO ? 2 * (h * NSTEP + k) + hl : h * NSTEP + k;
-                rd_off[k][hl] = (n32 * CH + (c ^ (n32 % CH))) * 16;
+                rd_off[k][hl] = (n32 * CH + (c ^ swz(n32))) * 16;
             }
         Words wA, wB;
         half8_t wf[2][NSTEP];
@@ -1504,7 +1514,7 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
         auto ot = [&](uint32_t b) __attribute__((always_inline)) -> float* {
             return reinterpret_cast<float*>(b == 0 ? q0 : b == 1 ? q1 : b == 2 ? q2 : q3);
         };
-        const uint32_t col = wv * 32 + n32;
+        const uint32_t col = wv * L::OCH + n32;
 #pragma unroll
         for (int tf = 0; tf < 4; ++tf)
 #pragma unroll
@@ -1527,7 +1537,7 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
             const uint32_t n = n0 + c_tok;
             if (n >= cnt)
                 continue;
-            const float* src = ot(c_tok / 32) + (c_tok % 32) * L::OPITCH + 32 * c_chunk;
+            const float* src = ot(c_tok / 32) + (c_tok % 32) * L::OPITCH + L::OCH * c_chunk;
             float v[32];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
