@@ -153,6 +153,7 @@ struct PrefillArgs {
     uint16_t* x_hi;            // [T][H] f16
     uint16_t* x_lo;            // [T][H] f16
     float* x_sum32;            // [T][H/32]
+    uint16_t* x_sumhl;         // [T][2][GP] f16 group sums hi, lo (GP = H/64 rounded up to 16)
     float* rowscale;           // [T*K + T] per grouped row: its token's x scale
     uint32_t* x_lo_any;        // [T*K + T] per grouped row: nonzero when its token's lo part is not all zero
     float* shared_logit;       // [T]

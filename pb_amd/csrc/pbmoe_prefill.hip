@@ -195,8 +195,12 @@ __device__ __forceinline__ bool gemm_unit(uint32_t ntiles, uint32_t RB, uint32_t
 // split: one workgroup per token row, one 8-column block per thread and
 // step (two 16-byte loads, one 16-byte store each for hi and lo).  hi/lo f16
 // of x * 2^-e in K order, sums of x * 2^-e per 32 columns (four lanes),
-// rowscale = 2^e (e > 0 only for rows whose magnitude would leave the f16
-// range), and whether any lo is nonzero (rows of f16-valued inputs have
+// with sum_hl also the group sums (ks = 2 sums of 32 columns) as f16 hi and
+// lo, the operand of the 128-token GEMM's bias term ([T][hi: GP][lo: GP],
+// GP = groups rounded up to 16, the padding zero), rowscale = 2^e (e > 0
+// only for rows whose elements would leave the f16 range, or whose group
+// sums, bounded by ks times the largest sum of 32 columns, would), and
+// whether any lo is nonzero (rows of f16-valued inputs have
 // lo == 0 throughout; the gate/up GEMM then skips the lo products, which
 // would add exact zeros).  The row scale and the lo flag are written in
 // grouped order, once per route of the token (out_idx) and for the shared
@@ -207,6 +211,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
                                                          uint16_t* __restrict__ hi,
                                                          uint16_t* __restrict__ lo,
                                                          float* __restrict__ sum32,
+                                                         uint16_t* __restrict__ sum_hl, uint32_t ks,
                                                          float* __restrict__ rowscale,
                                                          uint32_t* __restrict__ lo_any,
                                                          const uint32_t* __restrict__ out_idx, uint32_t k,
@@ -219,26 +224,38 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
             tile_table_wave(ta);
         return;
     }
-    __shared__ float red[4];
+    __shared__ float red[8];
     const uint32_t t = blockIdx.x - 1;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const float4* xr = reinterpret_cast<const float4*>(x + (uint64_t)t * cols);
     const uint32_t nb = cols / 8;
-    float amax = 0.0f;
+    float amax = 0.0f, smax = 0.0f;
     for (uint32_t b = threadIdx.x; b < nb; b += 256) {
         const float4 p = xr[2 * b], q = xr[2 * b + 1];
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w))));
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
+        float s = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        smax = fmaxf(smax, fabsf(s));
     }
     amax = wave_max(amax);
+    smax = wave_max(smax);
     if (lane == 0)
-        red[wv] = amax;
+        red[wv] = amax, red[4 + wv] = smax;
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    smax = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+    // e: elements within F16_SAFE and group sums (at most ks * smax, up to
+    // rounding) within 32768, so that their f16 hi parts stay finite; a
+    // power of two scales every element and sum exactly
+    const float r = fmaxf(amax / F16_SAFE, smax * (float)ks / 32768.0f);
     int e = 0;
-    if (amax > F16_SAFE)
-        (void)frexpf(amax / F16_SAFE, &e); // amax * 2^-e <= F16_SAFE
+    if (r > 1.0f)
+        (void)frexpf(r, &e); // r * 2^-e < 1
     const float f = ldexpf(1.0f, -e);
+    const uint32_t G = cols / 64, GP = (G + 15) / 16 * 16;
+    uint16_t* const hl = sum_hl != nullptr ? sum_hl + (uint64_t)t * 2 * GP : nullptr;
     int any_lo = 0;
     // nb is a multiple of 4: the four blocks of 32 columns are on four
     // consecutive lanes, all present or all absent
@@ -263,7 +280,20 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
         s += __shfl_xor(s, 2);
         if ((lane & 3) == 0)
             sum32[(uint64_t)t * (cols / 32) + b / 4] = s;
+        if (hl != nullptr) {
+            // the group of 64 columns on 8 lanes (cols is a multiple of 64):
+            // its two sums of 32 added as the GEMMs add them, then hi + lo
+            const float g = s + __shfl_xor(s, 4);
+            if ((lane & 7) == 0) {
+                const _Float16 gh = (_Float16)g;
+                hl[b / 8] = __builtin_bit_cast(uint16_t, gh);
+                hl[GP + b / 8] = __builtin_bit_cast(uint16_t, (_Float16)(g - (float)gh));
+            }
+        }
     }
+    if (hl != nullptr)
+        for (uint32_t gi = G + threadIdx.x; gi < GP; gi += 256)
+            hl[gi] = 0, hl[GP + gi] = 0;
     any_lo = __syncthreads_or(any_lo);
     const uint32_t j = threadIdx.x;
     if (j < k + (ta.has_shared ? 1u : 0u)) {
@@ -295,6 +325,7 @@ struct GemmArgs {
     const uint16_t* b_hi;
     const uint16_t* b_lo;
     const float* b_sum32;
+    const uint16_t* b_sumhl;  // 128-token gate/up: group sums as f16 hi, lo (split_rows_kernel's sum_hl)
     const float* rowscale;    // gate/up: per grouped row; down: unused
     const uint32_t* b_lo_any; // gate/up: per grouped row, its B row's lo part is not all zero (null: assume it is not)
     uint32_t kdim;            // H (gate/up) or I (down)
@@ -795,6 +826,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
     // round trip instead of MAXS); loads of a slice past G read in-bounds
     // neighbouring data or zeros and are masked below
     constexpr int MAXS = KS >= 4 ? 1 : 2;
+    bool sum_range = false; // a group sum outside the f16 range of its hi part
     for (uint32_t k00 = 0; k00 < G; k00 += 16 * MAXS) {
         uint32_t b2[MAXS][NMAT][4]; // 8 consecutive 16-bit biases per slice (4-byte aligned: G is even)
         u32x4 v4[MAXS][2][2 * KS];  // sums per 32 columns of groups gb .. gb + 7
@@ -845,6 +877,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
                         v += __uint_as_float(v4[sl][tf][(j * KS + c) / 4][(j * KS + c) % 4]);
                     if (!bvalid || gb + j >= G)
                         v = 0.0f;
+                    sum_range |= !(fabsf(v) <= 65504.0f);
                     const _Float16 hv = (_Float16)v;
                     xh[j] = hv;
                     xl[j] = (_Float16)(v - (float)hv);
@@ -864,6 +897,8 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void q4_group_gemm_kernel(GemmArgs
             }
         }
     }
+    if (sum_range)
+        atomicOr(a.status, ST_F16_RANGE);
 
     // ---- epilogue: accumulator element (token 32tf + 8(j/4) + 4h + (j%4),
     //      row wv*32 + n32 of the block) -> f32 tile in LDS -> each thread
@@ -1145,6 +1180,11 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
     //      sums split into f16 hi + lo).  Run before the group loop, with the
     //      loop's first loads in flight: acc is the only live state then ----
     const rsrc_t sum_r = make_rsrc(a.b_sum32, a.b_rows * C32 * 4);
+    // gate/up: the group sums as f16 hi and lo, [row][hi: GP][lo: GP], zero
+    // past G (split_rows_kernel), so a slice's 8 groups are one 16-byte load
+    // each and a slice past G reads zeros
+    const uint32_t GP = (G + 15) / 16 * 16;
+    const rsrc_t hl_r = make_rsrc(a.b_sumhl, GATEUP ? a.b_rows * GP * 4 : 0u);
     auto bias_term = [&](auto ntf_tag) __attribute__((always_inline)) {
         constexpr int NTF = decltype(ntf_tag)::value;
         uint32_t rrow[NTF];
@@ -1166,13 +1206,19 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     b2[m][q] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff[m], b_soff[m] + gb * 2 + 4 * q, 0);
-            u32x4 v4[T1 - T0][2 * KS];
+            constexpr int NV = GATEUP ? 2 : 2 * KS; // 16-byte loads per fragment: hi, lo / f32 sums
+            u32x4 v4[T1 - T0][NV];
 #pragma unroll
             for (int tf = T0; tf < T1; ++tf)
 #pragma unroll
-                for (int q = 0; q < 2 * KS; ++q)
-                    v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(sum_r, rrow[tf] * C32 * 4,
-                                                                           (gb * KS + 4 * q) * 4, 0);
+                for (int q = 0; q < NV; ++q) {
+                    if constexpr (GATEUP)
+                        v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(hl_r, rrow[tf] * GP * 4,
+                                                                               (q * GP + gb) * 2, 0);
+                    else
+                        v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(sum_r, rrow[tf] * C32 * 4,
+                                                                               (gb * KS + 4 * q) * 4, 0);
+                }
             half8_t bw[2];
 #pragma unroll
             for (int m = 0; m < 2; ++m)
@@ -1189,17 +1235,23 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
 #pragma unroll
             for (int tf = T0; tf < T1; ++tf) {
                 half8_t xh, xl;
+                if constexpr (GATEUP) {
+                    // rows past the item read row 0: their outputs are never stored
+                    xh = __builtin_bit_cast(half8_t, v4[tf - T0][0]);
+                    xl = __builtin_bit_cast(half8_t, v4[tf - T0][1]);
+                } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    float v = 0.0f;
+                    for (int j = 0; j < 8; ++j) {
+                        float v = 0.0f;
 #pragma unroll
-                    for (int c = 0; c < KS; ++c)
-                        v += __uint_as_float(v4[tf - T0][(j * KS + c) / 4][(j * KS + c) % 4]);
-                    if (!bvalid[tf] || gb + j >= G)
-                        v = 0.0f;
-                    const _Float16 hv = (_Float16)v;
-                    xh[j] = hv;
-                    xl[j] = (_Float16)(v - (float)hv);
+                        for (int c = 0; c < KS; ++c)
+                            v += __uint_as_float(v4[tf - T0][(j * KS + c) / 4][(j * KS + c) % 4]);
+                        if (!bvalid[tf] || gb + j >= G)
+                            v = 0.0f;
+                        const _Float16 hv = (_Float16)v;
+                        xh[j] = hv;
+                        xl[j] = (_Float16)(v - (float)hv);
+                    }
                 }
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
@@ -1576,6 +1628,12 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
                 reinterpret_cast<uint4*>(a.act_lo + o)[q] = lq;
             }
             a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + rb * (WGR / 32) + c_chunk] = sum;
+            // the down GEMM's group sum (this chunk and its pair, on the
+            // neighbouring lane, added as the down GEMM adds them) splits
+            // into an f16 hi part: it must be in range too
+            const float gsum = sum + __shfl_xor(sum, 1);
+            if (!(fabsf(gsum) <= 65504.0f))
+                atomicOr(a.status, ST_F16_RANGE);
         }
     } else {
         // y [grouped row][H] f32: each wave turns its 64 rows of one 32-token
@@ -1781,8 +1839,8 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     const bool t128 = KS == 2 && use_t128(p, routes);
     const TileArgs ta{p.plan.unique_count, p.plan.groups, p.plan.unique_ids, has_shared, T, routes, p.tiles,
                       p.tile_count, t128 ? (uint32_t)TOK_L : (uint32_t)TOK};
-    split_rows_kernel<<<T + 1, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, p.rowscale, p.x_lo_any,
-                                             p.plan.out_idx, K, ta);
+    split_rows_kernel<<<T + 1, 256, 0, st>>>(p.x, H, p.x_hi, p.x_lo, p.x_sum32, t128 ? p.x_sumhl : nullptr,
+                                             (uint32_t)KS, p.rowscale, p.x_lo_any, p.plan.out_idx, K, ta);
     if ((err = hipGetLastError()) != hipSuccess)
         return err;
     if (has_shared && p.sgate_w) {
@@ -1818,6 +1876,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.b_hi = p.x_hi;
     a.b_lo = p.x_lo;
     a.b_sum32 = p.x_sum32;
+    a.b_sumhl = p.x_sumhl;
     a.rowscale = p.rowscale;
     a.b_lo_any = p.x_lo_any;
     a.kdim = H;

@@ -201,3 +201,43 @@ def test_prefill_out_of_range_route_is_reported(ctx):
         ctx.sync()
     assert e.value.status == abi.ERR_ROUTE
     ctx.sync()
+
+
+@pytest.mark.parametrize("case", ["x_group_offset", "constant_rows"])
+def test_prefill_group_sums_beyond_f16(ctx, case):
+    """Rows whose elements fit the f16 operands but whose sums over a
+    quantisation group do not: "x_group_offset" adds 1100 to one group of
+    64 columns (x group sum >= 70400; the split then scales the row by a
+    power of two until its group sums fit), "constant_rows" sets three rows
+    to 0.25 everywhere, so that each of their SwiGLU activations is about
+    2300 and a group of 64 of them sums to about 147000, beyond the f16 hi
+    part of the down GEMM's bias-term operand.  Either the result matches
+    the oracle or the call reports PBMOE_ERR_NONFINITE (an activation or a
+    sum of 64 activations beyond f16); a non-finite output without that
+    report fails.  (The synthetic expert weights have a group mean of about
+    0.09, so an x group sum beyond f16 drives the activations beyond f16 as
+    well: the first case ends in the report, like the second.)"""
+    _say(f"[test] prefill group sums beyond f16: {case}")
+    dl = _layer(ctx, C1)
+    T = 40
+    xh, rh = synth.activations(SEED, 307, T, C1.hidden)
+    for r in (3, 17, 38):
+        if case == "x_group_offset":
+            xh[r, 64 * (r % 32):64 * (r % 32) + 64] += np.float32(1100.0)
+        else:
+            xh[r, :] = np.float32(0.25)
+    x, ids, w = _routes(ctx, dl, xh)
+    res = ctx.to_device(rh)
+    out = ctx.array((T, C1.hidden), np.float32)
+    dl.moe.qwen_layer_major_experts(x, res, ids, w, out)
+    try:
+        ctx.sync()
+    except abi.PbmoeError as e:
+        assert e.status == abi.ERR_NONFINITE, e
+        _say(f"[result] {case}: f16-range error reported")
+        ctx.sync()
+        return
+    got = out.download()
+    assert np.all(np.isfinite(got)), f"{np.count_nonzero(~np.isfinite(got))} non-finite outputs, no error"
+    _check_rows(dl, xh, rh, ids.download().astype(np.int32), w.download(), got, np.arange(T),
+                tag=f"group sums beyond f16: {case}")
