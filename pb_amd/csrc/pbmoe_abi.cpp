@@ -1596,12 +1596,12 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     // multiple of 8 records (the GEMM workgroups read their record before
     // checking it against the tile count, and the grid covers max_tiles
     // rounded up to 8)
-    size_t off[13], total = 0;
-    const size_t part[13] = {
+    size_t off[14], total = 0;
+    const size_t part[14] = {
         (size_t)((max_tiles + 7) / 8 * 8) * 32, 4,     T * H * 2, T * H * 2, T * (H / 32) * 4, rows * 4, T * 4,
         rows * I * 2,          rows * I * 2, rows * (I / 32) * 4, rows * H * 4, rows * 4,
-        T * ((H / 64 + 15) / 16 * 16) * 4};
-    for (int i = 0; i < 13; ++i) {
+        T * ((H / 64 + 15) / 16 * 16) * 4, rows * ((I / 64 + 15) / 16 * 16) * 4};
+    for (int i = 0; i < 14; ++i) {
         off[i] = total;
         total += align256(part[i]);
     }
@@ -1644,6 +1644,7 @@ PBMOE_API int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x,
     a.y = reinterpret_cast<float*>(base + off[10]);
     a.x_lo_any = reinterpret_cast<uint32_t*>(base + off[11]);
     a.x_sumhl = reinterpret_cast<uint16_t*>(base + off[12]);
+    a.act_sumhl = reinterpret_cast<uint16_t*>(base + off[13]);
     a.status = ctx->status;
     a.phase_timing = ctx->phase_timing;
     for (int i = 0; i < 6; ++i)

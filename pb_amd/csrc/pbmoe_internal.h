@@ -160,6 +160,7 @@ struct PrefillArgs {
     uint16_t* act_hi;          // [T*K + T][I] f16
     uint16_t* act_lo;          // [T*K + T][I] f16
     float* act_sum32;          // [T*K + T][I/32]
+    uint16_t* act_sumhl;       // [T*K + T][2][GP] f16 group sums hi, lo (GP = I/64 rounded up to 16)
     float* y;                  // [T*K + T][H]
     uint32_t* status;
     hipEvent_t phase_ev[6];    // start/stop of gate/up, down, combine

@@ -325,7 +325,7 @@ struct GemmArgs {
     const uint16_t* b_hi;
     const uint16_t* b_lo;
     const float* b_sum32;
-    const uint16_t* b_sumhl;  // 128-token gate/up: group sums as f16 hi, lo (split_rows_kernel's sum_hl)
+    const uint16_t* b_sumhl;  // 128-token GEMMs: group sums as f16 hi, lo [b_rows][hi: GP][lo: GP]
     const float* rowscale;    // gate/up: per grouped row; down: unused
     const uint32_t* b_lo_any; // gate/up: per grouped row, its B row's lo part is not all zero (null: assume it is not)
     uint32_t kdim;            // H (gate/up) or I (down)
@@ -334,7 +334,8 @@ struct GemmArgs {
     // outputs
     uint16_t* act_hi;         // [routes + T][I]
     uint16_t* act_lo;
-    float* act_sum32;         // [routes + T][I/32]
+    float* act_sum32;         // [routes + T][I/32] (64-token gate/up)
+    uint16_t* act_sumhl;      // [routes + T][2][GP] (128-token gate/up: the down GEMM's b_sumhl)
     float* y;                 // [routes + T][H]
     uint32_t* status;
 };
@@ -1179,21 +1180,19 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
     //      (K' = groups in slices of 16, lane half h: groups k0 + 8h .. +8;
     //      sums split into f16 hi + lo).  Run before the group loop, with the
     //      loop's first loads in flight: acc is the only live state then ----
-    const rsrc_t sum_r = make_rsrc(a.b_sum32, a.b_rows * C32 * 4);
-    // gate/up: the group sums as f16 hi and lo, [row][hi: GP][lo: GP], zero
-    // past G (split_rows_kernel), so a slice's 8 groups are one 16-byte load
-    // each and a slice past G reads zeros
+    // the group sums as f16 hi and lo, [row][hi: GP][lo: GP], zero past G
+    // (written by split_rows_kernel for gate/up, by the gate/up epilogue for
+    // down), so a slice's 8 groups are one 16-byte load each and a slice
+    // past G reads zeros
     const uint32_t GP = (G + 15) / 16 * 16;
-    const rsrc_t hl_r = make_rsrc(a.b_sumhl, GATEUP ? a.b_rows * GP * 4 : 0u);
+    const rsrc_t hl_r = make_rsrc(a.b_sumhl, a.b_rows * GP * 4);
     auto bias_term = [&](auto ntf_tag) __attribute__((always_inline)) {
         constexpr int NTF = decltype(ntf_tag)::value;
         uint32_t rrow[NTF];
-        bool bvalid[NTF];
 #pragma unroll
         for (int tf = 0; tf < NTF; ++tf) {
             const uint32_t brow = row_lds[32 * tf + n32];
-            bvalid[tf] = brow != 0xFFFFFFFFu;
-            rrow[tf] = bvalid[tf] ? brow : 0u;
+            rrow[tf] = brow != 0xFFFFFFFFu ? brow : 0u;
         }
         // slice k00 for fragments T0 .. T1 - 1 (FIRST: k00 = 0, which sets acc)
         auto slice = [&](uint32_t k00, auto first_tag, auto t0_tag, auto t1_tag) __attribute__((always_inline)) {
@@ -1206,19 +1205,13 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     b2[m][q] = __builtin_amdgcn_raw_buffer_load_b32(wr, sb_voff[m], b_soff[m] + gb * 2 + 4 * q, 0);
-            constexpr int NV = GATEUP ? 2 : 2 * KS; // 16-byte loads per fragment: hi, lo / f32 sums
-            u32x4 v4[T1 - T0][NV];
+            u32x4 v4[T1 - T0][2]; // hi, lo of groups gb .. gb + 7
 #pragma unroll
             for (int tf = T0; tf < T1; ++tf)
 #pragma unroll
-                for (int q = 0; q < NV; ++q) {
-                    if constexpr (GATEUP)
-                        v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(hl_r, rrow[tf] * GP * 4,
-                                                                               (q * GP + gb) * 2, 0);
-                    else
-                        v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(sum_r, rrow[tf] * C32 * 4,
-                                                                               (gb * KS + 4 * q) * 4, 0);
-                }
+                for (int q = 0; q < 2; ++q)
+                    v4[tf - T0][q] = __builtin_amdgcn_raw_buffer_load_b128(hl_r, rrow[tf] * GP * 4,
+                                                                           (q * GP + gb) * 2, 0);
             half8_t bw[2];
 #pragma unroll
             for (int m = 0; m < 2; ++m)
@@ -1234,25 +1227,9 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
                 }
 #pragma unroll
             for (int tf = T0; tf < T1; ++tf) {
-                half8_t xh, xl;
-                if constexpr (GATEUP) {
-                    // rows past the item read row 0: their outputs are never stored
-                    xh = __builtin_bit_cast(half8_t, v4[tf - T0][0]);
-                    xl = __builtin_bit_cast(half8_t, v4[tf - T0][1]);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        float v = 0.0f;
-#pragma unroll
-                        for (int c = 0; c < KS; ++c)
-                            v += __uint_as_float(v4[tf - T0][(j * KS + c) / 4][(j * KS + c) % 4]);
-                        if (!bvalid[tf] || gb + j >= G)
-                            v = 0.0f;
-                        const _Float16 hv = (_Float16)v;
-                        xh[j] = hv;
-                        xl[j] = (_Float16)(v - (float)hv);
-                    }
-                }
+                // rows past the item read row 0: their outputs are never stored
+                const half8_t xh = __builtin_bit_cast(half8_t, v4[tf - T0][0]);
+                const half8_t xl = __builtin_bit_cast(half8_t, v4[tf - T0][1]);
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     float16_t c;
@@ -1627,13 +1604,23 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
                 reinterpret_cast<uint4*>(a.act_hi + o)[q] = hq;
                 reinterpret_cast<uint4*>(a.act_lo + o)[q] = lq;
             }
-            a.act_sum32[(uint64_t)(g0 + n) * (I / 32) + rb * (WGR / 32) + c_chunk] = sum;
-            // the down GEMM's group sum (this chunk and its pair, on the
-            // neighbouring lane, added as the down GEMM adds them) splits
-            // into an f16 hi part: it must be in range too
+            // the down GEMM's bias-term operand: the group sum (this chunk
+            // and its pair on the neighbouring lane) as f16 hi + lo, in
+            // range like the activations; zeros for the groups past I/64
             const float gsum = sum + __shfl_xor(sum, 1);
             if (!(fabsf(gsum) <= 65504.0f))
                 atomicOr(a.status, ST_F16_RANGE);
+            const uint32_t GI = I / 64, GPI = (GI + 15) / 16 * 16;
+            uint16_t* const hl = a.act_sumhl + (uint64_t)(g0 + n) * 2 * GPI;
+            if ((c_chunk & 1) == 0) {
+                const uint32_t gi = rb * (WGR / 64) + c_chunk / 2;
+                const _Float16 gh = (_Float16)gsum;
+                hl[gi] = __builtin_bit_cast(uint16_t, gh);
+                hl[GPI + gi] = __builtin_bit_cast(uint16_t, (_Float16)(gsum - (float)gh));
+            }
+            if (rb == RB - 1 && c_chunk == 0)
+                for (uint32_t gi = GI; gi < GPI; ++gi)
+                    hl[gi] = 0, hl[GPI + gi] = 0;
         }
     } else {
         // y [grouped row][H] f32: each wave turns its 64 rows of one 32-token
@@ -1884,6 +1871,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.act_hi = p.act_hi;
     a.act_lo = p.act_lo;
     a.act_sum32 = p.act_sum32;
+    a.act_sumhl = p.act_sumhl;
     a.lo_delta = (uint32_t)((const uint8_t*)p.x_lo - (const uint8_t*)p.x_hi);
     const uint32_t tiles128 = max_tiles_of(TOK_L, T, K, ex.count, has_shared != 0);
     if (t128)
@@ -1896,6 +1884,7 @@ static hipError_t launch_prefill_typed(hipStream_t st, const PrefillArgs& p)
     a.b_hi = p.act_hi;
     a.b_lo = p.act_lo;
     a.b_sum32 = p.act_sum32;
+    a.b_sumhl = p.act_sumhl;
     a.rowscale = nullptr;
     a.b_lo_any = nullptr;
     a.kdim = I;
