@@ -57,6 +57,7 @@ int ok()
 
 // Limits of the current kernels (explicitly rejected beyond them).
 constexpr uint32_t MAX_EXPERTS = 1024;
+static_assert(MAX_EXPERTS + 1 <= pbmoe::TILE_TABLE_MAX_ITEMS, "prefill tile table too small");
 constexpr uint32_t MAX_K = 16;
 constexpr uint32_t MAX_DECODE_TOKENS = 16;
 constexpr uint32_t MAX_PREFILL_TOKENS = 32768;

@@ -168,6 +168,8 @@ struct PrefillArgs {
 };
 
 uint32_t prefill_max_tiles(uint32_t tokens, uint32_t k, uint32_t experts, bool has_shared);
+// items (used experts + the shared expert) the prefill tile table holds
+constexpr uint32_t TILE_TABLE_MAX_ITEMS = 1280;
 hipError_t launch_prefill(hipStream_t s, const PrefillArgs& p);
 
 hipError_t launch_q4_dequantize(hipStream_t s, const uint8_t* packed, const void* scales,

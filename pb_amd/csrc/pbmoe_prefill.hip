@@ -124,14 +124,44 @@ struct TileArgs {
 // row and token count, the expert slot (all ones: the shared expert), 3 unused
 constexpr int TILE_REC = 8;
 
-__device__ void tile_table_wave(const TileArgs& a)
+// Tile table, by one 256-thread workgroup: the items' token counts, first
+// grouped rows and expert slots are loaded into LDS first (one round trip
+// after the item count, every load issued at once), then wave 0 writes the
+// records class by class (loaded inside its loop, each class and chunk of
+// 64 items waited for its own loads: ~20 dependent round trips).
+constexpr uint32_t TT_PER_THREAD = (TILE_TABLE_MAX_ITEMS + 255) / 256;
+__device__ void tile_table_block(const TileArgs& a)
 {
+    __shared__ uint32_t t_cnt[TILE_TABLE_MAX_ITEMS], t_g0[TILE_TABLE_MAX_ITEMS], t_e[TILE_TABLE_MAX_ITEMS];
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t* groups = a.groups;
     const uint32_t has_shared = a.has_shared, tokens = a.tokens;
     uint32_t* tiles = a.tiles;
     const uint32_t U = a.unique_count[0];
-    const uint32_t items = U + has_shared;
+    const uint32_t items = U + has_shared; // <= experts + 1 <= TILE_TABLE_MAX_ITEMS (the ABI's limit)
+    {
+        // clamped indices, no branch around the loads (a load inside a
+        // divergent branch is waited for where the branch ends)
+        uint32_t c[TT_PER_THREAD], g[TT_PER_THREAD], e[TT_PER_THREAD];
+        const uint32_t last = U > 0 ? U - 1 : 0;
+#pragma unroll
+        for (int k = 0; k < (int)TT_PER_THREAD; ++k) {
+            const uint32_t u = min(threadIdx.x + 256u * k, last);
+            g[k] = a.groups[2 * u];
+            c[k] = a.groups[2 * u + 1];
+            e[k] = a.unique_ids[u];
+        }
+#pragma unroll
+        for (int k = 0; k < (int)TT_PER_THREAD; ++k) {
+            const uint32_t u = threadIdx.x + 256u * k;
+            if (u < U)
+                t_cnt[u] = c[k], t_g0[u] = g[k], t_e[u] = e[k];
+            else if (u < items) // the shared expert: every token, rows after the routes
+                t_cnt[u] = tokens, t_g0[u] = a.routes, t_e[u] = 0xFFFFFFFFu;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x >= 64)
+        return;
     const uint32_t nfrag = a.tok / 32;
     uint32_t base = 0;
     // class 0: full tiles; class c = 1 .. nfrag: the partial tile with
@@ -139,11 +169,7 @@ __device__ void tile_table_wave(const TileArgs& a)
     for (uint32_t c = 0; c <= nfrag; ++c) {
         for (uint32_t u0 = 0; u0 < items; u0 += 64) {
             const uint32_t u = u0 + lane;
-            uint32_t cnt = 0;
-            if (u < U)
-                cnt = groups[2 * u + 1];
-            else if (u < items)
-                cnt = tokens;
+            const uint32_t cnt = u < items ? t_cnt[u] : 0u;
             const uint32_t full = cnt / a.tok, rest = cnt % a.tok;
             uint32_t nt;
             if (c == 0)
@@ -159,8 +185,7 @@ __device__ void tile_table_wave(const TileArgs& a)
             }
             const uint32_t first = base + inc - nt;
             if (nt) {
-                const uint32_t g0 = u < U ? groups[2 * u] : a.routes;
-                const uint32_t e = u < U ? a.unique_ids[u] : 0xFFFFFFFFu;
+                const uint32_t g0 = t_g0[u], e = t_e[u];
                 for (uint32_t j = 0; j < nt; ++j) {
                     uint4* rec = reinterpret_cast<uint4*>(tiles + TILE_REC * (first + j));
                     rec[0] = make_uint4(u, c == 0 ? j * a.tok : full * a.tok, g0, cnt);
@@ -220,8 +245,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     // the tile table in the first workgroup, which starts before the token
     // rows' workgroups and runs beside them (it needs the plan only)
     if (blockIdx.x == 0) {
-        if (threadIdx.x < 64)
-            tile_table_wave(ta);
+        tile_table_block(ta);
         return;
     }
     __shared__ float red[8];
@@ -1103,7 +1127,7 @@ __global__ __launch_bounds__(GL_THREADS, WPC) void q4_gemm_t128_kernel(GemmArgs 
     const uint8_t* const slot = shared ? a.sh.base : a.ex.base + (uint64_t)e * a.ex.stride;
     const ExpertSet& set = shared ? a.sh : a.ex;
     const uint32_t K = a.kdim;
-    const uint32_t G = K / (32 * KS), C32 = K / 32, WPR = K / 8;
+    const uint32_t G = K / (32 * KS), WPR = K / 8;
     auto tok_row = [&](uint32_t n) __attribute__((always_inline)) -> uint32_t {
         return GATEUP ? (shared ? n : a.src_rows[g0 + n]) : g0 + n;
     };
