@@ -1965,8 +1965,9 @@ static bool route_separately(const DecodeArgs& d)
     return wgs > GATEUP_RESIDENT_WGS;
 }
 
-// resident workgroups of gateup_multi_kernel per CU
-constexpr uint32_t MULTI_WGS_PER_CU = 4;
+// resident workgroups of gateup_multi_kernel per CU, by its registers:
+// one chunk per lane (95 VGPRs) 5 waves per SIMD, two or four (140-146) 3
+static uint32_t multi_wgs_per_cu(uint32_t cpl) { return cpl <= 1 ? 5u : 3u; }
 // workgroups of down_rows_kernel per CU (its registers allow two; more only
 // wait)
 constexpr uint32_t ROWS_WGS_PER_CU = 2;
@@ -2000,7 +2001,7 @@ static hipError_t launch_gateup_multi(hipStream_t st, const DecodeArgs& d, bool 
     ea.status = d.status;
     const uint32_t cpl = (H / 32 + 63) / 64;
     const uint32_t rpw = cpl <= 2 ? 2u : 1u;
-    const uint32_t wgs_cu = cpl <= 2 ? MULTI_WGS_PER_CU : 3u;
+    const uint32_t wgs_cu = multi_wgs_per_cu(cpl);
     const uint32_t units = K * (I / rpw); // per token
     const uint32_t per_token = std::max(1u, std::min((units + 3) / 4, 256u * wgs_cu / T));
     const dim3 g1(per_token, T);
