@@ -387,64 +387,122 @@ __global__ __launch_bounds__(PLAN_WAVES * 64) void plan_count_kernel(
         cnt[(uint64_t)blockIdx.x * experts + e] = c[e];
 }
 
+// P = 1024 / experts threads per expert (a power of two, at most 64, the
+// lanes of one wave): thread (e, p) takes a contiguous range of blocks, so
+// every count is loaded once, in one round trip when a range holds at most
+// PLAN_SCAN_NB blocks (kept in registers for the bases); the prefix over
+// experts is a wave scan plus the sums of the earlier waves.
+constexpr uint32_t PLAN_SCAN_NB = 16;
 __global__ __launch_bounds__(PLAN_MAX_E) void plan_scan_kernel(const uint32_t* __restrict__ cnt,
                                                               uint32_t nblk, uint32_t experts, Plan plan,
                                                               uint32_t* __restrict__ base,
                                                               uint32_t* __restrict__ slot_of)
 {
-    __shared__ uint32_t sa[PLAN_MAX_E], sb[PLAN_MAX_E];
-    const uint32_t e = threadIdx.x;
-    constexpr uint32_t NB = 16; // block counts loaded together
-    uint32_t run = 0;
-    if (e < experts) {
-        for (uint32_t b0 = 0; b0 < nblk; b0 += NB) {
-            uint32_t v[NB];
+    __shared__ uint32_t tot[PLAN_MAX_E], start[PLAN_MAX_E], wtot[PLAN_MAX_E / 64][2];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t P = 1;
+    while (P < 64 && 2 * P * experts <= PLAN_MAX_E)
+        P *= 2;
+    const uint32_t e = tid / P, p = tid % P;
+    const uint32_t per = (nblk + P - 1) / P;
+    const uint32_t b0 = min(nblk, p * per), b1 = min(nblk, b0 + per);
+    const bool live = e < experts;
+    const bool held = per <= PLAN_SCAN_NB; // the range's counts stay in registers
+    uint32_t v[PLAN_SCAN_NB];
+    uint32_t part = 0;
+    if (held) {
 #pragma unroll
-            for (uint32_t j = 0; j < NB; ++j)
-                v[j] = b0 + j < nblk ? cnt[(uint64_t)(b0 + j) * experts + e] : 0u;
+        for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j) {
+            const uint32_t b = b0 + j;
+            v[j] = live && b < b1 ? cnt[(uint64_t)b * experts + e] : 0u;
+        }
 #pragma unroll
-            for (uint32_t j = 0; j < NB; ++j)
-                run += v[j];
+        for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j)
+            part += v[j];
+    } else if (live) {
+        for (uint32_t c0 = b0; c0 < b1; c0 += PLAN_SCAN_NB) {
+            uint32_t w[PLAN_SCAN_NB];
+#pragma unroll
+            for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j)
+                w[j] = c0 + j < b1 ? cnt[(uint64_t)(c0 + j) * experts + e] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j)
+                part += w[j];
         }
     }
-    sa[e] = run;
-    sb[e] = run > 0 ? 1u : 0u;
+    // exclusive prefix of the parts within the expert's P lanes, and its total
+    uint32_t incl = part;
+    for (uint32_t o = 1; o < P; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o);
+        if (p >= o)
+            incl += y;
+    }
+    const uint32_t run = __shfl(incl, (int)(lane | (P - 1))); // the group's last lane: the expert's count
+    const uint32_t before = incl - part;
+    if (p == 0 && live)
+        tot[e] = run;
     __syncthreads();
-    for (uint32_t off = 1; off < PLAN_MAX_E; off <<= 1) {
-        const uint32_t va = sa[e] + (e >= off ? sa[e - off] : 0u);
-        const uint32_t vb = sb[e] + (e >= off ? sb[e - off] : 0u);
-        __syncthreads();
-        sa[e] = va;
-        sb[e] = vb;
-        __syncthreads();
+    // per expert (one per thread): start = counts of the experts before,
+    // slot = used experts before
+    const uint32_t r = tid < experts ? tot[tid] : 0u;
+    uint32_t ir = r, iu = r > 0 ? 1u : 0u;
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t yr = __shfl_up(ir, o), yu = __shfl_up(iu, o);
+        if (lane >= o)
+            ir += yr, iu += yu;
     }
-    const uint32_t start = sa[e] - run;
-    if (e < experts) {
+    if (lane == 63)
+        wtot[wv][0] = ir, wtot[wv][1] = iu;
+    __syncthreads();
+    uint32_t pr = 0, pu = 0, all_u = 0;
+    for (uint32_t w = 0; w < PLAN_MAX_E / 64; ++w) {
+        if (w < wv)
+            pr += wtot[w][0], pu += wtot[w][1];
+        all_u += wtot[w][1];
+    }
+    if (tid < experts) {
+        const uint32_t st = pr + ir - r;
         uint32_t sl = 0xFFFFFFFFu;
-        if (run > 0) {
-            sl = sb[e] - 1u;
-            plan.unique_ids[sl] = e;
-            plan.groups[2 * sl] = start;
-            plan.groups[2 * sl + 1] = run;
+        if (r > 0) {
+            sl = pu + iu - 1u;
+            plan.unique_ids[sl] = tid;
+            plan.groups[2 * sl] = st;
+            plan.groups[2 * sl + 1] = r;
         }
-        slot_of[e] = sl;
-        // absolute base of every block: start + the counts of the blocks before
-        uint32_t acc = start;
-        for (uint32_t b0 = 0; b0 < nblk; b0 += NB) {
-            uint32_t v[NB];
+        slot_of[tid] = sl;
+        start[tid] = st;
+    }
+    if (tid == 0)
+        plan.unique_count[0] = all_u;
+    __syncthreads();
+    // absolute base of every block: the expert's start + the counts of its
+    // blocks before
+    if (live) {
+        uint32_t acc = start[e] + before;
+        if (held) {
 #pragma unroll
-            for (uint32_t j = 0; j < NB; ++j)
-                v[j] = b0 + j < nblk ? cnt[(uint64_t)(b0 + j) * experts + e] : 0u;
-#pragma unroll
-            for (uint32_t j = 0; j < NB; ++j)
-                if (b0 + j < nblk) {
-                    base[(uint64_t)(b0 + j) * experts + e] = acc;
+            for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j) {
+                const uint32_t b = b0 + j;
+                if (b < b1) {
+                    base[(uint64_t)b * experts + e] = acc;
                     acc += v[j];
                 }
+            }
+        } else {
+            for (uint32_t c0 = b0; c0 < b1; c0 += PLAN_SCAN_NB) {
+                uint32_t w[PLAN_SCAN_NB];
+#pragma unroll
+                for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j)
+                    w[j] = c0 + j < b1 ? cnt[(uint64_t)(c0 + j) * experts + e] : 0u;
+#pragma unroll
+                for (uint32_t j = 0; j < PLAN_SCAN_NB; ++j)
+                    if (c0 + j < b1) {
+                        base[(uint64_t)(c0 + j) * experts + e] = acc;
+                        acc += w[j];
+                    }
+            }
         }
     }
-    if (e == 0)
-        plan.unique_count[0] = sb[PLAN_MAX_E - 1];
 }
 
 __global__ __launch_bounds__(PLAN_WAVES * 64) void plan_place_kernel(
