@@ -910,7 +910,7 @@ def main() -> int:
                 "kernels_us": {k: round(v, 3) for k, v in leg["phase_us"].items()},
                 "spread": leg["spread"], "timing": leg["timing"]}
         pargs = argparse.Namespace(**vars(args))
-        pargs.tokens, pargs.steps, pargs.warmup = 1, 20, 3
+        pargs.tokens, pargs.steps, pargs.warmup = 1, 40, 20
         pargs.cpu_seconds = min(args.cpu_seconds, 4.0)
         from pb_amd.configs import C3
         prec = bench_prefill(pargs, C3, ctx, ev)
