@@ -337,26 +337,35 @@ __global__ __launch_bounds__(CHUNK_THREADS<NH>) void attn_chunk_kernel(AttnArgs 
 
 // merge the chunk partials of one q head: out = sum_c e^(m_c - M) o_c /
 // sum_c e^(m_c - M) l_c, i.e. softmax over every position (softmax_in_place,
-// math.rs:728-744) then the weighted sum of values.  Two threads per dim,
-// each over every other chunk.  The partials were just written by other
-// XCDs, so every round trip is slow: the values of the first MERGE_BLOCK
-// chunks are loaded together with the (m, l) pairs, before any reduction.
+// math.rs:728-744) then the weighted sum of values.  Workgroup (head h,
+// slice y) takes MERGE_DIMS of the head's dims, MERGE_PARTS threads per dim
+// (each over every MERGE_PARTS-th chunk), so that the head's loads spread
+// over MERGE_SPLIT CUs.  The partials were just written by other XCDs, so
+// every round trip is slow: the values of the first MERGE_BLOCK chunks are
+// loaded together with the (m, l) pairs, before any reduction.
 constexpr uint32_t MERGE_MAX_CHUNKS = 1024; // max_context / ATTN_CHUNK (65536 positions)
 constexpr int MERGE_BLOCK = 64;             // chunks whose values are loaded up front
+// workgroups per head (C4 stack, 32 heads at context 4096: 1 / 2 / 4 / 8
+// per head 1.943 / 1.884 / 1.848 / 1.838 ms per token)
+constexpr int MERGE_SPLIT = 8;
+constexpr int MERGE_DIMS = HD / MERGE_SPLIT;            // dims per workgroup
+constexpr int MERGE_PARTS = 256 / MERGE_DIMS;           // threads per dim
+static_assert(MERGE_DIMS * MERGE_PARTS == 256 && MERGE_BLOCK % MERGE_PARTS == 0, "merge tiling");
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, uint32_t chunks,
                                                          float* __restrict__ out)
 {
     __shared__ float ec[MERGE_MAX_CHUNKS];
     __shared__ float red[8];
-    __shared__ float half_acc[HD];
+    __shared__ float part_acc[MERGE_PARTS][MERGE_DIMS];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* ph = part + (uint64_t)h * chunks * (HD + 2);
-    const uint32_t d = tid & (HD - 1), part_i = tid / HD; // two threads per dim
-    constexpr int PV = MERGE_BLOCK / 2;
+    const uint32_t dl = tid % MERGE_DIMS, part_i = tid / MERGE_DIMS;
+    const uint32_t d = blockIdx.y * MERGE_DIMS + dl;
+    constexpr int PV = MERGE_BLOCK / MERGE_PARTS;
     float val[PV];
 #pragma unroll
     for (int u = 0; u < PV; ++u) {
-        const uint32_t c = part_i + 2 * u;
+        const uint32_t c = part_i + MERGE_PARTS * u;
         val[u] = c < chunks ? ph[(uint64_t)c * (HD + 2) + d] : 0.0f;
     }
     float m = -INFINITY;
@@ -394,18 +403,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < PV; ++u) {
-        const uint32_t c = part_i + 2 * u;
+        const uint32_t c = part_i + MERGE_PARTS * u;
         if (c < chunks)
             acc[u & 3] = fmaf(ec[c], val[u], acc[u & 3]);
     }
-    for (uint32_t c = part_i + MERGE_BLOCK; c < chunks; c += 2) // long contexts
+    for (uint32_t c = part_i + MERGE_BLOCK; c < chunks; c += MERGE_PARTS) // long contexts
         acc[0] = fmaf(ec[c], ph[(uint64_t)c * (HD + 2) + d], acc[0]);
-    const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    if (part_i == 1)
-        half_acc[d] = sum;
+    part_acc[part_i][dl] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     __syncthreads();
-    if (part_i == 0)
-        out[(uint64_t)h * HD + d] = (sum + half_acc[d]) / L;
+    if (part_i == 0) {
+        float sum = part_acc[0][dl];
+#pragma unroll
+        for (int q = 1; q < MERGE_PARTS; ++q)
+            sum += part_acc[q][dl];
+        out[(uint64_t)h * HD + d] = sum / L;
+    }
 }
 
 // RMSNorm with weight, one workgroup: rms_norm_with_weight_and_epsilon
@@ -504,7 +516,7 @@ hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
     // 3. merge
     if (chunks > MERGE_MAX_CHUNKS)
         return hipErrorInvalidValue;
-    hipExtLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads), dim3(256), 0, st, a.ev[4], a.ev[5], 0,
+    hipExtLaunchKernelGGL(attn_merge_kernel, dim3(a.q_heads, MERGE_SPLIT), dim3(256), 0, st, a.ev[4], a.ev[5], 0,
                           (const float*)a.part, chunks, a.attn_out);
     if ((e = hipGetLastError()) != hipSuccess)
         return e;
