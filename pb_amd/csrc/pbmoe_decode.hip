@@ -2155,7 +2155,6 @@ static hipError_t launch_experts_typed(hipStream_t st, const DecodeArgs& d, bool
                             I >= 1024 && I <= 2048 && H % WIDE_R == 0;
     const bool multi_gu = wide_shape && H <= 64 * 32 * 4 && (T > 1 || !route_here);
     const bool wide = wide_shape && (T == 1 || multi_gu);
-    const uint32_t max_items = use_plan ? std::min(ex.count, T * K) : T * K;
     ExpertArgs ea{};
     ea.ex = ex;
     ea.logits = d.logits;
