@@ -466,7 +466,7 @@ static hipError_t launch_rows(hipStream_t st, const RowsArgs& r, hipEvent_t e0, 
 
 // rows per wave: 2 for q/k/v (640 workgroups at C4), 1 for o_proj (512
 // workgroups instead of 256; measured on the C4 stack: 1.134 -> 1.079 ms of
-// attention per token; 4 for either was slower)
+// attention per token; 4 for either was slower, 1 for q/k/v the same)
 constexpr int RPW_QKV = 2, RPW_O = 1;
 
 hipError_t launch_attention_decode(hipStream_t st, const AttnArgs& a)
