@@ -518,6 +518,14 @@ __global__ __launch_bounds__(PLAN_WAVES * 64) void plan_place_kernel(
     const bool valid = r < routes;
     const uint32_t e = valid ? ids[r] : 0xFFFFFFFFu;
     const bool in_range = valid && e < experts;
+    // this block's bases (the scan's output), loaded beside the ids rather
+    // than after the two barriers below (experts <= 2 * PLAN_CHUNK)
+    uint32_t bpre[PLAN_MAX_E / PLAN_CHUNK];
+#pragma unroll
+    for (int j = 0; j < (int)(PLAN_MAX_E / PLAN_CHUNK); ++j) {
+        const uint32_t x = min(tid + (uint32_t)nthr * j, experts - 1);
+        bpre[j] = base[(uint64_t)blockIdx.x * experts + x];
+    }
     for (int i = tid; i < PLAN_WAVES * PLAN_MAX_E; i += nthr)
         (&wcnt[0][0])[i] = 0;
     for (uint32_t x = tid; x < experts; x += nthr)
@@ -527,8 +535,12 @@ __global__ __launch_bounds__(PLAN_WAVES * 64) void plan_place_kernel(
         atomicAdd(&wcnt[wv][e], 1u);
     __syncthreads();
     // per expert: the block's absolute base, then the exclusive prefix over waves
-    for (uint32_t x = tid; x < experts; x += nthr) {
-        uint32_t run = base[(uint64_t)blockIdx.x * experts + x];
+#pragma unroll
+    for (int j = 0; j < (int)(PLAN_MAX_E / PLAN_CHUNK); ++j) {
+        const uint32_t x = tid + (uint32_t)nthr * j;
+        if (x >= experts)
+            break;
+        uint32_t run = bpre[j];
         for (int w = 0; w < PLAN_WAVES; ++w) {
             const uint32_t c = wcnt[w][x];
             wcnt[w][x] = run;

@@ -254,15 +254,30 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     const float4* xr = reinterpret_cast<const float4*>(x + (uint64_t)t * cols);
     const uint32_t nb = cols / 8;
     float amax = 0.0f, smax = 0.0f;
-    for (uint32_t b = threadIdx.x; b < nb; b += 256) {
-        const float4 p = xr[2 * b], q = xr[2 * b + 1];
+    // the thread's first NBR blocks stay in registers for the second pass
+    // (cols <= 8192), loaded unconditionally (clamped) so that every load is
+    // in flight at once; blocks past them are read again there (L2 hits)
+    constexpr int NBR = 4;
+    float4 pr[NBR], qr[NBR];
+#pragma unroll
+    for (int k = 0; k < NBR; ++k) {
+        const uint32_t b = min(threadIdx.x + 256u * k, nb - 1);
+        pr[k] = xr[2 * b], qr[k] = xr[2 * b + 1];
+    }
+    auto first = [&](const float4 p, const float4 q) __attribute__((always_inline)) {
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w))));
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
         float s = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
         s += __shfl_xor(s, 1);
         s += __shfl_xor(s, 2);
         smax = fmaxf(smax, fabsf(s));
-    }
+    };
+#pragma unroll
+    for (int k = 0; k < NBR; ++k)
+        if (threadIdx.x + 256u * k < nb)
+            first(pr[k], qr[k]);
+    for (uint32_t b = threadIdx.x + 256u * NBR; b < nb; b += 256)
+        first(xr[2 * b], xr[2 * b + 1]);
     amax = wave_max(amax);
     smax = wave_max(smax);
     if (lane == 0)
@@ -283,8 +298,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     int any_lo = 0;
     // nb is a multiple of 4: the four blocks of 32 columns are on four
     // consecutive lanes, all present or all absent
-    for (uint32_t b = threadIdx.x; b < nb; b += 256) {
-        const float4 p = xr[2 * b], q = xr[2 * b + 1]; // L2 hits: read above
+    auto second = [&](uint32_t b, const float4 p, const float4 q) __attribute__((always_inline)) {
         const float v[8] = {p.x * f, p.y * f, p.z * f, p.w * f, q.x * f, q.y * f, q.z * f, q.w * f};
         uint32_t hw[4], lw[4];
         // K order inside the block: c0 c4 c1 c5 c2 c6 c3 c7 (word j = columns j, j + 4)
@@ -314,7 +328,15 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
                 hl[GP + b / 8] = __builtin_bit_cast(uint16_t, (_Float16)(g - (float)gh));
             }
         }
+    };
+#pragma unroll
+    for (int k = 0; k < NBR; ++k) {
+        const uint32_t b = threadIdx.x + 256u * k;
+        if (b < nb)
+            second(b, pr[k], qr[k]);
     }
+    for (uint32_t b = threadIdx.x + 256u * NBR; b < nb; b += 256)
+        second(b, xr[2 * b], xr[2 * b + 1]);
     if (hl != nullptr)
         for (uint32_t gi = G + threadIdx.x; gi < GP; gi += 256)
             hl[gi] = 0, hl[GP + gi] = 0;
