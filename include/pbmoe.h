@@ -358,8 +358,9 @@ int pbmoe_moe_layer_norm(pbmoe_ctx* ctx, uint32_t layer, const float* hidden,
  * metal/mod.rs:4015-4079).  Larger chunks build the dispatch plan on the
  * device and run the grouped expert GEMMs on the matrix cores (exact 4-bit
  * codes, activations as f16 hi + lo pairs), then the combine in route
- * order.  A SwiGLU activation beyond the f16 range (|a| > 65504) is
- * reported by pbmoe_sync as PBMOE_ERR_NONFINITE; the shared expert must
+ * order.  A SwiGLU activation beyond the f16 range (|a| > 65504), or a sum
+ * of 64 of them (the down GEMM's bias-term operand), is reported by
+ * pbmoe_sync as PBMOE_ERR_NONFINITE; the shared expert must
  * use the routed experts' group size and scale/bias dtype. */
 int pbmoe_moe_prefill(pbmoe_ctx* ctx, uint32_t layer, const float* x, const float* residual,
                       uint32_t tokens, const uint32_t* ids, const float* weights,
