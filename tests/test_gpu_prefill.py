@@ -26,6 +26,10 @@ T_G128 = MoeConfig("t_g128_bf16", hidden=1024, intermediate=512, experts=32, k=6
                    sb_dtype=abi.DTYPE_BF16)
 T_SHARED = MoeConfig("t_shared_bf16", hidden=512, intermediate=256, experts=16, k=4,
                      shared_intermediate=256, shared_gated=True, sb_dtype=abi.DTYPE_BF16)
+# the largest expert count (1024): up to 1024 + 1 items in the tile table,
+# and more than 2048 routes, so the multi-workgroup dispatch plan
+T_E1024 = MoeConfig("t_e1024", hidden=512, intermediate=256, experts=1024, k=8,
+                    shared_intermediate=256, shared_gated=True, sb_dtype=abi.DTYPE_F16)
 
 
 def _say(msg):
@@ -87,7 +91,7 @@ def _check_rows(dl, xh, rh, ids_h, w_h, got, rows, norm_h=None, got_n=None, tag=
 
 @pytest.mark.parametrize("cfg,T,with_norm", [(C1, 17, False), (C1, 200, True), (C2, 64, True),
                                              (T_G32, 100, False), (T_G128, 150, True),
-                                             (T_SHARED, 80, True)])
+                                             (T_SHARED, 80, True), (T_E1024, 600, False)])
 def test_prefill_matches_oracle(ctx, cfg, T, with_norm):
     _say(f"[test] prefill {cfg.name} T={T} norm={with_norm}")
     dl = _layer(ctx, cfg)
